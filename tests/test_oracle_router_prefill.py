@@ -1,0 +1,116 @@
+"""Pins the oracle's router and prefill restatements.
+
+Router (TsugumiKernelCheck/main.swift:384-402, moe.metal:281-329): on draws
+whose 8th/9th logit margin is far above fp32 noise the top-k must equal the
+fp64 brute-force top-k; explicit ties must resolve to the lower index; -inf
+and NaN never enter; softmax weights match fp64 closed form.
+
+Prefill reference (PrefillMoEGEMMCheck.swift:138-173): every partial must be
+within the fp16 roundings of the fp64 brute force; the token-major reduce
+(prefill.metal:796-817) is checked against its closed form.
+"""
+import numpy as np
+
+
+def test_router_reference_matches_fp64_topk(oracle):
+    rng = oracle.SplitMix64(31)
+    checked = 0
+    for draw in range(6):
+        w = oracle.bf16_to_float(rng.uniforms_bf16(-0.2, 0.2, 128 * 256)).reshape(128, 256)
+        x = oracle.f16_to_float(rng.uniforms_f16(-1.0, 1.0, 256))
+        pes = rng.uniforms(0.8, 1.2, 128)
+        idx, wts = oracle.router_reference(w, x, 8, pes)
+        logits = w.astype(np.float64) @ x.astype(np.float64)
+        order = np.lexsort((np.arange(128), -logits))
+        if logits[order[7]] - logits[order[8]] < 1e-4:
+            continue
+        checked += 1
+        assert list(idx) == list(order[:8])
+        top = logits[order[:8]]
+        e = np.exp(top - top.max())
+        assert np.allclose(wts, e / e.sum() * pes[order[:8]], rtol=1e-5)
+    assert checked >= 4
+
+
+def test_topk_ties_go_to_lower_index_and_nonfinite_never_enter(oracle):
+    logits = np.zeros(16, np.float32)
+    logits[[3, 9, 12]] = 2.0      # three-way tie above the rest
+    logits[5] = np.nan
+    logits[6] = -np.inf
+    logits[[1, 2, 4, 7, 8]] = 1.0  # five-way tie for the remaining slots
+    pes = np.ones(16, np.float32)
+    idx, w = oracle.topk_softmax(logits, 8, pes)
+    assert list(idx) == [3, 9, 12, 1, 2, 4, 7, 8]
+    wf = oracle.f16_to_float(w)
+    assert wf[0] == wf[1] == wf[2] and wf[3] == wf[7]
+    # all -inf: nothing enters, slots keep (0, -inf) exactly like the kernel
+    idx2, _ = oracle.topk_softmax(np.full(16, -np.inf, np.float32), 8, pes)
+    assert list(idx2) == [0] * 8
+
+
+def test_topk_softmax_matches_router_reference_order(oracle):
+    rng = oracle.SplitMix64(32)
+    for _ in range(20):
+        logits = rng.uniforms(-3, 3, 128)
+        pes = rng.uniforms(0.8, 1.2, 128)
+        i1, w1 = oracle.topk_softmax(logits, 8, pes)
+        order = np.lexsort((np.arange(128), -logits.astype(np.float64)))
+        assert list(i1) == list(order[:8])
+
+
+def _expert_blob(oracle, rng, d, f, group, symmetric, lo=-0.125, hi=0.125):
+    parts, offs, deq, cur = [], [], [], 0
+    for rows, cols in ((f, d), (f, d), (d, f)):
+        w = rng.uniforms(lo, hi, rows * cols).reshape(rows, cols)
+        p, s, b = oracle.quantize_int4(w, group, symmetric)
+        deq.append(oracle.dequantize_int4(p, s, b, cols, group).astype(np.float64))
+        for arr, is_bias in ((p, False), (s, False), (b, True)):
+            if is_bias and symmetric:
+                offs.append(offs[-1])
+                continue
+            raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
+            offs.append(cur)
+            parts.append(raw)
+            cur += raw.size
+    return np.concatenate(parts), np.array(offs, np.uint32), deq
+
+
+def test_prefill_reference_within_fp16_roundings_of_fp64(oracle):
+    rng = oracle.SplitMix64(33)
+    d, f, group, topk, t, ne = 128, 64, 32, 2, 6, 3
+    for symmetric in (True, False):
+        blobs, deqs = [], []
+        offs = None
+        for _ in range(ne):
+            b, offs, dq = _expert_blob(oracle, rng, d, f, group, symmetric)
+            blobs.append(b)
+            deqs.append(dq)
+        hidden = rng.uniforms_f16(-1.0, 1.0, t * d)
+        idx = np.array([[tok % ne, (tok + 1) % ne] for tok in range(t)], np.uint32)
+        pairs = oracle.make_token_expert_pairs(idx, np.zeros(t * topk, np.uint16), t, topk)
+        g = oracle.group_pairs(pairs, t, topk, ne)
+        P = oracle.prefill_moe_ref(blobs, offs, hidden, d, g["sorted_pairs"], topk, d, f,
+                                   group, symmetric)
+        x = oracle.f16_to_float(hidden).reshape(t, d).astype(np.float64)
+        for p in g["sorted_pairs"]:
+            gd, ud, dd = deqs[int(p["expert"])]
+            gx = gd @ x[p["token"]]
+            ux = ud @ x[p["token"]]
+            act = 0.5 * gx * (1 + np.tanh(0.7978845608028654 * (gx + 0.044715 * gx ** 3))) * ux
+            want = dd @ act
+            got = oracle.f16_to_float(P[p["token"] * topk + p["rank"]]).astype(np.float64)
+            # three fp16 roundings upstream (g, u, act) and one on the output
+            assert np.max(np.abs(got - want)) <= 4e-3 * np.max(np.abs(want)) + 1e-3
+
+
+def test_reduce_token_major_closed_form(oracle):
+    rng = oracle.SplitMix64(34)
+    t, k, d = 5, 8, 64
+    P = rng.uniforms_f16(-1, 1, t * k * d)
+    w = rng.uniforms_f16(0, 0.3, t * k)
+    h2 = oracle.reduce_token_major(P, w, t, k, d)
+    Pf = oracle.f16_to_float(P).reshape(t, k, d).astype(np.float64)
+    wf = oracle.f16_to_float(w).reshape(t, k).astype(np.float64)
+    want = np.einsum("tk,tkd->td", wf, Pf)
+    got = oracle.f16_to_float(h2)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0**-10 + 1e-6)
