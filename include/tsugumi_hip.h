@@ -1,0 +1,350 @@
+/*
+ * tsugumi_hip.h — C ABI of the MI355X (gfx950) int4 MoE expert-matmul path.
+ *
+ * Drop-in for the Swift encoders Tsugumi's decoder calls on this path. Each
+ * entry point replaces one `encode*` method (cited as reference file:line,
+ * relative to the he-be/tsugumi checkout). Conventions:
+ *
+ *  - All tensors are caller-owned DEVICE pointers (HBM), never copied. fp16
+ *    activations and bf16 scales travel as uint16_t bit patterns; packed int4
+ *    weights as bytes (low nibble = even element, high nibble = odd).
+ *  - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
+ *    default stream), the analogue of appending to an MTLCommandBuffer.
+ *  - Every call returns a tsg_status. Where the reference traps on a
+ *    precondition this returns TSG_ERR_INVALID_ARGUMENT (or _ALIGNMENT) and
+ *    enqueues nothing; where an optional fast path declines (returns 0/false
+ *    in Swift) this returns TSG_ERR_DECLINED. tsg_last_error() gives text
+ *    (thread-local).
+ *  - Objects (tsg_ctx, tsg_moe, tsg_layer) are not thread-safe; one encoding
+ *    thread per object, as with the reference's MetalContext/MoE.
+ */
+#ifndef TSUGUMI_HIP_H
+#define TSUGUMI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ types */
+
+typedef enum tsg_status {
+    TSG_OK = 0,
+    TSG_ERR_INVALID_ARGUMENT = 1, /* a reference precondition failed          */
+    TSG_ERR_ALIGNMENT = 2,        /* a pointer/offset breaks the kernel's alignment */
+    TSG_ERR_UNSUPPORTED = 3,      /* shape or configuration not built          */
+    TSG_ERR_DECLINED = 4,         /* optional path declines; caller falls back */
+    TSG_ERR_HIP = 5,              /* HIP runtime error                         */
+    TSG_ERR_OUT_OF_MEMORY = 6,
+    /* PrefillMoEGroupingError cases (PrefillMoEGrouping.swift:52-62) */
+    TSG_ERR_GROUPING_INVALID_QUERY_COUNT = 100,
+    TSG_ERR_GROUPING_INVALID_TOP_K = 101,
+    TSG_ERR_GROUPING_INVALID_NUM_EXPERTS = 102,
+    TSG_ERR_GROUPING_INVALID_TILE_EXPERT_COUNT = 103,
+    TSG_ERR_GROUPING_PAIR_COUNT_MISMATCH = 104,
+    TSG_ERR_GROUPING_TOKEN_OUT_OF_RANGE = 105,
+    TSG_ERR_GROUPING_RANK_OUT_OF_RANGE = 106,
+    TSG_ERR_GROUPING_EXPERT_OUT_OF_RANGE = 107,
+    TSG_ERR_GROUPING_DUPLICATE_TOKEN_RANK = 108,
+    TSG_ERR_GROUPING_SORT_KEY_COUNT_MISMATCH = 109
+} tsg_status;
+
+/* Quantization.AffineScheme (Quantization.swift:24-39). */
+typedef enum tsg_affine_scheme { TSG_AFFINE = 0, TSG_SYM = 1 } tsg_affine_scheme;
+
+/* MoE.GateActivation (MoE.swift:100-121). */
+typedef enum tsg_activation { TSG_ACT_GELU_TANH = 0, TSG_ACT_SILU = 1 } tsg_activation;
+
+/* MoEExpertOffsets (MoE.swift:4-29): byte offsets of an expert blob's nine
+ * sub-tensors. Under `sym` the bias offsets alias the scales and are never
+ * dereferenced. 36 bytes. */
+typedef struct tsg_expert_offsets {
+    uint32_t gate_w, gate_s, gate_b;
+    uint32_t up_w, up_s, up_b;
+    uint32_t down_w, down_s, down_b;
+} tsg_expert_offsets;
+
+/* PrefillTokenExpertPair (PrefillRouter.swift:4-28). 16 bytes. */
+typedef struct tsg_token_expert_pair {
+    uint32_t token, expert, rank, weight_bits; /* weight = fp16 bits in the low half */
+} tsg_token_expert_pair;
+
+/* PrefillMoEGroup / PrefillMoETile (PrefillMoEGrouping.swift:3-29). */
+typedef struct tsg_moe_group { uint32_t expert, pair_start, pair_count; } tsg_moe_group;
+typedef struct tsg_moe_tile {
+    uint32_t group_start, group_count, pair_start, pair_count;
+} tsg_moe_tile;
+
+/* PrefillRoutedGEMMBlock (PrefillGroupedRoutedMoE.swift:20-25). 16 bytes.
+ * `local_slot` names the expert: an index into the binding's expert ids, or
+ * the expert id itself when the whole layer is HBM-resident. */
+typedef struct tsg_routed_block {
+    uint32_t local_slot, pair_start, row_count, local_row;
+} tsg_routed_block;
+
+typedef struct tsg_ctx tsg_ctx;     /* MetalContext                      */
+typedef struct tsg_moe tsg_moe;     /* MoE / PrefillGroupedRoutedMoE      */
+typedef struct tsg_layer tsg_layer; /* one HBM-resident MoEPack layer     */
+typedef void* tsg_stream;           /* hipStream_t                        */
+
+/* ---------------------------------------------------------------- context */
+
+const char* tsg_last_error(void);
+const char* tsg_status_string(tsg_status status);
+/* Library version "major.minor.patch". */
+const char* tsg_version(void);
+
+/* MetalContext.init (MetalContext.swift:79-100): binds `device`. */
+tsg_status tsg_ctx_create(int device, tsg_ctx** out);
+void tsg_ctx_destroy(tsg_ctx* ctx);
+/* MetalContext.setAffineGroupSize / setAffineScheme (MetalContext.swift:135-175).
+ * Group sizes {32, 64}; defaults are 64 and TSG_AFFINE, as in the reference. */
+tsg_status tsg_ctx_set_affine_group_size(tsg_ctx* ctx, uint32_t group_size);
+tsg_status tsg_ctx_set_affine_scheme(tsg_ctx* ctx, tsg_affine_scheme scheme);
+tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream);
+
+/* ------------------------------------------------- HBM-resident layers ---
+ * Replace SSD streaming + MTLResidencySet (ModelExpertIO.swift:112-324,
+ * Infrastructure/Streaming): a layer file (`packed_experts/layer_XX.bin`,
+ * laid out by RepackPlanner.planLayerFile, RepackPlanner.swift:442-520) is held
+ * byte-for-byte in HBM; expert e's blob starts at e * expert_stride. */
+
+/* Allocates num_experts * expert_stride bytes of HBM owned by the layer. */
+tsg_status tsg_layer_create(tsg_ctx* ctx, uint32_t num_experts, uint64_t expert_stride,
+                            const tsg_expert_offsets* offsets, tsg_layer** out);
+/* Wraps caller-owned HBM holding the same image (no copy, not freed). */
+tsg_status tsg_layer_wrap(tsg_ctx* ctx, void* device_base, uint32_t num_experts,
+                          uint64_t expert_stride, const tsg_expert_offsets* offsets,
+                          tsg_layer** out);
+/* Copies `nbytes` of a host layer-file image to byte `dst_offset` of the layer. */
+tsg_status tsg_layer_upload(tsg_layer* layer, tsg_stream stream, const void* host_bytes,
+                            uint64_t nbytes, uint64_t dst_offset);
+void* tsg_layer_device_ptr(const tsg_layer* layer);
+void tsg_layer_destroy(tsg_layer* layer);
+
+/* ------------------------------------------------------------- decode ----
+ * MoE (Kernels/MoE/MoE.swift:42-662). */
+
+/* MoE.init(context:routerWeightBits:gateActivation:) (MoE.swift:123-199).
+ * router_weight_bits: 16 (bf16, the QAT checkpoints' router). */
+tsg_status tsg_moe_create(tsg_ctx* ctx, uint32_t router_weight_bits,
+                          tsg_activation gate_activation, tsg_moe** out);
+void tsg_moe_destroy(tsg_moe* moe);
+
+/* encodeRouterGemma4BF16 (MoE.swift:259-302): logits[e] = sum_i W[e,i] *
+ * (hidden[i] * effective_scale[i]) in fp32, top-k (ties -> lower index),
+ * softmax over the k, times per_expert_scale -> fp16 weights. One launch;
+ * indices and weights stay on the device. top_k == 8, num_experts <= 256. */
+tsg_status tsg_moe_router_bf16(tsg_moe* moe, tsg_stream stream, const uint16_t* weights,
+                               const uint16_t* hidden, const uint16_t* effective_scale,
+                               const uint16_t* per_expert_scale, uint32_t* out_indices,
+                               uint16_t* out_weights, uint32_t num_experts, uint32_t d,
+                               uint32_t top_k);
+/* encodeRouterGemma4BF16Rows (MoE.swift:404-466): the same for row_count <= 8
+ * rows at hidden_stride elements; each row is bit-identical to the one-row
+ * call. Returns TSG_ERR_DECLINED for row_count 0 or > 8. */
+tsg_status tsg_moe_router_bf16_rows(tsg_moe* moe, tsg_stream stream, const uint16_t* weights,
+                                    const uint16_t* hidden, uint32_t hidden_stride_elements,
+                                    const uint16_t* effective_scale,
+                                    const uint16_t* per_expert_scale, uint32_t* out_indices,
+                                    uint16_t* out_weights, uint32_t row_count,
+                                    uint32_t num_experts, uint32_t d, uint32_t top_k);
+/* encodeRouterLogitsBF16 (MoE.swift:316-345): the GEMV alone. */
+tsg_status tsg_moe_router_logits_bf16(tsg_moe* moe, tsg_stream stream, const uint16_t* weights,
+                                      const uint16_t* hidden, const uint16_t* effective_scale,
+                                      float* out_logits, uint32_t num_experts, uint32_t d);
+
+/* encodeRoutedPersistentPhase1U16Load (MoE.swift:529-562):
+ * acts[s*F + f] = half(act(gate_s[f].x) * (up_s[f].x)) for the top_k == 8
+ * expert blobs in routed_blobs (a host array of device pointers, the
+ * argument buffer's contents). */
+tsg_status tsg_moe_phase1(tsg_moe* moe, tsg_stream stream, const void* const* routed_blobs,
+                          const tsg_expert_offsets* offsets, const uint16_t* x, uint16_t* acts,
+                          uint32_t d, uint32_t f, uint32_t top_k);
+/* encodeRoutedPersistentPhase1SubsetU16Load (MoE.swift:564-607): only the
+ * slots listed in the device array active_slots[0..active_count). */
+tsg_status tsg_moe_phase1_subset(tsg_moe* moe, tsg_stream stream,
+                                 const void* const* routed_blobs,
+                                 const tsg_expert_offsets* offsets, const uint16_t* x,
+                                 uint16_t* acts, const uint32_t* active_slots,
+                                 uint32_t active_count, uint32_t d, uint32_t f, uint32_t top_k);
+/* encodeRoutedPersistentPhase2Reduce (MoE.swift:609-644):
+ * y[d] = half(residual[d] + sum_{s=0..7} w[s] * down_s[d].acts[s]), summed in
+ * slot order. */
+tsg_status tsg_moe_phase2(tsg_moe* moe, tsg_stream stream, const void* const* routed_blobs,
+                          const tsg_expert_offsets* offsets, const uint16_t* acts,
+                          const uint16_t* routing_weights, const uint16_t* residual,
+                          uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k);
+
+/* Phase 1 / phase 2 over an HBM-resident layer with the expert ids read on the
+ * device from `indices` (what the router wrote): the host never reads routing
+ * back (replaces RealForwardRunner.swift:3112-3151's readback + fetch). */
+tsg_status tsg_moe_phase1_resident(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                   const uint32_t* indices, const uint16_t* x,
+                                   uint16_t* acts, uint32_t d, uint32_t f, uint32_t top_k);
+tsg_status tsg_moe_phase2_resident(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                   const uint32_t* indices, const uint16_t* acts,
+                                   const uint16_t* routing_weights, const uint16_t* residual,
+                                   uint16_t* y, uint32_t d, uint32_t f, uint32_t top_k);
+
+/* One whole decode MoE layer on a resident layer: router -> top-8 -> gate/up +
+ * activation -> down + weighted combine + residual. The composition the
+ * decoder encodes per layer (RealForwardRunner.swift:3104-3330), with routing
+ * kept on the device. `router_hidden` feeds the router (with
+ * effective_scale), `x` the experts; they may alias. out_indices/out_weights
+ * receive the routing. acts_scratch holds top_k * f fp16 values. */
+tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                const uint16_t* router_weights, const uint16_t* router_hidden,
+                                const uint16_t* effective_scale,
+                                const uint16_t* per_expert_scale, const uint16_t* x,
+                                const uint16_t* residual, uint16_t* y, uint32_t* out_indices,
+                                uint16_t* out_weights, uint16_t* acts_scratch,
+                                uint32_t num_experts, uint32_t d, uint32_t f, uint32_t top_k);
+
+/* ---------------------------------------------------------------- QMV ----
+ * DequantInt4GEMV (Kernels/Quant/DequantInt4GEMV.swift:6-364). */
+
+/* encode (DequantInt4GEMV.swift:78-121): y[m] = half(sum_n W[m,n] x[n]).
+ * n % group == 0. biases may alias scales under sym. */
+tsg_status tsg_qmv_int4(tsg_ctx* ctx, tsg_stream stream, const uint8_t* weights,
+                        const uint16_t* scales, const uint16_t* biases, const uint16_t* x,
+                        uint16_t* y, uint32_t m, uint32_t n);
+/* encodeRows (DequantInt4GEMV.swift:130-182): t <= 8 activation rows against
+ * the same weights; row r is bit-identical to encode on that row. */
+tsg_status tsg_qmv_int4_rows(tsg_ctx* ctx, tsg_stream stream, const uint8_t* weights,
+                             const uint16_t* scales, const uint16_t* biases, const uint16_t* x,
+                             uint32_t x_stride_elements, uint16_t* y,
+                             uint32_t y_stride_elements, uint32_t t, uint32_t m, uint32_t n);
+/* Bit-exact dequantisation check: out[r*n + k] = half(fma(q, s, b)), the
+ * value the prefill GEMM stages (prefill.metal:1021-1026), rows x n.
+ * tsg_debug_dequant_f16 computes it directly in fp32; tsg_debug_gemm_dequant_f16
+ * runs the grouped GEMM's own staging routine (fp16 fast path included). */
+tsg_status tsg_debug_dequant_f16(tsg_ctx* ctx, tsg_stream stream, const uint8_t* weights,
+                                 const uint16_t* scales, const uint16_t* biases,
+                                 uint16_t* out, uint32_t rows, uint32_t n);
+tsg_status tsg_debug_gemm_dequant_f16(tsg_ctx* ctx, tsg_stream stream, const uint8_t* weights,
+                                      const uint16_t* scales, const uint16_t* biases,
+                                      uint16_t* out, uint32_t rows, uint32_t n);
+
+/* ------------------------------------------------------------ prefill ----
+ * PrefillRouter, PrefillMoEGrouping, PrefillGroupedRoutedMoE, PrefillMoE
+ * (Kernels/Prefill/MoE). */
+
+/* PrefillRouter.encodeGemma4BF16Block / GEMM (PrefillRouter.swift:127-236):
+ * the decode router for query_count rows at hidden_stride; every row's logits
+ * are summed in the decode kernel's order, so each row's choice is the one the
+ * decode router makes on that row. */
+tsg_status tsg_prefill_router_bf16(tsg_moe* moe, tsg_stream stream, const uint16_t* weights,
+                                   const uint16_t* hidden, uint32_t hidden_stride_elements,
+                                   const uint16_t* effective_scale,
+                                   const uint16_t* per_expert_scale, uint32_t* out_indices,
+                                   uint16_t* out_weights, uint32_t query_count,
+                                   uint32_t num_experts, uint32_t d, uint32_t top_k);
+
+/* PrefillRouter.makeTokenExpertPairs (PrefillRouter.swift:238-258), host. */
+tsg_status tsg_make_token_expert_pairs(const uint32_t* indices, const uint16_t* weights,
+                                       uint32_t query_count, uint32_t top_k,
+                                       tsg_token_expert_pair* out);
+/* PrefillMoEGrouping.groupTokenExpertPairs (PrefillMoEGrouping.swift:90-202),
+ * host: sort by (sort_key[expert], expert, token, rank), per-expert offsets
+ * (0xFFFFFFFF when absent) and counts, groups, tiles of <= tile_expert_count
+ * groups. sort_keys may be NULL; tile_break_after_group < 0 means none.
+ * Output arrays: sorted n_pairs, offsets/counts num_experts, groups and tiles
+ * n_pairs each at most. Errors: TSG_ERR_GROUPING_*. */
+tsg_status tsg_group_token_expert_pairs(const tsg_token_expert_pair* pairs, uint32_t n_pairs,
+                                        uint32_t query_count, uint32_t top_k,
+                                        uint32_t num_experts, uint32_t tile_expert_count,
+                                        const uint64_t* sort_keys, uint32_t n_sort_keys,
+                                        int32_t tile_break_after_group,
+                                        tsg_token_expert_pair* sorted, uint32_t* offsets,
+                                        uint32_t* counts, tsg_moe_group* groups,
+                                        uint32_t* n_groups, tsg_moe_tile* tiles,
+                                        uint32_t* n_tiles);
+/* PrefillRoutedGEMMPlanner.plan (PrefillGroupedRoutedMoE.swift:42-83), host:
+ * batches of <= 64-row blocks that never split a group that fits. Arrays are
+ * sized by the caller: blocks >= total pairs / 1 + n_groups, batches likewise. */
+tsg_status tsg_plan_routed_gemm(const tsg_moe_group* groups, uint32_t n_groups,
+                                uint32_t max_rows_per_batch, tsg_routed_block* blocks,
+                                uint32_t* n_blocks, uint32_t* batch_rows,
+                                uint32_t* batch_first_block, uint32_t* n_batches);
+
+/* The same grouping on the device, for an HBM-resident layer: token-major
+ * routing (indices/weights [query_count, top_k]) -> pairs sorted by
+ * (expert, token, rank) (bit-identical to the host sort), per-expert offsets
+ * and counts, and the GEMM's work list of <= tile_rows-row blocks with
+ * local_slot = expert id and local_row = pair_start. *n_blocks (device) gets
+ * the block count; max_blocks bounds the blocks array. tile_rows: 32 or 64.
+ * scratch: tsg_prefill_group_scratch_bytes(...) bytes of device memory. */
+size_t tsg_prefill_group_scratch_bytes(uint32_t query_count, uint32_t top_k,
+                                       uint32_t num_experts);
+tsg_status tsg_prefill_group_pairs_device(tsg_ctx* ctx, tsg_stream stream,
+                                          const uint32_t* indices, const uint16_t* weights,
+                                          uint32_t query_count, uint32_t top_k,
+                                          uint32_t num_experts, uint32_t tile_rows,
+                                          tsg_token_expert_pair* sorted, uint32_t* offsets,
+                                          uint32_t* counts, tsg_routed_block* blocks,
+                                          uint32_t max_blocks, uint32_t* n_blocks,
+                                          void* scratch);
+
+/* encodeStreamedTiled mode 0 + gelu_mul (PrefillGroupedRoutedMoE.swift:931-1051,
+ * prefill.metal:3664-3864, 1081-1092) on a resident layer: for every block,
+ * gather hidden rows by pair token, G = X Wg^T and U = X Wu^T on fp16 MFMA with
+ * fp32 accumulation, weights dequantised to fp16 exactly as the reference
+ * stages them; act[(local_row + r)*F + f] = half(act(half(G)) * half(U)).
+ * n_blocks_device: optional device count bounding `blocks` (may be NULL, then
+ * n_blocks is used). */
+tsg_status tsg_prefill_moe_gate_up(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                   const uint16_t* hidden, uint32_t hidden_stride_elements,
+                                   const tsg_token_expert_pair* sorted_pairs,
+                                   const tsg_routed_block* blocks, uint32_t n_blocks,
+                                   const uint32_t* n_blocks_device, uint16_t* act,
+                                   uint32_t d, uint32_t f);
+/* encodeStreamedTiled mode 1 (prefill.metal:3680-3716): P = act Wd^T,
+ * route_partials[(token*top_k + rank)*D + d] = half(P). */
+tsg_status tsg_prefill_moe_down(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                const uint16_t* act, const tsg_token_expert_pair* sorted_pairs,
+                                const tsg_routed_block* blocks, uint32_t n_blocks,
+                                const uint32_t* n_blocks_device, uint16_t* route_partials,
+                                uint32_t top_k, uint32_t d, uint32_t f);
+/* encodeStreamedRows (PrefillGroupedRoutedMoE.swift:793-917,
+ * prefill.metal:1489-1721): verify-width blocks (row_count <= 8), decode's
+ * per-row arithmetic with each weight read once per block; writes act rows
+ * (act_scratch, (max local_row + rows) * f fp16) and route partials. `blocks`
+ * is a HOST array (the reference passes it with setBytes); local_slot is the
+ * expert id in the resident layer. Returns TSG_ERR_DECLINED when a block holds
+ * more than 8 rows. */
+tsg_status tsg_prefill_moe_rows(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                const uint16_t* hidden, uint32_t hidden_stride_elements,
+                                const tsg_token_expert_pair* sorted_pairs,
+                                const tsg_routed_block* blocks, uint32_t n_blocks,
+                                uint16_t* act_scratch, uint16_t* route_partials,
+                                uint32_t top_k, uint32_t d, uint32_t f);
+/* PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38):
+ * h2[t,d] = half(sum_{r<top_k} fma(w[t,r], P[(t*top_k + r), d])). */
+tsg_status tsg_prefill_moe_reduce_token_major(tsg_ctx* ctx, tsg_stream stream,
+                                              const uint16_t* route_partials,
+                                              const uint16_t* route_weights, uint16_t* h2,
+                                              uint32_t query_count, uint32_t top_k,
+                                              uint32_t d);
+
+/* ---------------------------------------------- synthetic fixtures ------
+ * Device generators for benchmark inputs (no reference counterpart; the
+ * reference's fixtures come from SplitMix64 on the host). Element i of a
+ * stream keyed `seed` is derived from SplitMix64 output i of that seed
+ * (counter-based), so any slice can be regenerated independently. */
+/* n bytes of uniform nibbles. */
+tsg_status tsg_gen_bytes(tsg_stream stream, uint64_t seed, uint8_t* out, uint64_t n);
+/* n bf16 values sigma * N(0,1) (Irwin-Hall of 12 uniforms), abs_value: |.|,
+ * divisor applied after (scale = |N(0,0.02)|/7 -> sigma .02, abs 1, div 7). */
+tsg_status tsg_gen_bf16_normal(tsg_stream stream, uint64_t seed, uint16_t* out, uint64_t n,
+                               float sigma, int abs_value, float divisor);
+/* n fp16 values sigma * N(0,1), with |x| < 2^-17 flushed to zero. */
+tsg_status tsg_gen_f16_normal(tsg_stream stream, uint64_t seed, uint16_t* out, uint64_t n,
+                              float sigma);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TSUGUMI_HIP_H */

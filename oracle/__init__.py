@@ -111,6 +111,8 @@ def _declare(L):
                                                  C.c_int, _f32p]
     L.tsgo_router_reference.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p,
                                         _i32p, _f32p]
+    L.tsgo_router_logits_canonical.argtypes = [_u16p, _u16p, C.c_int, _u16p, C.c_int, C.c_int,
+                                               C.c_int, _f32p]
     L.tsgo_topk_softmax.argtypes = [_f32p, C.c_int, C.c_int, _f32p, _i32p, _u16p]
     L.tsgo_make_token_expert_pairs.argtypes = [_u32p, _u16p, C.c_int, C.c_int, C.c_void_p]
     L.tsgo_group_pairs.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
@@ -310,6 +312,18 @@ def router_reference(w_rows, x, top_k, per_expert_scale):
     lib().tsgo_router_reference(_p(w_rows, C.c_float), _p(x, C.c_float), ne, d, top_k,
                                 _p(pes, C.c_float), _p(idx, C.c_int32), _p(w, C.c_float))
     return idx, w
+
+
+def router_logits_canonical(w_bf16, hidden_f16, stride, es_bf16, rows, num_experts, d):
+    """Router logits in the MI355X kernels' summation order (see tsg_oracle.h)."""
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    h = np.ascontiguousarray(hidden_f16, np.uint16)
+    es = np.ascontiguousarray(es_bf16, np.uint16)
+    out = np.empty((rows, num_experts), np.float32)
+    lib().tsgo_router_logits_canonical(_p(w, C.c_uint16), _p(h, C.c_uint16), stride,
+                                       _p(es, C.c_uint16), rows, num_experts, d,
+                                       _p(out, C.c_float))
+    return out
 
 
 def topk_softmax(logits, top_k, per_expert_scale):

@@ -415,6 +415,35 @@ void tsgo_router_reference(const float* w, const float* x, int num_experts, int 
     free(order);
 }
 
+void tsgo_router_logits_canonical(const uint16_t* w_bf16, const uint16_t* hidden_f16,
+                                  int stride, const uint16_t* es_bf16, int rows,
+                                  int num_experts, int d, float* out_logits) {
+    const int nchunks = d / 8;
+    for (int row = 0; row < rows; ++row) {
+        const uint16_t* x = hidden_f16 + (size_t)row * stride;
+        for (int e = 0; e < num_experts; ++e) {
+            const uint16_t* w = w_bf16 + (size_t)e * d;
+            float p[32];
+            for (int l = 0; l < 32; ++l) {
+                float acc = 0.0f;
+                for (int c = l; c < nchunks; c += 32)
+                    for (int k = 0; k < 8; ++k) {
+                        const int i = c * 8 + k;
+                        const float xe = tsgo_f16_to_float(x[i]) * tsgo_bf16_to_float(es_bf16[i]);
+                        acc = fmaf(tsgo_bf16_to_float(w[i]), xe, acc);
+                    }
+                p[l] = acc;
+            }
+            for (int o = 16; o >= 1; o >>= 1) {
+                float q[32];
+                for (int l = 0; l < 32; ++l) q[l] = p[l] + p[l ^ o];
+                memcpy(p, q, sizeof(p));
+            }
+            out_logits[(size_t)row * num_experts + e] = p[0];
+        }
+    }
+}
+
 void tsgo_topk_softmax(const float* logits, int num_experts, int top_k,
                        const float* per_expert_scale, int32_t* out_idx, uint16_t* out_w) {
     int top_idx[64];

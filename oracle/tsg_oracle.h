@@ -94,6 +94,15 @@ void tsgo_moe_apply_streamed_routed(const uint8_t* const* blobs, const uint32_t*
 void tsgo_router_reference(const float* w, const float* x, int num_experts, int d,
                            int top_k, const float* per_expert_scale,
                            int32_t* out_idx, float* out_w);
+/* Router logits in the MI355X kernels' summation order (restated from
+ * tsugumi_amd/csrc/decode.hip router_row_dot, not from the reference, whose
+ * simd_sum order is Metal's): for each expert, 32 partial sums p_l over the
+ * 8-element chunks c = l, l+32, ... (acc = fma(w, x*es, acc), elements in
+ * order), then a xor butterfly p_l += p_{l^o} for o = 16, 8, 4, 2, 1. Inputs
+ * are bf16 weights, fp16 hidden rows at `stride`, bf16 effective scale. */
+void tsgo_router_logits_canonical(const uint16_t* w_bf16, const uint16_t* hidden_f16,
+                                  int stride, const uint16_t* es_bf16, int rows,
+                                  int num_experts, int d, float* out_logits);
 /* Top-k + softmax + gain over given logits with the kernels' rule
  * (moe.metal:281-329): insertion order, ties -> lower index, -inf/NaN never
  * enter; weights rounded to fp16 bits. */

@@ -1,0 +1,164 @@
+"""Fixtures of the reference's TsugumiKernelCheck harness, regenerated bit for
+bit from SplitMix64/SeedTree through the oracle, plus helpers shared by the
+GPU parity tests.
+
+Each builder cites the harness function whose fixture it reproduces
+(Sources/TsugumiKernelCheck/main.swift, PrefillMoEGEMMCheck.swift).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle
+
+# Tolerance.swift:4-21 and the north-star bound.
+FP16_REDUCTION = 5e-3
+FP16_CHAINED = 1e-2
+NORTH_STAR = 1e-3
+
+
+def quantized_rows(rng, count, n, group, symmetric, lo=-0.5, hi=0.5):
+    """quantizedRows (main.swift:120-131): row-major uniform draws, quantised."""
+    raw = rng.uniforms(lo, hi, count * n).reshape(count, n)
+    return oracle.quantize_int4(raw, group, symmetric)
+
+
+def int4_gemv_case(m, n, group, seed, symmetric):
+    """checkInt4GEMV fixture (main.swift:145-151)."""
+    rng = oracle.seed_tree_key(seed, f"int4-gemv-m{m}-n{n}-g{group}")
+    packed, scales, biases = quantized_rows(rng, m, n, group, symmetric)
+    x_bits = rng.uniforms_f16(-1.0, 1.0, n)
+    ref = oracle.dequant_int4_gemv_ref(packed, scales, biases, oracle.f16_to_float(x_bits), n,
+                                       group)
+    return dict(packed=packed, scales=scales, biases=biases, x_bits=x_bits, ref=ref)
+
+
+def pack_blob(parts, symmetric, keep_biases=True, align=16):
+    """Expert blob in the packer's order gate(W,S,[B]), up, down
+    (RepackPlanner.swift:442-520). Returns bytes and the 9 MoEExpertOffsets
+    (bias offsets alias the scales when the bias is left out). Sub-tensors are
+    placed at `align`-byte boundaries."""
+    chunks, offs, cur = [], [], 0
+    for (p, s, b) in parts:
+        for arr, is_bias in ((p, False), (s, False), (b, True)):
+            if is_bias and not keep_biases:
+                offs.append(offs[-1])
+                continue
+            raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
+            pad = (-cur) % align
+            if pad:
+                chunks.append(np.zeros(pad, np.uint8))
+                cur += pad
+            offs.append(cur)
+            chunks.append(raw)
+            cur += raw.size
+    return np.concatenate(chunks), np.array(offs, np.uint32)
+
+
+def routed_moe_case(d, f, group, seed, symmetric):
+    """checkRoutedMoE fixture (main.swift:194-231)."""
+    top_k = 8
+    rng = oracle.seed_tree_key(seed, f"routed-moe-d{d}-f{f}-g{group}")
+    mats = []
+    for _ in range(top_k):
+        g = rng.uniforms(-0.4, 0.4, f * d).reshape(f, d)
+        u = rng.uniforms(-0.4, 0.4, f * d).reshape(f, d)
+        dn = rng.uniforms(-0.4, 0.4, d * f).reshape(d, f)
+        mats.append((g, u, dn))
+    x_bits = oracle.f16_bits(rng.uniforms(-0.5, 0.5, d))
+    res_bits = oracle.f16_bits(rng.uniforms(-0.5, 0.5, d))
+    w = (np.float32(0.04) + np.arange(top_k, dtype=np.float32) * np.float32(0.015)).astype(np.float32)
+    w_bits = oracle.f16_bits(w)
+    blobs, offs = [], None
+    for (g, u, dn) in mats:
+        parts = [oracle.quantize_int4(g, group, symmetric),
+                 oracle.quantize_int4(u, group, symmetric),
+                 oracle.quantize_int4(dn, group, symmetric)]
+        blob, offs = pack_blob(parts, symmetric, keep_biases=True)
+        blobs.append(blob)
+    ref = oracle.moe_apply_streamed_routed(blobs, offs, oracle.f16_to_float(x_bits),
+                                           oracle.f16_to_float(res_bits),
+                                           oracle.f16_to_float(w_bits), d, f, group,
+                                           symmetric=False)
+    return dict(blobs=blobs, offsets=offs, x_bits=x_bits, res_bits=res_bits, w_bits=w_bits,
+                ref=ref)
+
+
+def router_case(d, ne, group, seed, draw):
+    """checkRouter(weightBits: 16) fixture (main.swift:419-458)."""
+    label = f"router-bf16 d={d} experts={ne}"
+    rng = oracle.seed_tree_key(seed + draw, f"{label}-g{group}")
+    w_bits = rng.uniforms_bf16(-0.2, 0.2, ne * d)
+    hidden = rng.uniforms_f16(-1.0, 1.0, d)
+    es_bits = oracle.bf16_bits(rng.uniforms(0.5, 1.5, d))
+    pes_bits = oracle.bf16_bits(rng.uniforms(0.8, 1.2, ne))
+    x = oracle.f16_to_float(hidden) * oracle.bf16_to_float(es_bits)
+    idx, wts = oracle.router_reference(oracle.bf16_to_float(w_bits).reshape(ne, d), x, 8,
+                                       oracle.bf16_to_float(pes_bits))
+    return dict(w_bits=w_bits, hidden=hidden, es_bits=es_bits, pes_bits=pes_bits, idx=idx,
+                wts=wts)
+
+
+def prefill_router_case(t, d, ne, kind, group, seed):
+    """checkPrefillRouterBF16 fixture (main.swift:525-548); stride d + 16."""
+    stride = d + 16
+    label = f"prefill-router-bf16-{kind} t={t} d={d} experts={ne}"
+    rng = oracle.seed_tree_key(seed, label.replace("-nax ", "-gemm "))
+    w_bits = rng.uniforms_bf16(-0.2, 0.2, ne * d)
+    hidden = rng.uniforms_f16(-1.0, 1.0, t * stride)
+    es_bits = oracle.bf16_bits(rng.uniforms(0.5, 1.5, d))
+    pes_bits = oracle.bf16_bits(rng.uniforms(0.8, 1.2, ne))
+    refs = []
+    wf = oracle.bf16_to_float(w_bits).reshape(ne, d)
+    for row in range(t):
+        x = oracle.f16_to_float(hidden[row * stride:row * stride + d]) * oracle.bf16_to_float(es_bits)
+        refs.append(oracle.router_reference(wf, x, 8, oracle.bf16_to_float(pes_bits)))
+    return dict(stride=stride, w_bits=w_bits, hidden=hidden, es_bits=es_bits,
+                pes_bits=pes_bits, refs=refs)
+
+
+def prefill_moe_gemm_case(group, seed, symmetric, d=2816, f=704, tokens=72, top_k=4,
+                          n_experts=16):
+    """checkPrefillRoutedMoEGEMM fixture (PrefillMoEGEMMCheck.swift:92-136):
+    16 experts, rank 0 always expert 0 (72 rows: a full block + a partial
+    one), the other ranks spread over experts 1..15."""
+    rng = oracle.seed_tree_key(seed, f"prefill-moe-gemm-g{group}")
+    experts = []
+    for _ in range(n_experts):
+        parts = [quantized_rows(rng, f, d, group, symmetric, -0.125, 0.125),
+                 quantized_rows(rng, f, d, group, symmetric, -0.125, 0.125),
+                 quantized_rows(rng, d, f, group, symmetric, -0.125, 0.125)]
+        experts.append(parts)
+    hidden = rng.uniforms_f16(-1.0, 1.0, tokens * d)
+    by_expert = [[] for _ in range(n_experts)]
+    for token in range(tokens):
+        picks = [0, 1 + token % 5, 6 + token % 4, 10 + token % 6]
+        for rank, e in enumerate(picks):
+            by_expert[e].append((token, e, rank, 0))
+    pairs, blocks = [], []
+    for e in range(n_experts):
+        start = 0
+        while start < len(by_expert[e]):
+            cnt = min(64, len(by_expert[e]) - start)
+            blocks.append((e, len(pairs) + start, cnt, len(pairs) + start))
+            start += cnt
+        pairs.extend(by_expert[e])
+    pairs = np.array(pairs, dtype=oracle.PAIR_DTYPE)
+    blocks = np.array(blocks, dtype=oracle.BLOCK_DTYPE)
+    return dict(experts=experts, hidden=hidden, pairs=pairs, blocks=blocks, tokens=tokens,
+                top_k=top_k, d=d, f=f)
+
+
+def layer_image(expert_parts, symmetric, keep_biases, stride_align=16384):
+    """A MoEPack layer file image: expert blobs at a common stride rounded up to
+    16 KiB (RepackPlanner.swift:514-516). Returns (bytes, stride, offsets9)."""
+    blobs, offs = [], None
+    for parts in expert_parts:
+        blob, offs = pack_blob(parts, symmetric, keep_biases=keep_biases)
+        blobs.append(blob)
+    size = max(b.size for b in blobs)
+    stride = (size + stride_align - 1) // stride_align * stride_align
+    image = np.zeros(stride * len(blobs), np.uint8)
+    for i, b in enumerate(blobs):
+        image[i * stride:i * stride + b.size] = b
+    return image, stride, offs, blobs

@@ -1,0 +1,277 @@
+"""GPU parity: int4 QMV, dequantisation, router and decode MoE phases against
+the oracle, on the reference KernelCheck fixtures (main.swift:2426-2443)
+regenerated bit for bit, plus the bitwise self-consistency invariants of the
+reference's own tests (rows == per-row, subset == full)."""
+import numpy as np
+import pytest
+
+import oracle
+from tests import kernelcheck as kc
+from tests.gpu_util import dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+SCHEMES = ["affine", "sym"]
+GROUPS = [64, 32]
+
+
+@pytest.fixture(scope="module")
+def tsg():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import tsugumi_amd
+    return tsugumi_amd
+
+
+@pytest.fixture(scope="module")
+def ctx(tsg):
+    return tsg.Context(0)
+
+
+def configure(ctx, group, scheme):
+    ctx.set_affine_group_size(group)
+    ctx.set_affine_scheme(scheme)
+
+
+@pytest.mark.parametrize("group", GROUPS)
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m,n,seed", [(128, 2816, 0xA1), (64, 4096, 0xA2), (128, 2112, 0xA3),
+                                      (128, 704, 0xA4)])
+def test_qmv_kernelcheck_cases(tsg, ctx, group, scheme, m, n, seed):
+    sym = scheme == "sym"
+    if n % group:
+        pytest.skip("shape not a multiple of the group")
+    configure(ctx, group, scheme)
+    c = kc.int4_gemv_case(m, n, group, seed, sym)
+    y = empty(m)
+    tsg.DequantInt4GEMV(ctx).encode(dev(c["packed"]), dev(c["scales"]),
+                                    dev(c["scales"] if sym else c["biases"]), dev(c["x_bits"]),
+                                    y, m, n)
+    got = oracle.f16_to_float(host(y, np.uint16))
+    rel = oracle.relative_error(got, c["ref"])
+    print(f"int4-gemv m={m} n={n} g={group} {scheme}: rel={rel:.3e}")
+    assert rel <= kc.FP16_REDUCTION
+    assert rel <= kc.NORTH_STAR
+
+
+def test_qmv_rows_bit_identical_to_single_row(tsg, ctx):
+    configure(ctx, 32, "sym")
+    m, n, t = 128, 2816, 5
+    c = kc.int4_gemv_case(m, n, 32, 0xA1, True)
+    rng = oracle.SplitMix64(77)
+    xs = rng.uniforms_f16(-1, 1, t * (n + 8)).reshape(t, n + 8)
+    q = tsg.DequantInt4GEMV(ctx)
+    W, S = dev(c["packed"]), dev(c["scales"])
+    yr = empty(t * m)
+    q.encode_rows(W, S, S, dev(xs), n + 8, yr, m, t, m, n)
+    rows = host(yr, np.uint16).reshape(t, m)
+    for r in range(t):
+        y1 = empty(m)
+        q.encode(W, S, S, dev(np.ascontiguousarray(xs[r, :n])), y1, m, n)
+        assert np.array_equal(rows[r], host(y1, np.uint16)), f"row {r} differs"
+
+
+@pytest.mark.parametrize("group", GROUPS)
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_dequant_f16_is_bit_exact(tsg, ctx, group, scheme):
+    """Dequantised weights, bit for bit: the GEMM's staging routine (fp16 fast
+    path and fp32 route) and the direct kernel against the oracle's
+    half(fma(q, s, b)) (prefill.metal:1021-1026). Scales span tiny (fp16
+    subnormal products, scales not exact in fp16) to large."""
+    sym = scheme == "sym"
+    configure(ctx, group, scheme)
+    rows, n = 96, 1024
+    rng = oracle.SplitMix64(0xDE)
+    w = rng.uniforms(-0.5, 0.5, rows * n).reshape(rows, n)
+    w *= np.exp2(np.linspace(-22, 6, rows, dtype=np.float32))[:, None]
+    packed, scales, biases = oracle.quantize_int4(w, group, sym)
+    want = oracle.dequantize_int4_f16(packed, scales, biases, n, group, sym)
+    q = tsg.DequantInt4GEMV(ctx)
+    for gemm_path in (False, True):
+        out = empty(rows * n)
+        q.debug_dequant_f16(dev(packed), dev(scales), dev(scales if sym else biases), out, rows,
+                            n, gemm_path=gemm_path)
+        got = host(out, np.uint16).reshape(rows, n)
+        bad = np.argwhere(got != want)
+        assert bad.size == 0, f"gemm_path={gemm_path}: {len(bad)} mismatches, first {bad[:3]}"
+
+
+@pytest.mark.parametrize("group", GROUPS)
+def test_router_kernelcheck_and_canonical_order(tsg, ctx, group):
+    """checkRouter(16) cases (main.swift:409-517, seed 0xD2, 4 draws): indices
+    equal routerReference's; weights within fp16Reduction; logits bit-equal to
+    the oracle's restatement of the kernel order, and the selection bit-equal
+    to the kernel rule applied to those logits."""
+    configure(ctx, group, "sym")
+    d, ne = 2816, 128
+    moe = tsg.MoE(ctx)
+    for draw in range(4):
+        c = kc.router_case(d, ne, group, 0xD2, draw)
+        W, H, ES, PES = dev(c["w_bits"]), dev(c["hidden"]), dev(c["es_bits"]), dev(c["pes_bits"])
+        idx, wts = empty(8, np.uint32), empty(8)
+        moe.encode_router_gemma4_bf16(W, H, ES, PES, idx, wts, ne, d)
+        gi = host(idx, np.uint32)
+        gw = oracle.f16_to_float(host(wts, np.uint16))
+        assert list(gi) == list(c["idx"]), f"draw {draw}: gpu={gi} cpu={c['idx']}"
+        assert oracle.relative_error(gw, c["wts"]) <= kc.FP16_REDUCTION
+        logits = empty(ne, np.float32)
+        moe.encode_router_logits_bf16(W, H, ES, logits, ne, d)
+        canon = oracle.router_logits_canonical(c["w_bits"], c["hidden"], d, c["es_bits"], 1, ne, d)
+        assert np.array_equal(host(logits, np.uint32), canon.view(np.uint32).ravel())
+        ci, cw = oracle.topk_softmax(canon[0], 8, oracle.bf16_to_float(c["pes_bits"]))
+        assert list(gi) == list(ci)
+        assert np.max(np.abs(host(wts, np.uint16).astype(np.int32) - cw.astype(np.int32))) <= 1
+
+
+def test_router_rows_bit_identical_to_single(tsg, ctx):
+    configure(ctx, 32, "sym")
+    d, ne, rows = 2816, 128, 5
+    moe = tsg.MoE(ctx)
+    c = kc.router_case(d, ne, 32, 0xD2, 0)
+    rng = oracle.SplitMix64(5)
+    stride = d + 16
+    hid = rng.uniforms_f16(-1, 1, rows * stride)
+    W, ES, PES = dev(c["w_bits"]), dev(c["es_bits"]), dev(c["pes_bits"])
+    idx, wts = empty(8 * rows, np.uint32), empty(8 * rows)
+    moe.encode_router_gemma4_bf16_rows(W, dev(hid), stride, ES, PES, idx, wts, rows, ne, d)
+    gi, gw = host(idx, np.uint32).reshape(rows, 8), host(wts, np.uint16).reshape(rows, 8)
+    for r in range(rows):
+        i1, w1 = empty(8, np.uint32), empty(8)
+        moe.encode_router_gemma4_bf16(W, dev(np.ascontiguousarray(hid[r * stride:r * stride + d])),
+                                      ES, PES, i1, w1, ne, d)
+        assert np.array_equal(gi[r], host(i1, np.uint32))
+        assert np.array_equal(gw[r], host(w1, np.uint16))
+    with pytest.raises(tsg.TsgError) as e:
+        moe.encode_router_gemma4_bf16_rows(W, dev(hid), stride, ES, PES, idx, wts, 9, ne, d)
+    assert e.value.status == 4  # declined, like the reference's `false`
+
+
+def _routed_blobs(case):
+    return [dev(b) for b in case["blobs"]]
+
+
+@pytest.mark.parametrize("group", GROUPS)
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_routed_moe_kernelcheck(tsg, ctx, group, scheme):
+    """checkRoutedMoE (main.swift:194-303, seed 0xB1): phase 1 + phase 2 at the
+    production decode shapes against MoeRef.applyStreamedRouted."""
+    sym = scheme == "sym"
+    configure(ctx, group, scheme)
+    d, f = 2816, 704
+    c = kc.routed_moe_case(d, f, group, 0xB1, sym)
+    moe = tsg.MoE(ctx)
+    blobs = _routed_blobs(c)
+    acts, y = empty(8 * f), empty(d)
+    moe.encode_routed_phase1(blobs, c["offsets"], dev(c["x_bits"]), acts, d, f)
+    moe.encode_routed_phase2(blobs, c["offsets"], acts, dev(c["w_bits"]), dev(c["res_bits"]), y,
+                             d, f)
+    got = oracle.f16_to_float(host(y, np.uint16))
+    rel = oracle.relative_error(got, c["ref"])
+    print(f"routed-moe d={d} f={f} g={group} {scheme}: rel={rel:.3e}")
+    assert rel <= kc.FP16_CHAINED
+    assert rel <= kc.NORTH_STAR
+
+
+def test_phase1_subset_matches_full_bitwise(tsg, ctx):
+    """MoEFusedFFNTests.swift: hit/miss-subset phase 1 == full phase 1."""
+    configure(ctx, 32, "sym")
+    d, f = 2816, 704
+    c = kc.routed_moe_case(d, f, 32, 0xB1, True)
+    moe = tsg.MoE(ctx)
+    blobs = _routed_blobs(c)
+    full = empty(8 * f)
+    moe.encode_routed_phase1(blobs, c["offsets"], dev(c["x_bits"]), full, d, f)
+    sub = empty(8 * f, fill=0)
+    active = np.array([6, 1, 3], np.uint32)
+    moe.encode_routed_phase1_subset(blobs, c["offsets"], dev(c["x_bits"]), sub, dev(active), 3,
+                                    d, f)
+    a, b = host(full, np.uint16).reshape(8, f), host(sub, np.uint16).reshape(8, f)
+    for s in active:
+        assert np.array_equal(a[s], b[s])
+    for s in set(range(8)) - set(active.tolist()):
+        assert np.all(b[s] == 0)
+
+
+def test_decode_preconditions_fail_loudly(tsg, ctx):
+    configure(ctx, 32, "sym")
+    moe = tsg.MoE(ctx)
+    c = kc.routed_moe_case(256, 64, 32, 0x1, True)
+    blobs = _routed_blobs(c)
+    with pytest.raises(tsg.TsgError) as e:
+        moe.encode_routed_phase1(blobs, c["offsets"], dev(c["x_bits"]), empty(8 * 64), 256, 64,
+                                 top_k=4)
+    assert e.value.status == 1
+    with pytest.raises(tsg.TsgError) as e:
+        moe.encode_routed_phase1(blobs, c["offsets"], dev(c["x_bits"]), empty(8 * 64), 250, 64)
+    assert e.value.status == 1
+
+
+# ---------------------------------------------------------------- config 2
+
+GEMMA = dict(d=2816, f=704, ne=128, group=32)
+
+
+def gemma_offsets(d=2816, f=704, group=32):
+    """Sym g32 expert blob: gate W, gate S, up W, up S, down W, down S; the
+    bias offsets alias the scales (ModelExpertIO.swift:69-84)."""
+    gw = f * d // 2
+    gs = f * (d // group) * 2
+    dw = d * f // 2
+    ds = d * (f // group) * 2
+    o_gw, o_gs = 0, gw
+    o_uw, o_us = gw + gs, 2 * gw + gs
+    o_dw, o_ds = 2 * (gw + gs), 2 * (gw + gs) + dw
+    payload = o_ds + ds
+    stride = (payload + 16383) // 16384 * 16384
+    return [o_gw, o_gs, o_gs, o_uw, o_us, o_us, o_dw, o_ds, o_ds], payload, stride
+
+
+def make_gemma_layer(tsg, ctx, seed, ne=128, d=2816, f=704):
+    """Nibbles uniform in [0, 15]; scales bf16(|N(0, 0.02)| / 7)."""
+    import torch
+    offs, payload, stride = gemma_offsets(d, f)
+    buf = torch.empty(ne * stride, dtype=torch.uint8, device="cuda")
+    tsg.generators.bytes(buf, seed)
+    scale_regions = [(offs[1], f * (d // 32)), (offs[4], f * (d // 32)), (offs[7], d * (f // 32))]
+    for e in range(ne):
+        for j, (o, n) in enumerate(scale_regions):
+            region = buf[e * stride + o:e * stride + o + 2 * n].view(torch.int16)
+            tsg.generators.bf16_normal(region, seed * 1000 + e * 3 + j + 1, 0.02, True, 7.0)
+    layer = tsg.ResidentLayer(ctx, ne, stride, offs, device_tensor=buf)
+    return layer, buf, offs, stride
+
+
+def test_resident_decode_layer_gemma_shape(tsg, ctx):
+    """One Gemma-4-26B-A4B-shaped decode MoE layer (config 2): router over
+    128 bf16 rows -> top-8 -> gate/up + GeGLU -> down + combine, all device
+    side. Routing bit-exact against the oracle (kernel-order logits + the
+    kernel's top-k rule); y within 1e-3 of MoeRef.applyStreamedRouted over the
+    chosen experts."""
+    import torch
+    configure(ctx, 32, "sym")
+    d, f, ne = GEMMA["d"], GEMMA["f"], GEMMA["ne"]
+    layer, buf, offs, stride = make_gemma_layer(tsg, ctx, 0x5EED)
+    rw = torch.empty(ne * d, dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(rw, 0xA11, 1.0 / np.sqrt(d))
+    x = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(x, 0xA12, 1.0)
+    ones_d = dev(np.full(d, 0x3F80, np.uint16))
+    ones_e = dev(np.full(ne, 0x3F80, np.uint16))
+    moe = tsg.MoE(ctx)
+    y, idx, wts, acts = empty(d), empty(8, np.uint32), empty(8), empty(8 * f)
+    moe.encode_decode_layer(layer, rw, x, ones_d, ones_e, x, x, y, idx, wts, acts, ne, d, f)
+    gi, gw = host(idx, np.uint32), host(wts, np.uint16)
+    xb, rwb = host(x, np.uint16), host(rw, np.uint16)
+    canon = oracle.router_logits_canonical(rwb, xb, d, np.full(d, 0x3F80, np.uint16), 1, ne, d)
+    ci, cw = oracle.topk_softmax(canon[0], 8, np.ones(ne, np.float32))
+    assert list(gi) == list(ci)
+    assert np.max(np.abs(gw.astype(np.int32) - cw.astype(np.int32))) <= 1
+    image = host(buf, np.uint8)
+    blobs = [np.ascontiguousarray(image[e * stride:(e + 1) * stride]) for e in gi]
+    xf = oracle.f16_to_float(xb)
+    ref = oracle.moe_apply_streamed_routed(blobs, np.array(offs, np.uint32), xf, xf,
+                                           oracle.f16_to_float(gw), d, f, 32, symmetric=True)
+    rel = oracle.relative_error(oracle.f16_to_float(host(y, np.uint16)), ref)
+    print(f"decode layer gemma: experts={list(gi)} rel={rel:.3e}")
+    assert rel <= kc.NORTH_STAR

@@ -1,0 +1,435 @@
+"""tsugumi_amd — Tsugumi's int4 MoE expert-matmul path on one MI355X (gfx950).
+
+Python mirror of the reference's Swift encoder classes over the C ABI in
+include/tsugumi_hip.h (libtsugumi_hip.so). Names follow the reference:
+
+    MetalContext            -> Context
+    MoE                     -> MoE            (Kernels/MoE/MoE.swift:42-662)
+    DequantInt4GEMV         -> DequantInt4GEMV (Kernels/Quant/DequantInt4GEMV.swift)
+    PrefillRouter           -> PrefillRouter  (Kernels/Prefill/MoE/PrefillRouter.swift)
+    PrefillMoEGrouping      -> PrefillMoEGrouping (PrefillMoEGrouping.swift:90-202)
+    PrefillRoutedGEMMPlanner-> PrefillRoutedGEMMPlanner (PrefillGroupedRoutedMoE.swift:42-83)
+    PrefillGroupedRoutedMoE -> PrefillGroupedRoutedMoE (PrefillGroupedRoutedMoE.swift)
+    PrefillMoE              -> PrefillMoE     (PrefillMoE.swift:11-38)
+    streamed experts        -> ResidentLayer  (whole layer held in HBM)
+
+Device buffers are torch CUDA tensors (plumbing only); `stream` defaults to
+torch's current stream. Every call raises TsgError on a non-OK status; there
+is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _abi
+from ._abi import (TSG_ACT_GELU_TANH, TSG_ACT_SILU, TSG_AFFINE, TSG_SYM, ExpertOffsets,
+                   RoutedBlock, TokenExpertPair, TsgError, check, load)
+
+__all__ = [
+    "Context", "MoE", "DequantInt4GEMV", "PrefillRouter", "PrefillMoEGrouping",
+    "PrefillRoutedGEMMPlanner", "PrefillGroupedRoutedMoE", "PrefillMoE", "ResidentLayer",
+    "ExpertOffsets", "TsgError", "PAIR_DTYPE", "BLOCK_DTYPE", "GROUP_DTYPE", "TILE_DTYPE",
+    "generators", "load",
+]
+
+PAIR_DTYPE = np.dtype([("token", "<u4"), ("expert", "<u4"), ("rank", "<u4"),
+                       ("weight_bits", "<u4")])
+GROUP_DTYPE = np.dtype([("expert", "<u4"), ("pair_start", "<u4"), ("pair_count", "<u4")])
+TILE_DTYPE = np.dtype([("group_start", "<u4"), ("group_count", "<u4"),
+                       ("pair_start", "<u4"), ("pair_count", "<u4")])
+BLOCK_DTYPE = np.dtype([("local_slot", "<u4"), ("pair_start", "<u4"),
+                        ("row_count", "<u4"), ("local_row", "<u4")])
+
+
+def _ptr(t) -> int | None:
+    """Device address of a contiguous torch CUDA tensor (None passes NULL)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    assert t.is_cuda, "device buffers must be CUDA (HIP) tensors"
+    assert t.is_contiguous(), "device buffers must be contiguous"
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is not None:
+        return stream if isinstance(stream, int) else stream.cuda_stream
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _np_ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def offsets_from(seq) -> ExpertOffsets:
+    if isinstance(seq, ExpertOffsets):
+        return seq
+    return ExpertOffsets(*[int(v) for v in seq])
+
+
+# ------------------------------------------------------------------ context
+
+class Context:
+    """MetalContext analogue: device binding, affine group size and scheme
+    (MetalContext.swift:79-175). Defaults: group 64, affine."""
+
+    def __init__(self, device: int = 0, group_size: int | None = None,
+                 scheme: str | None = None):
+        self.lib = load()
+        h = C.c_void_p()
+        check(self.lib.tsg_ctx_create(device, C.byref(h)))
+        self.handle = h
+        self.device = device
+        if group_size is not None:
+            self.set_affine_group_size(group_size)
+        if scheme is not None:
+            self.set_affine_scheme(scheme)
+
+    def set_affine_group_size(self, g: int) -> None:
+        check(self.lib.tsg_ctx_set_affine_group_size(self.handle, g))
+        self.group_size = g
+
+    def set_affine_scheme(self, scheme: str) -> None:
+        check(self.lib.tsg_ctx_set_affine_scheme(self.handle,
+                                                 TSG_SYM if scheme == "sym" else TSG_AFFINE))
+        self.scheme = scheme
+
+    def synchronize(self, stream=None) -> None:
+        check(self.lib.tsg_ctx_synchronize(self.handle, _stream(stream)))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.tsg_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ResidentLayer:
+    """One MoEPack layer file held byte-for-byte in HBM (replaces the SSD
+    streamer + MTLResidencySet, ModelExpertIO.swift:112-324)."""
+
+    def __init__(self, ctx: Context, num_experts: int, expert_stride: int, offsets,
+                 device_tensor=None):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        self.num_experts = num_experts
+        self.expert_stride = expert_stride
+        self.offsets = offsets_from(offsets)
+        self._keep = device_tensor
+        h = C.c_void_p()
+        if device_tensor is None:
+            check(self.lib.tsg_layer_create(ctx.handle, num_experts, expert_stride,
+                                            C.byref(self.offsets), C.byref(h)))
+        else:
+            check(self.lib.tsg_layer_wrap(ctx.handle, _ptr(device_tensor), num_experts,
+                                          expert_stride, C.byref(self.offsets), C.byref(h)))
+        self.handle = h
+
+    def upload(self, host_bytes: np.ndarray, dst_offset: int = 0, stream=None) -> None:
+        a = np.ascontiguousarray(host_bytes).view(np.uint8)
+        check(self.lib.tsg_layer_upload(self.handle, _stream(stream), _np_ptr(a), a.nbytes,
+                                        dst_offset))
+        self.ctx.synchronize(stream)
+
+    @property
+    def device_ptr(self) -> int:
+        return int(self.lib.tsg_layer_device_ptr(self.handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.tsg_layer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------ decode
+
+class MoE:
+    """MoE (MoE.swift:42-662): router + top-8, phase 1 gate/up + activation,
+    phase 2 down + weighted combine."""
+
+    def __init__(self, ctx: Context, router_weight_bits: int = 16,
+                 gate_activation: str = "gelu"):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        h = C.c_void_p()
+        act = TSG_ACT_SILU if gate_activation == "silu" else TSG_ACT_GELU_TANH
+        check(self.lib.tsg_moe_create(ctx.handle, router_weight_bits, act, C.byref(h)))
+        self.handle = h
+
+    def encode_router_gemma4_bf16(self, weights, hidden, effective_scale, per_expert_scale,
+                                  out_indices, out_weights, num_experts, d, top_k=8,
+                                  stream=None):
+        check(self.lib.tsg_moe_router_bf16(
+            self.handle, _stream(stream), _ptr(weights), _ptr(hidden), _ptr(effective_scale),
+            _ptr(per_expert_scale), _ptr(out_indices), _ptr(out_weights), num_experts, d,
+            top_k))
+
+    def encode_router_gemma4_bf16_rows(self, weights, hidden, hidden_stride_elements,
+                                       effective_scale, per_expert_scale, out_indices,
+                                       out_weights, row_count, num_experts, d, top_k=8,
+                                       stream=None):
+        check(self.lib.tsg_moe_router_bf16_rows(
+            self.handle, _stream(stream), _ptr(weights), _ptr(hidden), hidden_stride_elements,
+            _ptr(effective_scale), _ptr(per_expert_scale), _ptr(out_indices),
+            _ptr(out_weights), row_count, num_experts, d, top_k))
+
+    def encode_router_logits_bf16(self, weights, hidden, effective_scale, out_logits,
+                                  num_experts, d, stream=None):
+        check(self.lib.tsg_moe_router_logits_bf16(
+            self.handle, _stream(stream), _ptr(weights), _ptr(hidden), _ptr(effective_scale),
+            _ptr(out_logits), num_experts, d))
+
+    @staticmethod
+    def _blobs(blobs):
+        arr = (C.c_void_p * len(blobs))()
+        for i, b in enumerate(blobs):
+            arr[i] = _ptr(b)
+        return arr
+
+    def encode_routed_phase1(self, routed_blobs, routed_offsets, x, acts, d, f, top_k=8,
+                             stream=None):
+        check(self.lib.tsg_moe_phase1(self.handle, _stream(stream), self._blobs(routed_blobs),
+                                      C.byref(offsets_from(routed_offsets)), _ptr(x),
+                                      _ptr(acts), d, f, top_k))
+
+    def encode_routed_phase1_subset(self, routed_blobs, routed_offsets, x, acts,
+                                    active_slots, active_count, d, f, top_k=8, stream=None):
+        check(self.lib.tsg_moe_phase1_subset(
+            self.handle, _stream(stream), self._blobs(routed_blobs),
+            C.byref(offsets_from(routed_offsets)), _ptr(x), _ptr(acts), _ptr(active_slots),
+            active_count, d, f, top_k))
+
+    def encode_routed_phase2(self, routed_blobs, routed_offsets, acts, routing_weights,
+                             residual, y, d, f, top_k=8, stream=None):
+        check(self.lib.tsg_moe_phase2(self.handle, _stream(stream), self._blobs(routed_blobs),
+                                      C.byref(offsets_from(routed_offsets)), _ptr(acts),
+                                      _ptr(routing_weights), _ptr(residual), _ptr(y), d, f,
+                                      top_k))
+
+    def encode_phase1_resident(self, layer: ResidentLayer, indices, x, acts, d, f, top_k=8,
+                               stream=None):
+        check(self.lib.tsg_moe_phase1_resident(self.handle, _stream(stream), layer.handle,
+                                               _ptr(indices), _ptr(x), _ptr(acts), d, f, top_k))
+
+    def encode_phase2_resident(self, layer: ResidentLayer, indices, acts, routing_weights,
+                               residual, y, d, f, top_k=8, stream=None):
+        check(self.lib.tsg_moe_phase2_resident(self.handle, _stream(stream), layer.handle,
+                                               _ptr(indices), _ptr(acts), _ptr(routing_weights),
+                                               _ptr(residual), _ptr(y), d, f, top_k))
+
+    def encode_decode_layer(self, layer: ResidentLayer, router_weights, router_hidden,
+                            effective_scale, per_expert_scale, x, residual, y, out_indices,
+                            out_weights, acts_scratch, num_experts, d, f, top_k=8,
+                            stream=None):
+        check(self.lib.tsg_moe_decode_layer(
+            self.handle, _stream(stream), layer.handle, _ptr(router_weights),
+            _ptr(router_hidden), _ptr(effective_scale), _ptr(per_expert_scale), _ptr(x),
+            _ptr(residual), _ptr(y), _ptr(out_indices), _ptr(out_weights), _ptr(acts_scratch),
+            num_experts, d, f, top_k))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.tsg_moe_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DequantInt4GEMV:
+    """DequantInt4GEMV (DequantInt4GEMV.swift:6-364)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def encode(self, weights, scales, biases, x, y, m, n, stream=None):
+        check(self.lib.tsg_qmv_int4(self.ctx.handle, _stream(stream), _ptr(weights),
+                                    _ptr(scales), _ptr(biases), _ptr(x), _ptr(y), m, n))
+
+    def encode_rows(self, weights, scales, biases, x, x_stride, y, y_stride, t, m, n,
+                    stream=None):
+        check(self.lib.tsg_qmv_int4_rows(self.ctx.handle, _stream(stream), _ptr(weights),
+                                         _ptr(scales), _ptr(biases), _ptr(x), x_stride, _ptr(y),
+                                         y_stride, t, m, n))
+
+    def debug_dequant_f16(self, weights, scales, biases, out, rows, n, gemm_path=False,
+                          stream=None):
+        fn = self.lib.tsg_debug_gemm_dequant_f16 if gemm_path else self.lib.tsg_debug_dequant_f16
+        check(fn(self.ctx.handle, _stream(stream), _ptr(weights), _ptr(scales), _ptr(biases),
+                 _ptr(out), rows, n))
+
+
+# ----------------------------------------------------------------- prefill
+
+class PrefillRouter:
+    """PrefillRouter (PrefillRouter.swift:69-258)."""
+
+    def __init__(self, moe: MoE):
+        self.moe = moe
+        self.lib = moe.lib
+
+    def encode_gemma4_bf16(self, weights, hidden, hidden_stride_elements, effective_scale,
+                           per_expert_scale, out_indices, out_weights, query_count,
+                           num_experts, d, top_k=8, stream=None):
+        check(self.lib.tsg_prefill_router_bf16(
+            self.moe.handle, _stream(stream), _ptr(weights), _ptr(hidden),
+            hidden_stride_elements, _ptr(effective_scale), _ptr(per_expert_scale),
+            _ptr(out_indices), _ptr(out_weights), query_count, num_experts, d, top_k))
+
+    @staticmethod
+    def make_token_expert_pairs(indices, weights_bits, query_count, top_k) -> np.ndarray:
+        idx = np.ascontiguousarray(indices, np.uint32).ravel()
+        w = np.ascontiguousarray(weights_bits, np.uint16).ravel()
+        out = np.empty(query_count * top_k, PAIR_DTYPE)
+        check(load().tsg_make_token_expert_pairs(_np_ptr(idx), _np_ptr(w), query_count, top_k,
+                                                 _np_ptr(out)))
+        return out
+
+
+class PrefillMoEGrouping:
+    """PrefillMoEGrouping.groupTokenExpertPairs (PrefillMoEGrouping.swift:90-202),
+    host side, with the reference's error cases (TsgError.case)."""
+
+    @staticmethod
+    def group_token_expert_pairs(pairs, query_count, top_k, num_experts,
+                                 tile_expert_count=16, expert_sort_keys=None,
+                                 tile_break_after_group=None):
+        lib = load()
+        pairs = np.ascontiguousarray(pairs, PAIR_DTYPE)
+        n = pairs.size
+        sorted_pairs = np.empty(max(n, 1), PAIR_DTYPE)
+        offsets = np.empty(max(num_experts, 1), np.uint32)
+        counts = np.empty(max(num_experts, 1), np.uint32)
+        groups = np.empty(max(n, 1), GROUP_DTYPE)
+        tiles = np.empty(max(n, 1), TILE_DTYPE)
+        ng, nt = C.c_uint32(0), C.c_uint32(0)
+        keys, nkeys = None, 0
+        if expert_sort_keys is not None:
+            keys = np.ascontiguousarray(expert_sort_keys, np.uint64)
+            nkeys = keys.size
+        check(lib.tsg_group_token_expert_pairs(
+            _np_ptr(pairs), n, query_count & 0xFFFFFFFF, top_k & 0xFFFFFFFF,
+            num_experts & 0xFFFFFFFF, tile_expert_count,
+            _np_ptr(keys) if keys is not None else None, nkeys,
+            -1 if tile_break_after_group is None else tile_break_after_group,
+            _np_ptr(sorted_pairs), _np_ptr(offsets), _np_ptr(counts), _np_ptr(groups),
+            C.byref(ng), _np_ptr(tiles), C.byref(nt)))
+        return dict(sorted_pairs=sorted_pairs[:n], offsets=offsets[:num_experts],
+                    counts=counts[:num_experts], groups=groups[:ng.value],
+                    tiles=tiles[:nt.value])
+
+
+class PrefillRoutedGEMMPlanner:
+    """PrefillRoutedGEMMPlanner.plan (PrefillGroupedRoutedMoE.swift:42-83)."""
+    tile_rows = 64
+
+    @staticmethod
+    def plan(groups, max_rows_per_batch):
+        lib = load()
+        groups = np.ascontiguousarray(groups, GROUP_DTYPE)
+        total = int(groups["pair_count"].sum()) if groups.size else 0
+        cap = total + groups.size + 1
+        blocks = np.empty(cap, BLOCK_DTYPE)
+        rows = np.empty(cap, np.uint32)
+        first = np.empty(cap, np.uint32)
+        nb, nbatch = C.c_uint32(0), C.c_uint32(0)
+        check(lib.tsg_plan_routed_gemm(_np_ptr(groups) if groups.size else None, groups.size,
+                                       max_rows_per_batch, _np_ptr(blocks), C.byref(nb),
+                                       _np_ptr(rows), _np_ptr(first), C.byref(nbatch)))
+        out = []
+        for i in range(nbatch.value):
+            end = first[i + 1] if i + 1 < nbatch.value else nb.value
+            out.append((int(rows[i]), blocks[first[i]:end].copy()))
+        return out
+
+
+class PrefillGroupedRoutedMoE:
+    """PrefillGroupedRoutedMoE (PrefillGroupedRoutedMoE.swift:174-1051) on an
+    HBM-resident layer: device grouping, tiled gate/up + down GEMMs, rows path."""
+
+    def __init__(self, moe: MoE):
+        self.moe = moe
+        self.ctx = moe.ctx
+        self.lib = moe.lib
+
+    def scratch_bytes(self, query_count, top_k, num_experts) -> int:
+        return int(self.lib.tsg_prefill_group_scratch_bytes(query_count, top_k, num_experts))
+
+    def group_pairs_device(self, indices, weights, query_count, top_k, num_experts, sorted_pairs,
+                           offsets, counts, blocks, max_blocks, n_blocks, scratch, tile_rows=64,
+                           stream=None):
+        check(self.lib.tsg_prefill_group_pairs_device(
+            self.ctx.handle, _stream(stream), _ptr(indices), _ptr(weights), query_count, top_k,
+            num_experts, tile_rows, _ptr(sorted_pairs), _ptr(offsets), _ptr(counts),
+            _ptr(blocks), max_blocks, _ptr(n_blocks), _ptr(scratch)))
+
+    def encode_gate_up(self, layer, hidden, hidden_stride, sorted_pairs, blocks, n_blocks, act,
+                       d, f, n_blocks_device=None, stream=None):
+        check(self.lib.tsg_prefill_moe_gate_up(
+            self.moe.handle, _stream(stream), layer.handle, _ptr(hidden), hidden_stride,
+            _ptr(sorted_pairs), _ptr(blocks), n_blocks, _ptr(n_blocks_device), _ptr(act), d, f))
+
+    def encode_down(self, layer, act, sorted_pairs, blocks, n_blocks, route_partials, top_k, d,
+                    f, n_blocks_device=None, stream=None):
+        check(self.lib.tsg_prefill_moe_down(
+            self.moe.handle, _stream(stream), layer.handle, _ptr(act), _ptr(sorted_pairs),
+            _ptr(blocks), n_blocks, _ptr(n_blocks_device), _ptr(route_partials), top_k, d, f))
+
+    def encode_streamed_rows(self, layer, hidden, hidden_stride, sorted_pairs, host_blocks,
+                             act_scratch, route_partials, top_k, d, f, stream=None):
+        hb = np.ascontiguousarray(host_blocks, BLOCK_DTYPE)
+        check(self.lib.tsg_prefill_moe_rows(
+            self.moe.handle, _stream(stream), layer.handle, _ptr(hidden), hidden_stride,
+            _ptr(sorted_pairs), _np_ptr(hb) if hb.size else None, hb.size, _ptr(act_scratch),
+            _ptr(route_partials), top_k, d, f))
+
+
+class PrefillMoE:
+    """PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def encode_reduce_token_major(self, route_partials, route_weights, h2, query_count, top_k,
+                                  d, stream=None):
+        check(self.lib.tsg_prefill_moe_reduce_token_major(
+            self.ctx.handle, _stream(stream), _ptr(route_partials), _ptr(route_weights),
+            _ptr(h2), query_count, top_k, d))
+
+
+class generators:
+    """Device-side synthetic fixtures (counter-based SplitMix64)."""
+
+    @staticmethod
+    def bytes(out, seed, stream=None):
+        check(load().tsg_gen_bytes(_stream(stream), seed, _ptr(out), out.numel() * out.element_size()))
+
+    @staticmethod
+    def bf16_normal(out, seed, sigma, abs_value=False, divisor=1.0, stream=None):
+        check(load().tsg_gen_bf16_normal(_stream(stream), seed, _ptr(out), out.numel(), sigma,
+                                         int(abs_value), divisor))
+
+    @staticmethod
+    def f16_normal(out, seed, sigma=1.0, stream=None):
+        check(load().tsg_gen_f16_normal(_stream(stream), seed, _ptr(out), out.numel(), sigma))

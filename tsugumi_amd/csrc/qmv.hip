@@ -1,0 +1,207 @@
+// qmv.hip — dense int4 GEMV (DequantInt4GEMV.swift:6-364,
+// dequant_int4.metal:135-358) and the bit-exact dequantisation check.
+//
+// One output row per 8 lanes, 16-byte weight chunks (one g32 group, half a
+// g64 group) streamed with all loads in flight, nibbles -> fp16 by the 0x6400
+// exponent trick, v_dot2_f32_f16 against x staged in LDS, fp32 scale fma.
+// The rows form keeps T <= 8 accumulators per lane so a weight chunk is read
+// once for all rows; each row's sum runs in exactly the one-row order.
+#include "tsg_internal.hpp"
+
+namespace tsg {
+namespace {
+
+constexpr int kQBatch = 12;
+constexpr uint32_t kMaxRows = 8;
+
+template <int G, bool SYM, int T>
+__global__ __launch_bounds__(128) void qmv_kernel(const uint8_t* __restrict__ w,
+                                                  const uint16_t* __restrict__ scales,
+                                                  const uint16_t* __restrict__ biases,
+                                                  const uint16_t* __restrict__ x,
+                                                  uint32_t x_stride, uint16_t* __restrict__ y,
+                                                  uint32_t y_stride, uint32_t t, uint32_t m,
+                                                  uint32_t n) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                  // T * n
+    float* xsum = reinterpret_cast<float*>(smem + (size_t)T * n * 2u);  // T * n / 32
+    for (uint32_t r = 0; r < t; ++r)
+        stage_x<SYM>(x + (uint64_t)r * x_stride, n, xs + (size_t)r * n, xsum + r * (n / 32u));
+    __syncthreads();
+
+    const uint32_t row = blockIdx.x * 16u + (threadIdx.x >> 3);
+    const uint32_t j = threadIdx.x & 7u;
+    if (row >= m) return;
+    const uint32_t ngroups = n / G;
+    const uint32_t nchunks = n / 32u;
+    const uint8_t* wr = w + (uint64_t)row * (n / 2u);
+    const uint16_t* sr = scales + (uint64_t)row * ngroups;
+    const uint16_t* br = biases + (uint64_t)row * ngroups;
+    const h2_t bias = SYM ? h2_t{(_Float16)1032.0f, (_Float16)1032.0f}
+                          : h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+    float acc[T];
+#pragma unroll
+    for (int r = 0; r < T; ++r) acc[r] = 0.0f;
+    for (uint32_t base = 0; base < nchunks; base += 8u * kQBatch) {
+        uint4 wv[kQBatch];
+        uint16_t sv[kQBatch];
+#pragma unroll
+        for (int i = 0; i < kQBatch; ++i) {
+            const uint32_t c = base + j + 8u * i;
+            if (c < nchunks) {
+                wv[i] = load16_nt(reinterpret_cast<const uint4*>(wr) + c);
+                sv[i] = sr[c * 32u / G];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kQBatch; ++i) {
+            const uint32_t c = base + j + 8u * i;
+            if (c < nchunks) {
+                const float s = bf16_to_f32(sv[i]);
+                float b = 0.0f;
+                if constexpr (!SYM) b = bf16_to_f32(br[c * 32u / G]);
+#pragma unroll
+                for (int r = 0; r < T; ++r) {
+                    if ((uint32_t)r < t) {
+                        const h2_t* xp = reinterpret_cast<const h2_t*>(xs + (size_t)r * n + c * 32u);
+                        acc[r] = __builtin_fmaf(s, chunk_dot(wv[i], xp, bias), acc[r]);
+                        if constexpr (!SYM)
+                            acc[r] = __builtin_fmaf(b, xsum[r * nchunks + c], acc[r]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < T; ++r) {
+#pragma unroll
+        for (int off = 4; off >= 1; off >>= 1) acc[r] += shfl_xor(acc[r], off);
+    }
+    if (j == 0) {
+#pragma unroll
+        for (int r = 0; r < T; ++r)
+            if ((uint32_t)r < t) y[(uint64_t)r * y_stride + row] = f32_to_f16(acc[r]);
+    }
+}
+
+// out[r, k] = half(fma(q, s, b)), b = -8 s under sym (prefill.metal:1021-1026).
+template <int G, bool SYM>
+__global__ void dequant_f16_kernel(const uint8_t* __restrict__ w,
+                                   const uint16_t* __restrict__ scales,
+                                   const uint16_t* __restrict__ biases,
+                                   uint16_t* __restrict__ out, uint32_t rows, uint32_t n) {
+    const uint64_t total = (uint64_t)rows * n;
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < total;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t r = i / n;
+        const uint32_t k = (uint32_t)(i - r * n);
+        const uint8_t byte = w[r * (n / 2u) + k / 2u];
+        const uint32_t q = (k & 1u) ? (byte >> 4) : (byte & 0xFu);
+        const uint32_t g = k / G;
+        const float s = bf16_to_f32(scales[r * (n / G) + g]);
+        const float b = SYM ? -8.0f * s : bf16_to_f32(biases[r * (n / G) + g]);
+        out[i] = f32_to_f16(__builtin_fmaf((float)q, s, b));
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int G, bool SYM>
+tsg_status launch_qmv(hipStream_t s, const uint8_t* w, const uint16_t* sc, const uint16_t* bi,
+                      const uint16_t* x, uint32_t xs, uint16_t* y, uint32_t ys, uint32_t t,
+                      uint32_t m, uint32_t n) {
+    const dim3 grid((m + 15) / 16);
+    const size_t lds_per_row = (size_t)n * 2u + (SYM ? 0u : (n / 32u) * 4u);
+#define TSG_QMV_CASE(TT)                                                                   \
+    case TT:                                                                               \
+        hipLaunchKernelGGL((qmv_kernel<G, SYM, TT>), grid, dim3(128), lds_per_row * TT, s, \
+                           w, sc, bi, x, xs, y, ys, t, m, n);                              \
+        break;
+    switch (t) {
+        TSG_QMV_CASE(1)
+        TSG_QMV_CASE(2)
+        TSG_QMV_CASE(3)
+        TSG_QMV_CASE(4)
+        TSG_QMV_CASE(5)
+        TSG_QMV_CASE(6)
+        TSG_QMV_CASE(7)
+        TSG_QMV_CASE(8)
+        default: return fail(TSG_ERR_INVALID_ARGUMENT, "t=%u not in 1..8", t);
+    }
+#undef TSG_QMV_CASE
+    return check_launch("qmv_int4");
+}
+
+tsg_status qmv_dispatch(tsg_ctx* ctx, hipStream_t s, const uint8_t* w, const uint16_t* sc,
+                        const uint16_t* bi, const uint16_t* x, uint32_t xs, uint16_t* y,
+                        uint32_t ys, uint32_t t, uint32_t m, uint32_t n) {
+    TSG_REQUIRE(ctx, TSG_ERR_INVALID_ARGUMENT, "ctx is NULL");
+    TSG_REQUIRE(w && sc && x && y, TSG_ERR_INVALID_ARGUMENT, "NULL operand");
+    TSG_REQUIRE(ctx->scheme == TSG_SYM || bi, TSG_ERR_INVALID_ARGUMENT,
+                "biases is NULL under the affine scheme");
+    TSG_REQUIRE(n > 0 && n % ctx->group_size == 0, TSG_ERR_INVALID_ARGUMENT,
+                "N must be a multiple of %u, got %u", ctx->group_size, n);
+    TSG_REQUIRE(m > 0, TSG_ERR_INVALID_ARGUMENT, "m must be positive");
+    // The reference reads weights through ushort* and needs a 2-aligned
+    // weightsOffset (DequantInt4GEMV.swift:91-96); these kernels stream 16-byte
+    // chunks, so rows must start on 16 bytes: n % 32 == 0 (always, n % G == 0)
+    // and a 16-byte aligned base.
+    TSG_REQUIRE(aligned16(w), TSG_ERR_ALIGNMENT,
+                "weights must be 16-byte aligned (got %p)", (const void*)w);
+    TSG_REQUIRE(aligned16(x) && xs % 8 == 0, TSG_ERR_ALIGNMENT,
+                "x rows must be 16-byte aligned");
+    const size_t lds = (size_t)t * ((size_t)n * 2u + (n / 32u) * 4u);
+    TSG_REQUIRE(lds <= 160u * 1024u, TSG_ERR_UNSUPPORTED,
+                "t=%u rows of n=%u do not fit the LDS staging", t, n);
+    const bool sym = ctx->scheme == TSG_SYM;
+    if (ctx->group_size == 32)
+        return sym ? launch_qmv<32, true>(s, w, sc, sc, x, xs, y, ys, t, m, n)
+                   : launch_qmv<32, false>(s, w, sc, bi, x, xs, y, ys, t, m, n);
+    return sym ? launch_qmv<64, true>(s, w, sc, sc, x, xs, y, ys, t, m, n)
+               : launch_qmv<64, false>(s, w, sc, bi, x, xs, y, ys, t, m, n);
+}
+
+}  // namespace
+}  // namespace tsg
+
+using namespace tsg;
+
+extern "C" tsg_status tsg_qmv_int4(tsg_ctx* ctx, tsg_stream stream, const uint8_t* w,
+                                   const uint16_t* scales, const uint16_t* biases,
+                                   const uint16_t* x, uint16_t* y, uint32_t m, uint32_t n) {
+    return qmv_dispatch(ctx, as_stream(stream), w, scales, biases, x, n, y, m, 1, m, n);
+}
+
+extern "C" tsg_status tsg_qmv_int4_rows(tsg_ctx* ctx, tsg_stream stream, const uint8_t* w,
+                                        const uint16_t* scales, const uint16_t* biases,
+                                        const uint16_t* x, uint32_t x_stride, uint16_t* y,
+                                        uint32_t y_stride, uint32_t t, uint32_t m,
+                                        uint32_t n) {
+    TSG_REQUIRE(t >= 1 && t <= kMaxRows, TSG_ERR_INVALID_ARGUMENT, "t=%u not in 1..%u", t,
+                kMaxRows);
+    return qmv_dispatch(ctx, as_stream(stream), w, scales, biases, x, x_stride, y, y_stride, t,
+                        m, n);
+}
+
+extern "C" tsg_status tsg_debug_dequant_f16(tsg_ctx* ctx, tsg_stream stream, const uint8_t* w,
+                                            const uint16_t* scales, const uint16_t* biases,
+                                            uint16_t* out, uint32_t rows, uint32_t n) {
+    TSG_REQUIRE(ctx && w && scales && out, TSG_ERR_INVALID_ARGUMENT, "NULL operand");
+    TSG_REQUIRE(ctx->scheme == TSG_SYM || biases, TSG_ERR_INVALID_ARGUMENT,
+                "biases is NULL under the affine scheme");
+    TSG_REQUIRE(n > 0 && n % ctx->group_size == 0 && rows > 0, TSG_ERR_INVALID_ARGUMENT,
+                "bad shape rows=%u n=%u", rows, n);
+    const uint64_t total = (uint64_t)rows * n;
+    uint64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipStream_t s = as_stream(stream);
+    const bool sym = ctx->scheme == TSG_SYM;
+    if (ctx->group_size == 32) {
+        if (sym) hipLaunchKernelGGL((dequant_f16_kernel<32, true>), dim3(blocks), dim3(256), 0, s, w, scales, scales, out, rows, n);
+        else hipLaunchKernelGGL((dequant_f16_kernel<32, false>), dim3(blocks), dim3(256), 0, s, w, scales, biases, out, rows, n);
+    } else {
+        if (sym) hipLaunchKernelGGL((dequant_f16_kernel<64, true>), dim3(blocks), dim3(256), 0, s, w, scales, scales, out, rows, n);
+        else hipLaunchKernelGGL((dequant_f16_kernel<64, false>), dim3(blocks), dim3(256), 0, s, w, scales, biases, out, rows, n);
+    }
+    return check_launch("debug_dequant_f16");
+}
