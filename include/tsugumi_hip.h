@@ -203,6 +203,12 @@ tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream, const tsg_layer
                                 uint16_t* out_weights, uint16_t* acts_scratch,
                                 uint32_t num_experts, uint32_t d, uint32_t f, uint32_t top_k);
 
+/* tsg_moe_decode_layer runs as one launch (grid barriers between router,
+ * gate/up and down) whenever every block fits on the device at once, else as
+ * router + phase 1 + phase 2 launches; both give identical bits. enabled = 0
+ * forces the three-launch form (no reference counterpart; for A/B checks). */
+tsg_status tsg_moe_set_fused_decode(tsg_moe* moe, int enabled);
+
 /* ---------------------------------------------------------------- QMV ----
  * DequantInt4GEMV (Kernels/Quant/DequantInt4GEMV.swift:6-364). */
 

@@ -423,10 +423,10 @@ void tsgo_router_logits_canonical(const uint16_t* w_bf16, const uint16_t* hidden
         const uint16_t* x = hidden_f16 + (size_t)row * stride;
         for (int e = 0; e < num_experts; ++e) {
             const uint16_t* w = w_bf16 + (size_t)e * d;
-            float p[32];
-            for (int l = 0; l < 32; ++l) {
+            float p[64];
+            for (int l = 0; l < 64; ++l) {
                 float acc = 0.0f;
-                for (int c = l; c < nchunks; c += 32)
+                for (int c = l; c < nchunks; c += 64)
                     for (int k = 0; k < 8; ++k) {
                         const int i = c * 8 + k;
                         const float xe = tsgo_f16_to_float(x[i]) * tsgo_bf16_to_float(es_bf16[i]);
@@ -434,9 +434,9 @@ void tsgo_router_logits_canonical(const uint16_t* w_bf16, const uint16_t* hidden
                     }
                 p[l] = acc;
             }
-            for (int o = 16; o >= 1; o >>= 1) {
-                float q[32];
-                for (int l = 0; l < 32; ++l) q[l] = p[l] + p[l ^ o];
+            for (int o = 32; o >= 1; o >>= 1) {
+                float q[64];
+                for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ o];
                 memcpy(p, q, sizeof(p));
             }
             out_logits[(size_t)row * num_experts + e] = p[0];

@@ -96,9 +96,9 @@ void tsgo_router_reference(const float* w, const float* x, int num_experts, int 
                            int32_t* out_idx, float* out_w);
 /* Router logits in the MI355X kernels' summation order (restated from
  * tsugumi_amd/csrc/decode.hip router_row_dot, not from the reference, whose
- * simd_sum order is Metal's): for each expert, 32 partial sums p_l over the
- * 8-element chunks c = l, l+32, ... (acc = fma(w, x*es, acc), elements in
- * order), then a xor butterfly p_l += p_{l^o} for o = 16, 8, 4, 2, 1. Inputs
+ * simd_sum order is Metal's): for each expert, 64 partial sums p_l over the
+ * 8-element chunks c = l, l+64, ... (acc = fma(w, x*es, acc), elements in
+ * order), then a xor butterfly p_l += p_{l^o} for o = 32, 16, 8, 4, 2, 1. Inputs
  * are bf16 weights, fp16 hidden rows at `stride`, bf16 effective scale. */
 void tsgo_router_logits_canonical(const uint16_t* w_bf16, const uint16_t* hidden_f16,
                                   int stride, const uint16_t* es_bf16, int rows,

@@ -275,3 +275,97 @@ def test_resident_decode_layer_gemma_shape(tsg, ctx):
     rel = oracle.relative_error(oracle.f16_to_float(host(y, np.uint16)), ref)
     print(f"decode layer gemma: experts={list(gi)} rel={rel:.3e}")
     assert rel <= kc.NORTH_STAR
+
+
+def layer_offsets(d, f, group, symmetric):
+    """Expert blob gate(W,S,[B]), up(W,S,[B]), down(W,S,[B]) at a 16 KiB
+    stride; without biases the bias offsets alias the scales."""
+    regions = []
+    cur = 0
+    for rows, k in ((f, d), (f, d), (d, f)):
+        w = cur
+        cur += rows * k // 2
+        s = cur
+        cur += rows * (k // group) * 2
+        if symmetric:
+            b = s
+        else:
+            b = cur
+            cur += rows * (k // group) * 2
+        regions += [w, s, b]
+    stride = (cur + 16383) // 16384 * 16384
+    return regions, stride
+
+
+def make_layer(tsg, ctx, seed, ne, d, f, group, symmetric):
+    import torch
+    offs, stride = layer_offsets(d, f, group, symmetric)
+    buf = torch.empty(ne * stride, dtype=torch.uint8, device="cuda")
+    tsg.generators.bytes(buf, seed)
+    dims = ((f, d), (f, d), (d, f))
+    for e in range(ne):
+        for m, (rows, k) in enumerate(dims):
+            n = rows * (k // group)
+            s_off, b_off = offs[3 * m + 1], offs[3 * m + 2]
+            sreg = buf[e * stride + s_off:e * stride + s_off + 2 * n].view(torch.int16)
+            tsg.generators.bf16_normal(sreg, seed * 1000 + e * 7 + 2 * m + 1, 0.02, True, 7.0)
+            if not symmetric:
+                breg = buf[e * stride + b_off:e * stride + b_off + 2 * n].view(torch.int16)
+                tsg.generators.bf16_normal(breg, seed * 1000 + e * 7 + 2 * m + 2, 0.01)
+    layer = tsg.ResidentLayer(ctx, ne, stride, offs, device_tensor=buf)
+    return layer, buf, offs, stride
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d,f,ne,group,scheme,act", [
+    (2816, 704, 128, 32, "sym", "gelu"),
+    (1024, 512, 64, 64, "affine", "silu"),
+    (768, 256, 32, 32, "affine", "gelu"),
+])
+def test_fused_decode_layer_matches_three_launches(tsg, ctx, d, f, ne, group, scheme, act):
+    """The one-launch decode layer (router, top-8, gate/up, down and combine
+    separated by in-kernel grid barriers) gives the same bits as the
+    three-launch sequence, and both match the oracle (routing bit-exact on the
+    kernel's logit order, y within 1e-3 of MoeRef.applyStreamedRouted)."""
+    import torch
+    configure(ctx, group, scheme)
+    sym = scheme == "sym"
+    layer, buf, offs, stride = make_layer(tsg, ctx, 0x1234 + d, ne, d, f, group, sym)
+    rw = torch.empty(ne * d, dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(rw, 0xB11 + d, 1.0 / np.sqrt(d))
+    es = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(es, 0xB13, 0.1)
+    es_h = (host(es, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    es_bits = oracle.bf16_bits(np.float32(1.0) + np.abs(es_h))
+    pes_bits = oracle.bf16_bits(np.linspace(0.8, 1.2, ne).astype(np.float32))
+    x = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(x, 0xB12 + d, 1.0)
+    res = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(res, 0xB14 + d, 0.5)
+    moe = tsg.MoE(ctx, gate_activation=act)
+    outs = {}
+    for fused in (True, False):
+        moe.set_fused_decode(fused)
+        y, idx, wts, acts = empty(d), empty(8, np.uint32), empty(8), empty(8 * f)
+        moe.encode_decode_layer(layer, rw, x, dev(es_bits), dev(pes_bits), x, res, y, idx, wts,
+                                acts, ne, d, f)
+        ctx.synchronize()  # raises if the fused launch's grid barrier timed out
+        outs[fused] = [host(t, np.uint16 if t is not idx else np.uint32)
+                       for t in (y, idx, wts, acts)]
+    for a, b in zip(outs[True], outs[False]):
+        assert np.array_equal(a, b)
+    y, gi, gw, _ = outs[True]
+    xb, rwb = host(x, np.uint16), host(rw, np.uint16)
+    canon = oracle.router_logits_canonical(rwb, xb, d, es_bits, 1, ne, d)
+    ci, cw = oracle.topk_softmax(canon[0], 8, oracle.bf16_to_float(pes_bits))
+    assert list(gi) == list(ci)
+    assert np.max(np.abs(gw.astype(np.int32) - cw.astype(np.int32))) <= 1
+    image = host(buf, np.uint8)
+    blobs = [np.ascontiguousarray(image[e * stride:(e + 1) * stride]) for e in gi]
+    ref = oracle.moe_apply_streamed_routed(
+        blobs, np.array(offs, np.uint32), oracle.f16_to_float(xb),
+        oracle.f16_to_float(host(res, np.uint16)), oracle.f16_to_float(gw), d, f, group,
+        symmetric=sym, act=1 if act == "silu" else 0)
+    rel = oracle.relative_error(oracle.f16_to_float(y), ref)
+    print(f"fused decode d={d} f={f} ne={ne} g{group} {scheme} {act}: rel={rel:.3e}")
+    assert rel <= kc.NORTH_STAR

@@ -172,6 +172,11 @@ class MoE:
         check(self.lib.tsg_moe_create(ctx.handle, router_weight_bits, act, C.byref(h)))
         self.handle = h
 
+    def set_fused_decode(self, enabled: bool) -> None:
+        """One-launch decode layer when it fits (default) or the three-launch
+        sequence; both give identical bits."""
+        check(self.lib.tsg_moe_set_fused_decode(self.handle, int(enabled)))
+
     def encode_router_gemma4_bf16(self, weights, hidden, effective_scale, per_expert_scale,
                                   out_indices, out_weights, num_experts, d, top_k=8,
                                   stream=None):

@@ -85,7 +85,7 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
     ctx->num_cus = prop.multiProcessorCount;
     hipError_t e = hipMalloc(&ctx->counters, sizeof(uint32_t) * kMaxCounters);
     if (e == hipSuccess)
-        e = hipMalloc(&ctx->logits, sizeof(float) * kMaxRouterRows * kMaxExperts);
+        e = hipMalloc(&ctx->logits, sizeof(float) * kMaxPromptRows * kMaxExperts);
     if (e == hipSuccess) e = hipMemset(ctx->counters, 0, sizeof(uint32_t) * kMaxCounters);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -126,6 +126,16 @@ extern "C" tsg_status tsg_ctx_set_affine_scheme(tsg_ctx* ctx, tsg_affine_scheme 
 extern "C" tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream) {
     TSG_REQUIRE(ctx, TSG_ERR_INVALID_ARGUMENT, "ctx is NULL");
     TSG_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
+    // A fused decode launch whose grid barrier timed out has set this word;
+    // that launch's outputs are invalid.
+    uint32_t err = 0;
+    TSG_HIP_TRY(hipMemcpy(&err, ctx->counters + kBarrierWord + 2, sizeof(err),
+                          hipMemcpyDeviceToHost));
+    if (err) {
+        TSG_HIP_TRY(hipMemset(ctx->counters + kBarrierWord + 2, 0, sizeof(err)));
+        return fail(TSG_ERR_HIP, "fused decode grid barrier timed out: outputs of the "
+                                 "affected launch are invalid");
+    }
     return TSG_OK;
 }
 

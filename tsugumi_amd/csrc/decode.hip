@@ -4,9 +4,9 @@
 // Reference semantics: moe.metal:136-687, MoE.swift:259-644.
 //
 // Layout of the work (wave64):
-//  * router: a 32-lane half-wave owns one expert row; lane l sums the 8-element
-//    chunks c = l, l+32, ... in order with fma, then a xor butterfly over the 32
-//    lanes (16, 8, 4, 2, 1). The oracle restates exactly this order, which is
+//  * router: a wave owns one expert row; lane l sums the 8-element chunks
+//    c = l, l+64, ... in order with fma, then a xor butterfly over the 64
+//    lanes (32, 16, 8, 4, 2, 1). The oracle restates exactly this order, which is
 //    what makes the selected experts bit-exact (and identical between decode
 //    and the prompt router, which runs the same body per row).
 //  * phase 1: 8 lanes own one (slot, f) row pair of gate and up. Lane j streams
@@ -17,7 +17,7 @@
 //  * phase 2: a wave owns 4 output rows x 8 slots x 2 half-rows; the 8 slot
 //    values of a row are combined in slot order in one lane, as the reference
 //    does (moe.metal:678-686).
-#include "tsg_internal.hpp"
+#include "gemv_lane.hpp"
 
 namespace tsg {
 namespace {
@@ -44,38 +44,6 @@ __device__ __forceinline__ const uint8_t* blob_for(const BlobSource& src, uint32
 
 // ----------------------------------------------------------------- router
 
-// Sum of one expert row against x*es in the canonical order (see file
-// comment). `lane` is 0..31 within the half-wave; all 32 lanes return the sum.
-__device__ __forceinline__ float router_row_dot(const uint16_t* __restrict__ w_row,
-                                                const uint16_t* __restrict__ x,
-                                                const uint16_t* __restrict__ es,
-                                                uint32_t d, uint32_t lane) {
-    const uint32_t nchunks = d / 8u;
-    float acc = 0.0f;
-    for (uint32_t c = lane; c < nchunks; c += 32u) {
-        const uint4 wv = *reinterpret_cast<const uint4*>(w_row + c * 8u);
-        const uint4 xv = *reinterpret_cast<const uint4*>(x + c * 8u);
-        const uint4 ev = *reinterpret_cast<const uint4*>(es + c * 8u);
-        const uint32_t wa[4] = {wv.x, wv.y, wv.z, wv.w};
-        const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
-        const uint32_t ea[4] = {ev.x, ev.y, ev.z, ev.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float x0 = f16_to_f32((uint16_t)(xa[k] & 0xFFFFu));
-            const float x1 = f16_to_f32((uint16_t)(xa[k] >> 16));
-            const float e0 = bf16_to_f32((uint16_t)(ea[k] & 0xFFFFu));
-            const float e1 = bf16_to_f32((uint16_t)(ea[k] >> 16));
-            const float w0 = bf16_to_f32((uint16_t)(wa[k] & 0xFFFFu));
-            const float w1 = bf16_to_f32((uint16_t)(wa[k] >> 16));
-            acc = __builtin_fmaf(w0, x0 * e0, acc);
-            acc = __builtin_fmaf(w1, x1 * e1, acc);
-        }
-    }
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) acc += shfl_xor(acc, off);
-    return acc;
-}
-
 // Wave-wide top-k over `ne` logits with the reference's rule
 // (moe.metal:281-329): descending score, ties to the lower index, -inf and NaN
 // never enter; unfilled slots keep (0, -inf). Softmax over the k with the
@@ -91,7 +59,7 @@ __device__ void wave_topk_softmax(const float* logits, uint32_t ne, uint32_t top
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t e = lane + 64u * j;
-        float s = e < ne ? logits[e] : -INFINITY;
+        const float s = e < ne ? logits[e] : -INFINITY;
         v[j] = s;
         eligible[j] = e < ne && s == s && s != -INFINITY;
     }
@@ -144,220 +112,460 @@ __device__ void wave_topk_softmax(const float* logits, uint32_t ne, uint32_t top
     }
 }
 
-// grid (ceil(ne / 8), rows), block 256: half-wave h of wave w owns expert
-// blockIdx.x * 8 + w * 2 + h. With SELECT, the last block to finish a row
-// (completion counter) runs the top-k for it and resets the counter.
+constexpr uint32_t kRouterRows = 16;      // rows sharing one weight read per wave
+constexpr uint32_t kRouterWaves = 4;      // experts per block
+constexpr int kRouterChunks = 8;          // 8-element chunks per lane: d <= 4096
+
+// The canonical router sum over one row held in registers: lane l owns chunks
+// l, l+64, ... (8 elements each, summed in order with fma(w, x*es, acc)), then
+// a xor butterfly 32, 16, 8, 4, 2, 1; every lane returns the full sum.
+__device__ __forceinline__ float router_chunks_dot(const uint4* wv, const uint4* xv,
+                                                   const uint4* ev, uint32_t nchunks,
+                                                   uint32_t lane) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRouterChunks; ++i) {
+        if (lane + 64u * i >= nchunks) break;  // lanes past the row end add nothing
+        const uint32_t wa[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+        const uint32_t xa[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+        const uint32_t ea[4] = {ev[i].x, ev[i].y, ev[i].z, ev[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float x0 = f16_to_f32((uint16_t)(xa[k] & 0xFFFFu));
+            const float x1 = f16_to_f32((uint16_t)(xa[k] >> 16));
+            const float e0 = __uint_as_float(ea[k] << 16);
+            const float e1 = __uint_as_float(ea[k] & 0xFFFF0000u);
+            const float w0 = __uint_as_float(wa[k] << 16);
+            const float w1 = __uint_as_float(wa[k] & 0xFFFF0000u);
+            acc = __builtin_fmaf(w0, x0 * e0, acc);
+            acc = __builtin_fmaf(w1, x1 * e1, acc);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += shfl_xor(acc, off);
+    return acc;
+}
+
+// One router row (loads + canonical sum) on one wave.
+__device__ __forceinline__ float router_dot(const uint16_t* __restrict__ w_row,
+                                            const uint16_t* __restrict__ x,
+                                            const uint16_t* __restrict__ es, uint32_t d,
+                                            uint32_t lane) {
+    const uint32_t nchunks = d / 8u;
+    uint4 wv[kRouterChunks], ev[kRouterChunks], xv[kRouterChunks];
+#pragma unroll
+    for (int i = 0; i < kRouterChunks; ++i) {
+        const uint32_t cc = min(lane + 64u * i, nchunks - 1u);
+        wv[i] = *reinterpret_cast<const uint4*>(w_row + cc * 8u);
+        ev[i] = *reinterpret_cast<const uint4*>(es + cc * 8u);
+        xv[i] = *reinterpret_cast<const uint4*>(x + cc * 8u);
+    }
+    return router_chunks_dot(wv, xv, ev, nchunks, lane);
+}
+
+// One expert row against up to kRouterRows activation rows in the canonical
+// order (see file comment): lane l sums chunks l, l+64, ... (elements in
+// order, acc = fma(w, x*es, acc)), then a xor butterfly 32, 16, 8, 4, 2, 1.
+// Every lane ends with the full sum. Loads for all chunks are issued before
+// any arithmetic; out-of-range chunks load a clamped address and contribute
+// nothing.
 template <bool SELECT>
 __global__ __launch_bounds__(256) void router_kernel(
     const uint16_t* __restrict__ w, const uint16_t* __restrict__ hidden, uint32_t hidden_stride,
     const uint16_t* __restrict__ es, const uint16_t* __restrict__ pes,
     float* __restrict__ logits, uint32_t logits_stride, uint32_t* __restrict__ counters,
     uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w, uint32_t ne, uint32_t d,
-    uint32_t top_k) {
-    const uint32_t row = blockIdx.y;
-    const uint32_t lane32 = threadIdx.x & 31u;
-    const uint32_t e = blockIdx.x * 8u + (threadIdx.x >> 5);
-    const uint16_t* x = hidden + (uint64_t)row * hidden_stride;
-    float* row_logits = logits + (uint64_t)row * logits_stride;
+    uint32_t rows, uint32_t top_k) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t e = blockIdx.x * kRouterWaves + wave;
+    const uint32_t r0 = blockIdx.y * kRouterRows;
+    const uint32_t nr = min(kRouterRows, rows - r0);
+    const uint32_t nchunks = d / 8u;
     if (e < ne) {
-        const float s = router_row_dot(w + (uint64_t)e * d, x, es, d, lane32);
-        if (lane32 == 0) row_logits[e] = s;
+        const uint16_t* wr = w + (uint64_t)e * d;
+        uint4 wv[kRouterChunks], ev[kRouterChunks], xv[kRouterChunks];
+#pragma unroll
+        for (int i = 0; i < kRouterChunks; ++i) {
+            const uint32_t cc = min(lane + 64u * i, nchunks - 1u);
+            wv[i] = *reinterpret_cast<const uint4*>(wr + cc * 8u);
+            ev[i] = *reinterpret_cast<const uint4*>(es + cc * 8u);
+            xv[i] = *reinterpret_cast<const uint4*>(hidden + (uint64_t)r0 * hidden_stride + cc * 8u);
+        }
+        for (uint32_t r = 0; r < nr; ++r) {
+            // next row's activations go out before this row's arithmetic
+            uint4 xn[kRouterChunks];
+            const uint32_t rn = (r + 1 < nr) ? r + 1 : r;
+            const uint16_t* xnext = hidden + (uint64_t)(r0 + rn) * hidden_stride;
+#pragma unroll
+            for (int i = 0; i < kRouterChunks; ++i) {
+                const uint32_t cc = min(lane + 64u * i, nchunks - 1u);
+                xn[i] = *reinterpret_cast<const uint4*>(xnext + cc * 8u);
+            }
+            const float acc = router_chunks_dot(wv, xv, ev, nchunks, lane);
+#pragma unroll
+            for (int i = 0; i < kRouterChunks; ++i) xv[i] = xn[i];
+            if (lane == 0) logits[(uint64_t)(r0 + r) * logits_stride + e] = acc;
+        }
     }
     if constexpr (SELECT) {
         __shared__ uint32_t is_last;
         __threadfence();
         __syncthreads();
         if (threadIdx.x == 0) {
-            const uint32_t done = atomicAdd(&counters[row], 1u);
+            const uint32_t done = atomicAdd(&counters[blockIdx.y], 1u);
             is_last = (done == gridDim.x - 1u) ? 1u : 0u;
         }
         __syncthreads();
         if (is_last) {
             __threadfence();
-            if (threadIdx.x < 64u) {
-                wave_topk_softmax(row_logits, ne, top_k, pes, out_idx + (uint64_t)row * top_k,
-                                  out_w + (uint64_t)row * top_k);
-            }
-            if (threadIdx.x == 0) atomicExch(&counters[row], 0u);
+            for (uint32_t r = wave; r < nr; r += kRouterWaves)
+                wave_topk_softmax(logits + (uint64_t)(r0 + r) * logits_stride, ne, top_k, pes,
+                                  out_idx + (uint64_t)(r0 + r) * top_k,
+                                  out_w + (uint64_t)(r0 + r) * top_k);
+            if (threadIdx.x == 0) atomicExch(&counters[blockIdx.y], 0u);
         }
     }
 }
 
-// ---------------------------------------------------------------- phase 1
+// ------------------------------------------------------- phase geometry
 
-constexpr int kP1Batch = 12;  // chunks per lane in flight per matrix
+// Phase 1: a block owns `pairs` (slot, f) row pairs, 32 lanes each (16 on the
+// gate row, 16 on the up row). Phase 2: a block owns `rows` output rows, one
+// wave each: 8 slots x 8 lanes. Blocks are sized so the grid is about one
+// block per CU (Gemma: 5632 pairs = 256 x 22, 2816 rows = 256 x 11).
+struct DecodeGeometry {
+    uint32_t pairs_per_block;  // even
+    uint32_t p1_blocks;
+    uint32_t rows_per_block;
+    uint32_t p2_blocks;
+    uint32_t threads;          // max(32 * pairs, 64 * rows)
+};
 
-// grid ceil(rows / 16), block 128: 16 (slot, f) row pairs per block, 8 lanes
-// each. rows = top_k * F, or active_count * F for the subset form.
-template <int G, bool SYM, int ACT, bool SUBSET>
-__global__ __launch_bounds__(128) void phase1_kernel(BlobSource src, tsg_expert_offsets o,
-                                                     const uint16_t* __restrict__ x,
-                                                     uint16_t* __restrict__ acts, uint32_t d,
-                                                     uint32_t f, uint32_t top_k) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-    float* xsum = reinterpret_cast<float*>(smem + d * 2u);
-    stage_x<SYM>(x, d, xs, xsum);
-    __syncthreads();
+inline DecodeGeometry decode_geometry(uint32_t d, uint32_t f, uint32_t n_pairs_total,
+                                      uint32_t target_blocks) {
+    DecodeGeometry g{};
+    uint32_t p = (n_pairs_total + target_blocks - 1) / target_blocks;
+    p = p < 2u ? 2u : (p > 32u ? 32u : p);
+    p += p & 1u;
+    g.pairs_per_block = p;
+    g.p1_blocks = (n_pairs_total + p - 1) / p;
+    uint32_t q = (d + target_blocks - 1) / target_blocks;
+    q = q < 1u ? 1u : (q > 16u ? 16u : q);
+    g.rows_per_block = q;
+    g.p2_blocks = (d + q - 1) / q;
+    const uint32_t t1 = 32u * p, t2 = 64u * q;
+    g.threads = t1 > t2 ? t1 : t2;
+    (void)f;
+    return g;
+}
 
-    const uint32_t rows = (SUBSET ? src.active_count : top_k) * f;
-    const uint32_t rowg = blockIdx.x * 16u + (threadIdx.x >> 3);
-    const uint32_t j = threadIdx.x & 7u;
-    if (rowg >= rows) return;
-    uint32_t slot = rowg / f;
-    const uint32_t fr = rowg - slot * f;
-    if constexpr (SUBSET) {
-        slot = src.active_slots[slot];
-        if (slot >= top_k) return;
-    }
+// ------------------------------------------------------ phase 1 / phase 2 bodies
+
+// Addresses of one lane's gate or up row: 32 lanes per (slot, f) pair, lanes
+// 0..15 on the gate row, 16..31 on the up row. A lane whose pair is not live
+// (past the end, or a rejected subset slot) reads row 0 of slot 0 and stores
+// nothing.
+struct GULane {
+    const uint8_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+    uint32_t slot, fr;
+    bool live;
+};
+
+__device__ __forceinline__ GULane gu_lane(const BlobSource& src, const tsg_expert_offsets& o,
+                                          uint32_t d, uint32_t g, uint32_t slot, uint32_t fr,
+                                          bool live) {
+    const bool is_up = (threadIdx.x >> 4) & 1u;
+    if (!live) { slot = 0u; fr = 0u; }
     const uint8_t* blob = blob_for(src, slot);
-    const uint32_t row_bytes = d / 2u;
-    const uint32_t ngroups = d / G;
-    const uint8_t* gw = blob + o.gate_w + (uint64_t)fr * row_bytes;
-    const uint8_t* uw = blob + o.up_w + (uint64_t)fr * row_bytes;
-    const uint16_t* gs = reinterpret_cast<const uint16_t*>(blob + o.gate_s) + (uint64_t)fr * ngroups;
-    const uint16_t* us = reinterpret_cast<const uint16_t*>(blob + o.up_s) + (uint64_t)fr * ngroups;
-    const uint16_t* gb = reinterpret_cast<const uint16_t*>(blob + o.gate_b) + (uint64_t)fr * ngroups;
-    const uint16_t* ub = reinterpret_cast<const uint16_t*>(blob + o.up_b) + (uint64_t)fr * ngroups;
+    const uint32_t ngroups = d / g;
+    GULane l;
+    l.w = blob + (is_up ? o.up_w : o.gate_w) + (uint64_t)fr * (d / 2u);
+    l.s = reinterpret_cast<const uint16_t*>(blob + (is_up ? o.up_s : o.gate_s)) + (uint64_t)fr * ngroups;
+    l.b = reinterpret_cast<const uint16_t*>(blob + (is_up ? o.up_b : o.gate_b)) + (uint64_t)fr * ngroups;
+    l.slot = slot;
+    l.fr = fr;
+    l.live = live;
+    return l;
+}
 
+// Gate/up dot products of one pair (x staged in LDS) and the activation:
+// acts[slot * f + fr] = half(act(gate) * up). `bt` holds the first batch.
+template <int G, bool SYM, int ACT>
+__device__ __forceinline__ void phase1_compute(const GULane& l, ChunkBatch<kGUBatch>& bt,
+                                               const uint16_t* xs, const float* xsum,
+                                               uint16_t* __restrict__ acts, uint32_t d,
+                                               uint32_t f) {
+    const uint32_t j = threadIdx.x & 15u;
+    const bool is_up = (threadIdx.x >> 4) & 1u;
     const uint32_t nchunks = d / 32u;
-    const h2_t bias = SYM ? h2_t{(_Float16)1032.0f, (_Float16)1032.0f}
-                          : h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
-    float g_acc = 0.0f, u_acc = 0.0f;
-    for (uint32_t base = 0; base < nchunks; base += 8u * kP1Batch) {
-        uint4 gv[kP1Batch], uv[kP1Batch];
-        uint16_t gsv[kP1Batch], usv[kP1Batch];
-#pragma unroll
-        for (int i = 0; i < kP1Batch; ++i) {
-            const uint32_t c = base + j + 8u * i;
-            if (c < nchunks) {
-                gv[i] = load16_nt(reinterpret_cast<const uint4*>(gw) + c);
-                uv[i] = load16_nt(reinterpret_cast<const uint4*>(uw) + c);
-                gsv[i] = gs[c * 32u / G];
-                usv[i] = us[c * 32u / G];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kP1Batch; ++i) {
-            const uint32_t c = base + j + 8u * i;
-            if (c < nchunks) {
-                const h2_t* xp = reinterpret_cast<const h2_t*>(xs + c * 32u);
-                const float gd = chunk_dot(gv[i], xp, bias);
-                const float ud = chunk_dot(uv[i], xp, bias);
-                const float gsc = bf16_to_f32(gsv[i]);
-                const float usc = bf16_to_f32(usv[i]);
-                g_acc = __builtin_fmaf(gsc, gd, g_acc);
-                u_acc = __builtin_fmaf(usc, ud, u_acc);
-                if constexpr (!SYM) {
-                    const uint32_t g = c * 32u / G;
-                    g_acc = __builtin_fmaf(bf16_to_f32(gb[g]), xsum[c], g_acc);
-                    u_acc = __builtin_fmaf(bf16_to_f32(ub[g]), xsum[c], u_acc);
-                }
-            }
-        }
+    float acc[1] = {0.0f};
+    for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
+        if (base) load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, base, j, nchunks, bt);
+        compute_batch<G, SYM, kGUBatch, kGULanes, 1>(bt, base, j, nchunks, xs, 0u, xsum, 1u, acc);
     }
 #pragma unroll
-    for (int off = 4; off >= 1; off >>= 1) {
-        g_acc += shfl_xor(g_acc, off);
-        u_acc += shfl_xor(u_acc, off);
-    }
-    if (j == 0) acts[slot * f + fr] = f32_to_f16(gate_activation<ACT>(g_acc) * u_acc);
+    for (int off = 8; off >= 1; off >>= 1) acc[0] += shfl_xor(acc[0], off);
+    const float up = shfl_xor(acc[0], 16);  // gate lanes receive the up sum
+    if (l.live && !is_up && j == 0)
+        acts[l.slot * f + l.fr] = f32_to_f16(gate_activation<ACT>(acc[0]) * up);
 }
 
-// ---------------------------------------------------------------- phase 2
-
-constexpr int kP2Batch = 12;
-
-// grid ceil(d / 16), block 256: wave w owns rows blockIdx.x * 16 + w * 4 .. +3;
-// lane = row_in_wave * 16 + slot * 2 + half.
+// Down + combine for output row `row` (< d) on one wave: lane = slot * 8 + j.
+// acts staged in LDS (slot stride slot_h). y[row] = half(res + sum_s w_s v_s)
+// in slot order (moe.metal:678-686).
 template <int G, bool SYM>
-__global__ __launch_bounds__(256) void phase2_kernel(BlobSource src, tsg_expert_offsets o,
-                                                     const uint16_t* __restrict__ acts,
-                                                     const uint16_t* __restrict__ routing_w,
-                                                     const uint16_t* __restrict__ residual,
-                                                     uint16_t* __restrict__ y, uint32_t d,
-                                                     uint32_t f) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    uint16_t* as = reinterpret_cast<uint16_t*>(smem);              // 8 * f
-    float* asum = reinterpret_cast<float*>(smem + kTopK * f * 2u); // 8 * f / 32
-    for (uint32_t s = 0; s < kTopK; ++s) {
-        // stage_x works on threadIdx-strided blocks; do each slot in turn
-        const uint16_t* a = acts + s * f;
-        for (uint32_t b = threadIdx.x; b < f / 8u; b += blockDim.x) {
-            const uint4 v = *reinterpret_cast<const uint4*>(a + b * 8u);
-            uint4 ov;
-            ov.x = (v.x & 0xFFFFu) | (v.z << 16);
-            ov.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
-            ov.z = (v.y & 0xFFFFu) | (v.w << 16);
-            ov.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
-            *reinterpret_cast<uint4*>(as + s * f + b * 8u) = ov;
-        }
-        if constexpr (!SYM) {
-            for (uint32_t c = threadIdx.x; c < f / 32u; c += blockDim.x) {
-                float sum = 0.0f;
-                for (uint32_t k = 0; k < 32u; ++k) sum += f16_to_f32(a[c * 32u + k]);
-                asum[s * (f / 32u) + c] = sum;
-            }
-        }
-    }
-    __syncthreads();
-
+__device__ __forceinline__ void phase2_body(const BlobSource& src, const tsg_expert_offsets& o,
+                                            const uint16_t* as, uint32_t slot_h,
+                                            const float* asum, const uint16_t* __restrict__ rw,
+                                            const uint16_t* __restrict__ residual,
+                                            uint16_t* __restrict__ y, uint32_t d, uint32_t f,
+                                            uint32_t row, ChunkBatch<kDBatch>& bt,
+                                            bool preloaded) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t rl = lane >> 4;
-    const uint32_t slot = (lane >> 1) & 7u;
-    const uint32_t half = lane & 1u;
-    const uint32_t row = blockIdx.x * 16u + wave * 4u + rl;
+    const uint32_t slot = lane >> 3, j = lane & 7u;
     const bool live = row < d;
+    const uint32_t rr = live ? row : 0u;
     const uint8_t* blob = blob_for(src, slot);
-    const uint32_t row_bytes = f / 2u;
-    const uint32_t ngroups = f / G;
-    const uint32_t nchunks = f / 32u;
-    const uint8_t* w = blob + o.down_w + (uint64_t)(live ? row : 0u) * row_bytes;
-    const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + o.down_s) + (uint64_t)(live ? row : 0u) * ngroups;
-    const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + o.down_b) + (uint64_t)(live ? row : 0u) * ngroups;
-    const h2_t bias = SYM ? h2_t{(_Float16)1032.0f, (_Float16)1032.0f}
-                          : h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
-    float acc = 0.0f;
-    if (live) {
-        for (uint32_t base = 0; base < nchunks; base += 2u * kP2Batch) {
-            uint4 wv[kP2Batch];
-            uint16_t sv[kP2Batch];
-#pragma unroll
-            for (int i = 0; i < kP2Batch; ++i) {
-                const uint32_t c = base + half + 2u * i;
-                if (c < nchunks) {
-                    wv[i] = load16_nt(reinterpret_cast<const uint4*>(w) + c);
-                    sv[i] = sc[c * 32u / G];
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < kP2Batch; ++i) {
-                const uint32_t c = base + half + 2u * i;
-                if (c < nchunks) {
-                    const h2_t* xp = reinterpret_cast<const h2_t*>(as + slot * f + c * 32u);
-                    acc = __builtin_fmaf(bf16_to_f32(sv[i]), chunk_dot(wv[i], xp, bias), acc);
-                    if constexpr (!SYM)
-                        acc = __builtin_fmaf(bf16_to_f32(bi[c * 32u / G]),
-                                             asum[slot * nchunks + c], acc);
-                }
-            }
-        }
+    const uint32_t ngroups = f / G, nchunks = f / 32u;
+    const uint8_t* w = blob + o.down_w + (uint64_t)rr * (f / 2u);
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + o.down_s) + (uint64_t)rr * ngroups;
+    const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + o.down_b) + (uint64_t)rr * ngroups;
+    float acc[1] = {0.0f};
+    for (uint32_t base = 0; base < nchunks; base += kDLanes * kDBatch) {
+        if (base || !preloaded) load_batch<G, SYM, kDBatch, kDLanes>(w, sc, bi, base, j, nchunks, bt);
+        compute_batch<G, SYM, kDBatch, kDLanes, 1>(bt, base, j, nchunks, as + slot * slot_h, 0u,
+                                                   asum + slot * nchunks, 1u, acc);
     }
-    acc += shfl_xor(acc, 1);
-    // slot values of row rl live in lanes rl*16 + 2s; combine in slot order
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1) acc[0] += shfl_xor(acc[0], off);
     float vals[kTopK];
 #pragma unroll
-    for (int s = 0; s < (int)kTopK; ++s) vals[s] = __shfl(acc, (int)(rl * 16u + 2u * s), 64);
-    if ((lane & 15u) == 0 && live) {
+    for (int s = 0; s < (int)kTopK; ++s) vals[s] = __shfl(acc[0], s * 8, 64);
+    if (lane == 0 && live) {
         float out = f16_to_f32(residual[row]);
 #pragma unroll
         for (int s = 0; s < (int)kTopK; ++s) {
-            const float p = f16_to_f32(routing_w[s]) * vals[s];
+            const float p = f16_to_f32(rw[s]) * vals[s];
             out = out + p;
         }
         y[row] = f32_to_f16(out);
     }
+}
+
+// Prefetch of a lane's phase-2 weights (issued early, consumed after a barrier).
+template <int G, bool SYM>
+__device__ __forceinline__ void phase2_prefetch(const BlobSource& src, const tsg_expert_offsets& o,
+                                                uint32_t d, uint32_t f, uint32_t row,
+                                                ChunkBatch<kDBatch>& bt) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t slot = lane >> 3, j = lane & 7u;
+    const uint32_t rr = row < d ? row : 0u;
+    const uint8_t* blob = blob_for(src, slot);
+    const uint32_t ngroups = f / G, nchunks = f / 32u;
+    load_batch<G, SYM, kDBatch, kDLanes>(blob + o.down_w + (uint64_t)rr * (f / 2u),
+                                         reinterpret_cast<const uint16_t*>(blob + o.down_s) + (uint64_t)rr * ngroups,
+                                         reinterpret_cast<const uint16_t*>(blob + o.down_b) + (uint64_t)rr * ngroups,
+                                         0u, j, nchunks, bt);
+}
+
+__host__ __device__ __forceinline__ uint32_t p2_slot_halves(uint32_t f) {
+    return lds_chunks_halves(f) + 8u;
+}
+
+// ---------------------------------------------------------------- phase 1
+
+// grid p1_blocks, block 32 * pairs_per_block: pair = blockIdx.x * ppb + t / 32,
+// pair = slot * f + fr. Subset form: pair = a * f + fr with slot
+// active_slots[a]. Weight loads go out before x is staged.
+template <int G, bool SYM, int ACT, bool SUBSET>
+__global__ __launch_bounds__(1024) void phase1_kernel(BlobSource src, tsg_expert_offsets o,
+                                                      const uint16_t* __restrict__ x,
+                                                      uint16_t* __restrict__ acts, uint32_t d,
+                                                      uint32_t f, uint32_t top_k,
+                                                      uint32_t pairs_per_block) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+    float* xsum = reinterpret_cast<float*>(smem + lds_chunks_halves(d) * 2u);
+    const uint32_t n_pairs = (SUBSET ? src.active_count : top_k) * f;
+    const uint32_t pair = blockIdx.x * pairs_per_block + (threadIdx.x >> 5);
+    bool live = pair < n_pairs;
+    const uint32_t pp = live ? pair : 0u;
+    uint32_t slot = pp / f;
+    const uint32_t fr = pp - slot * f;
+    if constexpr (SUBSET) {
+        slot = src.active_slots[slot];
+        if (slot >= top_k) live = false;
+    }
+    const GULane l = gu_lane(src, o, d, G, slot, fr, live);
+    ChunkBatch<kGUBatch> bt;
+    load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, 0u, threadIdx.x & 15u, d / 32u, bt);
+    stage_act_rows<SYM>(x, 0u, 1u, d, xs, 0u, xsum);
+    __syncthreads();
+    phase1_compute<G, SYM, ACT>(l, bt, xs, xsum, acts, d, f);
+}
+
+// ---------------------------------------------------------------- phase 2
+
+// grid p2_blocks, block 64 * rows_per_block: row = blockIdx.x * rpb + wave.
+template <int G, bool SYM>
+__global__ __launch_bounds__(1024) void phase2_kernel(BlobSource src, tsg_expert_offsets o,
+                                                      const uint16_t* __restrict__ acts,
+                                                      const uint16_t* __restrict__ routing_w,
+                                                      const uint16_t* __restrict__ residual,
+                                                      uint16_t* __restrict__ y, uint32_t d,
+                                                      uint32_t f, uint32_t rows_per_block) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t slot_h = p2_slot_halves(f);
+    uint16_t* as = reinterpret_cast<uint16_t*>(smem);
+    float* asum = reinterpret_cast<float*>(smem + kTopK * slot_h * 2u);
+    const uint32_t row = blockIdx.x * rows_per_block + (threadIdx.x >> 6);
+    ChunkBatch<kDBatch> bt;
+    phase2_prefetch<G, SYM>(src, o, d, f, row, bt);
+    stage_act_rows<SYM>(acts, f, kTopK, f, as, slot_h, asum);
+    __syncthreads();
+    phase2_body<G, SYM>(src, o, as, slot_h, asum, routing_w, residual, y, d, f, row, bt, true);
+}
+
+// ---------------------------------------------------------- grid barrier
+
+// Generation barrier over the blocks of one launch, all co-resident (the host
+// checks occupancy before launching). The last block to arrive may run
+// `on_last` (block-wide) before releasing the others. Waiting is bounded: after
+// kSpinLimit polls a block records an error and proceeds, so every wave
+// reaches the end of the kernel whatever happens to another block.
+struct GridBarrier {
+    uint32_t count;
+    uint32_t gen;
+    uint32_t error;
+    uint32_t pad;
+};
+
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+__device__ __forceinline__ uint32_t atomic_load_acq(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every thread releases its own global writes at agent scope before the block
+// arrives: __syncthreads() alone does not wait for outstanding global stores,
+// so a single thread's fence would not cover the other waves' writes. The
+// last block to arrive runs `on_last` (after an acquire) and opens the next
+// generation; the others spin on the generation word, bounded by kSpinLimit
+// (on timeout they set `error`, which tsg_ctx_synchronize reports).
+template <typename F>
+__device__ __forceinline__ void grid_barrier(GridBarrier* bar, uint32_t nblocks, F&& on_last) {
+    __shared__ uint32_t last_flag, gen_seen;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        gen_seen = atomic_load_acq(&bar->gen);  // read before arriving
+        const uint32_t arrived = __hip_atomic_fetch_add(&bar->count, 1u, __ATOMIC_ACQ_REL,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+        last_flag = arrived == nblocks - 1u ? 1u : 0u;
+    }
+    __syncthreads();
+    if (last_flag) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        on_last();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __hip_atomic_store(&bar->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(&bar->gen, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else if (threadIdx.x == 0) {
+        uint32_t spins = 0;
+        while (atomic_load_acq(&bar->gen) == gen_seen) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > kSpinLimit) {
+                atomicOr(&bar->error, 1u);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// -------------------------------------------------- fused decode layer
+
+struct DecodeLayerArgs {
+    const uint8_t* layer_base;
+    uint64_t expert_stride;
+    tsg_expert_offsets o;
+    const uint16_t* router_w;
+    const uint16_t* router_hidden;
+    const uint16_t* es;
+    const uint16_t* pes;
+    const uint16_t* x;
+    const uint16_t* residual;
+    uint16_t* y;
+    uint32_t* out_idx;
+    uint16_t* out_w;
+    uint16_t* acts;
+    float* logits;
+    GridBarrier* bar;
+    uint32_t ne, d, f, pairs_per_block, rows_per_block;
+};
+
+// One decode MoE layer in one launch (grid = one block per CU, all
+// co-resident): router logits (one expert row per block, the router kernel's
+// canonical order) -> barrier whose last block runs the top-k -> every block:
+// prefetch its down-projection weights, gate/up + activation for its row
+// pairs -> barrier -> down + slot-ordered combine for its output rows. The
+// arithmetic of every phase is the separate kernels' (shared bodies), so the
+// fused and unfused paths agree bit for bit.
+template <int G, bool SYM, int ACT>
+__global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t nb = gridDim.x;
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+    float* xsum = reinterpret_cast<float*>(smem + lds_chunks_halves(a.d) * 2u);
+
+    // router rows: wave 0 of block b takes experts b, b + nb, ...
+    if (wave == 0)
+        for (uint32_t e = blockIdx.x; e < a.ne; e += nb) {
+            const float s = router_dot(a.router_w + (uint64_t)e * a.d, a.router_hidden, a.es,
+                                       a.d, lane);
+            if (lane == 0) a.logits[e] = s;
+        }
+    stage_act_rows<SYM>(a.x, 0u, 1u, a.d, xs, 0u, xsum);
+    grid_barrier(a.bar, nb, [&] {
+        if (wave == 0) wave_topk_softmax(a.logits, a.ne, kTopK, a.pes, a.out_idx, a.out_w);
+    });
+
+    BlobSource src{};
+    src.resident = 1;
+    src.base = a.layer_base;
+    src.stride = a.expert_stride;
+    src.indices = a.out_idx;
+    const uint32_t row = blockIdx.x * a.rows_per_block + wave;
+    ChunkBatch<kDBatch> dbt;
+    const bool p2_wave = wave < a.rows_per_block;
+    if (p2_wave) phase2_prefetch<G, SYM>(src, a.o, a.d, a.f, row, dbt);
+    {
+        const uint32_t pair = blockIdx.x * a.pairs_per_block + (threadIdx.x >> 5);
+        const bool live = (threadIdx.x >> 5) < a.pairs_per_block && pair < kTopK * a.f;
+        const uint32_t pp = live ? pair : 0u;
+        const uint32_t slot = pp / a.f;
+        const GULane l = gu_lane(src, a.o, a.d, G, slot, pp - slot * a.f, live);
+        ChunkBatch<kGUBatch> gbt;
+        load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, 0u, threadIdx.x & 15u, a.d / 32u, gbt);
+        phase1_compute<G, SYM, ACT>(l, gbt, xs, xsum, a.acts, a.d, a.f);
+    }
+    grid_barrier(a.bar, nb, [] {});
+
+    const uint32_t slot_h = p2_slot_halves(a.f);
+    uint16_t* as = reinterpret_cast<uint16_t*>(smem);
+    float* asum = reinterpret_cast<float*>(smem + kTopK * slot_h * 2u);
+    stage_act_rows<SYM>(a.acts, a.f, kTopK, a.f, as, slot_h, asum);
+    __syncthreads();
+    if (p2_wave)
+        phase2_body<G, SYM>(src, a.o, as, slot_h, asum, a.out_w, a.residual, a.y, a.d, a.f, row,
+                            dbt, true);
 }
 
 // ------------------------------------------------------------ host helpers
@@ -386,52 +594,55 @@ tsg_status router_launch(tsg_moe* moe, hipStream_t stream, const uint16_t* w,
                          uint32_t top_k, bool select) {
     TSG_REQUIRE(ne > 0 && ne <= kMaxExperts, TSG_ERR_INVALID_ARGUMENT,
                 "numExperts %u not in 1..%u", ne, kMaxExperts);
-    TSG_REQUIRE(d > 0 && d % 8 == 0, TSG_ERR_INVALID_ARGUMENT, "d=%u must be a multiple of 8", d);
+    TSG_REQUIRE(d > 0 && d % 8 == 0 && d <= 8u * 64u * kRouterChunks, TSG_ERR_INVALID_ARGUMENT,
+                "d=%u must be a multiple of 8 and at most %u", d, 8u * 64u * kRouterChunks);
     TSG_REQUIRE(stride % 8 == 0, TSG_ERR_ALIGNMENT, "hidden stride %u must be a multiple of 8",
                 stride);
     TSG_REQUIRE(w && hidden && es, TSG_ERR_INVALID_ARGUMENT, "NULL router operand");
     TSG_REQUIRE(aligned16(w) && aligned16(hidden) && aligned16(es), TSG_ERR_ALIGNMENT,
                 "router weights, hidden and effective_scale must be 16-byte aligned");
+    TSG_REQUIRE(rows > 0 && rows <= kMaxPromptRows, TSG_ERR_INVALID_ARGUMENT,
+                "rows=%u not in 1..%u", rows, kMaxPromptRows);
     tsg_ctx* ctx = moe->ctx;
-    const dim3 grid((ne + 7) / 8, rows);
+    const dim3 grid((ne + kRouterWaves - 1) / kRouterWaves, (rows + kRouterRows - 1) / kRouterRows);
     if (select) {
         TSG_REQUIRE(top_k == kTopK, TSG_ERR_INVALID_ARGUMENT, "topK must be %u, got %u", kTopK,
                     top_k);
         TSG_REQUIRE(pes && out_idx && out_w, TSG_ERR_INVALID_ARGUMENT, "NULL router output");
         hipLaunchKernelGGL(router_kernel<true>, grid, dim3(256), 0, stream, w, hidden, stride, es,
                            pes, ctx->logits, kMaxExperts, ctx->counters, out_idx, out_w, ne, d,
-                           top_k);
+                           rows, top_k);
     } else {
         TSG_REQUIRE(logits_out, TSG_ERR_INVALID_ARGUMENT, "out_logits is NULL");
         hipLaunchKernelGGL(router_kernel<false>, grid, dim3(256), 0, stream, w, hidden, stride,
-                           es, pes, logits_out, ne, ctx->counters, out_idx, out_w, ne, d, top_k);
+                           es, pes, logits_out, ne, ctx->counters, out_idx, out_w, ne, d, rows,
+                           top_k);
     }
     return check_launch("router");
 }
+
+constexpr uint32_t kTargetBlocks = 256;  // about one block per CU
 
 template <int G, bool SYM>
 tsg_status launch_phase1(tsg_moe* moe, hipStream_t stream, const BlobSource& src,
                          const tsg_expert_offsets& o, const uint16_t* x, uint16_t* acts,
                          uint32_t d, uint32_t f, uint32_t top_k, bool subset) {
-    const uint32_t rows = (subset ? src.active_count : top_k) * f;
-    if (rows == 0) return TSG_OK;
-    const dim3 grid((rows + 15) / 16);
-    const size_t lds = d * 2u + (SYM ? 0u : (d / 32u) * 4u);
+    const uint32_t n_pairs = (subset ? src.active_count : top_k) * f;
+    if (n_pairs == 0) return TSG_OK;
+    const DecodeGeometry g = decode_geometry(d, f, n_pairs, kTargetBlocks);
+    const dim3 grid(g.p1_blocks), block(32u * g.pairs_per_block);
+    const size_t lds = lds_chunks_halves(d) * 2u + (SYM ? 0u : (d / 32u) * 4u);
+#define TSG_P1(ACT, SUB)                                                                      \
+    hipLaunchKernelGGL((phase1_kernel<G, SYM, ACT, SUB>), grid, block, lds, stream, src, o, x, \
+                       acts, d, f, top_k, g.pairs_per_block)
     if (moe->activation == TSG_ACT_SILU) {
-        if (subset)
-            hipLaunchKernelGGL((phase1_kernel<G, SYM, TSG_ACT_SILU, true>), grid, dim3(128), lds,
-                               stream, src, o, x, acts, d, f, top_k);
-        else
-            hipLaunchKernelGGL((phase1_kernel<G, SYM, TSG_ACT_SILU, false>), grid, dim3(128), lds,
-                               stream, src, o, x, acts, d, f, top_k);
+        if (subset) TSG_P1(TSG_ACT_SILU, true);
+        else TSG_P1(TSG_ACT_SILU, false);
     } else {
-        if (subset)
-            hipLaunchKernelGGL((phase1_kernel<G, SYM, TSG_ACT_GELU_TANH, true>), grid, dim3(128),
-                               lds, stream, src, o, x, acts, d, f, top_k);
-        else
-            hipLaunchKernelGGL((phase1_kernel<G, SYM, TSG_ACT_GELU_TANH, false>), grid,
-                               dim3(128), lds, stream, src, o, x, acts, d, f, top_k);
+        if (subset) TSG_P1(TSG_ACT_GELU_TANH, true);
+        else TSG_P1(TSG_ACT_GELU_TANH, false);
     }
+#undef TSG_P1
     return check_launch("phase1");
 }
 
@@ -440,7 +651,7 @@ tsg_status phase1_dispatch(tsg_moe* moe, hipStream_t stream, const BlobSource& s
                            uint32_t d, uint32_t f, uint32_t top_k, bool subset) {
     TSG_REQUIRE(x && acts, TSG_ERR_INVALID_ARGUMENT, "NULL x/acts");
     TSG_REQUIRE(aligned16(x), TSG_ERR_ALIGNMENT, "x must be 16-byte aligned");
-    TSG_REQUIRE(d * 2u + (d / 32u) * 4u <= 160u * 1024u, TSG_ERR_UNSUPPORTED,
+    TSG_REQUIRE(lds_chunks_halves(d) * 2u + (d / 32u) * 4u <= 160u * 1024u, TSG_ERR_UNSUPPORTED,
                 "d=%u does not fit the LDS staging", d);
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
@@ -451,33 +662,71 @@ tsg_status phase1_dispatch(tsg_moe* moe, hipStream_t stream, const BlobSource& s
                : launch_phase1<64, false>(moe, stream, src, o, x, acts, d, f, top_k, subset);
 }
 
+size_t phase2_lds(uint32_t f, bool sym) {
+    return kTopK * p2_slot_halves(f) * 2u + (sym ? 0u : kTopK * (f / 32u) * 4u);
+}
+
 tsg_status phase2_dispatch(tsg_moe* moe, hipStream_t stream, const BlobSource& src,
                            const tsg_expert_offsets& o, const uint16_t* acts,
                            const uint16_t* rw, const uint16_t* residual, uint16_t* y,
                            uint32_t d, uint32_t f) {
     TSG_REQUIRE(acts && rw && residual && y, TSG_ERR_INVALID_ARGUMENT, "NULL phase-2 operand");
     TSG_REQUIRE(aligned16(acts), TSG_ERR_ALIGNMENT, "acts must be 16-byte aligned");
-    const size_t lds = kTopK * f * 2u + kTopK * (f / 32u) * 4u;
-    TSG_REQUIRE(lds <= 160u * 1024u, TSG_ERR_UNSUPPORTED, "f=%u does not fit the LDS staging", f);
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
-    const dim3 grid((d + 15) / 16);
+    const size_t lds = phase2_lds(f, sym);
+    TSG_REQUIRE(lds <= 160u * 1024u, TSG_ERR_UNSUPPORTED, "f=%u does not fit the LDS staging", f);
+    const DecodeGeometry g = decode_geometry(d, f, kTopK * f, kTargetBlocks);
+    const dim3 grid(g.p2_blocks), block(64u * g.rows_per_block);
+#define TSG_P2(GG, SS)                                                                       \
+    hipLaunchKernelGGL((phase2_kernel<GG, SS>), grid, block, lds, stream, src, o, acts, rw, \
+                       residual, y, d, f, g.rows_per_block)
     if (ctx->group_size == 32) {
-        if (sym)
-            hipLaunchKernelGGL((phase2_kernel<32, true>), grid, dim3(256), lds, stream, src, o,
-                               acts, rw, residual, y, d, f);
-        else
-            hipLaunchKernelGGL((phase2_kernel<32, false>), grid, dim3(256), lds, stream, src, o,
-                               acts, rw, residual, y, d, f);
+        if (sym) TSG_P2(32, true);
+        else TSG_P2(32, false);
     } else {
-        if (sym)
-            hipLaunchKernelGGL((phase2_kernel<64, true>), grid, dim3(256), lds, stream, src, o,
-                               acts, rw, residual, y, d, f);
-        else
-            hipLaunchKernelGGL((phase2_kernel<64, false>), grid, dim3(256), lds, stream, src, o,
-                               acts, rw, residual, y, d, f);
+        if (sym) TSG_P2(64, true);
+        else TSG_P2(64, false);
     }
+#undef TSG_P2
     return check_launch("phase2");
+}
+
+// The fused one-launch decode layer, when every block fits on the device at
+// once (the grid barriers need all blocks resident). Returns TSG_ERR_DECLINED
+// otherwise and the caller runs the three-kernel sequence.
+template <int G, bool SYM, int ACT>
+tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, const DecodeLayerArgs& a,
+                        const DecodeGeometry& g) {
+    const uint32_t nb = g.p1_blocks > g.p2_blocks ? g.p1_blocks : g.p2_blocks;
+    const size_t lds_a = lds_chunks_halves(a.d) * 2u + (SYM ? 0u : (a.d / 32u) * 4u);
+    const size_t lds_b = phase2_lds(a.f, SYM);
+    const size_t lds = lds_a > lds_b ? lds_a : lds_b;
+    auto kern = decode_layer_kernel<G, SYM, ACT>;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, (int)g.threads, lds) !=
+            hipSuccess ||
+        (uint64_t)per_cu * (uint64_t)moe->ctx->num_cus < nb)
+        return TSG_ERR_DECLINED;
+    hipLaunchKernelGGL(kern, dim3(nb), dim3(g.threads), lds, stream, a);
+    return check_launch("decode_layer");
+}
+
+tsg_status fused_dispatch(tsg_moe* moe, hipStream_t stream, const DecodeLayerArgs& a,
+                          const DecodeGeometry& g) {
+    const tsg_ctx* ctx = moe->ctx;
+    const bool sym = ctx->scheme == TSG_SYM;
+    const bool silu = moe->activation == TSG_ACT_SILU;
+#define TSG_FU(GG, SS)                                                             \
+    return silu ? launch_fused<GG, SS, TSG_ACT_SILU>(moe, stream, a, g)            \
+                : launch_fused<GG, SS, TSG_ACT_GELU_TANH>(moe, stream, a, g)
+    if (ctx->group_size == 32) {
+        if (sym) TSG_FU(32, true);
+        TSG_FU(32, false);
+    }
+    if (sym) TSG_FU(64, true);
+    TSG_FU(64, false);
+#undef TSG_FU
 }
 
 tsg_status blobs_from_ptrs(const void* const* routed_blobs, const tsg_expert_offsets* offsets,
@@ -657,9 +906,43 @@ extern "C" tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream,
     if (st) return st;
     if ((st = check_decode_shape(moe->ctx, d, f, top_k))) return st;
     TSG_REQUIRE(layer, TSG_ERR_INVALID_ARGUMENT, "layer is NULL");
-    TSG_REQUIRE(ne <= layer->num_experts, TSG_ERR_INVALID_ARGUMENT,
+    TSG_REQUIRE(ne > 0 && ne <= layer->num_experts && ne <= kMaxExperts, TSG_ERR_INVALID_ARGUMENT,
                 "router has %u experts but the layer holds %u", ne, layer->num_experts);
+    TSG_REQUIRE(router_w && router_hidden && es && pes && x && residual && y && out_idx &&
+                    out_w && acts,
+                TSG_ERR_INVALID_ARGUMENT, "NULL decode-layer operand");
+    TSG_REQUIRE(aligned16(router_w) && aligned16(router_hidden) && aligned16(es) &&
+                    aligned16(x) && aligned16(acts),
+                TSG_ERR_ALIGNMENT, "router weights, activations and acts must be 16-byte aligned");
+    TSG_REQUIRE(d % 8 == 0 && d <= 8u * 64u * kRouterChunks, TSG_ERR_INVALID_ARGUMENT,
+                "d=%u out of the router's range", d);
     hipStream_t s = as_stream(stream);
+    const DecodeGeometry g = decode_geometry(d, f, kTopK * f, kTargetBlocks);
+    DecodeLayerArgs a{};
+    a.layer_base = layer->base;
+    a.expert_stride = layer->expert_stride;
+    a.o = layer->offsets;
+    a.router_w = router_w;
+    a.router_hidden = router_hidden;
+    a.es = es;
+    a.pes = pes;
+    a.x = x;
+    a.residual = residual;
+    a.y = y;
+    a.out_idx = out_idx;
+    a.out_w = out_w;
+    a.acts = acts;
+    a.logits = moe->ctx->logits;
+    a.bar = reinterpret_cast<GridBarrier*>(moe->ctx->counters + kBarrierWord);
+    a.ne = ne;
+    a.d = d;
+    a.f = f;
+    a.pairs_per_block = g.pairs_per_block;
+    a.rows_per_block = g.rows_per_block;
+    if (!moe->unfused_decode) {
+        st = fused_dispatch(moe, s, a, g);
+        if (st != TSG_ERR_DECLINED) return st;
+    }
     if ((st = router_launch(moe, s, router_w, router_hidden, d, es, pes, out_idx, out_w, nullptr,
                             1, ne, d, top_k, true)))
         return st;
@@ -670,7 +953,15 @@ extern "C" tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream,
     return phase2_dispatch(moe, s, src, layer->offsets, acts, out_w, residual, y, d, f);
 }
 
-// Prompt router: the decode router body per row (bit-identical per row).
+extern "C" tsg_status tsg_moe_set_fused_decode(tsg_moe* moe, int enabled) {
+    tsg_status st = check_moe(moe);
+    if (st) return st;
+    moe->unfused_decode = enabled ? false : true;
+    return TSG_OK;
+}
+
+// Prompt router: the decode router body per row (bit-identical per row), all
+// rows in one launch.
 extern "C" tsg_status tsg_prefill_router_bf16(tsg_moe* moe, tsg_stream stream,
                                               const uint16_t* w, const uint16_t* hidden,
                                               uint32_t stride, const uint16_t* es,
@@ -682,15 +973,8 @@ extern "C" tsg_status tsg_prefill_router_bf16(tsg_moe* moe, tsg_stream stream,
     TSG_REQUIRE(query_count > 0, TSG_ERR_INVALID_ARGUMENT, "queryCount must be positive");
     TSG_REQUIRE(top_k == kTopK, TSG_ERR_UNSUPPORTED, "topK %u: the prompt router is built for 8",
                 top_k);
-    hipStream_t s = as_stream(stream);
-    // Rows go through in chunks of kMaxRouterRows so the context's logit
-    // staging and counters are reused; launches are stream-ordered.
-    for (uint32_t r0 = 0; r0 < query_count; r0 += kMaxRouterRows) {
-        const uint32_t rows = (query_count - r0 < kMaxRouterRows) ? query_count - r0 : kMaxRouterRows;
-        if ((st = router_launch(moe, s, w, hidden + (uint64_t)r0 * stride, stride, es, pes,
-                                out_idx + (uint64_t)r0 * top_k, out_w + (uint64_t)r0 * top_k,
-                                nullptr, rows, ne, d, top_k, true)))
-            return st;
-    }
-    return TSG_OK;
+    TSG_REQUIRE(query_count <= kMaxPromptRows, TSG_ERR_UNSUPPORTED,
+                "queryCount %u exceeds the %u-row prompt chunk", query_count, kMaxPromptRows);
+    return router_launch(moe, as_stream(stream), w, hidden, stride, es, pes, out_idx, out_w,
+                         nullptr, query_count, ne, d, top_k, true);
 }

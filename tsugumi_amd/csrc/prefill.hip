@@ -14,7 +14,7 @@
 // v_mfma_f32_32x32x16_f16 (fp32 accumulation). Gate and up share the block:
 // weight rows 0..63 are gate f0..f0+63, 64..127 up f0..f0+63, so the GeGLU
 // epilogue finds both halves in the same lane.
-#include "tsg_internal.hpp"
+#include "gemv_lane.hpp"
 
 namespace tsg {
 namespace {
@@ -191,16 +191,6 @@ __device__ __forceinline__ h8v_t lds_h8(const uint16_t* p) {
     return __builtin_bit_cast(h8v_t, *reinterpret_cast<const uint4*>(p));
 }
 
-// Permute 8 fp16 (one uint4) into paired order.
-__device__ __forceinline__ uint4 pair_permute(uint4 v) {
-    uint4 o;
-    o.x = (v.x & 0xFFFFu) | (v.z << 16);
-    o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
-    o.z = (v.y & 0xFFFFu) | (v.w << 16);
-    o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
-    return o;
-}
-
 struct GemmArgs {
     const uint8_t* layer_base;
     uint64_t expert_stride;
@@ -358,7 +348,6 @@ __global__ __launch_bounds__(256) void reduce_token_major_kernel(
 // --------------------------------------------------------- rows path
 
 constexpr uint32_t kRowsMax = 8;
-constexpr int kRBatch = 12;
 constexpr uint32_t kRowsBlocksPerLaunch = 64;
 
 // The rows path's block list travels in the kernel arguments, as the
@@ -367,162 +356,103 @@ struct RowsBlocks {
     tsg_routed_block b[kRowsBlocksPerLaunch];
 };
 
-// grid (ceil(F / 16), n_blocks), block 128: 8 lanes per f row, every row of
-// the routed block (<= 8) against one weight read. Per row the arithmetic is
-// phase 1's (decode.hip) operation for operation.
+// grid (ceil(F / 8), n_blocks), block 256: 32 lanes per f row (16 on the gate
+// row, 16 on the up row), every row of the routed block (<= 8) against one
+// weight read. Per row the arithmetic is decode phase 1's (decode.hip
+// phase1_compute): the same gemv_lane.hpp steps, batch and reduction, so one
+// row here is bit-identical to decode.
 template <int G, bool SYM, int ACT>
-__global__ __launch_bounds__(128) void rows_gate_up_kernel(GemmArgs args, RowsBlocks rb) {
+__global__ __launch_bounds__(256) void rows_gate_up_kernel(GemmArgs args, RowsBlocks rb) {
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ uint32_t tok[kRowsMax];
     const tsg_routed_block blk = rb.b[blockIdx.y];
     const uint32_t rows = blk.row_count < kRowsMax ? blk.row_count : kRowsMax;
     const uint32_t d = args.d, f = args.f;
+    const uint32_t row_h = lds_chunks_halves(d);
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-    float* xsum = reinterpret_cast<float*>(smem + (size_t)kRowsMax * d * 2u);
-    for (uint32_t r = 0; r < rows; ++r) {
-        const tsg_token_expert_pair pr = args.pairs[blk.pair_start + r];
-        stage_x<SYM>(args.a + (uint64_t)pr.token * args.a_stride, d, xs + (size_t)r * d,
-                     xsum + r * (d / 32u));
-    }
-    __syncthreads();
-    const uint32_t fr = blockIdx.x * 16u + (threadIdx.x >> 3);
-    const uint32_t j = threadIdx.x & 7u;
-    if (fr >= f) return;
+    float* xsum = reinterpret_cast<float*>(smem + (size_t)kRowsMax * row_h * 2u);
+
+    const uint32_t fr_raw = blockIdx.x * 8u + (threadIdx.x >> 5);
+    const uint32_t j = threadIdx.x & 15u;
+    const bool is_up = (threadIdx.x >> 4) & 1u;
+    const bool live = fr_raw < f;
+    const uint32_t fr = live ? fr_raw : 0u;
     const uint8_t* blob = args.layer_base + (uint64_t)blk.local_slot * args.expert_stride;
-    const uint32_t row_bytes = d / 2u, ngroups = d / G, nchunks = d / 32u;
-    const uint8_t* gw = blob + args.o.gate_w + (uint64_t)fr * row_bytes;
-    const uint8_t* uw = blob + args.o.up_w + (uint64_t)fr * row_bytes;
-    const uint16_t* gs = reinterpret_cast<const uint16_t*>(blob + args.o.gate_s) + (uint64_t)fr * ngroups;
-    const uint16_t* us = reinterpret_cast<const uint16_t*>(blob + args.o.up_s) + (uint64_t)fr * ngroups;
-    const uint16_t* gb = reinterpret_cast<const uint16_t*>(blob + args.o.gate_b) + (uint64_t)fr * ngroups;
-    const uint16_t* ub = reinterpret_cast<const uint16_t*>(blob + args.o.up_b) + (uint64_t)fr * ngroups;
-    const h2_t bias = SYM ? h2_t{(_Float16)1032.0f, (_Float16)1032.0f}
-                          : h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
-    float g_acc[kRowsMax], u_acc[kRowsMax];
+    const uint32_t ngroups = d / G, nchunks = d / 32u;
+    const uint8_t* w = blob + (is_up ? args.o.up_w : args.o.gate_w) + (uint64_t)fr * (d / 2u);
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + (is_up ? args.o.up_s : args.o.gate_s)) + (uint64_t)fr * ngroups;
+    const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + (is_up ? args.o.up_b : args.o.gate_b)) + (uint64_t)fr * ngroups;
+    ChunkBatch<kGUBatch> bt;
+    load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, 0u, j, nchunks, bt);
+    if (threadIdx.x < rows) tok[threadIdx.x] = args.pairs[blk.pair_start + threadIdx.x].token;
+    __syncthreads();
+    stage_act_rows<SYM>(args.a, args.a_stride, rows, d, xs, row_h, xsum, tok);
+    __syncthreads();
+    float acc[kRowsMax];
 #pragma unroll
-    for (uint32_t r = 0; r < kRowsMax; ++r) { g_acc[r] = 0.0f; u_acc[r] = 0.0f; }
-    for (uint32_t base = 0; base < nchunks; base += 8u * kRBatch) {
-        uint4 gv[kRBatch], uv[kRBatch];
-        uint16_t gsv[kRBatch], usv[kRBatch];
-#pragma unroll
-        for (int i = 0; i < kRBatch; ++i) {
-            const uint32_t c = base + j + 8u * i;
-            if (c < nchunks) {
-                gv[i] = load16_nt(reinterpret_cast<const uint4*>(gw) + c);
-                uv[i] = load16_nt(reinterpret_cast<const uint4*>(uw) + c);
-                gsv[i] = gs[c * 32u / G];
-                usv[i] = us[c * 32u / G];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kRBatch; ++i) {
-            const uint32_t c = base + j + 8u * i;
-            if (c >= nchunks) continue;
-            const float gsc = bf16_to_f32(gsv[i]), usc = bf16_to_f32(usv[i]);
-#pragma unroll
-            for (uint32_t r = 0; r < kRowsMax; ++r) {
-                if (r >= rows) break;
-                const h2_t* xp = reinterpret_cast<const h2_t*>(xs + (size_t)r * d + c * 32u);
-                g_acc[r] = __builtin_fmaf(gsc, chunk_dot(gv[i], xp, bias), g_acc[r]);
-                u_acc[r] = __builtin_fmaf(usc, chunk_dot(uv[i], xp, bias), u_acc[r]);
-                if constexpr (!SYM) {
-                    const uint32_t g = c * 32u / G;
-                    g_acc[r] = __builtin_fmaf(bf16_to_f32(gb[g]), xsum[r * nchunks + c], g_acc[r]);
-                    u_acc[r] = __builtin_fmaf(bf16_to_f32(ub[g]), xsum[r * nchunks + c], u_acc[r]);
-                }
-            }
-        }
+    for (uint32_t r = 0; r < kRowsMax; ++r) acc[r] = 0.0f;
+    for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
+        if (base) load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, base, j, nchunks, bt);
+        compute_batch<G, SYM, kGUBatch, kGULanes, kRowsMax>(bt, base, j, nchunks, xs, row_h, xsum,
+                                                            rows, acc);
     }
 #pragma unroll
     for (uint32_t r = 0; r < kRowsMax; ++r) {
 #pragma unroll
-        for (int off = 4; off >= 1; off >>= 1) {
-            g_acc[r] += shfl_xor(g_acc[r], off);
-            u_acc[r] += shfl_xor(u_acc[r], off);
-        }
-    }
-    if (j == 0) {
-        for (uint32_t r = 0; r < rows; ++r)
+        for (int off = 8; off >= 1; off >>= 1) acc[r] += shfl_xor(acc[r], off);
+        const float up = shfl_xor(acc[r], 16);
+        if (live && !is_up && j == 0 && r < rows)
             args.out[(uint64_t)(blk.local_row + r) * f + fr] =
-                f32_to_f16(gate_activation<ACT>(g_acc[r]) * u_acc[r]);
+                f32_to_f16(gate_activation<ACT>(acc[r]) * up);
     }
 }
 
-// grid (ceil(D / 32), n_blocks), block 64: lane = row_in_wave * 2 + half,
-// each of the block's rows against one weight read. Per row the arithmetic is
-// phase 2's per-slot GEMV (decode.hip) operation for operation.
+// grid (ceil(D / 8), n_blocks), block 64: 8 lanes per output row, each of the
+// block's rows against one weight read. Per row the arithmetic is decode phase
+// 2's per-slot GEMV (decode.hip phase2_body): the same gemv_lane.hpp steps.
 template <int G, bool SYM>
 __global__ __launch_bounds__(64) void rows_down_kernel(GemmArgs args, RowsBlocks rb,
                                                        uint16_t* partials) {
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ uint32_t dst[kRowsMax];
     const tsg_routed_block blk = rb.b[blockIdx.y];
     const uint32_t rows = blk.row_count < kRowsMax ? blk.row_count : kRowsMax;
     const uint32_t d = args.d, f = args.f;
+    const uint32_t row_h = lds_chunks_halves(f);
     uint16_t* as = reinterpret_cast<uint16_t*>(smem);
-    float* asum = reinterpret_cast<float*>(smem + (size_t)kRowsMax * f * 2u);
-    __shared__ uint32_t dst[kRowsMax];
-    for (uint32_t r = 0; r < rows; ++r) {
-        const uint16_t* a = args.a + (uint64_t)(blk.local_row + r) * f;
-        for (uint32_t b = threadIdx.x; b < f / 8u; b += blockDim.x)
-            *reinterpret_cast<uint4*>(as + r * f + b * 8u) =
-                pair_permute(*reinterpret_cast<const uint4*>(a + b * 8u));
-        if constexpr (!SYM) {
-            for (uint32_t c = threadIdx.x; c < f / 32u; c += blockDim.x) {
-                float sum = 0.0f;
-                for (uint32_t k = 0; k < 32u; ++k) sum += f16_to_f32(a[c * 32u + k]);
-                asum[r * (f / 32u) + c] = sum;
-            }
-        }
-        if (threadIdx.x == 0) {
-            const tsg_token_expert_pair pr = args.pairs[blk.pair_start + r];
-            dst[r] = (pr.token * args.top_k + pr.rank) * d;
-        }
-    }
-    __syncthreads();
-    const uint32_t lane = threadIdx.x;
-    const uint32_t half = lane & 1u;
-    const uint32_t row = blockIdx.x * 32u + (lane >> 1);
-    const bool live = row < d;
+    float* asum = reinterpret_cast<float*>(smem + (size_t)kRowsMax * row_h * 2u);
+
+    const uint32_t j = threadIdx.x & 7u;
+    const uint32_t row = blockIdx.x * 8u + (threadIdx.x >> 3);
+    const bool live_row = row < d;
+    const uint32_t rr = live_row ? row : 0u;
     const uint8_t* blob = args.layer_base + (uint64_t)blk.local_slot * args.expert_stride;
     const uint32_t ngroups = f / G, nchunks = f / 32u;
-    const uint8_t* w = blob + args.o.down_w + (uint64_t)(live ? row : 0u) * (f / 2u);
-    const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + args.o.down_s) + (uint64_t)(live ? row : 0u) * ngroups;
-    const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + args.o.down_b) + (uint64_t)(live ? row : 0u) * ngroups;
-    const h2_t bias = SYM ? h2_t{(_Float16)1032.0f, (_Float16)1032.0f}
-                          : h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+    const uint8_t* w = blob + args.o.down_w + (uint64_t)rr * (f / 2u);
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + args.o.down_s) + (uint64_t)rr * ngroups;
+    const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + args.o.down_b) + (uint64_t)rr * ngroups;
+    ChunkBatch<kDBatch> bt;
+    load_batch<G, SYM, kDBatch, kDLanes>(w, sc, bi, 0u, j, nchunks, bt);
+    if (threadIdx.x < rows) {
+        const tsg_token_expert_pair pr = args.pairs[blk.pair_start + threadIdx.x];
+        dst[threadIdx.x] = (pr.token * args.top_k + pr.rank) * d;
+    }
+    stage_act_rows<SYM>(args.a + (uint64_t)blk.local_row * f, f, rows, f, as, row_h, asum);
+    __syncthreads();
     float acc[kRowsMax];
 #pragma unroll
     for (uint32_t r = 0; r < kRowsMax; ++r) acc[r] = 0.0f;
-    if (live) {
-        for (uint32_t base = 0; base < nchunks; base += 2u * kRBatch) {
-            uint4 wv[kRBatch];
-            uint16_t sv[kRBatch];
-#pragma unroll
-            for (int i = 0; i < kRBatch; ++i) {
-                const uint32_t c = base + half + 2u * i;
-                if (c < nchunks) {
-                    wv[i] = load16_nt(reinterpret_cast<const uint4*>(w) + c);
-                    sv[i] = sc[c * 32u / G];
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < kRBatch; ++i) {
-                const uint32_t c = base + half + 2u * i;
-                if (c >= nchunks) continue;
-                const float s = bf16_to_f32(sv[i]);
-#pragma unroll
-                for (uint32_t r = 0; r < kRowsMax; ++r) {
-                    if (r >= rows) break;
-                    const h2_t* xp = reinterpret_cast<const h2_t*>(as + r * f + c * 32u);
-                    acc[r] = __builtin_fmaf(s, chunk_dot(wv[i], xp, bias), acc[r]);
-                    if constexpr (!SYM)
-                        acc[r] = __builtin_fmaf(bf16_to_f32(bi[c * 32u / G]), asum[r * nchunks + c], acc[r]);
-                }
-            }
-        }
+    for (uint32_t base = 0; base < nchunks; base += kDLanes * kDBatch) {
+        if (base) load_batch<G, SYM, kDBatch, kDLanes>(w, sc, bi, base, j, nchunks, bt);
+        compute_batch<G, SYM, kDBatch, kDLanes, kRowsMax>(bt, base, j, nchunks, as, row_h, asum,
+                                                          rows, acc);
     }
 #pragma unroll
-    for (uint32_t r = 0; r < kRowsMax; ++r) acc[r] += shfl_xor(acc[r], 1);
-    if (live && half == 0)
+    for (uint32_t r = 0; r < kRowsMax; ++r) {
+#pragma unroll
+        for (int off = 4; off >= 1; off >>= 1) acc[r] += shfl_xor(acc[r], off);
+    }
+    if (live_row && j == 0)
         for (uint32_t r = 0; r < rows; ++r) partials[dst[r] + row] = f32_to_f16(acc[r]);
 }
 
@@ -682,8 +612,8 @@ extern "C" tsg_status tsg_prefill_moe_rows(tsg_moe* moe, tsg_stream stream,
     TSG_REQUIRE(aligned16(act_scratch), TSG_ERR_ALIGNMENT, "act_scratch must be 16-byte aligned");
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
-    const size_t lds1 = (size_t)kRowsMax * d * 2u + (sym ? 0u : kRowsMax * (d / 32u) * 4u);
-    const size_t lds2 = (size_t)kRowsMax * f * 2u + (sym ? 0u : kRowsMax * (f / 32u) * 4u);
+    const size_t lds1 = (size_t)kRowsMax * lds_chunks_halves(d) * 2u + (sym ? 0u : kRowsMax * (d / 32u) * 4u);
+    const size_t lds2 = (size_t)kRowsMax * lds_chunks_halves(f) * 2u + (sym ? 0u : kRowsMax * (f / 32u) * 4u);
     TSG_REQUIRE(lds1 <= 160u * 1024u && lds2 <= 160u * 1024u, TSG_ERR_UNSUPPORTED,
                 "d=%u / f=%u do not fit the rows path's LDS staging", d, f);
     hipStream_t s = as_stream(stream);
@@ -694,14 +624,14 @@ extern "C" tsg_status tsg_prefill_moe_rows(tsg_moe* moe, tsg_stream stream,
         const uint32_t nb = n_blocks - b0 < kRowsBlocksPerLaunch ? n_blocks - b0 : kRowsBlocksPerLaunch;
         RowsBlocks rb{};
         for (uint32_t i = 0; i < nb; ++i) rb.b[i] = blocks[b0 + i];
-        const dim3 g1((f + 15) / 16, nb), g2((d + 31) / 32, nb);
+        const dim3 g1((f + 7) / 8, nb), g2((d + 7) / 8, nb);
 #define TSG_ROWS_LAUNCH(GG, SS)                                                                  \
     do {                                                                                         \
         if (moe->activation == TSG_ACT_SILU)                                                     \
-            hipLaunchKernelGGL((rows_gate_up_kernel<GG, SS, TSG_ACT_SILU>), g1, dim3(128), lds1, \
+            hipLaunchKernelGGL((rows_gate_up_kernel<GG, SS, TSG_ACT_SILU>), g1, dim3(256), lds1, \
                                s, a, rb);                                                        \
         else                                                                                     \
-            hipLaunchKernelGGL((rows_gate_up_kernel<GG, SS, TSG_ACT_GELU_TANH>), g1, dim3(128),  \
+            hipLaunchKernelGGL((rows_gate_up_kernel<GG, SS, TSG_ACT_GELU_TANH>), g1, dim3(256),  \
                                lds1, s, a, rb);                                                  \
         if ((st = check_launch("rows gate/up"))) return st;                                     \
         hipLaunchKernelGGL((rows_down_kernel<GG, SS>), g2, dim3(64), lds2, s, a2, rb, partials); \

@@ -6,16 +6,15 @@
 // exponent trick, v_dot2_f32_f16 against x staged in LDS, fp32 scale fma.
 // The rows form keeps T <= 8 accumulators per lane so a weight chunk is read
 // once for all rows; each row's sum runs in exactly the one-row order.
-#include "tsg_internal.hpp"
+#include "gemv_lane.hpp"
 
 namespace tsg {
 namespace {
 
-constexpr int kQBatch = 12;
 constexpr uint32_t kMaxRows = 8;
 
 template <int G, bool SYM, int T>
-__global__ __launch_bounds__(128) void qmv_kernel(const uint8_t* __restrict__ w,
+__global__ __launch_bounds__(256) void qmv_kernel(const uint8_t* __restrict__ w,
                                                   const uint16_t* __restrict__ scales,
                                                   const uint16_t* __restrict__ biases,
                                                   const uint16_t* __restrict__ x,
@@ -23,61 +22,35 @@ __global__ __launch_bounds__(128) void qmv_kernel(const uint8_t* __restrict__ w,
                                                   uint32_t y_stride, uint32_t t, uint32_t m,
                                                   uint32_t n) {
     extern __shared__ __align__(16) uint8_t smem[];
-    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                  // T * n
-    float* xsum = reinterpret_cast<float*>(smem + (size_t)T * n * 2u);  // T * n / 32
-    for (uint32_t r = 0; r < t; ++r)
-        stage_x<SYM>(x + (uint64_t)r * x_stride, n, xs + (size_t)r * n, xsum + r * (n / 32u));
-    __syncthreads();
+    const uint32_t row_h = lds_chunks_halves(n);
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                        // T rows
+    float* xsum = reinterpret_cast<float*>(smem + (size_t)T * row_h * 2u);  // T * n / 32
 
-    const uint32_t row = blockIdx.x * 16u + (threadIdx.x >> 3);
-    const uint32_t j = threadIdx.x & 7u;
-    if (row >= m) return;
-    const uint32_t ngroups = n / G;
-    const uint32_t nchunks = n / 32u;
-    const uint8_t* wr = w + (uint64_t)row * (n / 2u);
-    const uint16_t* sr = scales + (uint64_t)row * ngroups;
-    const uint16_t* br = biases + (uint64_t)row * ngroups;
-    const h2_t bias = SYM ? h2_t{(_Float16)1032.0f, (_Float16)1032.0f}
-                          : h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+    const uint32_t row = blockIdx.x * 16u + (threadIdx.x >> 4);
+    const uint32_t j = threadIdx.x & 15u;
+    const bool live = row < m;
+    const uint32_t rr = live ? row : 0u;
+    const uint32_t ngroups = n / G, nchunks = n / 32u;
+    const uint8_t* wr = w + (uint64_t)rr * (n / 2u);
+    const uint16_t* sr = scales + (uint64_t)rr * ngroups;
+    const uint16_t* br = biases + (uint64_t)rr * ngroups;
+    ChunkBatch<kGUBatch> bt;
+    load_batch<G, SYM, kGUBatch, kGULanes>(wr, sr, br, 0u, j, nchunks, bt);
+    stage_act_rows<SYM>(x, x_stride, t, n, xs, row_h, xsum);
+    __syncthreads();
     float acc[T];
 #pragma unroll
     for (int r = 0; r < T; ++r) acc[r] = 0.0f;
-    for (uint32_t base = 0; base < nchunks; base += 8u * kQBatch) {
-        uint4 wv[kQBatch];
-        uint16_t sv[kQBatch];
-#pragma unroll
-        for (int i = 0; i < kQBatch; ++i) {
-            const uint32_t c = base + j + 8u * i;
-            if (c < nchunks) {
-                wv[i] = load16_nt(reinterpret_cast<const uint4*>(wr) + c);
-                sv[i] = sr[c * 32u / G];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kQBatch; ++i) {
-            const uint32_t c = base + j + 8u * i;
-            if (c < nchunks) {
-                const float s = bf16_to_f32(sv[i]);
-                float b = 0.0f;
-                if constexpr (!SYM) b = bf16_to_f32(br[c * 32u / G]);
-#pragma unroll
-                for (int r = 0; r < T; ++r) {
-                    if ((uint32_t)r < t) {
-                        const h2_t* xp = reinterpret_cast<const h2_t*>(xs + (size_t)r * n + c * 32u);
-                        acc[r] = __builtin_fmaf(s, chunk_dot(wv[i], xp, bias), acc[r]);
-                        if constexpr (!SYM)
-                            acc[r] = __builtin_fmaf(b, xsum[r * nchunks + c], acc[r]);
-                    }
-                }
-            }
-        }
+    for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
+        if (base) load_batch<G, SYM, kGUBatch, kGULanes>(wr, sr, br, base, j, nchunks, bt);
+        compute_batch<G, SYM, kGUBatch, kGULanes, T>(bt, base, j, nchunks, xs, row_h, xsum, t, acc);
     }
 #pragma unroll
     for (int r = 0; r < T; ++r) {
 #pragma unroll
-        for (int off = 4; off >= 1; off >>= 1) acc[r] += shfl_xor(acc[r], off);
+        for (int off = 8; off >= 1; off >>= 1) acc[r] += shfl_xor(acc[r], off);
     }
-    if (j == 0) {
+    if (live && j == 0) {
 #pragma unroll
         for (int r = 0; r < T; ++r)
             if ((uint32_t)r < t) y[(uint64_t)r * y_stride + row] = f32_to_f16(acc[r]);
@@ -111,10 +84,10 @@ tsg_status launch_qmv(hipStream_t s, const uint8_t* w, const uint16_t* sc, const
                       const uint16_t* x, uint32_t xs, uint16_t* y, uint32_t ys, uint32_t t,
                       uint32_t m, uint32_t n) {
     const dim3 grid((m + 15) / 16);
-    const size_t lds_per_row = (size_t)n * 2u + (SYM ? 0u : (n / 32u) * 4u);
+    const size_t lds_per_row = (size_t)lds_chunks_halves(n) * 2u + (SYM ? 0u : (n / 32u) * 4u);
 #define TSG_QMV_CASE(TT)                                                                   \
     case TT:                                                                               \
-        hipLaunchKernelGGL((qmv_kernel<G, SYM, TT>), grid, dim3(128), lds_per_row * TT, s, \
+        hipLaunchKernelGGL((qmv_kernel<G, SYM, TT>), grid, dim3(256), lds_per_row * TT, s, \
                            w, sc, bi, x, xs, y, ys, t, m, n);                              \
         break;
     switch (t) {
@@ -150,7 +123,7 @@ tsg_status qmv_dispatch(tsg_ctx* ctx, hipStream_t s, const uint8_t* w, const uin
                 "weights must be 16-byte aligned (got %p)", (const void*)w);
     TSG_REQUIRE(aligned16(x) && xs % 8 == 0, TSG_ERR_ALIGNMENT,
                 "x rows must be 16-byte aligned");
-    const size_t lds = (size_t)t * ((size_t)n * 2u + (n / 32u) * 4u);
+    const size_t lds = (size_t)t * ((size_t)lds_chunks_halves(n) * 2u + (n / 32u) * 4u);
     TSG_REQUIRE(lds <= 160u * 1024u, TSG_ERR_UNSUPPORTED,
                 "t=%u rows of n=%u do not fit the LDS staging", t, n);
     const bool sym = ctx->scheme == TSG_SYM;

@@ -45,7 +45,7 @@ struct tsg_ctx {
     // Device scratch owned by the context: completion counters for the
     // last-block patterns (zeroed once, self-resetting) and router logits.
     uint32_t* counters = nullptr;        // kMaxCounters
-    float* logits = nullptr;             // kMaxRouterRows * kMaxExperts
+    float* logits = nullptr;             // kMaxPromptRows * kMaxExperts
     int num_cus = 256;
 };
 
@@ -53,6 +53,7 @@ struct tsg_moe {
     tsg_ctx* ctx = nullptr;
     uint32_t router_weight_bits = 16;
     tsg_activation activation = TSG_ACT_GELU_TANH;
+    bool unfused_decode = false;  // tsg_moe_set_fused_decode(moe, 0)
 };
 
 struct tsg_layer {
@@ -67,8 +68,12 @@ struct tsg_layer {
 namespace tsg {
 
 constexpr uint32_t kMaxExperts = 256;
-constexpr uint32_t kMaxRouterRows = 8;
+constexpr uint32_t kMaxRouterRows = 8;      // MoE.maxRouterRows (verify rows)
+constexpr uint32_t kMaxPromptRows = 4096;   // rows one router launch may route
 constexpr uint32_t kMaxCounters = 4096;
+// The fused decode layer's grid barrier {count, gen, error, pad} occupies the
+// last four counter words.
+constexpr uint32_t kBarrierWord = kMaxCounters - 4;
 constexpr uint32_t kTopK = 8;
 
 inline hipStream_t as_stream(tsg_stream s) { return reinterpret_cast<hipStream_t>(s); }
@@ -161,28 +166,79 @@ __device__ __forceinline__ float gate_activation(float x) {
     }
 }
 
-// Stage `n` fp16 activations into LDS in paired order (see nib8_to_pairs),
-// plus, for the affine scheme, the fp32 sum of each 32-element chunk.
-template <bool SYM>
-__device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, uint32_t n,
-                                        uint16_t* xs, float* xsum) {
-    for (uint32_t b = threadIdx.x; b < n / 8u; b += blockDim.x) {
-        const uint4 v = *reinterpret_cast<const uint4*>(x + b * 8u);
-        // in: e0 e1 | e2 e3 | e4 e5 | e6 e7 ; out: (e0,e4) (e1,e5) (e2,e6) (e3,e7)
-        uint4 o;
-        o.x = (v.x & 0xFFFFu) | (v.z << 16);
-        o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
-        o.z = (v.y & 0xFFFFu) | (v.w << 16);
-        o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
-        *reinterpret_cast<uint4*>(xs + b * 8u) = o;
-    }
-    if constexpr (!SYM) {
-        for (uint32_t c = threadIdx.x; c < n / 32u; c += blockDim.x) {
-            float s = 0.0f;
-            for (uint32_t k = 0; k < 32u; ++k) s += f16_to_f32(x[c * 32u + k]);
-            xsum[c] = s;
+// LDS layout of staged activations: each 32-element chunk (the span of one
+// 16-byte weight chunk) occupies kChunkLds halves = 80 bytes, its four
+// 8-element blocks in "paired" order (see nib8_to_pairs). The 16-byte pad
+// spreads the chunks that neighbouring lanes read over distinct LDS banks.
+constexpr uint32_t kChunkLds = 40;
+
+__host__ __device__ __forceinline__ uint32_t lds_chunks_halves(uint32_t n) {
+    return (n / 32u) * kChunkLds;
+}
+
+// 8 fp16 (one uint4, elements e0..e7) -> paired order (e0,e4)(e1,e5)(e2,e6)(e3,e7).
+__device__ __forceinline__ uint4 pair_permute(uint4 v) {
+    uint4 o;
+    o.x = (v.x & 0xFFFFu) | (v.z << 16);
+    o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+    o.z = (v.y & 0xFFFFu) | (v.w << 16);
+    o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+    return o;
+}
+
+// Stage `rows` activation rows of `n` fp16 each (row r at src + r*src_stride)
+// into LDS at dst + r*dst_stride halves, padded chunk layout. Every global load
+// a thread makes in one pass is issued before any of its LDS stores
+// (out-of-range slots load a clamped address and store nothing), so staging
+// costs one memory round trip per pass, not one per loop iteration. For the
+// affine scheme the fp32 sum of each 32-element chunk is then computed from
+// the staged copy, in element order, into sums[r * n/32 + c]. The caller
+// synchronises before reading.
+// `row_index` (may be NULL) maps staged row r to source row row_index[r].
+template <bool SYM, int PER_THREAD = 4>
+__device__ __forceinline__ void stage_act_rows(const uint16_t* __restrict__ src,
+                                               uint32_t src_stride, uint32_t rows, uint32_t n,
+                                               uint16_t* dst, uint32_t dst_stride,
+                                               float* sums,
+                                               const uint32_t* row_index = nullptr) {
+    const uint32_t bpr = n / 8u;
+    const uint32_t total = rows * bpr;
+    for (uint32_t q0 = 0; q0 < total; q0 += blockDim.x * PER_THREAD) {
+        uint4 v[PER_THREAD];
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) {
+            const uint32_t q = min(q0 + threadIdx.x + i * blockDim.x, total - 1u);
+            const uint32_t r = q / bpr, b = q - r * bpr;
+            const uint32_t sr = row_index ? row_index[r] : r;
+            v[i] = *reinterpret_cast<const uint4*>(src + (uint64_t)sr * src_stride + b * 8u);
+        }
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) {
+            const uint32_t q = q0 + threadIdx.x + i * blockDim.x;
+            if (q < total) {
+                const uint32_t r = q / bpr, b = q - r * bpr;
+                *reinterpret_cast<uint4*>(dst + (size_t)r * dst_stride + (b >> 2) * kChunkLds +
+                                          (b & 3u) * 8u) = pair_permute(v[i]);
+            }
         }
     }
+    if constexpr (!SYM) {
+        __syncthreads();
+        const uint32_t cpr = n / 32u;
+        for (uint32_t q = threadIdx.x; q < rows * cpr; q += blockDim.x) {
+            const uint32_t r = q / cpr, c = q - r * cpr;
+            const uint16_t* chunk = dst + (size_t)r * dst_stride + c * kChunkLds;
+            float s = 0.0f;
+            for (uint32_t k = 0; k < 32u; ++k)
+                s += f16_to_f32(chunk[(k >> 3) * 8u + paired_pos(k & 7u)]);
+            sums[q] = s;
+        }
+    }
+}
+
+// Activations of chunk c in the staged layout.
+__device__ __forceinline__ const h2_t* staged_chunk(const uint16_t* xs, uint32_t c) {
+    return reinterpret_cast<const h2_t*>(xs + c * kChunkLds);
 }
 
 template <typename T>
