@@ -86,11 +86,14 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
     hipError_t e = hipMalloc(&ctx->counters, sizeof(uint32_t) * kMaxCounters);
     if (e == hipSuccess)
         e = hipMalloc(&ctx->logits, sizeof(float) * kMaxPromptRows * kMaxExperts);
+    if (e == hipSuccess)
+        e = hipMalloc(&ctx->act_replicas, sizeof(uint16_t) * kActReplicas * kActReplicaHalves);
     if (e == hipSuccess) e = hipMemset(ctx->counters, 0, sizeof(uint32_t) * kMaxCounters);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         (void)hipFree(ctx->counters);
         (void)hipFree(ctx->logits);
+        (void)hipFree(ctx->act_replicas);
         delete ctx;
         return fail(TSG_ERR_OUT_OF_MEMORY, "context scratch: %s", hipGetErrorString(e));
     }
@@ -104,6 +107,7 @@ extern "C" void tsg_ctx_destroy(tsg_ctx* ctx) {
     (void)hipDeviceSynchronize();
     (void)hipFree(ctx->counters);
     (void)hipFree(ctx->logits);
+    (void)hipFree(ctx->act_replicas);
     delete ctx;
 }
 
@@ -129,12 +133,12 @@ extern "C" tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream) {
     // A fused decode launch whose grid barrier timed out has set this word;
     // that launch's outputs are invalid.
     uint32_t err = 0;
-    TSG_HIP_TRY(hipMemcpy(&err, ctx->counters + kBarrierWord + 2, sizeof(err),
+    TSG_HIP_TRY(hipMemcpy(&err, ctx->counters + kSyncErrorWord, sizeof(err),
                           hipMemcpyDeviceToHost));
     if (err) {
-        TSG_HIP_TRY(hipMemset(ctx->counters + kBarrierWord + 2, 0, sizeof(err)));
-        return fail(TSG_ERR_HIP, "fused decode grid barrier timed out: outputs of the "
-                                 "affected launch are invalid");
+        TSG_HIP_TRY(hipMemset(ctx->counters + kSyncErrorWord, 0, sizeof(err)));
+        return fail(TSG_ERR_HIP, "fused decode layer: a block timed out waiting for the "
+                                 "others; outputs of the affected launch are invalid");
     }
     return TSG_OK;
 }

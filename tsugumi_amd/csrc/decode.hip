@@ -24,9 +24,10 @@ namespace {
 
 // ------------------------------------------------------------ blob lookup
 
-// Where each routed slot's expert blob lives: either explicit pointers (the
-// reference's argument buffer of 8 MTLBuffers) or base + expert_id * stride
-// with the ids read on the device.
+// Where each routed slot's expert blob lives: explicit pointers (the
+// reference's argument buffer of 8 MTLBuffers), or base + expert_id * stride
+// with the ids read from device memory (written by an earlier launch) or from
+// LDS (the one-launch layer, which routes in-kernel).
 struct BlobSource {
     const uint8_t* ptrs[kTopK];
     const uint8_t* base;
@@ -35,79 +36,152 @@ struct BlobSource {
     const uint32_t* active_slots; // device, subset mode
     uint32_t active_count;
     uint32_t resident;            // 0: ptrs, 1: base + indices[slot] * stride
+
+    __device__ __forceinline__ const uint8_t* blob(uint32_t slot) const {
+        if (resident) return base + (uint64_t)indices[slot] * stride;
+        return ptrs[slot];
+    }
 };
 
-__device__ __forceinline__ const uint8_t* blob_for(const BlobSource& src, uint32_t slot) {
-    if (src.resident) return src.base + (uint64_t)src.indices[slot] * src.stride;
-    return src.ptrs[slot];
-}
+// The one-launch layer's lookup: expert ids chosen in-kernel, held in LDS.
+struct LdsBlobs {
+    const uint8_t* base;
+    uint64_t stride;
+    const uint32_t* ids;  // LDS
+
+    __device__ __forceinline__ const uint8_t* blob(uint32_t slot) const {
+        return base + (uint64_t)ids[slot] * stride;
+    }
+};
 
 // ----------------------------------------------------------------- router
 
-// Wave-wide top-k over `ne` logits with the reference's rule
+// Wave-wide top-8 over `ne` logits with the reference's rule
 // (moe.metal:281-329): descending score, ties to the lower index, -inf and NaN
-// never enter; unfilled slots keep (0, -inf). Softmax over the k with the
-// per-expert gain, rounded to fp16. Runs on one full wave.
-__device__ void wave_topk_softmax(const float* logits, uint32_t ne, uint32_t top_k,
-                                  const uint16_t* __restrict__ per_expert_scale,
-                                  uint32_t* __restrict__ out_idx,
-                                  uint16_t* __restrict__ out_w) {
+// never enter; unfilled slots keep (0, -inf). Softmax over the 8 with the
+// per-expert gain, rounded to fp16. Runs on one full wave; lane l holds the
+// logits of experts l + 64 j (j < 4). Every lane returns the same result.
+//
+// Scores become order-preserving 32-bit keys (0 marks "not eligible"; -0 is
+// keyed as +0, the two compare equal). Each round takes the wave-wide max key
+// on DPP moves inside 16-lane rows and permlane swaps across rows, then the
+// lowest expert holding it from per-j ballots (experts l + 64 j ascend with j
+// and, within j, with the lane).
+struct TopK {
+    uint32_t idx[kTopK];
+    uint16_t w[kTopK];
+};
+
+__device__ __forceinline__ uint32_t order_key(float v) {
+    const uint32_t u = __float_as_uint(v + 0.0f);  // -0 -> +0
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float order_key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t k) {
+    return __builtin_amdgcn_update_dpp(0u, k, CTRL, 0xF, 0xF, false);
+}
+
+// Of the two results of a permlane swap each lane finds its partner's value
+// in one and its own in the other, so the max of both is the pairwise max
+// whichever holds which.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
+    k = max(k, dpp_u32<0xB1>(k));   // quad_perm [1,0,3,2]
+    k = max(k, dpp_u32<0x4E>(k));   // quad_perm [2,3,0,1]
+    k = max(k, dpp_u32<0x141>(k));  // row_half_mirror
+    k = max(k, dpp_u32<0x140>(k));  // row_mirror
+    const auto a = __builtin_amdgcn_permlane16_swap(k, k, false, false);
+    k = max(k, max((uint32_t)a[0], (uint32_t)a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(k, k, false, false);
+    k = max(k, max((uint32_t)b[0], (uint32_t)b[1]));
+    return k;
+}
+
+// Lane l's per-expert gains (bf16 bits) of experts l + 64 j, loaded early so
+// their latency is off the top-k's critical path.
+__device__ __forceinline__ void load_expert_gains(const uint16_t* __restrict__ per_expert_scale,
+                                                  uint32_t ne, uint32_t (&pes)[4]) {
     const uint32_t lane = threadIdx.x & 63u;
-    // up to kMaxExperts / 64 = 4 candidates per lane: expert lane + 64 * j
-    float v[4];
-    bool eligible[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t e = lane + 64u * j;
-        const float s = e < ne ? logits[e] : -INFINITY;
-        v[j] = s;
-        eligible[j] = e < ne && s == s && s != -INFINITY;
+        pes[j] = e < ne ? per_expert_scale[e] : 0u;
     }
-    float top_s[kTopK];
-    uint32_t top_i[kTopK];
-    for (uint32_t r = 0; r < top_k; ++r) {
-        float best = -INFINITY;
-        uint32_t best_i = 0xFFFFFFFFu;
+}
+
+__device__ __forceinline__ TopK wave_topk_softmax_regs(const float (&logit)[4], uint32_t ne,
+                                                      const uint32_t (&pes)[4]) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t key[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t e = lane + 64u * j;
-            if (eligible[j] && (best_i == 0xFFFFFFFFu || v[j] > best ||
-                                (v[j] == best && e < best_i))) {
-                best = v[j];
-                best_i = e;
-            }
-        }
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t e = lane + 64u * j;
+        const float s = logit[j];
+        const bool eligible = e < ne && s == s && s != -INFINITY;
+        key[j] = eligible ? order_key(s) : 0u;
+    }
+    TopK t;
+    float top_s[kTopK], gain[kTopK];
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ob = shfl_xor(best, off);
-            const uint32_t oi = shfl_xor(best_i, off);
-            const bool take = oi != 0xFFFFFFFFu &&
-                              (best_i == 0xFFFFFFFFu || ob > best || (ob == best && oi < best_i));
-            if (take) { best = ob; best_i = oi; }
-        }
-        if (best_i == 0xFFFFFFFFu) {
+    for (uint32_t r = 0; r < kTopK; ++r) {
+        const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+        if (m == 0u) {  // unfilled: (expert 0, -inf)
             top_s[r] = -INFINITY;
-            top_i[r] = 0u;
+            t.idx[r] = 0u;
+            gain[r] = bf16_to_f32((uint16_t)__builtin_amdgcn_readlane(pes[0], 0));
         } else {
-            top_s[r] = best;
-            top_i[r] = best_i;
+            const uint64_t b0 = __ballot(key[0] == m), b1 = __ballot(key[1] == m);
+            const uint64_t b2 = __ballot(key[2] == m), b3 = __ballot(key[3] == m);
+            const uint32_t jj = b0 ? 0u : b1 ? 1u : b2 ? 2u : 3u;
+            const uint64_t bj = b0 ? b0 : b1 ? b1 : b2 ? b2 : b3;
+            const uint32_t l = (uint32_t)__builtin_ctzll(bj);
+            top_s[r] = order_key_value(m);
+            t.idx[r] = 64u * jj + l;
+            const uint32_t mine = jj == 0 ? pes[0] : jj == 1 ? pes[1] : jj == 2 ? pes[2] : pes[3];
+            gain[r] = bf16_to_f32((uint16_t)__builtin_amdgcn_readlane(mine, l));
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                if (lane + 64u * j == best_i) eligible[j] = false;
+                if ((uint32_t)j == jj && lane == l) key[j] = 0u;
         }
     }
+    // softmax: lane r < 8 owns slot r's exponential; the sum runs in slot order
+    const uint32_t r_l = lane & (kTopK - 1u);
+    float my_s = top_s[0], my_gain = gain[0];
+#pragma unroll
+    for (uint32_t r = 1; r < kTopK; ++r)
+        if (r_l == r) { my_s = top_s[r]; my_gain = gain[r]; }
+    const float my_exp = expf(my_s - top_s[0]);
+    float sum_exp = lane_value(my_exp, 0);
+#pragma unroll
+    for (uint32_t r = 1; r < kTopK; ++r) sum_exp += lane_value(my_exp, r);
+    const uint32_t my_w = f32_to_f16(my_exp / sum_exp * my_gain);
+#pragma unroll
+    for (uint32_t r = 0; r < kTopK; ++r) t.w[r] = (uint16_t)__builtin_amdgcn_readlane(my_w, r);
+    return t;
+}
+
+// The same over logits in memory written earlier in this launch by other
+// blocks (read with agent-coherent loads); lane 0 stores the result.
+__device__ void wave_topk_softmax(const float* logits, uint32_t ne, const uint32_t (&pes)[4],
+                                  uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w) {
+    const uint32_t lane = threadIdx.x & 63u;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t e = lane + 64u * j;
+        v[j] = e < ne ? __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(logits) + e))
+                      : -INFINITY;
+    }
+    const TopK t = wave_topk_softmax_regs(v, ne, pes);
     if (lane == 0) {
-        const float max_s = top_s[0];
-        float exps[kTopK];
-        float sum_exp = 0.0f;
-        for (uint32_t r = 0; r < top_k; ++r) {
-            exps[r] = expf(top_s[r] - max_s);
-            sum_exp += exps[r];
-        }
-        for (uint32_t r = 0; r < top_k; ++r) {
-            const float weight = exps[r] / sum_exp;
-            out_idx[r] = top_i[r];
-            out_w[r] = f32_to_f16(weight * bf16_to_f32(per_expert_scale[top_i[r]]));
+#pragma unroll
+        for (uint32_t r = 0; r < kTopK; ++r) {
+            out_idx[r] = t.idx[r];
+            out_w[r] = t.w[r];
         }
     }
 }
@@ -181,6 +255,8 @@ __global__ __launch_bounds__(256) void router_kernel(
     const uint32_t r0 = blockIdx.y * kRouterRows;
     const uint32_t nr = min(kRouterRows, rows - r0);
     const uint32_t nchunks = d / 8u;
+    uint32_t gains[4] = {0u, 0u, 0u, 0u};
+    if constexpr (SELECT) load_expert_gains(pes, ne, gains);
     if (e < ne) {
         const uint16_t* wr = w + (uint64_t)e * d;
         uint4 wv[kRouterChunks], ev[kRouterChunks], xv[kRouterChunks];
@@ -204,12 +280,16 @@ __global__ __launch_bounds__(256) void router_kernel(
             const float acc = router_chunks_dot(wv, xv, ev, nchunks, lane);
 #pragma unroll
             for (int i = 0; i < kRouterChunks; ++i) xv[i] = xn[i];
-            if (lane == 0) logits[(uint64_t)(r0 + r) * logits_stride + e] = acc;
+            if (lane == 0)
+                st_coherent(reinterpret_cast<uint32_t*>(logits) + (uint64_t)(r0 + r) * logits_stride + e,
+                            __float_as_uint(acc));
         }
     }
     if constexpr (SELECT) {
+        // logits travel by agent-coherent stores/loads: completing this
+        // block's stores before it counts itself is all the last block needs
         __shared__ uint32_t is_last;
-        __threadfence();
+        wait_vector_memory();
         __syncthreads();
         if (threadIdx.x == 0) {
             const uint32_t done = atomicAdd(&counters[blockIdx.y], 1u);
@@ -217,11 +297,10 @@ __global__ __launch_bounds__(256) void router_kernel(
         }
         __syncthreads();
         if (is_last) {
-            __threadfence();
             for (uint32_t r = wave; r < nr; r += kRouterWaves)
-                wave_topk_softmax(logits + (uint64_t)(r0 + r) * logits_stride, ne, top_k, pes,
-                                  out_idx + (uint64_t)(r0 + r) * top_k,
-                                  out_w + (uint64_t)(r0 + r) * top_k);
+                wave_topk_softmax(logits + (uint64_t)(r0 + r) * logits_stride, ne, gains,
+                                  out_idx + (uint64_t)(r0 + r) * kTopK,
+                                  out_w + (uint64_t)(r0 + r) * kTopK);
             if (threadIdx.x == 0) atomicExch(&counters[blockIdx.y], 0u);
         }
     }
@@ -273,12 +352,13 @@ struct GULane {
     bool live;
 };
 
-__device__ __forceinline__ GULane gu_lane(const BlobSource& src, const tsg_expert_offsets& o,
+template <typename Src>
+__device__ __forceinline__ GULane gu_lane(const Src& src, const tsg_expert_offsets& o,
                                           uint32_t d, uint32_t g, uint32_t slot, uint32_t fr,
                                           bool live) {
     const bool is_up = (threadIdx.x >> 4) & 1u;
     if (!live) { slot = 0u; fr = 0u; }
-    const uint8_t* blob = blob_for(src, slot);
+    const uint8_t* blob = src.blob(slot);
     const uint32_t ngroups = d / g;
     GULane l;
     l.w = blob + (is_up ? o.up_w : o.gate_w) + (uint64_t)fr * (d / 2u);
@@ -290,13 +370,13 @@ __device__ __forceinline__ GULane gu_lane(const BlobSource& src, const tsg_exper
     return l;
 }
 
-// Gate/up dot products of one pair (x staged in LDS) and the activation:
-// acts[slot * f + fr] = half(act(gate) * up). `bt` holds the first batch.
+// Gate/up dot products of one pair (x staged in LDS) and the activation
+// half(act(gate) * up), the pair's entry acts[slot * f + fr]. Returns true on
+// the one lane that holds it (in `out`). `bt` holds the first batch.
 template <int G, bool SYM, int ACT>
-__device__ __forceinline__ void phase1_compute(const GULane& l, ChunkBatch<kGUBatch>& bt,
+__device__ __forceinline__ bool phase1_compute(const GULane& l, ChunkBatch<kGUBatch>& bt,
                                                const uint16_t* xs, const float* xsum,
-                                               uint16_t* __restrict__ acts, uint32_t d,
-                                               uint32_t f) {
+                                               uint32_t d, uint16_t& out) {
     const uint32_t j = threadIdx.x & 15u;
     const bool is_up = (threadIdx.x >> 4) & 1u;
     const uint32_t nchunks = d / 32u;
@@ -305,29 +385,27 @@ __device__ __forceinline__ void phase1_compute(const GULane& l, ChunkBatch<kGUBa
         if (base) load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, base, j, nchunks, bt);
         compute_batch<G, SYM, kGUBatch, kGULanes, 1>(bt, base, j, nchunks, xs, 0u, xsum, 1u, acc);
     }
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) acc[0] += shfl_xor(acc[0], off);
+    acc[0] = group16_sum(acc[0]);
     const float up = shfl_xor(acc[0], 16);  // gate lanes receive the up sum
-    if (l.live && !is_up && j == 0)
-        acts[l.slot * f + l.fr] = f32_to_f16(gate_activation<ACT>(acc[0]) * up);
+    out = f32_to_f16(gate_activation<ACT>(acc[0]) * up);
+    return l.live && !is_up && j == 0;
 }
 
 // Down + combine for output row `row` (< d) on one wave: lane = slot * 8 + j.
 // acts staged in LDS (slot stride slot_h). y[row] = half(res + sum_s w_s v_s)
 // in slot order (moe.metal:678-686).
-template <int G, bool SYM>
-__device__ __forceinline__ void phase2_body(const BlobSource& src, const tsg_expert_offsets& o,
+template <int G, bool SYM, typename Src>
+__device__ __forceinline__ void phase2_body(const Src& src, const tsg_expert_offsets& o,
                                             const uint16_t* as, uint32_t slot_h,
                                             const float* asum, const uint16_t* __restrict__ rw,
-                                            const uint16_t* __restrict__ residual,
-                                            uint16_t* __restrict__ y, uint32_t d, uint32_t f,
-                                            uint32_t row, ChunkBatch<kDBatch>& bt,
-                                            bool preloaded) {
+                                            uint16_t res_bits, uint16_t* __restrict__ y,
+                                            uint32_t d, uint32_t f, uint32_t row,
+                                            ChunkBatch<kDBatch>& bt, bool preloaded) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t slot = lane >> 3, j = lane & 7u;
     const bool live = row < d;
     const uint32_t rr = live ? row : 0u;
-    const uint8_t* blob = blob_for(src, slot);
+    const uint8_t* blob = src.blob(slot);
     const uint32_t ngroups = f / G, nchunks = f / 32u;
     const uint8_t* w = blob + o.down_w + (uint64_t)rr * (f / 2u);
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + o.down_s) + (uint64_t)rr * ngroups;
@@ -338,13 +416,12 @@ __device__ __forceinline__ void phase2_body(const BlobSource& src, const tsg_exp
         compute_batch<G, SYM, kDBatch, kDLanes, 1>(bt, base, j, nchunks, as + slot * slot_h, 0u,
                                                    asum + slot * nchunks, 1u, acc);
     }
-#pragma unroll
-    for (int off = 4; off >= 1; off >>= 1) acc[0] += shfl_xor(acc[0], off);
+    acc[0] = group8_sum(acc[0]);
     float vals[kTopK];
 #pragma unroll
-    for (int s = 0; s < (int)kTopK; ++s) vals[s] = __shfl(acc[0], s * 8, 64);
+    for (int s = 0; s < (int)kTopK; ++s) vals[s] = lane_value(acc[0], s * 8);
     if (lane == 0 && live) {
-        float out = f16_to_f32(residual[row]);
+        float out = f16_to_f32(res_bits);
 #pragma unroll
         for (int s = 0; s < (int)kTopK; ++s) {
             const float p = f16_to_f32(rw[s]) * vals[s];
@@ -354,15 +431,18 @@ __device__ __forceinline__ void phase2_body(const BlobSource& src, const tsg_exp
     }
 }
 
-// Prefetch of a lane's phase-2 weights (issued early, consumed after a barrier).
-template <int G, bool SYM>
-__device__ __forceinline__ void phase2_prefetch(const BlobSource& src, const tsg_expert_offsets& o,
+// Prefetch of a lane's phase-2 weights and its row's residual (issued early,
+// consumed after a rendezvous).
+template <int G, bool SYM, typename Src>
+__device__ __forceinline__ void phase2_prefetch(const Src& src, const tsg_expert_offsets& o,
+                                                const uint16_t* __restrict__ residual,
                                                 uint32_t d, uint32_t f, uint32_t row,
-                                                ChunkBatch<kDBatch>& bt) {
+                                                ChunkBatch<kDBatch>& bt, uint16_t& res_bits) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t slot = lane >> 3, j = lane & 7u;
     const uint32_t rr = row < d ? row : 0u;
-    const uint8_t* blob = blob_for(src, slot);
+    res_bits = residual[rr];
+    const uint8_t* blob = src.blob(slot);
     const uint32_t ngroups = f / G, nchunks = f / 32u;
     load_batch<G, SYM, kDBatch, kDLanes>(blob + o.down_w + (uint64_t)rr * (f / 2u),
                                          reinterpret_cast<const uint16_t*>(blob + o.down_s) + (uint64_t)rr * ngroups,
@@ -403,7 +483,8 @@ __global__ __launch_bounds__(1024) void phase1_kernel(BlobSource src, tsg_expert
     load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, 0u, threadIdx.x & 15u, d / 32u, bt);
     stage_act_rows<SYM>(x, 0u, 1u, d, xs, 0u, xsum);
     __syncthreads();
-    phase1_compute<G, SYM, ACT>(l, bt, xs, xsum, acts, d, f);
+    uint16_t v;
+    if (phase1_compute<G, SYM, ACT>(l, bt, xs, xsum, d, v)) acts[l.slot * f + l.fr] = v;
 }
 
 // ---------------------------------------------------------------- phase 2
@@ -422,71 +503,95 @@ __global__ __launch_bounds__(1024) void phase2_kernel(BlobSource src, tsg_expert
     float* asum = reinterpret_cast<float*>(smem + kTopK * slot_h * 2u);
     const uint32_t row = blockIdx.x * rows_per_block + (threadIdx.x >> 6);
     ChunkBatch<kDBatch> bt;
-    phase2_prefetch<G, SYM>(src, o, d, f, row, bt);
+    uint16_t res_bits;
+    phase2_prefetch<G, SYM>(src, o, residual, d, f, row, bt, res_bits);
     stage_act_rows<SYM>(acts, f, kTopK, f, as, slot_h, asum);
     __syncthreads();
-    phase2_body<G, SYM>(src, o, as, slot_h, asum, routing_w, residual, y, d, f, row, bt, true);
+    phase2_body<G, SYM>(src, o, as, slot_h, asum, routing_w, res_bits, y, d, f, row, bt, true);
 }
 
-// ---------------------------------------------------------- grid barrier
+// ------------------------------------------------- in-launch rendezvous
 
-// Generation barrier over the blocks of one launch, all co-resident (the host
-// checks occupancy before launching). The last block to arrive may run
-// `on_last` (block-wide) before releasing the others. Waiting is bounded: after
-// kSpinLimit polls a block records an error and proceeds, so every wave
-// reaches the end of the kernel whatever happens to another block.
-struct GridBarrier {
-    uint32_t count;
-    uint32_t gen;
-    uint32_t error;
-    uint32_t pad;
+// The one-launch layer has two points where blocks need what others produced:
+// the router logits (for the top-8) and the phase-1 activations (for phase 2).
+// Neither uses a shared atomic counter (arrivals on one address serialize at
+// the memory-side atomic unit) nor has every block poll every other (the
+// polls then queue on the same few lines). Words travel by agent-coherent
+// stores and loads, tagged with the launch's epoch, along a shallow tree:
+//   - router: each expert's logit is posted as a (tag << 32 | bits) word;
+//     block 0 gathers them, runs the top-8 and posts (tag, weight, id) words
+//     to kSyncReplicas lines; block b reads line b % kSyncReplicas;
+//   - phase 1 done: block b posts flag b; the leader of each 16 blocks
+//     gathers its group and posts a group flag; block 0 gathers the groups
+//     and posts the go word to kSyncReplicas lines.
+// A word carries its own tag, so no reader can mistake an earlier launch's
+// words for this one's. The epoch (read at launch start, advanced by block 0
+// once every block has passed both rendezvous) makes each launch's tag new,
+// also across HIP graph replays. Polls are bounded by kSpinLimit; a block
+// that gives up sets the error word (reported by tsg_ctx_synchronize) and
+// carries on, so every wave reaches the end of the kernel.
+constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr uint32_t kSyncFanIn = 16;
+
+struct DecodeSync {
+    uint32_t* epoch;
+    uint32_t* error;
+    uint32_t* flags;
+    uint32_t* groups;
+    uint32_t* go;       // kSyncReplicas lines
+    uint64_t* topk;     // kSyncReplicas lines of kTopK words
+    uint64_t* logits;   // kMaxExperts words
 };
 
-constexpr uint32_t kSpinLimit = 1u << 22;
-
-__device__ __forceinline__ uint32_t atomic_load_acq(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ DecodeSync decode_sync(uint32_t* words) {
+    DecodeSync s;
+    s.epoch = words + kSyncEpochWord;
+    s.error = words + kSyncErrorWord;
+    s.flags = words + kSyncFlagWord;
+    s.groups = words + kSyncGroupWord;
+    s.go = words + kSyncGoWord;
+    s.topk = reinterpret_cast<uint64_t*>(words + kSyncTopkWord);
+    s.logits = reinterpret_cast<uint64_t*>(words + kSyncLogitWord);
+    return s;
 }
 
-// Every thread releases its own global writes at agent scope before the block
-// arrives: __syncthreads() alone does not wait for outstanding global stores,
-// so a single thread's fence would not cover the other waves' writes. The
-// last block to arrive runs `on_last` (after an acquire) and opens the next
-// generation; the others spin on the generation word, bounded by kSpinLimit
-// (on timeout they set `error`, which tsg_ctx_synchronize reports).
+// One wave polls until `ready()` holds on every lane (bounded).
 template <typename F>
-__device__ __forceinline__ void grid_barrier(GridBarrier* bar, uint32_t nblocks, F&& on_last) {
-    __shared__ uint32_t last_flag, gen_seen;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        gen_seen = atomic_load_acq(&bar->gen);  // read before arriving
-        const uint32_t arrived = __hip_atomic_fetch_add(&bar->count, 1u, __ATOMIC_ACQ_REL,
-                                                        __HIP_MEMORY_SCOPE_AGENT);
-        last_flag = arrived == nblocks - 1u ? 1u : 0u;
-    }
-    __syncthreads();
-    if (last_flag) {
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        on_last();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            __hip_atomic_store(&bar->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_fetch_add(&bar->gen, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void wave_poll(const DecodeSync& sy, F&& ready) {
+    for (uint32_t spins = 0;; ++spins) {
+        if (__all(ready())) return;
+        if (spins > kSpinLimit) {
+            if ((threadIdx.x & 63u) == 0) atomicOr(sy.error, 1u);
+            return;
         }
-    } else if (threadIdx.x == 0) {
-        uint32_t spins = 0;
-        while (atomic_load_acq(&bar->gen) == gen_seen) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > kSpinLimit) {
-                atomicOr(&bar->error, 1u);
-                break;
-            }
-        }
+        __builtin_amdgcn_s_sleep(1);
     }
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// One wave: `count` packed words at `w` all equal `tag`.
+__device__ __forceinline__ void wave_wait_words(const DecodeSync& sy, const uint32_t* w,
+                                                uint32_t count, uint32_t tag) {
+    const uint32_t lane = threadIdx.x & 63u;
+    wave_poll(sy, [&] {
+        bool ok = true;
+        for (uint32_t i = lane; i < count; i += 64u) ok = ok && ld_coherent(w + i) == tag;
+        return ok;
+    });
+}
+
+// One wave: every block of the launch has posted flag == tag.
+__device__ __forceinline__ void rendezvous_all(const DecodeSync& sy, uint32_t nb, uint32_t tag) {
+    const uint32_t b = blockIdx.x, lane = threadIdx.x & 63u;
+    if (b % kSyncFanIn == 0) {
+        const uint32_t n = min(kSyncFanIn, nb - b);
+        wave_wait_words(sy, sy.flags + b, n, tag);
+        if (lane == 0) st_coherent(sy.groups + b / kSyncFanIn, tag);
+    }
+    if (b == 0) {
+        wave_wait_words(sy, sy.groups, (nb + kSyncFanIn - 1) / kSyncFanIn, tag);
+        if (lane < kSyncReplicas) st_coherent(sy.go + lane * kSyncLineWords, tag);
+    }
+    wave_wait_words(sy, sy.go + (b % kSyncReplicas) * kSyncLineWords, 1u, tag);
 }
 
 // -------------------------------------------------- fused decode layer
@@ -505,47 +610,101 @@ struct DecodeLayerArgs {
     uint32_t* out_idx;
     uint16_t* out_w;
     uint16_t* acts;
-    float* logits;
-    GridBarrier* bar;
+    uint16_t* act_rep;  // kActReplicas copies of the activations
+    uint32_t* sync_words;
     uint32_t ne, d, f, pairs_per_block, rows_per_block;
 };
 
 // One decode MoE layer in one launch (grid = one block per CU, all
 // co-resident): router logits (one expert row per block, the router kernel's
-// canonical order) -> barrier whose last block runs the top-k -> every block:
-// prefetch its down-projection weights, gate/up + activation for its row
-// pairs -> barrier -> down + slot-ordered combine for its output rows. The
+// canonical order) -> rendezvous, every block runs the top-k -> prefetch of
+// its down-projection weights, gate/up + activation for its row pairs ->
+// rendezvous -> down + slot-ordered combine for its output rows. The
 // arithmetic of every phase is the separate kernels' (shared bodies), so the
 // fused and unfused paths agree bit for bit.
 template <int G, bool SYM, int ACT>
 __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ uint32_t s_tag;
+    __shared__ uint16_t s_w[kTopK];
+    __shared__ uint32_t s_idx[kTopK];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t nb = gridDim.x;
+    const DecodeSync sy = decode_sync(a.sync_words);
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
     float* xsum = reinterpret_cast<float*>(smem + lds_chunks_halves(a.d) * 2u);
 
+    uint32_t gains[4] = {0u, 0u, 0u, 0u};
+    if (blockIdx.x == 0 && wave == 0) load_expert_gains(a.pes, a.ne, gains);
+    uint32_t tag = 0;
+    if (threadIdx.x == 0) {
+        tag = ld_coherent(sy.epoch) + 1u;
+        tag = tag ? tag : 1u;
+        s_tag = tag;
+    }
     // router rows: wave 0 of block b takes experts b, b + nb, ...
     if (wave == 0)
         for (uint32_t e = blockIdx.x; e < a.ne; e += nb) {
             const float s = router_dot(a.router_w + (uint64_t)e * a.d, a.router_hidden, a.es,
                                        a.d, lane);
-            if (lane == 0) a.logits[e] = s;
+            if (lane == 0)
+                st_coherent(sy.logits + e, ((uint64_t)tag << 32) | __float_as_uint(s));
         }
     stage_act_rows<SYM>(a.x, 0u, 1u, a.d, xs, 0u, xsum);
-    grid_barrier(a.bar, nb, [&] {
-        if (wave == 0) wave_topk_softmax(a.logits, a.ne, kTopK, a.pes, a.out_idx, a.out_w);
-    });
+    __syncthreads();
+    tag = s_tag;
+    if (wave == 0) {
+        if (blockIdx.x == 0) {
+            // gather the logits, run the top-8, post it to every replica line
+            float v[4];
+            wave_poll(sy, [&] {
+                bool ok = true;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t e = lane + 64u * j;
+                    v[j] = -INFINITY;
+                    if (e < a.ne) {
+                        const uint64_t w = ld_coherent(sy.logits + e);
+                        v[j] = __uint_as_float((uint32_t)w);
+                        ok = ok && (uint32_t)(w >> 32) == tag;
+                    }
+                }
+                return ok;
+            });
+            const TopK t = wave_topk_softmax_regs(v, a.ne, gains);
+            const uint32_t r = lane & (kTopK - 1u);
+            uint32_t id = 0, wb = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < kTopK; ++q)
+                if (r == q) { id = t.idx[q]; wb = t.w[q]; }
+            for (uint32_t q = lane / kTopK; q < kSyncReplicas; q += 64u / kTopK)
+                st_coherent(sy.topk + q * (kSyncLineWords / 2) + r,
+                            ((uint64_t)tag << 32) | (wb << 16) | id);
+            if (lane < kTopK) {
+                a.out_idx[lane] = id;
+                a.out_w[lane] = (uint16_t)wb;
+            }
+        }
+        const uint64_t* line = sy.topk + (blockIdx.x % kSyncReplicas) * (kSyncLineWords / 2);
+        uint64_t w = 0;
+        wave_poll(sy, [&] {
+            if (lane >= kTopK) return true;
+            w = ld_coherent(line + lane);
+            return (uint32_t)(w >> 32) == tag;
+        });
+        if (lane < kTopK) {
+            s_idx[lane] = (uint32_t)w & 0xFFFFu;
+            s_w[lane] = (uint16_t)(w >> 16);
+        }
+    }
+    __syncthreads();
 
-    BlobSource src{};
-    src.resident = 1;
-    src.base = a.layer_base;
-    src.stride = a.expert_stride;
-    src.indices = a.out_idx;
+    const LdsBlobs src{a.layer_base, a.expert_stride, s_idx};
     const uint32_t row = blockIdx.x * a.rows_per_block + wave;
     ChunkBatch<kDBatch> dbt;
+    uint16_t res_bits = 0;
     const bool p2_wave = wave < a.rows_per_block;
-    if (p2_wave) phase2_prefetch<G, SYM>(src, a.o, a.d, a.f, row, dbt);
+    if (p2_wave) phase2_prefetch<G, SYM>(src, a.o, a.residual, a.d, a.f, row, dbt, res_bits);
     {
         const uint32_t pair = blockIdx.x * a.pairs_per_block + (threadIdx.x >> 5);
         const bool live = (threadIdx.x >> 5) < a.pairs_per_block && pair < kTopK * a.f;
@@ -554,18 +713,32 @@ __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a) {
         const GULane l = gu_lane(src, a.o, a.d, G, slot, pp - slot * a.f, live);
         ChunkBatch<kGUBatch> gbt;
         load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, 0u, threadIdx.x & 15u, a.d / 32u, gbt);
-        phase1_compute<G, SYM, ACT>(l, gbt, xs, xsum, a.acts, a.d, a.f);
+        uint16_t v;
+        if (phase1_compute<G, SYM, ACT>(l, gbt, xs, xsum, a.d, v)) {
+            const uint32_t at = l.slot * a.f + l.fr;
+            a.acts[at] = v;
+#pragma unroll
+            for (uint32_t r = 0; r < kActReplicas; ++r)
+                st_coherent(a.act_rep + (size_t)r * kActReplicaHalves + at, v);
+        }
     }
-    grid_barrier(a.bar, nb, [] {});
+    wait_vector_memory();  // this wave's activation stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) st_coherent(sy.flags + blockIdx.x, tag);
+    if (wave == 0) rendezvous_all(sy, nb, tag);
+    __syncthreads();
 
     const uint32_t slot_h = p2_slot_halves(a.f);
     uint16_t* as = reinterpret_cast<uint16_t*>(smem);
     float* asum = reinterpret_cast<float*>(smem + kTopK * slot_h * 2u);
-    stage_act_rows<SYM>(a.acts, a.f, kTopK, a.f, as, slot_h, asum);
+    stage_act_rows<SYM, 4, true>(a.act_rep + (size_t)(blockIdx.x % kActReplicas) * kActReplicaHalves,
+                                 a.f, kTopK, a.f, as, slot_h, asum);
     __syncthreads();
     if (p2_wave)
-        phase2_body<G, SYM>(src, a.o, as, slot_h, asum, a.out_w, a.residual, a.y, a.d, a.f, row,
+        phase2_body<G, SYM>(src, a.o, as, slot_h, asum, s_w, res_bits, a.y, a.d, a.f, row,
                             dbt, true);
+    // every block has passed both rendezvous: the next launch may use tag + 1
+    if (blockIdx.x == 0 && threadIdx.x == 0) st_coherent(sy.epoch, tag);
 }
 
 // ------------------------------------------------------------ host helpers
@@ -693,7 +866,7 @@ tsg_status phase2_dispatch(tsg_moe* moe, hipStream_t stream, const BlobSource& s
 }
 
 // The fused one-launch decode layer, when every block fits on the device at
-// once (the grid barriers need all blocks resident). Returns TSG_ERR_DECLINED
+// once (the rendezvous need all blocks resident). Returns TSG_ERR_DECLINED
 // otherwise and the caller runs the three-kernel sequence.
 template <int G, bool SYM, int ACT>
 tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, const DecodeLayerArgs& a,
@@ -704,7 +877,8 @@ tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, const DecodeLayerArgs&
     const size_t lds = lds_a > lds_b ? lds_a : lds_b;
     auto kern = decode_layer_kernel<G, SYM, ACT>;
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, (int)g.threads, lds) !=
+    if (nb > kMaxFusedBlocks || a.ne > kMaxExperts || kTopK * a.f > kActReplicaHalves ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, (int)g.threads, lds) !=
             hipSuccess ||
         (uint64_t)per_cu * (uint64_t)moe->ctx->num_cus < nb)
         return TSG_ERR_DECLINED;
@@ -932,8 +1106,8 @@ extern "C" tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream,
     a.out_idx = out_idx;
     a.out_w = out_w;
     a.acts = acts;
-    a.logits = moe->ctx->logits;
-    a.bar = reinterpret_cast<GridBarrier*>(moe->ctx->counters + kBarrierWord);
+    a.sync_words = moe->ctx->counters;
+    a.act_rep = moe->ctx->act_replicas;
     a.ne = ne;
     a.d = d;
     a.f = f;

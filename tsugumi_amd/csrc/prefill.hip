@@ -398,8 +398,7 @@ __global__ __launch_bounds__(256) void rows_gate_up_kernel(GemmArgs args, RowsBl
     }
 #pragma unroll
     for (uint32_t r = 0; r < kRowsMax; ++r) {
-#pragma unroll
-        for (int off = 8; off >= 1; off >>= 1) acc[r] += shfl_xor(acc[r], off);
+        acc[r] = group16_sum(acc[r]);
         const float up = shfl_xor(acc[r], 16);
         if (live && !is_up && j == 0 && r < rows)
             args.out[(uint64_t)(blk.local_row + r) * f + fr] =
@@ -449,8 +448,7 @@ __global__ __launch_bounds__(64) void rows_down_kernel(GemmArgs args, RowsBlocks
     }
 #pragma unroll
     for (uint32_t r = 0; r < kRowsMax; ++r) {
-#pragma unroll
-        for (int off = 4; off >= 1; off >>= 1) acc[r] += shfl_xor(acc[r], off);
+        acc[r] = group8_sum(acc[r]);
     }
     if (live_row && j == 0)
         for (uint32_t r = 0; r < rows; ++r) partials[dst[r] + row] = f32_to_f16(acc[r]);

@@ -47,8 +47,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint8_t* __restrict__ w,
     }
 #pragma unroll
     for (int r = 0; r < T; ++r) {
-#pragma unroll
-        for (int off = 8; off >= 1; off >>= 1) acc[r] += shfl_xor(acc[r], off);
+        acc[r] = group16_sum(acc[r]);
     }
     if (live && j == 0) {
 #pragma unroll

@@ -46,6 +46,7 @@ struct tsg_ctx {
     // last-block patterns (zeroed once, self-resetting) and router logits.
     uint32_t* counters = nullptr;        // kMaxCounters
     float* logits = nullptr;             // kMaxPromptRows * kMaxExperts
+    uint16_t* act_replicas = nullptr;    // kActReplicas * kActReplicaHalves
     int num_cus = 256;
 };
 
@@ -71,9 +72,28 @@ constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kMaxRouterRows = 8;      // MoE.maxRouterRows (verify rows)
 constexpr uint32_t kMaxPromptRows = 4096;   // rows one router launch may route
 constexpr uint32_t kMaxCounters = 4096;
-// The fused decode layer's grid barrier {count, gen, error, pad} occupies the
-// last four counter words.
-constexpr uint32_t kBarrierWord = kMaxCounters - 4;
+// Words of ctx->counters used by the one-launch decode layer (below them, words
+// [0, kMaxPromptRows / 16) are the router's per-row-group completion
+// counters). Each area starts on its own 128-byte line; replicated words sit
+// one per line.
+constexpr uint32_t kSyncEpochWord = 1024;                       // launch epoch
+constexpr uint32_t kSyncErrorWord = 1056;                       // rendezvous timeout
+constexpr uint32_t kMaxFusedBlocks = 1024;
+constexpr uint32_t kSyncFlagWord = 1088;                        // per block, packed
+constexpr uint32_t kSyncGroupWord = kSyncFlagWord + kMaxFusedBlocks;  // per 16 blocks, packed
+constexpr uint32_t kSyncReplicas = 16;
+// The one-launch layer's phase-1 activations are published in this many
+// copies (block b stages copy b % kActReplicas) so that no line is read by
+// every block; each copy holds up to kTopK * 4096 fp16 values.
+constexpr uint32_t kActReplicas = 8;
+constexpr uint32_t kActReplicaHalves = 8u * 4096u;
+constexpr uint32_t kSyncLineWords = 32;
+constexpr uint32_t kSyncGoWord = kSyncGroupWord + 64;           // kSyncReplicas lines
+constexpr uint32_t kSyncTopkWord = kSyncGoWord + kSyncReplicas * kSyncLineWords;
+constexpr uint32_t kSyncLogitWord = kSyncTopkWord + kSyncReplicas * kSyncLineWords;
+static_assert(kSyncLogitWord + 2 * kMaxExperts <= kMaxCounters, "sync area overflow");
+static_assert(kSyncTopkWord % 2 == 0 && kSyncLogitWord % 2 == 0, "64-bit words must be aligned");
+
 constexpr uint32_t kTopK = 8;
 
 inline hipStream_t as_stream(tsg_stream s) { return reinterpret_cast<hipStream_t>(s); }
@@ -94,6 +114,30 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load16_nt(const void* p) {
     const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Agent-coherent accesses for the few values the blocks of one launch hand to
+// each other (router logits, the top-k, phase-1 activations). A relaxed
+// agent-scope atomic compiles to a plain load/store with the sc1 bit, which
+// is coherent across the XCDs' separate L2 caches without a cache-wide
+// writeback or invalidate.
+template <typename T>
+__device__ __forceinline__ T ld_coherent(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void st_coherent(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint4 ld_coherent16(const void* p) {
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    const uint64_t lo = ld_coherent(q), hi = ld_coherent(q + 1);
+    return make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+}
+// Blocks until this wave's outstanding vector memory operations (coherent
+// stores included) have completed; also a compiler barrier.
+__device__ __forceinline__ void wait_vector_memory() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
@@ -195,7 +239,9 @@ __device__ __forceinline__ uint4 pair_permute(uint4 v) {
 // the staged copy, in element order, into sums[r * n/32 + c]. The caller
 // synchronises before reading.
 // `row_index` (may be NULL) maps staged row r to source row row_index[r].
-template <bool SYM, int PER_THREAD = 4>
+// COHERENT reads the source with agent-coherent loads (data written earlier
+// in the same launch by other blocks).
+template <bool SYM, int PER_THREAD = 4, bool COHERENT = false>
 __device__ __forceinline__ void stage_act_rows(const uint16_t* __restrict__ src,
                                                uint32_t src_stride, uint32_t rows, uint32_t n,
                                                uint16_t* dst, uint32_t dst_stride,
@@ -207,10 +253,16 @@ __device__ __forceinline__ void stage_act_rows(const uint16_t* __restrict__ src,
         uint4 v[PER_THREAD];
 #pragma unroll
         for (int i = 0; i < PER_THREAD; ++i) {
-            const uint32_t q = min(q0 + threadIdx.x + i * blockDim.x, total - 1u);
+            // plain loads clamp (a repeated unit is a cache hit and keeps the
+            // loads branch-free); coherent loads skip: each is a memory-side
+            // access, and repeats of one unit would all queue on one line
+            const uint32_t q_raw = q0 + threadIdx.x + i * blockDim.x;
+            const uint32_t q = min(q_raw, total - 1u);
             const uint32_t r = q / bpr, b = q - r * bpr;
             const uint32_t sr = row_index ? row_index[r] : r;
-            v[i] = *reinterpret_cast<const uint4*>(src + (uint64_t)sr * src_stride + b * 8u);
+            const uint16_t* sp = src + (uint64_t)sr * src_stride + b * 8u;
+            if constexpr (COHERENT) v[i] = q_raw < total ? ld_coherent16(sp) : make_uint4(0, 0, 0, 0);
+            else v[i] = *reinterpret_cast<const uint4*>(sp);
         }
 #pragma unroll
         for (int i = 0; i < PER_THREAD; ++i) {
@@ -244,6 +296,31 @@ __device__ __forceinline__ const h2_t* staged_chunk(const uint16_t* xs, uint32_t
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) {
     return __shfl_xor(v, mask, 64);
+}
+
+// Cross-lane sums on DPP moves (VALU; no LDS round trip). Lanes form aligned
+// groups of 8 (16); afterwards every lane of a group holds the group's sum,
+// added as pairs (i, i^1), then pairs of pairs (i, i^2), then quads mirrored
+// within the 8 (i, 7-i) [, then 8s mirrored within the 16 (i, 15-i)]. Every
+// lane ends with the same value since each step adds two equal-for-the-pair
+// operands in either order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float group8_sum(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    return v;
+}
+__device__ __forceinline__ float group16_sum(float v) {
+    v = group8_sum(v);
+    v += dpp_f32<0x140>(v);  // row_mirror
+    return v;
+}
+__device__ __forceinline__ float lane_value(float v, uint32_t lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
 }  // namespace tsg
