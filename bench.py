@@ -5,23 +5,25 @@ Workload (BASELINE.json configs[1] and [3]):
   decode  Gemma-4-26B-A4B-shaped MoE layer, 1 token: H=2816, 128 experts of
           gate/up [2x704, 2816] + down [2816, 704], int4 sym group-32 with bf16
           scales, bf16 router [128, 2816] -> top-8 -> GeGLU. 30 layers
-          (12.9 GB of experts) resident in HBM and chained (layer l's output is
-          layer l+1's input), so every layer routes fresh experts. One step =
-          one token through the 30 layers; captured once in a HIP graph.
+          (12.9 GB of experts) resident in HBM, run back to back on one stream
+          with a fresh N(0,1) hidden state per (token, layer), so every layer
+          routes fresh experts. One step = one token through the 30 layers;
+          8 tokens are captured once in a HIP graph (6.6 GB of expert reads
+          per replay: nothing is served from cache across replays).
   prefill the same layer shape, T=2048 tokens, top-8 Zipf(1.1) routing:
           device grouping -> gate/up GEMM + GeGLU -> down GEMM -> token-major
           reduce.
 
 `value` is the decode layer's algorithmic HBM throughput (GB/s): 27,506,944
-bytes per layer / measured time per layer (one token through 30 chained
-layers, input copies included). The roofline object is for the dominant (and
+bytes per layer / measured time per layer (one token through the 30
+layers). The roofline object is for the dominant (and
 only) decode kernel, decode_layer_kernel, which runs the whole layer in one
 launch; its 27,506,944 algorithmic bytes per launch / its average launch
 duration, timed with HIP events on the stream it runs on over a graph of
 launches alone. `traffic` is the HBM bytes per launch that rocprofv3's
 FETCH_SIZE + WRITE_SIZE counters report, scaled by the factor a plain copy
 kernel of known size reads on the same counters (constant TRAFFIC_BYTES,
-refreshed from the committed profile; None until measured). cpu_baseline times the oracle's restatement of the
+measured with `--traffic-probe` under rocprofv3). cpu_baseline times the oracle's restatement of the
 reference's CPU path (DequantInt4GemvRef + MoeRef + routerReference) on the
 host cores, on a bounded sample of the same layers.
 """
@@ -48,7 +50,11 @@ LAYER_BYTES = TOPK * EXPERT_BYTES + ROUTER_BYTES + H * 2 + E * 2 + 3 * H * 2  # 
 PREFILL_T = 2048
 PREFILL_FLOP = 2 * PREFILL_T * TOPK * 3 * F * H  # 194,884,141,056
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_BYTES = None
+# HBM bytes per decode_layer_kernel launch: rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE over `bench.py --traffic-probe` (13,926.84 KiB fetched, 749.09 KiB
+# written per dispatch), scaled by the counters of a plain 64 MiB device copy in
+# the same runs (fetch x 1.9990, write x 1.000).
+TRAFFIC_BYTES = 29275474
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
@@ -91,21 +97,29 @@ def run_decode(tsg, torch, ctx, args, layers, routers):
     ones_h = torch.full((H,), 0x3F80, dtype=torch.int16, device="cuda")
     ones_e = torch.full((E,), 0x3F80, dtype=torch.int16, device="cuda")
     n_inputs = 8
-    inputs = torch.empty(n_inputs * H, dtype=torch.int16, device="cuda")
+    # a fresh N(0,1) hidden state per (token, layer): fresh routing everywhere
+    # (chaining raw layer outputs without the model's norms overflows fp16
+    # within a few layers and would collapse the routing)
+    inputs = torch.empty(n_inputs * LAYERS * H, dtype=torch.int16, device="cuda")
     tsg.generators.f16_normal(inputs, 0x1A2B, 1.0)
-    xs = [torch.empty(H, dtype=torch.int16, device="cuda") for _ in range(LAYERS + 1)]
+    ys = torch.empty(LAYERS * H, dtype=torch.int16, device="cuda")
     idx = torch.empty(LAYERS * TOPK, dtype=torch.int32, device="cuda")
     wts = torch.empty(LAYERS * TOPK, dtype=torch.int16, device="cuda")
     acts = torch.empty(LAYERS * TOPK * F, dtype=torch.int16, device="cuda")
     stream = torch.cuda.Stream()
 
+    def x_of(k, l):
+        return inputs[(k * LAYERS + l) * H:(k * LAYERS + l + 1) * H]
+
+    def layer(k, l):
+        moe.encode_decode_layer(layers[l], routers[l], x_of(k, l), ones_h, ones_e, x_of(k, l),
+                                x_of(k, l), ys[l * H:(l + 1) * H], idx[l * TOPK:(l + 1) * TOPK],
+                                wts[l * TOPK:(l + 1) * TOPK],
+                                acts[l * TOPK * F:(l + 1) * TOPK * F], E, H, F, stream=stream)
+
     def one_token(k):
-        xs[0].copy_(inputs[k * H:(k + 1) * H])
         for l in range(LAYERS):
-            moe.encode_decode_layer(layers[l], routers[l], xs[l], ones_h, ones_e, xs[l], xs[l],
-                                    xs[l + 1], idx[l * TOPK:(l + 1) * TOPK],
-                                    wts[l * TOPK:(l + 1) * TOPK],
-                                    acts[l * TOPK * F:(l + 1) * TOPK * F], E, H, F, stream=stream)
+            layer(k, l)
 
     # one graph = n_inputs tokens (each a 30-layer pass from its own input)
     with torch.cuda.stream(stream):
@@ -139,18 +153,14 @@ def run_decode(tsg, torch, ctx, args, layers, routers):
     us_per_layer = ms * 1000.0 / (tokens * LAYERS)
     log(f"decode: {tokens} tokens x {LAYERS} layers in {ms:.3f} ms (wall {wall*1e3:.1f} ms): "
         f"{us_per_layer:.3f} us/layer")
-    # dominant kernel: the one-launch decode layer alone (no input copies),
-    # 4 x 30 launches per graph, timed on the stream the launches go to.
+    check_decode_outputs(torch, ys, idx)
+    # dominant kernel: the one-launch decode layer alone, 4 tokens x 30 layers
+    # per graph, timed on the stream the launches go to.
     g2 = torch.cuda.CUDAGraph()
     k_reps = 4
     with torch.cuda.graph(g2, stream=stream):
-        for _ in range(k_reps):
-            for l in range(LAYERS):
-                moe.encode_decode_layer(layers[l], routers[l], xs[l], ones_h, ones_e, xs[l],
-                                        xs[l], xs[l + 1], idx[l * TOPK:(l + 1) * TOPK],
-                                        wts[l * TOPK:(l + 1) * TOPK],
-                                        acts[l * TOPK * F:(l + 1) * TOPK * F], E, H, F,
-                                        stream=stream)
+        for k in range(k_reps):
+            one_token(k)
     with torch.cuda.stream(stream):
         g2.replay()
     torch.cuda.synchronize()
@@ -163,8 +173,27 @@ def run_decode(tsg, torch, ctx, args, layers, routers):
     torch.cuda.synchronize()
     k_us = start.elapsed_time(stop) * 1000.0 / (reps * k_reps * LAYERS)
     log(f"decode_layer_kernel alone: {k_us:.3f} us/launch")
+    check_decode_outputs(torch, ys, idx)
+    # the graph's last token is the last one executed: its inputs and routing
+    last = [x_of(n_inputs - 1, l) for l in range(LAYERS)]
+    with torch.cuda.stream(stream):
+        one_token(n_inputs - 1)
+    torch.cuda.synchronize()
     return dict(ms_per_step=ms / tokens, us_per_layer=us_per_layer, tokens=tokens,
-                kernel_us=k_us, idx=idx, xs=xs, wts=wts)
+                kernel_us=k_us, idx=idx, xs=last, wts=wts)
+
+
+def check_decode_outputs(torch, ys, idx):
+    """The measured work must be the claimed work: finite outputs and routing
+    that spreads over many experts (a collapsed routing reads one expert)."""
+    y = ys.view(torch.float16).float()
+    if not bool(torch.isfinite(y).all()):
+        raise RuntimeError("decode produced non-finite outputs: the benchmark would not "
+                           "measure the claimed work")
+    per_layer = idx.view(LAYERS, TOPK).cpu().numpy()
+    distinct = min(len(set(row.tolist())) for row in per_layer)
+    if distinct != TOPK:
+        raise RuntimeError(f"a decode layer routed to only {distinct} distinct experts")
 
 
 def zipf_routing(t, ne, k, s, seed):
@@ -279,6 +308,38 @@ def cpu_baseline(torch, dec, bufs, routers, offs, stride, budget_s=12.0):
                        f"{us:.0f} us/layer on {threads} threads")
 
 
+COPY_BYTES = 64 << 20
+
+
+def traffic_probe(tsg, torch, ctx, layers, routers):
+    """For rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a plain device copy of
+    COPY_BYTES (three dispatches; its counters give the factor between counter
+    KiB and bytes moved) and one token through the layers (one
+    decode_layer_kernel dispatch per layer)."""
+    src = torch.ones(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    moe = tsg.MoE(ctx)
+    ones_h = torch.full((H,), 0x3F80, dtype=torch.int16, device="cuda")
+    ones_e = torch.full((E,), 0x3F80, dtype=torch.int16, device="cuda")
+    xs = torch.empty(LAYERS * H, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(xs, 0x1A2B, 1.0)
+    ys = torch.empty(LAYERS * H, dtype=torch.int16, device="cuda")
+    idx = torch.empty(LAYERS * TOPK, dtype=torch.int32, device="cuda")
+    wts = torch.empty(TOPK, dtype=torch.int16, device="cuda")
+    acts = torch.empty(TOPK * F, dtype=torch.int16, device="cuda")
+    for l in range(LAYERS):
+        x = xs[l * H:(l + 1) * H]
+        moe.encode_decode_layer(layers[l], routers[l], x, ones_h, ones_e, x, x,
+                                ys[l * H:(l + 1) * H], idx[l * TOPK:(l + 1) * TOPK], wts, acts,
+                                E, H, F)
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    check_decode_outputs(torch, ys, idx)
+    log(f"traffic probe: 3 copies of {COPY_BYTES} bytes, {LAYERS} decode layers")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -286,6 +347,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run the copy + one-token dispatches for rocprofv3 --pmc and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -299,6 +362,9 @@ def main():
     ctx = tsg.Context(0, group_size=GROUP, scheme="sym")
     log(f"building {LAYERS} resident layers ({LAYERS * E * gemma_offsets()[1] / 1e9:.2f} GB)")
     layers, bufs, routers, offs, stride = make_layers(tsg, ctx, torch, LAYERS)
+    if args.traffic_probe:
+        traffic_probe(tsg, torch, ctx, layers, routers)
+        return
     dec = run_decode(tsg, torch, ctx, args, layers, routers)
     pre = None if args.no_prefill else run_prefill(tsg, torch, ctx, args, layers[0])
     gbs = LAYER_BYTES / (dec["us_per_layer"] * 1e-6) / 1e9
@@ -318,7 +384,7 @@ def main():
         "dtype": "int4xfp16->fp32",
         "data": "synthetic (seeded device generators; nibbles U{0..15}, scales bf16(|N(0,.02)|/7), "
                 "x fp16 N(0,1))",
-        "config": {"workload": "gemma4-26b-a4b decode MoE layer, 1 token, 30 chained "
+        "config": {"workload": "gemma4-26b-a4b decode MoE layer, 1 token, 30 "
                                "HBM-resident layers (config 2); prefill T=2048 top-8 "
                                "Zipf(1.1) (config 4)",
                    "hidden": H, "intermediate": F, "experts": E, "top_k": TOPK,

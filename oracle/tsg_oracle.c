@@ -434,12 +434,20 @@ void tsgo_router_logits_canonical(const uint16_t* w_bf16, const uint16_t* hidden
                     }
                 p[l] = acc;
             }
-            for (int o = 32; o >= 1; o >>= 1) {
-                float q[64];
-                for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ o];
-                memcpy(p, q, sizeof(p));
+            /* each 16-lane row: pairs (l, l^1), pairs of pairs (l, l^2), the
+             * quads of each 8 mirrored (l, 7-l), the 8s of the row mirrored
+             * (l, 15-l); then the row sums as (r0 + r1) + (r2 + r3) */
+            float r[4];
+            for (int k = 0; k < 4; ++k) {
+                float* q = p + 16 * k;
+                float t[16];
+                for (int l = 0; l < 16; ++l) t[l] = q[l] + q[l ^ 1];
+                for (int l = 0; l < 16; ++l) q[l] = t[l] + t[l ^ 2];
+                for (int l = 0; l < 16; ++l) t[l] = q[l] + q[(l & 8) | (7 - (l & 7))];
+                for (int l = 0; l < 16; ++l) q[l] = t[l] + t[15 - l];
+                r[k] = q[0];
             }
-            out_logits[(size_t)row * num_experts + e] = p[0];
+            out_logits[(size_t)row * num_experts + e] = (r[0] + r[1]) + (r[2] + r[3]);
         }
     }
 }

@@ -95,11 +95,15 @@ void tsgo_router_reference(const float* w, const float* x, int num_experts, int 
                            int top_k, const float* per_expert_scale,
                            int32_t* out_idx, float* out_w);
 /* Router logits in the MI355X kernels' summation order (restated from
- * tsugumi_amd/csrc/decode.hip router_row_dot, not from the reference, whose
+ * tsugumi_amd/csrc/decode.hip router_chunks_dot, not from the reference, whose
  * simd_sum order is Metal's): for each expert, 64 partial sums p_l over the
  * 8-element chunks c = l, l+64, ... (acc = fma(w, x*es, acc), elements in
- * order), then a xor butterfly p_l += p_{l^o} for o = 32, 16, 8, 4, 2, 1. Inputs
- * are bf16 weights, fp16 hidden rows at `stride`, bf16 effective scale. */
+ * order); each group of 16 partials sums as pairs (l, l^1), pairs of pairs
+ * (l, l^2), quads mirrored within the 8 (l, 7-l), 8s mirrored within the 16
+ * (l, 15-l); the four group sums add as (r0 + r1) + (r2 + r3). Inputs are bf16
+ * weights, fp16 hidden rows at `stride`, bf16 effective scale.
+ * Parity pinned by exact-arithmetic inputs (any order gives the fp64 sum) and
+ * the fp32 error bound on random inputs (tests/test_oracle_router_prefill.py). */
 void tsgo_router_logits_canonical(const uint16_t* w_bf16, const uint16_t* hidden_f16,
                                   int stride, const uint16_t* es_bf16, int rows,
                                   int num_experts, int d, float* out_logits);

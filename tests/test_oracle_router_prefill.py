@@ -114,3 +114,42 @@ def test_reduce_token_major_closed_form(oracle):
     want = np.einsum("tk,tkd->td", wf, Pf)
     got = oracle.f16_to_float(h2)
     assert np.all(np.abs(got - want) <= np.abs(want) * 2.0**-10 + 1e-6)
+
+
+def _bf16(oracle, a):
+    return oracle.bf16_bits(np.asarray(a, np.float32))
+
+
+def test_router_canonical_order_is_exact_on_exact_inputs(oracle):
+    """router_logits_canonical restates the kernels' summation order. On inputs
+    whose products and partial sums are all exactly representable (small
+    integers times powers of two), every order gives the fp64 sum exactly, and
+    a dropped term, a wrong element or a missing effective scale shows up."""
+    rng = np.random.default_rng(5)
+    ne, d, rows, stride = 16, 2816, 3, 2816 + 16
+    w = rng.integers(-8, 8, size=(ne, d)).astype(np.float32) * np.float32(0.25)
+    x = rng.integers(-4, 5, size=(rows, stride)).astype(np.float32) * np.float32(0.5)
+    es = rng.choice([0.5, 1.0, 2.0], size=d).astype(np.float32)
+    got = oracle.router_logits_canonical(_bf16(oracle, w.ravel()), oracle.f16_bits(x.ravel()),
+                                         stride, _bf16(oracle, es), rows, ne, d)
+    want = (x[:, :d].astype(np.float64) * es) @ w.T.astype(np.float64)
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+def test_router_canonical_within_fp32_bound(oracle):
+    rng = oracle.SplitMix64(77)
+    ne, d = 32, 2816
+    w = rng.uniforms_bf16(-0.2, 0.2, ne * d)
+    h = rng.uniforms_f16(-1.0, 1.0, d)
+    es = oracle.bf16_bits(rng.uniforms(0.5, 1.5, d))
+    got = oracle.router_logits_canonical(w, h, d, es, 1, ne, d)[0]
+    wf = oracle.bf16_to_float(w).reshape(ne, d).astype(np.float64)
+    xe = (oracle.f16_to_float(h).astype(np.float32) * oracle.bf16_to_float(es)).astype(np.float64)
+    want = wf @ xe
+    bound = (d + 8) * 2.0 ** -24 * (np.abs(wf) @ np.abs(xe))
+    assert np.all(np.abs(got - want) <= bound)
+    # and it is not the naive sequential order (the restated order matters)
+    seq = np.zeros(ne, np.float32)
+    for i in range(d):
+        seq = (seq + wf[:, i].astype(np.float32) * xe[i].astype(np.float32)).astype(np.float32)
+    assert not np.array_equal(seq, got)

@@ -215,9 +215,9 @@ __device__ __forceinline__ float router_chunks_dot(const uint4* wv, const uint4*
             acc = __builtin_fmaf(w1, x1 * e1, acc);
         }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc += shfl_xor(acc, off);
-    return acc;
+    // 16-lane row sums on DPP, then the four rows in the order (0 + 1) + (2 + 3)
+    acc = group16_sum(acc);
+    return (lane_value(acc, 0) + lane_value(acc, 16)) + (lane_value(acc, 32) + lane_value(acc, 48));
 }
 
 // One router row (loads + canonical sum) on one wave.
@@ -238,9 +238,10 @@ __device__ __forceinline__ float router_dot(const uint16_t* __restrict__ w_row,
 }
 
 // One expert row against up to kRouterRows activation rows in the canonical
-// order (see file comment): lane l sums chunks l, l+64, ... (elements in
-// order, acc = fma(w, x*es, acc)), then a xor butterfly 32, 16, 8, 4, 2, 1.
-// Every lane ends with the full sum. Loads for all chunks are issued before
+// order: lane l sums chunks l, l+64, ... (elements in order, acc = fma(w,
+// x*es, acc)); each 16-lane row then sums as group16_sum does (pairs, pairs of
+// pairs, mirrored quads, mirrored 8s) and the four row sums add as
+// (r0 + r1) + (r2 + r3). Every lane ends with the full sum. Loads for all chunks are issued before
 // any arithmetic; out-of-range chunks load a clamped address and contribute
 // nothing.
 template <bool SELECT>
