@@ -218,7 +218,8 @@ def run_prefill(tsg, torch, ctx, args, layer):
     w = torch.from_numpy(w_np.ravel().view(np.int16)).cuda()
     hidden = torch.empty(t * H, dtype=torch.int16, device="cuda")
     tsg.generators.f16_normal(hidden, 0x33, 1.0)
-    max_blocks = t * k // 64 + E
+    tile_rows = 128  # the grouped GEMM's widest row tile
+    max_blocks = t * k // tile_rows + E
     sp = torch.empty(t * k * 4, dtype=torch.int32, device="cuda")
     off = torch.empty(E, dtype=torch.int32, device="cuda")
     cnt = torch.empty(E, dtype=torch.int32, device="cuda")
@@ -235,7 +236,7 @@ def run_prefill(tsg, torch, ctx, args, layer):
         if record:
             ev[0].record(stream)
         g.group_pairs_device(idx, w, t, k, E, sp, off, cnt, blocks, max_blocks, nb, scratch,
-                             stream=stream)
+                             tile_rows=tile_rows, stream=stream)
         if record:
             ev[1].record(stream)
         g.encode_gate_up(layer, hidden, H, sp, blocks, max_blocks, act, H, F,
@@ -347,6 +348,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the prefill layer (for profiling) and print its figures")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the copy + one-token dispatches for rocprofv3 --pmc and exit")
     args = ap.parse_args()
@@ -364,6 +367,11 @@ def main():
     layers, bufs, routers, offs, stride = make_layers(tsg, ctx, torch, LAYERS)
     if args.traffic_probe:
         traffic_probe(tsg, torch, ctx, layers, routers)
+        return
+    if args.prefill_only:
+        pre = run_prefill(tsg, torch, ctx, args, layers[0])
+        print(json.dumps({"prefill_gemm_us": round(pre["gemm_us"], 2),
+                          "gemm_TFLOPs": round(pre["gemm_tflops"], 2)}), flush=True)
         return
     dec = run_decode(tsg, torch, ctx, args, layers, routers)
     pre = None if args.no_prefill else run_prefill(tsg, torch, ctx, args, layers[0])

@@ -113,22 +113,24 @@ def _zipf_routing(rng, t, ne, k, s):
     return idx, oracle.f16_bits(w).reshape(t, k)
 
 
-@pytest.mark.parametrize("t,ne,k,s", [(2048, 128, 8, 1.1), (301, 256, 8, 1.0), (5, 128, 8, 1.1),
-                                      (64, 16, 4, 0.5)])
-def test_device_grouping_matches_host_sort(tsg, ctx, t, ne, k, s):
+@pytest.mark.parametrize("t,ne,k,s,tile", [(2048, 128, 8, 1.1, 64), (2048, 128, 8, 1.1, 128),
+                                           (301, 256, 8, 1.0, 64), (5, 128, 8, 1.1, 128),
+                                           (64, 16, 4, 0.5, 32)])
+def test_device_grouping_matches_host_sort(tsg, ctx, t, ne, k, s, tile):
     """The on-device counting sort yields exactly groupTokenExpertPairs'
     permutation (PrefillMoEGrouping.swift:141-150), offsets and counts; the
-    block list covers every pair once in <= 64-row slices of one expert."""
+    block list covers every pair once in <= tile-row slices of one expert."""
     rng = np.random.default_rng(t * 7 + ne)
     idx, w = _zipf_routing(rng, t, ne, k, s)
     pairs = oracle.make_token_expert_pairs(idx, w, t, k)
     want = oracle.group_pairs(pairs, t, k, ne)
     g = tsg.PrefillGroupedRoutedMoE(tsg.MoE(ctx))
-    max_blocks = t * k // 64 + ne + 1
+    max_blocks = t * k // tile + ne + 1
     sp, off, cnt = empty(t * k * 4, np.uint32), empty(ne, np.uint32), empty(ne, np.uint32)
     blocks, nb = empty(max_blocks * 4, np.uint32), empty(1, np.uint32)
     scratch = empty(g.scratch_bytes(t, k, ne) // 4 + 1, np.uint32)
-    g.group_pairs_device(dev(idx), dev(w), t, k, ne, sp, off, cnt, blocks, max_blocks, nb, scratch)
+    g.group_pairs_device(dev(idx), dev(w), t, k, ne, sp, off, cnt, blocks, max_blocks, nb, scratch,
+                         tile_rows=tile)
     got = host(sp, np.uint32).view(oracle.PAIR_DTYPE)
     assert np.array_equal(got, want["sorted_pairs"])
     assert np.array_equal(host(off, np.uint32), want["offsets"])
@@ -137,7 +139,7 @@ def test_device_grouping_matches_host_sort(tsg, ctx, t, ne, k, s):
     bl = host(blocks, np.uint32).view(oracle.BLOCK_DTYPE)[:n]
     covered = np.zeros(t * k, np.int32)
     for b in bl:
-        assert 1 <= b["row_count"] <= 64 and b["local_row"] == b["pair_start"]
+        assert 1 <= b["row_count"] <= tile and b["local_row"] == b["pair_start"]
         sl = got[b["pair_start"]:b["pair_start"] + b["row_count"]]
         assert np.all(sl["expert"] == b["local_slot"])
         covered[b["pair_start"]:b["pair_start"] + b["row_count"]] += 1
@@ -192,10 +194,12 @@ def test_reduce_token_major_bit_exact(tsg, ctx):
     assert np.array_equal(host(h2, np.uint16), oracle.reduce_token_major(P, w, t, k, d).ravel())
 
 
-def test_prefill_pipeline_zipf_end_to_end(tsg, ctx):
+@pytest.mark.parametrize("tile", [64, 128])
+def test_prefill_pipeline_zipf_end_to_end(tsg, ctx, tile):
     """A Gemma-shaped prefill chunk (T=256, top-8, Zipf(1.1) over 128 experts):
     device grouping -> gate/up -> down -> token-major reduce, against the
-    oracle's grouping + expert-major reference + reduce."""
+    oracle's grouping + expert-major reference + reduce; GEMM blocks of the
+    reference's 64 rows and of the kernel's widest 128."""
     configure(ctx, 32, "sym")
     t, ne, k, d, f = 256, 128, 8, 2816, 704
     rng = np.random.default_rng(11)
@@ -208,11 +212,12 @@ def test_prefill_pipeline_zipf_end_to_end(tsg, ctx):
     hidden = orng.uniforms_f16(-1, 1, t * d)
     moe = tsg.MoE(ctx)
     g = tsg.PrefillGroupedRoutedMoE(moe)
-    max_blocks = t * k // 64 + ne
+    max_blocks = t * k // tile + ne
     sp, off, cnt = empty(t * k * 4, np.uint32), empty(ne, np.uint32), empty(ne, np.uint32)
     blocks, nb = empty(max_blocks * 4, np.uint32), empty(1, np.uint32)
     scratch = empty(g.scratch_bytes(t, k, ne) // 4 + 1, np.uint32)
-    g.group_pairs_device(dev(idx), dev(w), t, k, ne, sp, off, cnt, blocks, max_blocks, nb, scratch)
+    g.group_pairs_device(dev(idx), dev(w), t, k, ne, sp, off, cnt, blocks, max_blocks, nb, scratch,
+                         tile_rows=tile)
     act, partials, h2 = empty(t * k * f), empty(t * k * d), empty(t * d)
     H = dev(hidden)
     g.encode_gate_up(layer, H, d, sp, blocks, max_blocks, act, d, f, n_blocks_device=nb)

@@ -119,76 +119,177 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(
 
 // ------------------------------------------------------- fp16 dequant
 
-// Sixteen weights (two packed u32, elements 0..15 of a K run) -> eight fp16
-// pairs in paired order per 8-element half: out[0..3] from w0, out[4..7] from
-// w1. Each value is RNE(fma(q, s, b)) with b = -8 s under sym
-// (prefill.metal:1021-1026). The fp16 FMA is exact-then-round-once, so when s
-// and -8 s are exact in fp16 it reproduces half(fp32 fma) bit for bit; any
-// other group (tiny scales, and every affine group, whose bias would be
-// rounded twice) takes the fp32 route.
+typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
+
+// Per (weight row, 32-element run) dequantisation parameters. Every weight is
+// staged as RNE(fma(q, s, b)) with b = -8 s under sym (prefill.metal:1021-1026).
+// Fast route (sym, when 16 s and -24 s are exact in fp16): the nibble OR'ed
+// into mantissa bits 6..9 of 1.0 is the fp16 value 1 + q/16, and
+// fma(1 + q/16, 16 s, -24 s) = (q - 8) s is computed exactly and rounded
+// once, so it equals the fp32 route bit for bit. Otherwise (tiny or huge
+// scales, every affine group): fp32 fma, then one rounding to fp16.
+struct GroupScale {
+    h2_t S, C;
+    float s, b;
+    bool fast;
+};
+
 template <bool SYM>
-__device__ __forceinline__ void dequant16_f16(uint32_t w0, uint32_t w1, float s, float b,
-                                              h2_t out[8]) {
-    const h2_t k1024 = h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
-    h2_t q[8];
-    nib8_to_pairs(w0, k1024, q);
-    nib8_to_pairs(w1, k1024, q + 4);
-    bool fast = false;
-    _Float16 sh = (_Float16)s, bh = (_Float16)b;
-    if constexpr (SYM) fast = ((float)sh == s) && ((float)bh == b);
-    if (fast) {
-        const h2_t s2 = h2_t{sh, sh}, b2 = h2_t{bh, bh};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = __builtin_elementwise_fma(q[i], s2, b2);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float lo = __builtin_fmaf((float)q[i].x, s, b);
-            const float hi = __builtin_fmaf((float)q[i].y, s, b);
-            out[i] = h2_t{(_Float16)lo, (_Float16)hi};
-        }
-    }
+__device__ __forceinline__ GroupScale group_scale(uint16_t s_bits, uint16_t b_bits) {
+    GroupScale g;
+    g.s = bf16_to_f32(s_bits);
+    g.b = SYM ? -8.0f * g.s : bf16_to_f32(b_bits);
+    const float s16 = 16.0f * g.s, c24 = -24.0f * g.s;  // exact in fp32
+    const _Float16 sh = (_Float16)s16, ch = (_Float16)c24;
+    g.fast = SYM && (float)sh == s16 && (float)ch == c24;
+    g.S = h2_t{sh, sh};
+    g.C = h2_t{ch, ch};
+    return g;
 }
 
-// Un-paired debug dump of the same staging (tsg_debug_dequant_f16's twin for
-// the GEMM path): out[k] for the 16 weights of (w0, w1).
+// Eight weights (one packed u32, elements 0..7 of a K run), in element order.
+// Fast route per byte j (elements 2j, 2j+1): v_perm copies the byte into both
+// halves, a packed shift moves the low nibble to bits 6..9 of the low half and
+// the high nibble to bits 6..9 of the high half, and one packed fma turns
+// 1 + q/16 into (q - 8) s. `one` = 0x3C003C00 held in a VGPR lets the mask and
+// the OR fold into one v_and_or_b32.
+typedef unsigned short us2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h8v_t dequant8(uint32_t w, const GroupScale& g, uint32_t one) {
+    h2_t p[4];
+    if (g.fast) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t x = __builtin_amdgcn_perm(w, w, 0x0C000C00u | ((uint32_t)j << 16) | (uint32_t)j);
+            const us2_t y = __builtin_bit_cast(us2_t, x) << (us2_t){6, 2};
+            const uint32_t z = (__builtin_bit_cast(uint32_t, y) & 0x03C003C0u) | one;
+            p[j] = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, z), g.S, g.C);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float lo = (float)((w >> (8 * j)) & 0xFu);
+            const float hi = (float)((w >> (8 * j + 4)) & 0xFu);
+            p[j] = h2_t{(_Float16)__builtin_fmaf(lo, g.s, g.b), (_Float16)__builtin_fmaf(hi, g.s, g.b)};
+        }
+    }
+    return h8v_t{p[0].x, p[0].y, p[1].x, p[1].y, p[2].x, p[2].y, p[3].x, p[3].y};
+}
+
+__device__ __forceinline__ uint32_t vgpr_one() {
+    uint32_t one = 0x3C003C00u;
+    asm volatile("" : "+v"(one));
+    return one;
+}
+
+// Dump of the GEMM's staging (tsg_debug_gemm_dequant_f16): one thread per 8
+// weights. The eight values leave as one 16-byte vector: extracting them one
+// by one into 16-bit stores made this hipcc fold all eight to the first.
 template <int G, bool SYM>
 __global__ void gemm_dequant_probe_kernel(const uint8_t* __restrict__ w,
                                           const uint16_t* __restrict__ scales,
                                           const uint16_t* __restrict__ biases,
                                           uint16_t* __restrict__ out, uint32_t rows,
                                           uint32_t n) {
-    const uint64_t pieces = (uint64_t)rows * (n / 16u);
+    const uint32_t one = vgpr_one();
+    const uint64_t pieces = (uint64_t)rows * (n / 8u);
     for (uint64_t p = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; p < pieces;
          p += (uint64_t)gridDim.x * blockDim.x) {
-        const uint64_t r = p / (n / 16u);
-        const uint32_t k0 = (uint32_t)(p - r * (n / 16u)) * 16u;
-        const uint2 v = *reinterpret_cast<const uint2*>(w + r * (n / 2u) + k0 / 2u);
+        const uint64_t r = p / (n / 8u);
+        const uint32_t k0 = (uint32_t)(p - r * (n / 8u)) * 8u;
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(w + r * (n / 2u) + k0 / 2u);
         const uint32_t g = k0 / G;
-        const float s = bf16_to_f32(scales[r * (n / G) + g]);
-        const float b = SYM ? -8.0f * s : bf16_to_f32(biases[r * (n / G) + g]);
-        h2_t o[8];
-        dequant16_f16<SYM>(v.x, v.y, s, b, o);
-        for (int half = 0; half < 2; ++half)
-            for (int kk = 0; kk < 8; ++kk) {
-                const h2_t pr = o[half * 4 + (kk & 3)];
-                const _Float16 val = (kk >> 2) ? pr.y : pr.x;
-                out[r * n + k0 + half * 8 + kk] = __builtin_bit_cast(uint16_t, val);
-            }
+        const GroupScale gs = group_scale<SYM>(scales[r * (n / G) + g],
+                                               SYM ? (uint16_t)0 : biases[r * (n / G) + g]);
+        *reinterpret_cast<uint4*>(out + r * n + k0) = __builtin_bit_cast(uint4, dequant8(v, gs, one));
     }
 }
 
 // --------------------------------------------------------------- GEMM
 
-constexpr uint32_t kTM = 64;    // rows per routed block
-constexpr uint32_t kTN = 128;   // weight rows per block
-constexpr uint32_t kTK = 32;    // K per step
-constexpr uint32_t kLdsStride = kTK + 8;  // halves; pads rows off the same banks
+// Grouped int4 GEMM over routed blocks of up to kGemmRows rows of one expert.
+// Block = 4 waves; each wave owns 64 weight rows as two 32-row MFMA tiles
+// (gate/up: 32 gate + the same 32 up rows; down: 64 output rows) and every
+// live 32-row slice of the block's activation rows. K runs in 64-element
+// chunks through a kGemmStages-deep LDS ring filled by direct global->LDS
+// loads issued two chunks ahead, each stage holding
+//  - the activation tile: row r's 16-byte piece p in slot p ^ (r & 7) of the
+//    row, so the MFMA reads hit distinct banks;
+//  - the packed int4 weights, 1 KiB per (wave, tile): lane (n, h) of the wave
+//    brings the 16 bytes of weight row n holding K [64c + 32h, 64c + 32h + 32)
+//    and reads them back itself;
+//  - per (wave, tile) 256 bytes: the dword holding each lane's group scale
+//    (and, affine, bias).
+// Word s of a lane's 16 weight bytes is dequantised into the B operand of
+// MFMA step s, whose logical K 8h..8h+7 is physical 64c + 32h + 8s + (0..7);
+// the activations are read with the same mapping. Nothing is carried in
+// registers across chunks but the accumulators.
+constexpr uint32_t kGemmRows = 128;
+constexpr uint32_t kGemmKC = 64;
+constexpr uint32_t kGemmStages = 3;
+constexpr uint32_t kGemmAStage = kGemmRows * kGemmKC * 2u;   // 16 KiB
+constexpr uint32_t kGemmBStage = 4u * 2u * 1024u;            // 8 KiB
+constexpr uint32_t kGemmSStage = 4u * 2u * 256u;             // 2 KiB
+__host__ __device__ constexpr uint32_t gemm_stage_bytes(bool sym) {
+    return kGemmAStage + kGemmBStage + kGemmSStage * (sym ? 1u : 2u);
+}
+// sym: 78 KiB, two blocks per CU
+__host__ __device__ constexpr uint32_t gemm_lds_bytes(bool sym) {
+    return kGemmStages * gemm_stage_bytes(sym);
+}
 
-typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
+// LDS reads as inline ds_read_b128: the compiler cannot tell them from the
+// direct-to-LDS writes of other stages and would drain every outstanding load
+// before each one. lds_wait() waits for them; its operands tie the fragments
+// to the wait so no use is scheduled before it.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+__device__ __forceinline__ u32x4_t lds_read16(uint32_t addr) {
+    u32x4_t v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ void lds_wait(u32x4_t& a0, u32x4_t& a1, u32x4_t& a2, u32x4_t& a3) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3));
+}
+__device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ void lds_wait(u32x4_t& a0, u32x4_t& a1, uint32_t& s0, uint32_t& s1,
+                                         uint32_t& b0, uint32_t& b1) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a0), "+v"(a1), "+v"(s0), "+v"(s1), "+v"(b0), "+v"(b1));
+}
 
-__device__ __forceinline__ h8v_t lds_h8(const uint16_t* p) {
-    return __builtin_bit_cast(h8v_t, *reinterpret_cast<const uint4*>(p));
+// Wait until at most N of this wave's vector memory loads are outstanding
+// (loads complete in issue order); also a compiler barrier.
+template <uint32_t N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the memory fence of __syncthreads(), whose release
+// would wait for every outstanding load (the prefetches included). The
+// explicit vmcnt waits order the direct-to-LDS data; the asm statements keep
+// the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void block_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds_wave_base,
+                                     16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void* src, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds_wave_base,
+                                     4, 0, 0);
 }
 
 struct GemmArgs {
@@ -207,123 +308,176 @@ struct GemmArgs {
 
 // MODE 0: gate/up + activation; MODE 1: down + scatter.
 template <int G, bool SYM, int ACT, int MODE>
-__global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs args) {
-    __shared__ __align__(16) uint16_t As[kTM * kLdsStride];
-    __shared__ __align__(16) uint16_t Bs[kTN * kLdsStride];
-    __shared__ uint32_t row_src[kTM];
-    __shared__ uint32_t row_dst[kTM];
+__global__ __launch_bounds__(256, 2) void moe_gemm_kernel(GemmArgs args) {
+    extern __shared__ __align__(16) uint8_t smem[];  // gemm_lds_bytes(SYM)
 
     const uint32_t nb = args.n_blocks_device ? *args.n_blocks_device : args.n_blocks;
     if (blockIdx.y >= nb) return;
     const tsg_routed_block blk = args.blocks[blockIdx.y];
-    const uint32_t tid = threadIdx.x;
-    const uint32_t K = MODE == 0 ? args.d : args.f;       // reduction length
-    const uint32_t N = MODE == 0 ? args.f : args.d;       // output columns
+    const uint32_t rows = blk.row_count < kGemmRows ? blk.row_count : kGemmRows;
+    if (rows == 0) return;
+    const uint32_t n_mt = (rows + 31u) / 32u;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, h = lane >> 5;
+    const uint32_t K = MODE == 0 ? args.d : args.f;
     const uint8_t* blob = args.layer_base + (uint64_t)blk.local_slot * args.expert_stride;
 
-    if (tid < kTM) {
-        uint32_t src = 0, dst = 0;
-        if (tid < blk.row_count) {
-            const tsg_token_expert_pair pr = args.pairs[blk.pair_start + tid];
-            if (MODE == 0) {
-                src = pr.token * args.a_stride;
-                dst = (blk.local_row + tid) * args.f;
-            } else {
-                src = (blk.local_row + tid) * args.a_stride;
-                dst = (pr.token * args.top_k + pr.rank) * args.d;
+    // source row (element offset into args.a) and destination row of block
+    // row r; rows past the block use row 0's (their results are dropped)
+    auto src_row = [&](uint32_t r) -> uint32_t {
+        r = r < rows ? r : 0u;
+        if (MODE == 0) return args.pairs[blk.pair_start + r].token * args.a_stride;
+        return (blk.local_row + r) * args.a_stride;
+    };
+    auto dst_row = [&](uint32_t r) -> uint32_t {
+        if (MODE == 0) return (blk.local_row + r) * args.f;
+        const tsg_token_expert_pair pr = args.pairs[blk.pair_start + r];
+        return (pr.token * args.top_k + pr.rank) * args.d;
+    };
+
+    // this lane's two weight rows, as byte offsets into the expert blob
+    uint32_t n0, n1;
+    bool live0, live1;
+    uint32_t ow0, ow1, os0, os1, ob0, ob1;
+    const uint32_t ngroups = K / G;
+    if (MODE == 0) {
+        n0 = n1 = (blockIdx.x * 4u + wave) * 32u + (lane & 31u);
+        live0 = live1 = n0 < args.f;
+        const uint32_t r = live0 ? n0 : 0u;
+        ow0 = args.o.gate_w + r * (K / 2u);
+        ow1 = args.o.up_w + r * (K / 2u);
+        os0 = args.o.gate_s + r * ngroups * 2u;
+        os1 = args.o.up_s + r * ngroups * 2u;
+        ob0 = args.o.gate_b + r * ngroups * 2u;
+        ob1 = args.o.up_b + r * ngroups * 2u;
+    } else {
+        n0 = (blockIdx.x * 4u + wave) * 64u + (lane & 31u);
+        n1 = n0 + 32u;
+        live0 = n0 < args.d;
+        live1 = n1 < args.d;
+        const uint32_t r0 = live0 ? n0 : 0u, r1 = live1 ? n1 : 0u;
+        ow0 = args.o.down_w + r0 * (K / 2u);
+        ow1 = args.o.down_w + r1 * (K / 2u);
+        os0 = args.o.down_s + r0 * ngroups * 2u;
+        os1 = args.o.down_s + r1 * ngroups * 2u;
+        ob0 = args.o.down_b + r0 * ngroups * 2u;
+        ob1 = args.o.down_b + r1 * ngroups * 2u;
+    }
+    const uint32_t nchunks = K / kGemmKC;
+    constexpr uint32_t kStage = gemm_stage_bytes(SYM);
+
+    // activation DMA: wave w moves rows [32w, 32w + 32) (4 instructions of 8
+    // rows x 128 B); lane l carries row 8j + l/8, piece (l % 8) ^ (l / 8).
+    const bool a_wave = wave < n_mt;
+    uint32_t a_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t row = 32u * wave + 8u * i + (lane >> 3);
+        const uint32_t piece = (lane & 7u) ^ (lane >> 3);
+        a_off[i] = src_row(row) + piece * 8u;
+    }
+    // Chunk c into stage c % 3. Every chunk issues the same loads (chunks past
+    // the end re-read the last one into a stage no later chunk uses), so the
+    // vmcnt waits stay exact: A (4 if a_wave), weights (2), scale dwords (2),
+    // bias dwords (2, affine).
+    auto issue = [&](uint32_t c) {
+        const uint32_t cc = c < nchunks ? c : nchunks - 1u;
+        uint8_t* stage = smem + (c % kGemmStages) * kStage;
+        if (a_wave) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                lds_dma16(args.a + a_off[i] + cc * kGemmKC, stage + (32u * wave + 8u * i) * kGemmKC * 2u);
+        }
+        uint8_t* bst = stage + kGemmAStage + wave * 2048u;
+        const uint32_t byte = cc * (kGemmKC / 2u) + h * 16u;
+        lds_dma16(blob + ow0 + byte, bst);
+        lds_dma16(blob + ow1 + byte, bst + 1024u);
+        const uint32_t g2 = ((cc * kGemmKC + h * 32u) / G) * 2u;
+        uint8_t* sst = stage + kGemmAStage + kGemmBStage + wave * 512u;
+        lds_dma4(blob + ((os0 + g2) & ~3u), sst);
+        lds_dma4(blob + ((os1 + g2) & ~3u), sst + 256u);
+        if constexpr (!SYM) {
+            lds_dma4(blob + ((ob0 + g2) & ~3u), sst + kGemmSStage);
+            lds_dma4(blob + ((ob1 + g2) & ~3u), sst + kGemmSStage + 256u);
+        }
+    };
+
+    const uint32_t one = vgpr_one();
+    f16v_t acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i][0] = acc[i][1] = f16v_t{};
+
+    constexpr uint32_t kNW = SYM ? 4u : 6u;  // weight + scale (+ bias) loads per chunk
+    issue(0);
+    issue(1);
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        // chunk c landed (chunk c + 1's loads may still be in flight); after
+        // the barrier every wave is done with stage (c - 1) % 3 = (c + 2) % 3
+        if (a_wave) wait_vmcnt<4u + kNW>();
+        else wait_vmcnt<kNW>();
+        block_barrier();
+        const uint8_t* stage = smem + (c % kGemmStages) * kStage;
+        const uint32_t m = lane & 31u;
+        const uint32_t bbase = lds_addr(stage + kGemmAStage + wave * 2048u) + lane * 16u;
+        const uint32_t sbase = lds_addr(stage + kGemmAStage + kGemmBStage + wave * 512u) + lane * 4u;
+        u32x4_t bw0 = lds_read16(bbase), bw1 = lds_read16(bbase + 1024u);
+        uint32_t sw0 = lds_read4(sbase), sw1 = lds_read4(sbase + 256u);
+        uint32_t bb0 = 0u, bb1 = 0u;
+        if constexpr (!SYM) {
+            bb0 = lds_read4(sbase + kGemmSStage);
+            bb1 = lds_read4(sbase + kGemmSStage + 256u);
+        }
+        lds_wait(bw0, bw1, sw0, sw1, bb0, bb1);
+        // the 16-bit value inside each loaded dword
+        const uint32_t g2 = ((c * kGemmKC + h * 32u) / G) * 2u;
+        const uint32_t sh0 = ((os0 + g2) & 2u) * 8u, sh1 = ((os1 + g2) & 2u) * 8u;
+        const uint32_t bh0 = ((ob0 + g2) & 2u) * 8u, bh1 = ((ob1 + g2) & 2u) * 8u;
+        const GroupScale g0 = group_scale<SYM>((uint16_t)(sw0 >> sh0), (uint16_t)(bb0 >> bh0));
+        const GroupScale g1 = group_scale<SYM>((uint16_t)(sw1 >> sh1), (uint16_t)(bb1 >> bh1));
+        const uint32_t row_addr = lds_addr(stage) + m * kGemmKC * 2u;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const uint32_t at = row_addr + (((h * 4u + (uint32_t)st) ^ (m & 7u)) * 16u);
+            // all four slices are read (rows past the block hold stale data
+            // and feed no MFMA): a conditional read would let the compiler
+            // copy a register the read has not filled yet
+            u32x4_t af[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = lds_read16(at + i * 32u * kGemmKC * 2u);
+            const h8v_t bf0 = dequant8(bw0[st], g0, one);
+            const h8v_t bf1 = dequant8(bw1[st], g1, one);
+            lds_wait(af[0], af[1], af[2], af[3]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if ((uint32_t)i < n_mt) {
+                    const h8v_t a8 = __builtin_bit_cast(h8v_t, af[i]);
+                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, bf0, acc[i][0], 0, 0, 0);
+                    acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, bf1, acc[i][1], 0, 0, 0);
+                }
             }
         }
-        row_src[tid] = src;
-        row_dst[tid] = dst;
+        issue(c + 2u);
     }
+    wait_vmcnt<0>();  // no LDS write may land after the block ends
 
-    // Weight rows this thread dequantises: 128 rows x 2 halves of 16 weights.
-    const uint32_t wrow = tid >> 1, whalf = tid & 1u;
-    uint32_t n_w;
-    const uint8_t* wbase;
-    const uint16_t* sbase;
-    const uint16_t* bbase;
-    if (MODE == 0) {
-        const bool up = wrow >= 64u;
-        n_w = blockIdx.x * 64u + (wrow & 63u);
-        wbase = blob + (up ? args.o.up_w : args.o.gate_w);
-        sbase = reinterpret_cast<const uint16_t*>(blob + (up ? args.o.up_s : args.o.gate_s));
-        bbase = reinterpret_cast<const uint16_t*>(blob + (up ? args.o.up_b : args.o.gate_b));
-    } else {
-        n_w = blockIdx.x * kTN + wrow;
-        wbase = blob + args.o.down_w;
-        sbase = reinterpret_cast<const uint16_t*>(blob + args.o.down_s);
-        bbase = reinterpret_cast<const uint16_t*>(blob + args.o.down_b);
-    }
-    const bool w_live = n_w < N;
-    const uint32_t ngroups = K / G;
-    const uint8_t* wrow_p = wbase + (uint64_t)(w_live ? n_w : 0u) * (K / 2u);
-    const uint16_t* srow_p = sbase + (uint64_t)(w_live ? n_w : 0u) * ngroups;
-    const uint16_t* brow_p = bbase + (uint64_t)(w_live ? n_w : 0u) * ngroups;
-
-    // Activation piece this thread gathers: row tid/4, 8 halves at (tid%4)*8.
-    const uint32_t arow = tid >> 2, apiece = tid & 3u;
-    __syncthreads();
-    const bool a_live = arow < blk.row_count;
-    const uint16_t* a_p = args.a + row_src[arow] + apiece * 8u;
-
-    const uint32_t lane = tid & 63u, wave = tid >> 6;
-    const uint32_t wm = wave >> 1, wn = wave & 1u;
-    f16v_t acc0 = {}, acc1 = {};
-    // B rows for this wave's two 32-column accumulators.
-    const uint32_t b0 = MODE == 0 ? wn * 32u : wn * 64u;
-    const uint32_t b1 = MODE == 0 ? 64u + wn * 32u : wn * 64u + 32u;
-
-    for (uint32_t k0 = 0; k0 < K; k0 += kTK) {
-        uint4 av = make_uint4(0, 0, 0, 0);
-        if (a_live) av = *reinterpret_cast<const uint4*>(a_p + k0);
-        uint2 wv = make_uint2(0, 0);
-        uint16_t sv = 0, bv = 0;
-        const uint32_t kk = k0 + whalf * 16u;
-        if (w_live) {
-            wv = *reinterpret_cast<const uint2*>(wrow_p + kk / 2u);
-            sv = srow_p[kk / G];
-            if constexpr (!SYM) bv = brow_p[kk / G];
-        }
-        *reinterpret_cast<uint4*>(&As[arow * kLdsStride + apiece * 8u]) = pair_permute(av);
-        {
-            const float s = bf16_to_f32(sv);
-            const float b = SYM ? -8.0f * s : bf16_to_f32(bv);
-            h2_t o[8];
-            dequant16_f16<SYM>(wv.x, wv.y, s, b, o);
-            uint16_t* dst = &Bs[wrow * kLdsStride + whalf * 16u];
-            *reinterpret_cast<uint4*>(dst) = __builtin_bit_cast(uint4, (h8v_t){o[0].x, o[0].y, o[1].x, o[1].y, o[2].x, o[2].y, o[3].x, o[3].y});
-            *reinterpret_cast<uint4*>(dst + 8) = __builtin_bit_cast(uint4, (h8v_t){o[4].x, o[4].y, o[5].x, o[5].y, o[6].x, o[6].y, o[7].x, o[7].y});
-        }
-        __syncthreads();
+    // acc[i][t][v] of lane l: row 32 i + 8 (v / 4) + 4 h + v % 4 of the block,
+    // weight row n_t (column l % 32 of tile t).
 #pragma unroll
-        for (uint32_t ks = 0; ks < kTK; ks += 16u) {
-            const uint32_t kof = ks + 8u * (lane >> 5);
-            const h8v_t a = lds_h8(&As[(wm * 32u + (lane & 31u)) * kLdsStride + kof]);
-            const h8v_t bb0 = lds_h8(&Bs[(b0 + (lane & 31u)) * kLdsStride + kof]);
-            const h8v_t bb1 = lds_h8(&Bs[(b1 + (lane & 31u)) * kLdsStride + kof]);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bb0, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bb1, acc1, 0, 0, 0);
-        }
-        __syncthreads();
-    }
-
-    // acc[v] of lane l holds row 8*(v/4) + 4*(l/32) + v%4, column l%32.
-    const uint32_t col = lane & 31u;
+    for (int i = 0; i < 4; ++i) {
+        if ((uint32_t)i >= n_mt) continue;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const uint32_t m = wm * 32u + 8u * (v >> 2) + 4u * (lane >> 5) + (v & 3);
-        if (m >= blk.row_count) continue;
-        if (MODE == 0) {
-            const uint32_t fcol = blockIdx.x * 64u + wn * 32u + col;
-            if (fcol >= args.f) continue;
-            const float g = f16_to_f32(f32_to_f16(acc0[v]));
-            const float u = f16_to_f32(f32_to_f16(acc1[v]));
-            args.out[row_dst[m] + fcol] = f32_to_f16(gate_activation<ACT>(g) * u);
-        } else {
-            const uint32_t dcol0 = blockIdx.x * kTN + wn * 64u + col;
-            if (dcol0 < args.d) args.out[row_dst[m] + dcol0] = f32_to_f16(acc0[v]);
-            if (dcol0 + 32u < args.d) args.out[row_dst[m] + dcol0 + 32u] = f32_to_f16(acc1[v]);
+        for (int v = 0; v < 16; ++v) {
+            const uint32_t mm = 32u * i + 8u * (v >> 2) + 4u * h + (v & 3);
+            if (mm >= rows) continue;
+            const uint32_t dst = dst_row(mm);
+            if (MODE == 0) {
+                if (!live0) continue;
+                const float gt = f16_to_f32(f32_to_f16(acc[i][0][v]));
+                const float up = f16_to_f32(f32_to_f16(acc[i][1][v]));
+                args.out[dst + n0] = f32_to_f16(gate_activation<ACT>(gt) * up);
+            } else {
+                if (live0) args.out[dst + n0] = f32_to_f16(acc[i][0][v]);
+                if (live1) args.out[dst + n1] = f32_to_f16(acc[i][1][v]);
+            }
         }
     }
 }
@@ -464,12 +618,15 @@ tsg_status check_layer_moe(const tsg_moe* moe, const tsg_layer* layer) {
 
 template <int G, bool SYM, int MODE>
 tsg_status launch_gemm(const tsg_moe* moe, hipStream_t s, const GemmArgs& a, uint32_t max_blocks) {
-    const uint32_t ntiles = MODE == 0 ? (a.f + 63u) / 64u : (a.d + kTN - 1u) / kTN;
+    const uint32_t ntiles = MODE == 0 ? (a.f + 127u) / 128u : (a.d + 255u) / 256u;
     const dim3 grid(ntiles, max_blocks);
-    if (moe->activation == TSG_ACT_SILU)
-        hipLaunchKernelGGL((moe_gemm_kernel<G, SYM, TSG_ACT_SILU, MODE>), grid, dim3(256), 0, s, a);
-    else
-        hipLaunchKernelGGL((moe_gemm_kernel<G, SYM, TSG_ACT_GELU_TANH, MODE>), grid, dim3(256), 0, s, a);
+    auto kern = moe->activation == TSG_ACT_SILU ? moe_gemm_kernel<G, SYM, TSG_ACT_SILU, MODE>
+                                                : moe_gemm_kernel<G, SYM, TSG_ACT_GELU_TANH, MODE>;
+    // more than 64 KiB of dynamic LDS must be allowed per kernel (idempotent)
+    TSG_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)gemm_lds_bytes(SYM)));
+    hipLaunchKernelGGL(kern, grid, dim3(256), gemm_lds_bytes(SYM), s, a);
     return check_launch(MODE == 0 ? "moe_gemm gate/up" : "moe_gemm down");
 }
 
@@ -494,6 +651,8 @@ tsg_status fill_gemm_args(const tsg_moe* moe, const tsg_layer* layer, GemmArgs* 
     TSG_REQUIRE(d > 0 && f > 0 && d % ctx->group_size == 0 && f % ctx->group_size == 0,
                 TSG_ERR_INVALID_ARGUMENT, "d=%u, f=%u must be multiples of the group size %u",
                 d, f, ctx->group_size);
+    TSG_REQUIRE(d % kGemmKC == 0 && f % kGemmKC == 0, TSG_ERR_UNSUPPORTED,
+                "the grouped GEMM needs d=%u and f=%u to be multiples of %u", d, f, kGemmKC);
     TSG_REQUIRE(aligned16(act_in) && a_stride % 8 == 0, TSG_ERR_ALIGNMENT,
                 "activation rows must be 16-byte aligned");
     *a = GemmArgs{};
@@ -533,8 +692,8 @@ extern "C" tsg_status tsg_prefill_group_pairs_device(
     TSG_REQUIRE(k > 0, TSG_ERR_GROUPING_INVALID_TOP_K, "topK must be positive");
     TSG_REQUIRE(ne > 0 && ne <= kMaxExperts, TSG_ERR_GROUPING_INVALID_NUM_EXPERTS,
                 "numExperts %u not in 1..%u", ne, kMaxExperts);
-    TSG_REQUIRE(tile_rows == 32 || tile_rows == 64, TSG_ERR_INVALID_ARGUMENT,
-                "tile_rows must be 32 or 64, got %u", tile_rows);
+    TSG_REQUIRE(tile_rows == 32 || tile_rows == 64 || tile_rows == 128, TSG_ERR_INVALID_ARGUMENT,
+                "tile_rows must be 32, 64 or 128, got %u", tile_rows);
     TSG_REQUIRE(idx && w && sorted && offsets && counts && blocks && n_blocks && scratch,
                 TSG_ERR_INVALID_ARGUMENT, "NULL grouping operand");
     hipStream_t s = as_stream(stream);
@@ -674,9 +833,9 @@ extern "C" tsg_status tsg_debug_gemm_dequant_f16(tsg_ctx* ctx, tsg_stream stream
                 "biases is NULL under the affine scheme");
     TSG_REQUIRE(n % ctx->group_size == 0 && n % 16 == 0 && rows > 0, TSG_ERR_INVALID_ARGUMENT,
                 "bad shape rows=%u n=%u", rows, n);
-    TSG_REQUIRE(reinterpret_cast<uintptr_t>(w) % 8 == 0, TSG_ERR_ALIGNMENT,
-                "weights must be 8-byte aligned");
-    const uint64_t pieces = (uint64_t)rows * (n / 16u);
+    TSG_REQUIRE(reinterpret_cast<uintptr_t>(w) % 4 == 0 && aligned16(out), TSG_ERR_ALIGNMENT,
+                "weights must be 4-byte and out 16-byte aligned");
+    const uint64_t pieces = (uint64_t)rows * (n / 8u);
     uint64_t grid = (pieces + 255) / 256;
     if (grid > 65536) grid = 65536;
     hipStream_t s = as_stream(stream);
