@@ -121,65 +121,46 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(
 
 typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
 
-// Per (weight row, 32-element run) dequantisation parameters. Every weight is
-// staged as RNE(fma(q, s, b)) with b = -8 s under sym (prefill.metal:1021-1026).
-// Fast route (sym, when 16 s and -24 s are exact in fp16): the nibble OR'ed
-// into mantissa bits 6..9 of 1.0 is the fp16 value 1 + q/16, and
-// fma(1 + q/16, 16 s, -24 s) = (q - 8) s is computed exactly and rounded
-// once, so it equals the fp32 route bit for bit. Otherwise (tiny or huge
-// scales, every affine group): fp32 fma, then one rounding to fp16.
+// Per (weight row, group) dequantisation parameters. Every weight is staged
+// as RNE_f16(fmaf(q, s, b)) with b = -8 s under sym (prefill.metal:1021-1026).
+// The nibble q is isolated inside a 16-bit half, where as an fp16 bit pattern
+// it is the subnormal q * 2^-24 (bits 0..3) or q * 2^-20 (bits 4..7); the
+// scale is pre-multiplied by 2^24 or 2^20, so v_fma_mix computes the exact
+// product q * s, adds b with fmaf's single fp32 rounding and rounds once to
+// fp16: the reference's arithmetic bit for bit (for |s| < 2^103, where s * 2^24
+// stays finite), with no per-group test.
 struct GroupScale {
-    h2_t S, C;
-    float s, b;
-    bool fast;
+    float s_lo, s_hi, b;  // s * 2^24, s * 2^20, b
 };
 
 template <bool SYM>
 __device__ __forceinline__ GroupScale group_scale(uint16_t s_bits, uint16_t b_bits) {
+    const float s = bf16_to_f32(s_bits);
     GroupScale g;
-    g.s = bf16_to_f32(s_bits);
-    g.b = SYM ? -8.0f * g.s : bf16_to_f32(b_bits);
-    const float s16 = 16.0f * g.s, c24 = -24.0f * g.s;  // exact in fp32
-    const _Float16 sh = (_Float16)s16, ch = (_Float16)c24;
-    g.fast = SYM && (float)sh == s16 && (float)ch == c24;
-    g.S = h2_t{sh, sh};
-    g.C = h2_t{ch, ch};
+    g.s_lo = s * 16777216.0f;
+    g.s_hi = s * 1048576.0f;
+    g.b = SYM ? -8.0f * s : bf16_to_f32(b_bits);
     return g;
 }
 
-// Eight weights (one packed u32, elements 0..7 of a K run), in element order.
-// Fast route per byte j (elements 2j, 2j+1): v_perm copies the byte into both
-// halves, a packed shift moves the low nibble to bits 6..9 of the low half and
-// the high nibble to bits 6..9 of the high half, and one packed fma turns
-// 1 + q/16 into (q - 8) s. `one` = 0x3C003C00 held in a VGPR lets the mask and
-// the OR fold into one v_and_or_b32.
-typedef unsigned short us2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ h8v_t dequant8(uint32_t w, const GroupScale& g, uint32_t one) {
+// Eight weights (one packed u32, elements 0..7 of a K run), in element order:
+// per byte j (elements 2j, 2j+1) v_perm copies the byte into both halves, one
+// AND keeps the low nibble in the low half and the high nibble in the high
+// half, and two v_fma_mix produce the pair.
+__device__ __forceinline__ h8v_t dequant8(uint32_t w, const GroupScale& g) {
     h2_t p[4];
-    if (g.fast) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t x = __builtin_amdgcn_perm(w, w, 0x0C000C00u | ((uint32_t)j << 16) | (uint32_t)j);
-            const us2_t y = __builtin_bit_cast(us2_t, x) << (us2_t){6, 2};
-            const uint32_t z = (__builtin_bit_cast(uint32_t, y) & 0x03C003C0u) | one;
-            p[j] = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, z), g.S, g.C);
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float lo = (float)((w >> (8 * j)) & 0xFu);
-            const float hi = (float)((w >> (8 * j + 4)) & 0xFu);
-            p[j] = h2_t{(_Float16)__builtin_fmaf(lo, g.s, g.b), (_Float16)__builtin_fmaf(hi, g.s, g.b)};
-        }
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t x = __builtin_amdgcn_perm(w, w, 0x0C000C00u | ((uint32_t)j << 16) | (uint32_t)j);
+        const h2_t y = __builtin_bit_cast(h2_t, x & 0x00F0000Fu);
+        // the empty asm makes the low half a value of its own, so the pair
+        // becomes v_fma_mixlo_f16 + v_fma_mixhi_f16 rather than two
+        // v_fma_mix_f32 and a v_cvt_pk_f16_f32
+        _Float16 lo = (_Float16)__builtin_fmaf((float)y.x, g.s_lo, g.b);
+        asm("" : "+v"(lo));
+        p[j] = h2_t{lo, (_Float16)__builtin_fmaf((float)y.y, g.s_hi, g.b)};
     }
     return h8v_t{p[0].x, p[0].y, p[1].x, p[1].y, p[2].x, p[2].y, p[3].x, p[3].y};
-}
-
-__device__ __forceinline__ uint32_t vgpr_one() {
-    uint32_t one = 0x3C003C00u;
-    asm volatile("" : "+v"(one));
-    return one;
 }
 
 // Dump of the GEMM's staging (tsg_debug_gemm_dequant_f16): one thread per 8
@@ -191,7 +172,6 @@ __global__ void gemm_dequant_probe_kernel(const uint8_t* __restrict__ w,
                                           const uint16_t* __restrict__ biases,
                                           uint16_t* __restrict__ out, uint32_t rows,
                                           uint32_t n) {
-    const uint32_t one = vgpr_one();
     const uint64_t pieces = (uint64_t)rows * (n / 8u);
     for (uint64_t p = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; p < pieces;
          p += (uint64_t)gridDim.x * blockDim.x) {
@@ -201,7 +181,7 @@ __global__ void gemm_dequant_probe_kernel(const uint8_t* __restrict__ w,
         const uint32_t g = k0 / G;
         const GroupScale gs = group_scale<SYM>(scales[r * (n / G) + g],
                                                SYM ? (uint16_t)0 : biases[r * (n / G) + g]);
-        *reinterpret_cast<uint4*>(out + r * n + k0) = __builtin_bit_cast(uint4, dequant8(v, gs, one));
+        *reinterpret_cast<uint4*>(out + r * n + k0) = __builtin_bit_cast(uint4, dequant8(v, gs));
     }
 }
 
@@ -209,58 +189,78 @@ __global__ void gemm_dequant_probe_kernel(const uint8_t* __restrict__ w,
 
 // Grouped int4 GEMM over routed blocks of up to kGemmRows rows of one expert.
 // Block = 4 waves; each wave owns 64 weight rows as two 32-row MFMA tiles
-// (gate/up: 32 gate + the same 32 up rows; down: 64 output rows) and every
-// live 32-row slice of the block's activation rows. K runs in 64-element
-// chunks through a kGemmStages-deep LDS ring filled by direct global->LDS
-// loads issued two chunks ahead, each stage holding
-//  - the activation tile: row r's 16-byte piece p in slot p ^ (r & 7) of the
-//    row, so the MFMA reads hit distinct banks;
-//  - the packed int4 weights, 1 KiB per (wave, tile): lane (n, h) of the wave
-//    brings the 16 bytes of weight row n holding K [64c + 32h, 64c + 32h + 32)
-//    and reads them back itself;
-//  - per (wave, tile) 256 bytes: the dword holding each lane's group scale
+// (gate/up: 32 gate + the same 32 up rows, so the GeGLU epilogue finds both in
+// one lane; down: 64 output rows) and every live 32-row slice of the block's
+// activation rows. The slice count NT (1..4) is a template parameter, so the
+// inner loop has no per-slice tests. K runs in 64-element chunks through a
+// kGemmStages-deep LDS ring filled by direct global->LDS loads issued two
+// chunks ahead; the loop is unrolled by the ring depth so every LDS read is a
+// per-lane base register plus an immediate offset. LDS layout:
+//  [A x 3 stages][weights x 3][scale dwords x 3][bias dwords x 3, affine]
+//  - A: the activation tile, row r's 16-byte piece p in slot p ^ swz(r),
+//    swz(r) = (r & 7) ^ ((r >> 3) & 1): conflict-free MFMA reads whether the
+//    LDS serves 8 lanes of a b128 read per cycle over 32 banks or 16 over 64;
+//  - weights: 1 KiB per (wave, tile): lane (n, h) of the wave brings the 16
+//    bytes of weight row n holding K [64c + 32h, 64c + 32h + 32) and reads
+//    them back itself;
+//  - 256 bytes per (wave, tile): the dword holding each lane's group scale
 //    (and, affine, bias).
 // Word s of a lane's 16 weight bytes is dequantised into the B operand of
 // MFMA step s, whose logical K 8h..8h+7 is physical 64c + 32h + 8s + (0..7);
-// the activations are read with the same mapping. Nothing is carried in
+// the activations are read with the same mapping. The A fragments of step
+// s + 1 are read while the MFMAs of step s run. Nothing is carried in
 // registers across chunks but the accumulators.
 constexpr uint32_t kGemmRows = 128;
 constexpr uint32_t kGemmKC = 64;
 constexpr uint32_t kGemmStages = 3;
-constexpr uint32_t kGemmAStage = kGemmRows * kGemmKC * 2u;   // 16 KiB
-constexpr uint32_t kGemmBStage = 4u * 2u * 1024u;            // 8 KiB
-constexpr uint32_t kGemmSStage = 4u * 2u * 256u;             // 2 KiB
-__host__ __device__ constexpr uint32_t gemm_stage_bytes(bool sym) {
-    return kGemmAStage + kGemmBStage + kGemmSStage * (sym ? 1u : 2u);
-}
-// sym: 78 KiB, two blocks per CU
+constexpr uint32_t kGemmAStage = kGemmRows * kGemmKC * 2u;  // 16 KiB
+constexpr uint32_t kGemmBStage = 4u * 2u * 1024u;           // 8 KiB
+constexpr uint32_t kGemmSStage = 4u * 2u * 256u;            // 2 KiB
+constexpr uint32_t kGemmBBase = kGemmStages * kGemmAStage;
+constexpr uint32_t kGemmSBase = kGemmBBase + kGemmStages * kGemmBStage;
+constexpr uint32_t kGemmBiasBase = kGemmSBase + kGemmStages * kGemmSStage;
+// sym: 78 KiB, affine: 84 KiB; two blocks per CU either way
 __host__ __device__ constexpr uint32_t gemm_lds_bytes(bool sym) {
-    return kGemmStages * gemm_stage_bytes(sym);
+    return kGemmBiasBase + (sym ? 0u : kGemmStages * kGemmSStage);
 }
+static_assert((kGemmStages - 1) * kGemmAStage + 3u * 4096u < 65536u, "A offsets fit ds offset:");
 
-// LDS reads as inline ds_read_b128: the compiler cannot tell them from the
+// LDS reads as inline ds_read: the compiler cannot tell them from the
 // direct-to-LDS writes of other stages and would drain every outstanding load
-// before each one. lds_wait() waits for them; its operands tie the fragments
-// to the wait so no use is scheduled before it.
+// before each one. lds_wait() waits for them; its operands tie the results to
+// the wait so no use (or copy) is scheduled before it.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
 }
+template <uint32_t OFF>
 __device__ __forceinline__ u32x4_t lds_read16(uint32_t addr) {
+    static_assert(OFF < 65536u, "ds offset is 16 bits");
     u32x4_t v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
     return v;
 }
-__device__ __forceinline__ void lds_wait(u32x4_t& a0, u32x4_t& a1, u32x4_t& a2, u32x4_t& a3) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3));
-}
+template <uint32_t OFF>
 __device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
+    static_assert(OFF < 65536u, "ds offset is 16 bits");
     uint32_t v;
-    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
     return v;
 }
-__device__ __forceinline__ void lds_wait(u32x4_t& a0, u32x4_t& a1, uint32_t& s0, uint32_t& s1,
-                                         uint32_t& b0, uint32_t& b1) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a0), "+v"(a1), "+v"(s0), "+v"(s1), "+v"(b0), "+v"(b1));
+template <int NT>
+__device__ __forceinline__ void lds_wait(u32x4_t (&a)[NT]) {
+    if constexpr (NT == 1) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]));
+    if constexpr (NT == 2) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]));
+    if constexpr (NT == 3)
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]));
+    if constexpr (NT == 4)
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]));
+}
+template <int NT>
+__device__ __forceinline__ void lds_wait(u32x4_t (&a)[NT], u32x4_t& b0, u32x4_t& b1, uint32_t& s0,
+                                         uint32_t& s1, uint32_t& z0, uint32_t& z1) {
+    asm volatile("" : "+v"(b0), "+v"(b1), "+v"(s0), "+v"(s1), "+v"(z0), "+v"(z1));
+    lds_wait<NT>(a);
+    asm volatile("" : "+v"(b0), "+v"(b1), "+v"(s0), "+v"(s1), "+v"(z0), "+v"(z1));
 }
 
 // Wait until at most N of this wave's vector memory loads are outstanding
@@ -281,12 +281,12 @@ __device__ __forceinline__ void block_barrier() {
     asm volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds_wave_base) {
+__device__ __forceinline__ void lds_dma16(const void* src, uint8_t* lds_wave_base) {
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                      (__attribute__((address_space(3))) void*)lds_wave_base,
                                      16, 0, 0);
 }
-__device__ __forceinline__ void lds_dma4(const void* src, void* lds_wave_base) {
+__device__ __forceinline__ void lds_dma4(const void* src, uint8_t* lds_wave_base) {
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                      (__attribute__((address_space(3))) void*)lds_wave_base,
                                      4, 0, 0);
@@ -304,181 +304,272 @@ struct GemmArgs {
     const uint32_t* n_blocks_device;
     uint16_t* out;              // act (gate/up) or route partials (down)
     uint32_t d, f, top_k;
+    uint32_t ntiles;            // weight-row tiles per routed block
 };
 
-// MODE 0: gate/up + activation; MODE 1: down + scatter.
-template <int G, bool SYM, int ACT, int MODE>
-__global__ __launch_bounds__(256, 2) void moe_gemm_kernel(GemmArgs args) {
-    extern __shared__ __align__(16) uint8_t smem[];  // gemm_lds_bytes(SYM)
+// Per-lane state of one block's GEMM.
+struct GemmLane {
+    const uint8_t* blob;
+    const uint16_t* a_src[4];   // this lane's A piece for DMA j (chunk 0)
+    const uint8_t* w_src[2];    // this lane's weight bytes, tiles 0/1 (chunk 0)
+    uint32_t s_off[2], b_off[2];  // byte offsets of the lane's scale/bias for group 0 (+ 2h if G == 32)
+    uint32_t a_rd[4];           // LDS A read address per MFMA step (stage 0, slice 0)
+    uint32_t b_rd, s_rd;        // LDS weight / scale read addresses (stage 0, tile 0)
+    uint32_t wave, nchunks;
+    bool a_wave, live;
+};
 
-    const uint32_t nb = args.n_blocks_device ? *args.n_blocks_device : args.n_blocks;
-    if (blockIdx.y >= nb) return;
-    const tsg_routed_block blk = args.blocks[blockIdx.y];
-    const uint32_t rows = blk.row_count < kGemmRows ? blk.row_count : kGemmRows;
-    if (rows == 0) return;
-    const uint32_t n_mt = (rows + 31u) / 32u;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, h = lane >> 5;
-    const uint32_t K = MODE == 0 ? args.d : args.f;
-    const uint8_t* blob = args.layer_base + (uint64_t)blk.local_slot * args.expert_stride;
+// Byte offset of the group-scale (or bias) halfword for chunk c relative to
+// the lane's group-0 offset; G == 32 folds the K half into the lane offset.
+template <int G>
+__device__ __forceinline__ uint32_t group_byte(uint32_t c) {
+    return G == 32 ? 4u * c : 2u * ((c * kGemmKC) / G);
+}
 
-    // source row (element offset into args.a) and destination row of block
-    // row r; rows past the block use row 0's (their results are dropped)
-    auto src_row = [&](uint32_t r) -> uint32_t {
-        r = r < rows ? r : 0u;
-        if (MODE == 0) return args.pairs[blk.pair_start + r].token * args.a_stride;
-        return (blk.local_row + r) * args.a_stride;
-    };
-    auto dst_row = [&](uint32_t r) -> uint32_t {
-        if (MODE == 0) return (blk.local_row + r) * args.f;
-        const tsg_token_expert_pair pr = args.pairs[blk.pair_start + r];
-        return (pr.token * args.top_k + pr.rank) * args.d;
-    };
-
-    // this lane's two weight rows, as byte offsets into the expert blob
-    uint32_t n0, n1;
-    bool live0, live1;
-    uint32_t ow0, ow1, os0, os1, ob0, ob1;
-    const uint32_t ngroups = K / G;
-    if (MODE == 0) {
-        n0 = n1 = (blockIdx.x * 4u + wave) * 32u + (lane & 31u);
-        live0 = live1 = n0 < args.f;
-        const uint32_t r = live0 ? n0 : 0u;
-        ow0 = args.o.gate_w + r * (K / 2u);
-        ow1 = args.o.up_w + r * (K / 2u);
-        os0 = args.o.gate_s + r * ngroups * 2u;
-        os1 = args.o.up_s + r * ngroups * 2u;
-        ob0 = args.o.gate_b + r * ngroups * 2u;
-        ob1 = args.o.up_b + r * ngroups * 2u;
-    } else {
-        n0 = (blockIdx.x * 4u + wave) * 64u + (lane & 31u);
-        n1 = n0 + 32u;
-        live0 = n0 < args.d;
-        live1 = n1 < args.d;
-        const uint32_t r0 = live0 ? n0 : 0u, r1 = live1 ? n1 : 0u;
-        ow0 = args.o.down_w + r0 * (K / 2u);
-        ow1 = args.o.down_w + r1 * (K / 2u);
-        os0 = args.o.down_s + r0 * ngroups * 2u;
-        os1 = args.o.down_s + r1 * ngroups * 2u;
-        ob0 = args.o.down_b + r0 * ngroups * 2u;
-        ob1 = args.o.down_b + r1 * ngroups * 2u;
+// Chunk c (clamped to the last one) into ring stage ST. Every chunk issues the
+// same loads, so the vmcnt waits are exact: A 4 (if the wave moves A rows),
+// weights 2, scale dwords 2, bias dwords 2 (affine).
+template <int G, bool SYM, int ST>
+__device__ __forceinline__ void gemm_issue(const GemmLane& L, uint8_t* smem, uint32_t c) {
+    const uint32_t cc = c < L.nchunks ? c : L.nchunks - 1u;
+    if (L.a_wave) {
+        uint8_t* dst = smem + ST * kGemmAStage + L.wave * 32u * kGemmKC * 2u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lds_dma16(L.a_src[j] + cc * kGemmKC, dst + j * 8u * kGemmKC * 2u);
     }
-    const uint32_t nchunks = K / kGemmKC;
-    constexpr uint32_t kStage = gemm_stage_bytes(SYM);
-
-    // activation DMA: wave w moves rows [32w, 32w + 32) (4 instructions of 8
-    // rows x 128 B); lane l carries row 8j + l/8, piece (l % 8) ^ (l / 8).
-    const bool a_wave = wave < n_mt;
-    uint32_t a_off[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t row = 32u * wave + 8u * i + (lane >> 3);
-        const uint32_t piece = (lane & 7u) ^ (lane >> 3);
-        a_off[i] = src_row(row) + piece * 8u;
+    uint8_t* bst = smem + kGemmBBase + ST * kGemmBStage + L.wave * 2048u;
+    lds_dma16(L.w_src[0] + cc * (kGemmKC / 2u), bst);
+    lds_dma16(L.w_src[1] + cc * (kGemmKC / 2u), bst + 1024u);
+    const uint32_t gb = group_byte<G>(cc);
+    uint8_t* sst = smem + kGemmSBase + ST * kGemmSStage + L.wave * 512u;
+    lds_dma4(L.blob + ((L.s_off[0] + gb) & ~3u), sst);
+    lds_dma4(L.blob + ((L.s_off[1] + gb) & ~3u), sst + 256u);
+    if constexpr (!SYM) {
+        uint8_t* zst = smem + kGemmBiasBase + ST * kGemmSStage + L.wave * 512u;
+        lds_dma4(L.blob + ((L.b_off[0] + gb) & ~3u), zst);
+        lds_dma4(L.blob + ((L.b_off[1] + gb) & ~3u), zst + 256u);
     }
-    // Chunk c into stage c % 3. Every chunk issues the same loads (chunks past
-    // the end re-read the last one into a stage no later chunk uses), so the
-    // vmcnt waits stay exact: A (4 if a_wave), weights (2), scale dwords (2),
-    // bias dwords (2, affine).
-    auto issue = [&](uint32_t c) {
-        const uint32_t cc = c < nchunks ? c : nchunks - 1u;
-        uint8_t* stage = smem + (c % kGemmStages) * kStage;
-        if (a_wave) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                lds_dma16(args.a + a_off[i] + cc * kGemmKC, stage + (32u * wave + 8u * i) * kGemmKC * 2u);
-        }
-        uint8_t* bst = stage + kGemmAStage + wave * 2048u;
-        const uint32_t byte = cc * (kGemmKC / 2u) + h * 16u;
-        lds_dma16(blob + ow0 + byte, bst);
-        lds_dma16(blob + ow1 + byte, bst + 1024u);
-        const uint32_t g2 = ((cc * kGemmKC + h * 32u) / G) * 2u;
-        uint8_t* sst = stage + kGemmAStage + kGemmBStage + wave * 512u;
-        lds_dma4(blob + ((os0 + g2) & ~3u), sst);
-        lds_dma4(blob + ((os1 + g2) & ~3u), sst + 256u);
-        if constexpr (!SYM) {
-            lds_dma4(blob + ((ob0 + g2) & ~3u), sst + kGemmSStage);
-            lds_dma4(blob + ((ob1 + g2) & ~3u), sst + kGemmSStage + 256u);
-        }
-    };
+}
 
-    const uint32_t one = vgpr_one();
-    f16v_t acc[4][2];
+// The MFMA work of chunk c (stage ST). Step s + 1's activation reads and
+// weight dequantisation are issued ahead of step s's MFMAs, which do not
+// depend on them, so the scheduler can overlap the VALU work with the matrix
+// core.
+template <int NT, int ST>
+__device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT], const u32x4_t& bw0,
+                                         const u32x4_t& bw1, const GroupScale& g0,
+                                         const GroupScale& g1, f16v_t (&acc)[NT][2]) {
+    h8v_t bf[2][2];
+    bf[0][0] = dequant8(bw0[0], g0);
+    bf[0][1] = dequant8(bw1[0], g1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i][0] = acc[i][1] = f16v_t{};
-
-    constexpr uint32_t kNW = SYM ? 4u : 6u;  // weight + scale (+ bias) loads per chunk
-    issue(0);
-    issue(1);
-    for (uint32_t c = 0; c < nchunks; ++c) {
-        // chunk c landed (chunk c + 1's loads may still be in flight); after
-        // the barrier every wave is done with stage (c - 1) % 3 = (c + 2) % 3
-        if (a_wave) wait_vmcnt<4u + kNW>();
-        else wait_vmcnt<kNW>();
-        block_barrier();
-        const uint8_t* stage = smem + (c % kGemmStages) * kStage;
-        const uint32_t m = lane & 31u;
-        const uint32_t bbase = lds_addr(stage + kGemmAStage + wave * 2048u) + lane * 16u;
-        const uint32_t sbase = lds_addr(stage + kGemmAStage + kGemmBStage + wave * 512u) + lane * 4u;
-        u32x4_t bw0 = lds_read16(bbase), bw1 = lds_read16(bbase + 1024u);
-        uint32_t sw0 = lds_read4(sbase), sw1 = lds_read4(sbase + 256u);
-        uint32_t bb0 = 0u, bb1 = 0u;
-        if constexpr (!SYM) {
-            bb0 = lds_read4(sbase + kGemmSStage);
-            bb1 = lds_read4(sbase + kGemmSStage + 256u);
-        }
-        lds_wait(bw0, bw1, sw0, sw1, bb0, bb1);
-        // the 16-bit value inside each loaded dword
-        const uint32_t g2 = ((c * kGemmKC + h * 32u) / G) * 2u;
-        const uint32_t sh0 = ((os0 + g2) & 2u) * 8u, sh1 = ((os1 + g2) & 2u) * 8u;
-        const uint32_t bh0 = ((ob0 + g2) & 2u) * 8u, bh1 = ((ob1 + g2) & 2u) * 8u;
-        const GroupScale g0 = group_scale<SYM>((uint16_t)(sw0 >> sh0), (uint16_t)(bb0 >> bh0));
-        const GroupScale g1 = group_scale<SYM>((uint16_t)(sw1 >> sh1), (uint16_t)(bb1 >> bh1));
-        const uint32_t row_addr = lds_addr(stage) + m * kGemmKC * 2u;
+    for (int st = 0; st < 4; ++st) {
+        const int cur = st & 1, nxt = cur ^ 1;
+        if (st < 3) {
+            const uint32_t a = L.a_rd[st + 1];
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const uint32_t at = row_addr + (((h * 4u + (uint32_t)st) ^ (m & 7u)) * 16u);
-            // all four slices are read (rows past the block hold stale data
-            // and feed no MFMA): a conditional read would let the compiler
-            // copy a register the read has not filled yet
-            u32x4_t af[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) af[i] = lds_read16(at + i * 32u * kGemmKC * 2u);
-            const h8v_t bf0 = dequant8(bw0[st], g0, one);
-            const h8v_t bf1 = dequant8(bw1[st], g1, one);
-            lds_wait(af[0], af[1], af[2], af[3]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if ((uint32_t)i < n_mt) {
-                    const h8v_t a8 = __builtin_bit_cast(h8v_t, af[i]);
-                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, bf0, acc[i][0], 0, 0, 0);
-                    acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, bf1, acc[i][1], 0, 0, 0);
+            for (int i = 0; i < NT; ++i) {
+                switch (i) {
+                    case 0: af[nxt][i] = lds_read16<ST * kGemmAStage + 0u * 4096u>(a); break;
+                    case 1: af[nxt][i] = lds_read16<ST * kGemmAStage + 1u * 4096u>(a); break;
+                    case 2: af[nxt][i] = lds_read16<ST * kGemmAStage + 2u * 4096u>(a); break;
+                    default: af[nxt][i] = lds_read16<ST * kGemmAStage + 3u * 4096u>(a); break;
                 }
             }
+            bf[nxt][0] = dequant8(bw0[st + 1], g0);
+            bf[nxt][1] = dequant8(bw1[st + 1], g1);
         }
-        issue(c + 2u);
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            const h8v_t a8 = __builtin_bit_cast(h8v_t, af[cur][i]);
+            acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, bf[cur][0], acc[i][0], 0, 0, 0);
+            acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, bf[cur][1], acc[i][1], 0, 0, 0);
+        }
+        if (st < 3) lds_wait<NT>(af[nxt]);
+    }
+}
+
+// One chunk: wait for it, read its weights, scales and step-0 activations,
+// run its MFMAs, then start chunk c + 2 into the stage chunk c - 1 used.
+template <int G, bool SYM, int NT, int ST>
+__device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uint32_t c,
+                                           f16v_t (&acc)[NT][2]) {
+    constexpr uint32_t kNW = SYM ? 4u : 6u;
+    // chunk c landed (chunk c + 1 may still be in flight); after the barrier
+    // every wave is done with stage (c + 2) % 3
+    if (L.a_wave) wait_vmcnt<4u + kNW>();
+    else wait_vmcnt<kNW>();
+    block_barrier();
+    if (L.live) {
+        u32x4_t af[2][NT];
+        u32x4_t bw0 = lds_read16<ST * kGemmBStage>(L.b_rd);
+        u32x4_t bw1 = lds_read16<ST * kGemmBStage + 1024u>(L.b_rd);
+        uint32_t sw0 = lds_read4<ST * kGemmSStage>(L.s_rd);
+        uint32_t sw1 = lds_read4<ST * kGemmSStage + 256u>(L.s_rd);
+        uint32_t zw0 = 0u, zw1 = 0u;
+        if constexpr (!SYM) {
+            zw0 = lds_read4<kGemmBiasBase - kGemmSBase + ST * kGemmSStage>(L.s_rd);
+            zw1 = lds_read4<kGemmBiasBase - kGemmSBase + ST * kGemmSStage + 256u>(L.s_rd);
+        }
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            switch (i) {
+                case 0: af[0][i] = lds_read16<ST * kGemmAStage + 0u * 4096u>(L.a_rd[0]); break;
+                case 1: af[0][i] = lds_read16<ST * kGemmAStage + 1u * 4096u>(L.a_rd[0]); break;
+                case 2: af[0][i] = lds_read16<ST * kGemmAStage + 2u * 4096u>(L.a_rd[0]); break;
+                default: af[0][i] = lds_read16<ST * kGemmAStage + 3u * 4096u>(L.a_rd[0]); break;
+            }
+        }
+        lds_wait<NT>(af[0], bw0, bw1, sw0, sw1, zw0, zw1);
+        // the 16-bit value inside each loaded dword
+        const uint32_t gb = group_byte<G>(c);
+        const uint32_t sh0 = ((L.s_off[0] + gb) & 2u) * 8u, sh1 = ((L.s_off[1] + gb) & 2u) * 8u;
+        const uint32_t bh0 = ((L.b_off[0] + gb) & 2u) * 8u, bh1 = ((L.b_off[1] + gb) & 2u) * 8u;
+        const GroupScale g0 = group_scale<SYM>((uint16_t)(sw0 >> sh0), (uint16_t)(zw0 >> bh0));
+        const GroupScale g1 = group_scale<SYM>((uint16_t)(sw1 >> sh1), (uint16_t)(zw1 >> bh1));
+        gemm_mma<NT, ST>(L, af, bw0, bw1, g0, g1, acc);
+    }
+    gemm_issue<G, SYM, (ST + 2) % 3>(L, smem, c + 2u);
+}
+
+// MODE 0: gate/up + activation; MODE 1: down + scatter.
+template <int G, bool SYM, int ACT, int MODE, int NT>
+__device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_routed_block& blk,
+                                           uint32_t rows, uint32_t tile, uint8_t* smem) {
+    const uint32_t lane = threadIdx.x & 63u, h = lane >> 5, m = lane & 31u;
+    GemmLane L;
+    L.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t K = MODE == 0 ? args.d : args.f;
+    L.nchunks = K / kGemmKC;
+    L.blob = args.layer_base + (uint64_t)blk.local_slot * args.expert_stride;
+    L.a_wave = L.wave < (uint32_t)NT;
+
+    // weight rows of this lane (each wave's rows are all live or all dead:
+    // d and f are multiples of 64)
+    const uint32_t ngroups = K / G;
+    uint32_t n0, n1, ow0, ow1;
+    if (MODE == 0) {
+        n0 = n1 = (tile * 4u + L.wave) * 32u + m;
+        L.live = (tile * 4u + L.wave) * 32u < args.f;
+        const uint32_t r = L.live ? n0 : 0u;
+        ow0 = args.o.gate_w + r * (K / 2u);
+        ow1 = args.o.up_w + r * (K / 2u);
+        L.s_off[0] = args.o.gate_s + r * ngroups * 2u;
+        L.s_off[1] = args.o.up_s + r * ngroups * 2u;
+        L.b_off[0] = args.o.gate_b + r * ngroups * 2u;
+        L.b_off[1] = args.o.up_b + r * ngroups * 2u;
+    } else {
+        n0 = (tile * 4u + L.wave) * 64u + m;
+        n1 = n0 + 32u;
+        L.live = (tile * 4u + L.wave) * 64u < args.d;
+        const uint32_t r0 = L.live ? n0 : 0u, r1 = L.live ? n1 : 0u;
+        ow0 = args.o.down_w + r0 * (K / 2u);
+        ow1 = args.o.down_w + r1 * (K / 2u);
+        L.s_off[0] = args.o.down_s + r0 * ngroups * 2u;
+        L.s_off[1] = args.o.down_s + r1 * ngroups * 2u;
+        L.b_off[0] = args.o.down_b + r0 * ngroups * 2u;
+        L.b_off[1] = args.o.down_b + r1 * ngroups * 2u;
+    }
+    L.w_src[0] = L.blob + ow0 + h * 16u;
+    L.w_src[1] = L.blob + ow1 + h * 16u;
+    if (G == 32) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            L.s_off[t] += 2u * h;
+            L.b_off[t] += 2u * h;
+        }
+    }
+
+    // activation DMA j of wave w moves rows 32w + 8j + l/8, lane l bringing
+    // the piece stored in slot l % 8; rows past the block repeat row 0
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t row = 32u * L.wave + 8u * j + (lane >> 3);
+        row = row < rows ? row : 0u;
+        const uint32_t piece = (lane & 7u) ^ (lane >> 3) ^ ((uint32_t)j & 1u);
+        const uint32_t src = MODE == 0 ? args.pairs[blk.pair_start + row].token * args.a_stride
+                                       : (blk.local_row + row) * args.a_stride;
+        L.a_src[j] = args.a + src + piece * 8u;
+    }
+    const uint32_t base = lds_addr(smem);
+    const uint32_t swz = (m & 7u) ^ ((m >> 3) & 1u);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) L.a_rd[st] = base + m * kGemmKC * 2u + (((h * 4u + st) ^ swz) << 4);
+    L.b_rd = base + kGemmBBase + L.wave * 2048u + lane * 16u;
+    L.s_rd = base + kGemmSBase + L.wave * 512u + lane * 4u;
+
+    f16v_t acc[NT][2];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) acc[i][0] = acc[i][1] = f16v_t{};
+
+    gemm_issue<G, SYM, 0>(L, smem, 0u);
+    gemm_issue<G, SYM, 1>(L, smem, 1u);
+    for (uint32_t c = 0;;) {
+        gemm_chunk<G, SYM, NT, 0>(L, smem, c, acc);
+        if (++c == L.nchunks) break;
+        gemm_chunk<G, SYM, NT, 1>(L, smem, c, acc);
+        if (++c == L.nchunks) break;
+        gemm_chunk<G, SYM, NT, 2>(L, smem, c, acc);
+        if (++c == L.nchunks) break;
     }
     wait_vmcnt<0>();  // no LDS write may land after the block ends
+    if (!L.live) return;
 
     // acc[i][t][v] of lane l: row 32 i + 8 (v / 4) + 4 h + v % 4 of the block,
     // weight row n_t (column l % 32 of tile t).
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if ((uint32_t)i >= n_mt) continue;
+    for (int i = 0; i < NT; ++i) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const uint32_t mm = 32u * i + 8u * (v >> 2) + 4u * h + (v & 3);
             if (mm >= rows) continue;
-            const uint32_t dst = dst_row(mm);
             if (MODE == 0) {
-                if (!live0) continue;
+                const uint32_t dst = (blk.local_row + mm) * args.f;
                 const float gt = f16_to_f32(f32_to_f16(acc[i][0][v]));
                 const float up = f16_to_f32(f32_to_f16(acc[i][1][v]));
                 args.out[dst + n0] = f32_to_f16(gate_activation<ACT>(gt) * up);
             } else {
-                if (live0) args.out[dst + n0] = f32_to_f16(acc[i][0][v]);
-                if (live1) args.out[dst + n1] = f32_to_f16(acc[i][1][v]);
+                const tsg_token_expert_pair pr = args.pairs[blk.pair_start + mm];
+                const uint32_t dst = (pr.token * args.top_k + pr.rank) * args.d;
+                args.out[dst + n0] = f32_to_f16(acc[i][0][v]);
+                args.out[dst + n1] = f32_to_f16(acc[i][1][v]);
             }
         }
+    }
+}
+
+// Workgroups go to the 8 XCDs (each with its own L2) round-robin by linear
+// id. Work item order (routed block major, weight tile minor) is dealt out so
+// that each XCD runs one contiguous range of it: the tiles of a routed block
+// share its activation rows, and neighbouring routed blocks mostly share the
+// expert's weights, in the same L2 at about the same time. Bijective on
+// [0, total).
+__device__ __forceinline__ uint32_t xcd_order(uint32_t pid, uint32_t total) {
+    constexpr uint32_t kXcds = 8;
+    const uint32_t per = (total + kXcds - 1u) / kXcds;
+    const uint32_t tall = total - (per - 1u) * kXcds;  // XCDs that run `per` items
+    const uint32_t xcd = pid % kXcds, local = pid / kXcds;
+    return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1u) + local;
+}
+
+// 1-D grid of ntiles x (routed block capacity) workgroups; those past the
+// live count exit at once.
+template <int G, bool SYM, int ACT, int MODE>
+__global__ __launch_bounds__(256, 2) void moe_gemm_kernel(GemmArgs args) {
+    extern __shared__ __align__(16) uint8_t smem[];  // gemm_lds_bytes(SYM)
+    const uint32_t nb = args.n_blocks_device ? *args.n_blocks_device : args.n_blocks;
+    const uint32_t total = nb * args.ntiles;
+    if (blockIdx.x >= total) return;
+    const uint32_t item = xcd_order(blockIdx.x, total);
+    const uint32_t yb = item / args.ntiles, tile = item - yb * args.ntiles;
+    const tsg_routed_block blk = args.blocks[yb];
+    const uint32_t rows = blk.row_count < kGemmRows ? blk.row_count : kGemmRows;
+    switch ((rows + 31u) / 32u) {
+        case 0: return;
+        case 1: gemm_block<G, SYM, ACT, MODE, 1>(args, blk, rows, tile, smem); break;
+        case 2: gemm_block<G, SYM, ACT, MODE, 2>(args, blk, rows, tile, smem); break;
+        case 3: gemm_block<G, SYM, ACT, MODE, 3>(args, blk, rows, tile, smem); break;
+        default: gemm_block<G, SYM, ACT, MODE, 4>(args, blk, rows, tile, smem); break;
     }
 }
 
@@ -618,15 +709,18 @@ tsg_status check_layer_moe(const tsg_moe* moe, const tsg_layer* layer) {
 
 template <int G, bool SYM, int MODE>
 tsg_status launch_gemm(const tsg_moe* moe, hipStream_t s, const GemmArgs& a, uint32_t max_blocks) {
-    const uint32_t ntiles = MODE == 0 ? (a.f + 127u) / 128u : (a.d + 255u) / 256u;
-    const dim3 grid(ntiles, max_blocks);
+    GemmArgs args = a;
+    args.ntiles = MODE == 0 ? (a.f + 127u) / 128u : (a.d + 255u) / 256u;
+    TSG_REQUIRE((uint64_t)args.ntiles * max_blocks <= 0x7FFFFFFFu, TSG_ERR_INVALID_ARGUMENT,
+                "moe_gemm: %u routed blocks x %u tiles exceed the grid", max_blocks, args.ntiles);
+    const dim3 grid(args.ntiles * max_blocks);
     auto kern = moe->activation == TSG_ACT_SILU ? moe_gemm_kernel<G, SYM, TSG_ACT_SILU, MODE>
                                                 : moe_gemm_kernel<G, SYM, TSG_ACT_GELU_TANH, MODE>;
     // more than 64 KiB of dynamic LDS must be allowed per kernel (idempotent)
     TSG_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int)gemm_lds_bytes(SYM)));
-    hipLaunchKernelGGL(kern, grid, dim3(256), gemm_lds_bytes(SYM), s, a);
+    hipLaunchKernelGGL(kern, grid, dim3(256), gemm_lds_bytes(SYM), s, args);
     return check_launch(MODE == 0 ? "moe_gemm gate/up" : "moe_gemm down");
 }
 
