@@ -218,7 +218,7 @@ def run_prefill(tsg, torch, ctx, args, layer):
     w = torch.from_numpy(w_np.ravel().view(np.int16)).cuda()
     hidden = torch.empty(t * H, dtype=torch.int16, device="cuda")
     tsg.generators.f16_normal(hidden, 0x33, 1.0)
-    tile_rows = 128  # the grouped GEMM's widest row tile
+    tile_rows = 128  # the grouped GEMM's widest pass
     max_blocks = t * k // tile_rows + E
     sp = torch.empty(t * k * 4, dtype=torch.int32, device="cuda")
     off = torch.empty(E, dtype=torch.int32, device="cuda")

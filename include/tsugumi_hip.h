@@ -282,7 +282,7 @@ tsg_status tsg_plan_routed_gemm(const tsg_moe_group* groups, uint32_t n_groups,
  * and counts, and the GEMM's work list of <= tile_rows-row blocks with
  * local_slot = expert id and local_row = pair_start. *n_blocks (device) gets
  * the block count; max_blocks bounds the blocks array. tile_rows: 32, 64 (the
- * reference's block) or 128 (the grouped GEMM's widest tile).
+ * reference's block), 128 (the grouped GEMM's widest pass) or 256.
  * scratch: tsg_prefill_group_scratch_bytes(...) bytes of device memory. */
 size_t tsg_prefill_group_scratch_bytes(uint32_t query_count, uint32_t top_k,
                                        uint32_t num_experts);
@@ -300,7 +300,9 @@ tsg_status tsg_prefill_group_pairs_device(tsg_ctx* ctx, tsg_stream stream,
  * gather hidden rows by pair token, G = X Wg^T and U = X Wu^T on fp16 MFMA with
  * fp32 accumulation, weights dequantised to fp16 exactly as the reference
  * stages them; act[(local_row + r)*F + f] = half(act(half(G)) * half(U)).
- * Blocks of up to 128 rows. d and f must be multiples of 64.
+ * Blocks of any size (the kernel runs 128 rows per pass). d and f must be
+ * multiples of 64; at group size 32 the scale/bias sub-tensor offsets must be
+ * 4-byte aligned (TSG_ERR_ALIGNMENT).
  * n_blocks_device: optional device count bounding `blocks` (may be NULL, then
  * n_blocks is used). */
 tsg_status tsg_prefill_moe_gate_up(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,

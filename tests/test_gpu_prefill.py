@@ -114,6 +114,7 @@ def _zipf_routing(rng, t, ne, k, s):
 
 
 @pytest.mark.parametrize("t,ne,k,s,tile", [(2048, 128, 8, 1.1, 64), (2048, 128, 8, 1.1, 128),
+                                           (2048, 128, 8, 1.1, 256),
                                            (301, 256, 8, 1.0, 64), (5, 128, 8, 1.1, 128),
                                            (64, 16, 4, 0.5, 32)])
 def test_device_grouping_matches_host_sort(tsg, ctx, t, ne, k, s, tile):
@@ -194,12 +195,13 @@ def test_reduce_token_major_bit_exact(tsg, ctx):
     assert np.array_equal(host(h2, np.uint16), oracle.reduce_token_major(P, w, t, k, d).ravel())
 
 
-@pytest.mark.parametrize("tile", [64, 128])
+@pytest.mark.parametrize("tile", [64, 128, 256])
 def test_prefill_pipeline_zipf_end_to_end(tsg, ctx, tile):
     """A Gemma-shaped prefill chunk (T=256, top-8, Zipf(1.1) over 128 experts):
     device grouping -> gate/up -> down -> token-major reduce, against the
     oracle's grouping + expert-major reference + reduce; GEMM blocks of the
-    reference's 64 rows and of the kernel's widest 128."""
+    reference's 64 rows, the kernel's widest pass of 128, and 256-row blocks
+    that the kernel runs as two passes."""
     configure(ctx, 32, "sym")
     t, ne, k, d, f = 256, 128, 8, 2816, 704
     rng = np.random.default_rng(11)

@@ -188,42 +188,55 @@ __global__ void gemm_dequant_probe_kernel(const uint8_t* __restrict__ w,
 // --------------------------------------------------------------- GEMM
 
 // Grouped int4 GEMM over routed blocks of up to kGemmRows rows of one expert.
-// Block = 4 waves; each wave owns 64 weight rows as two 32-row MFMA tiles
-// (gate/up: 32 gate + the same 32 up rows, so the GeGLU epilogue finds both in
-// one lane; down: 64 output rows) and every live 32-row slice of the block's
-// activation rows. The slice count NT (1..4) is a template parameter, so the
-// inner loop has no per-slice tests. K runs in 64-element chunks through a
-// kGemmStages-deep LDS ring filled by direct global->LDS loads issued two
-// chunks ahead; the loop is unrolled by the ring depth so every LDS read is a
-// per-lane base register plus an immediate offset. LDS layout:
-//  [A x 3 stages][weights x 3][scale dwords x 3][bias dwords x 3, affine]
-//  - A: the activation tile, row r's 16-byte piece p in slot p ^ swz(r),
-//    swz(r) = (r & 7) ^ ((r >> 3) & 1): conflict-free MFMA reads whether the
-//    LDS serves 8 lanes of a b128 read per cycle over 32 banks or 16 over 64;
-//  - weights: 1 KiB per (wave, tile): lane (n, h) of the wave brings the 16
-//    bytes of weight row n holding K [64c + 32h, 64c + 32h + 32) and reads
-//    them back itself;
-//  - 256 bytes per (wave, tile): the dword holding each lane's group scale
-//    (and, affine, bias).
+// Block = 4 waves, two blocks per CU; each wave owns 64 weight rows as two
+// 32-row MFMA tiles (gate/up: 32 gate + the same 32 up rows, so the GeGLU
+// epilogue finds both in one lane; down: 64 output rows) against every live
+// 32-row slice of the block's activation rows (NT = 1..4, a template
+// parameter, so the inner loop has no per-slice tests). Each activation
+// fragment read from LDS feeds two MFMAs, which keeps LDS read traffic near
+// half its bandwidth at full MFMA rate. K runs in 64-element chunks. Operands
+// arrive by direct global->LDS loads laid out so that each 64-lane load
+// touches as few cache sectors as its data allows: the vector L1's access
+// rate, not bandwidth, bounds scattered loads.
+//  - activations, shared by the block: a 3-stage ring; row r's 16-byte piece
+//    p sits in slot p ^ swz(r), swz(r) = (r & 7) ^ ((r >> 3) & 1); waves
+//    w < NT load rows [32w, 32w + 32).
+//  - weights, per (wave, tile): a 3-stage ring of 32 rows x 32 bytes (one
+//    chunk), two lanes per row; row r's half h sits in slot h ^ swzb(r),
+//    swzb(r) = ((r >> 2) ^ (r >> 3)) & 1.
+//  - group scales (and affine biases), per wave: windows of 8 groups (16
+//    bytes of each of its 64 rows; 7 groups when rows are only 2-byte
+//    aligned, G = 64), double-buffered, loaded once per window, four lanes
+//    per row.
+// The swizzles keep the MFMA-side LDS reads conflict-free whether the LDS
+// serves 8 lanes of a 16-byte read per cycle over 32 banks or 16 over 64.
 // Word s of a lane's 16 weight bytes is dequantised into the B operand of
 // MFMA step s, whose logical K 8h..8h+7 is physical 64c + 32h + 8s + (0..7);
-// the activations are read with the same mapping. The A fragments of step
-// s + 1 are read while the MFMAs of step s run. Nothing is carried in
-// registers across chunks but the accumulators.
+// the activations are read with the same mapping. Step s + 1's activation
+// reads and dequantisation are issued ahead of step s's MFMAs.
 constexpr uint32_t kGemmRows = 128;
+constexpr uint32_t kGemmWaves = 4;
+constexpr uint32_t kGemmThreads = kGemmWaves * 64u;
 constexpr uint32_t kGemmKC = 64;
 constexpr uint32_t kGemmStages = 3;
-constexpr uint32_t kGemmAStage = kGemmRows * kGemmKC * 2u;  // 16 KiB
-constexpr uint32_t kGemmBStage = 4u * 2u * 1024u;           // 8 KiB
-constexpr uint32_t kGemmSStage = 4u * 2u * 256u;            // 2 KiB
-constexpr uint32_t kGemmBBase = kGemmStages * kGemmAStage;
+constexpr uint32_t kGemmAStage = kGemmRows * kGemmKC * 2u;            // 16 KiB
+constexpr uint32_t kGemmBTile = 32u * kGemmKC / 2u;                   // 1 KiB
+constexpr uint32_t kGemmBWave = 2u * kGemmBTile;
+constexpr uint32_t kGemmBStage = kGemmWaves * kGemmBWave;             // 8 KiB
+constexpr uint32_t kGemmSWave = 64u * 16u;                            // 1 KiB
+constexpr uint32_t kGemmSSlot = kGemmWaves * kGemmSWave;              // 4 KiB
+constexpr uint32_t kGemmBBase = kGemmStages * kGemmAStage;            // 48 KiB
 constexpr uint32_t kGemmSBase = kGemmBBase + kGemmStages * kGemmBStage;
-constexpr uint32_t kGemmBiasBase = kGemmSBase + kGemmStages * kGemmSStage;
-// sym: 78 KiB, affine: 84 KiB; two blocks per CU either way
+constexpr uint32_t kGemmZBase = kGemmSBase + 2u * kGemmSSlot;
+// sym: 80 KiB (two blocks per CU), affine: 88 KiB (one)
 __host__ __device__ constexpr uint32_t gemm_lds_bytes(bool sym) {
-    return kGemmBiasBase + (sym ? 0u : kGemmStages * kGemmSStage);
+    return kGemmZBase + (sym ? 0u : 2u * kGemmSSlot);
 }
-static_assert((kGemmStages - 1) * kGemmAStage + 3u * 4096u < 65536u, "A offsets fit ds offset:");
+static_assert(gemm_lds_bytes(true) * 2u <= 160u * 1024u, "two sym blocks per CU");
+
+// Chunks per scale window: 8 groups of 32 (two per chunk), or 7 of 64.
+template <int G>
+__host__ __device__ constexpr uint32_t gemm_window() { return G == 32 ? 4u : 7u; }
 
 // LDS reads as inline ds_read: the compiler cannot tell them from the
 // direct-to-LDS writes of other stages and would drain every outstanding load
@@ -239,11 +252,9 @@ __device__ __forceinline__ u32x4_t lds_read16(uint32_t addr) {
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
     return v;
 }
-template <uint32_t OFF>
-__device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
-    static_assert(OFF < 65536u, "ds offset is 16 bits");
+__device__ __forceinline__ uint32_t lds_read_u16(uint32_t addr) {
     uint32_t v;
-    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(addr));
     return v;
 }
 template <int NT>
@@ -254,6 +265,20 @@ __device__ __forceinline__ void lds_wait(u32x4_t (&a)[NT]) {
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]));
     if constexpr (NT == 4)
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]));
+    if constexpr (NT == 5)
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]));
+    if constexpr (NT == 6)
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]));
+    if constexpr (NT == 7)
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]),
+                       "+v"(a[6]));
+    if constexpr (NT == 8)
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]),
+                       "+v"(a[6]), "+v"(a[7]));
 }
 template <int NT>
 __device__ __forceinline__ void lds_wait(u32x4_t (&a)[NT], u32x4_t& b0, u32x4_t& b1, uint32_t& s0,
@@ -261,6 +286,18 @@ __device__ __forceinline__ void lds_wait(u32x4_t (&a)[NT], u32x4_t& b0, u32x4_t&
     asm volatile("" : "+v"(b0), "+v"(b1), "+v"(s0), "+v"(s1), "+v"(z0), "+v"(z1));
     lds_wait<NT>(a);
     asm volatile("" : "+v"(b0), "+v"(b1), "+v"(s0), "+v"(s1), "+v"(z0), "+v"(z1));
+}
+template <int NT, uint32_t BASE>
+__device__ __forceinline__ void lds_read_slices(u32x4_t (&a)[NT], uint32_t addr) {
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        switch (i) {
+            case 0: a[i] = lds_read16<BASE + 0u * 4096u>(addr); break;
+            case 1: a[i] = lds_read16<BASE + 1u * 4096u>(addr); break;
+            case 2: a[i] = lds_read16<BASE + 2u * 4096u>(addr); break;
+            default: a[i] = lds_read16<BASE + 3u * 4096u>(addr); break;
+        }
+    }
 }
 
 // Wait until at most N of this wave's vector memory loads are outstanding
@@ -310,26 +347,32 @@ struct GemmArgs {
 // Per-lane state of one block's GEMM.
 struct GemmLane {
     const uint8_t* blob;
-    const uint16_t* a_src[4];   // this lane's A piece for DMA j (chunk 0)
-    const uint8_t* w_src[2];    // this lane's weight bytes, tiles 0/1 (chunk 0)
-    uint32_t s_off[2], b_off[2];  // byte offsets of the lane's scale/bias for group 0 (+ 2h if G == 32)
-    uint32_t a_rd[4];           // LDS A read address per MFMA step (stage 0, slice 0)
-    uint32_t b_rd, s_rd;        // LDS weight / scale read addresses (stage 0, tile 0)
-    uint32_t wave, nchunks;
+    const uint16_t* a_src[4];   // the lane's activation piece for DMA j (chunk 0)
+    const uint8_t* w_src[2];    // the lane's weight piece per tile (chunk 0)
+    uint32_t s_ld[4], z_ld[4];  // scale / bias row starts of the rows this lane loads
+    uint32_t s_own[2], z_own[2];  // scale / bias row starts of the lane's own rows (m, tile)
+    uint32_t s_last, z_last;    // last dword of the scale / bias sub-tensors
+    uint32_t a_rd[4];           // LDS activation read address per MFMA step (stage 0, slice 0)
+    uint32_t b_rd;              // LDS weight read address (stage 0)
+    uint32_t s_rd;              // LDS scale read address of row m (slot 0)
+    uint32_t wave, nchunks, nwin;
     bool a_wave, live;
 };
 
-// Byte offset of the group-scale (or bias) halfword for chunk c relative to
-// the lane's group-0 offset; G == 32 folds the K half into the lane offset.
+// Byte offset of the first group of scale window w within a row, and of the
+// lane's group for chunk c (half h).
 template <int G>
-__device__ __forceinline__ uint32_t group_byte(uint32_t c) {
-    return G == 32 ? 4u * c : 2u * ((c * kGemmKC) / G);
+__device__ __forceinline__ uint32_t window_byte(uint32_t w) {
+    return 2u * w * (G == 32 ? 8u : 7u);
+}
+template <int G>
+__device__ __forceinline__ uint32_t group_byte(uint32_t c, uint32_t h) {
+    return G == 32 ? 4u * c + 2u * h : 2u * c;
 }
 
-// Chunk c (clamped to the last one) into ring stage ST. Every chunk issues the
-// same loads, so the vmcnt waits are exact: A 4 (if the wave moves A rows),
-// weights 2, scale dwords 2, bias dwords 2 (affine).
-template <int G, bool SYM, int ST>
+// Chunk c (clamped to the last one) into ring stage ST: activations (4 loads
+// if the wave moves activation rows) and weights (2 loads).
+template <int ST>
 __device__ __forceinline__ void gemm_issue(const GemmLane& L, uint8_t* smem, uint32_t c) {
     const uint32_t cc = c < L.nchunks ? c : L.nchunks - 1u;
     if (L.a_wave) {
@@ -337,24 +380,35 @@ __device__ __forceinline__ void gemm_issue(const GemmLane& L, uint8_t* smem, uin
 #pragma unroll
         for (int j = 0; j < 4; ++j) lds_dma16(L.a_src[j] + cc * kGemmKC, dst + j * 8u * kGemmKC * 2u);
     }
-    uint8_t* bst = smem + kGemmBBase + ST * kGemmBStage + L.wave * 2048u;
+    uint8_t* bst = smem + kGemmBBase + ST * kGemmBStage + L.wave * kGemmBWave;
     lds_dma16(L.w_src[0] + cc * (kGemmKC / 2u), bst);
-    lds_dma16(L.w_src[1] + cc * (kGemmKC / 2u), bst + 1024u);
-    const uint32_t gb = group_byte<G>(cc);
-    uint8_t* sst = smem + kGemmSBase + ST * kGemmSStage + L.wave * 512u;
-    lds_dma4(L.blob + ((L.s_off[0] + gb) & ~3u), sst);
-    lds_dma4(L.blob + ((L.s_off[1] + gb) & ~3u), sst + 256u);
+    lds_dma16(L.w_src[1] + cc * (kGemmKC / 2u), bst + kGemmBTile);
+}
+
+// Scale (and bias) window w (clamped) into slot w & 1: 4 loads (8 affine).
+template <int G, bool SYM>
+__device__ __forceinline__ void gemm_issue_scales(const GemmLane& L, uint8_t* smem, uint32_t w) {
+    const uint32_t wc = w < L.nwin ? w : L.nwin - 1u;
+    const uint32_t wb = window_byte<G>(wc);
+    const uint32_t dw = 4u * (threadIdx.x & 3u);
+    uint8_t* dst = smem + kGemmSBase + (w & 1u) * kGemmSSlot + L.wave * kGemmSWave;
+    // a window may reach past its row; bytes past the sub-tensor are never
+    // used, so those addresses are clamped to stay inside it
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t o = ((L.s_ld[j] + wb) & ~3u) + dw;
+        lds_dma4(L.blob + (o < L.s_last ? o : L.s_last), dst + j * 256u);
+    }
     if constexpr (!SYM) {
-        uint8_t* zst = smem + kGemmBiasBase + ST * kGemmSStage + L.wave * 512u;
-        lds_dma4(L.blob + ((L.b_off[0] + gb) & ~3u), zst);
-        lds_dma4(L.blob + ((L.b_off[1] + gb) & ~3u), zst + 256u);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t o = ((L.z_ld[j] + wb) & ~3u) + dw;
+            lds_dma4(L.blob + (o < L.z_last ? o : L.z_last), dst + (kGemmZBase - kGemmSBase) + j * 256u);
+        }
     }
 }
 
-// The MFMA work of chunk c (stage ST). Step s + 1's activation reads and
-// weight dequantisation are issued ahead of step s's MFMAs, which do not
-// depend on them, so the scheduler can overlap the VALU work with the matrix
-// core.
+// The MFMA work of one chunk (stage ST) for the wave's two weight tiles.
 template <int NT, int ST>
 __device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT], const u32x4_t& bw0,
                                          const u32x4_t& bw1, const GroupScale& g0,
@@ -366,16 +420,7 @@ __device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT]
     for (int st = 0; st < 4; ++st) {
         const int cur = st & 1, nxt = cur ^ 1;
         if (st < 3) {
-            const uint32_t a = L.a_rd[st + 1];
-#pragma unroll
-            for (int i = 0; i < NT; ++i) {
-                switch (i) {
-                    case 0: af[nxt][i] = lds_read16<ST * kGemmAStage + 0u * 4096u>(a); break;
-                    case 1: af[nxt][i] = lds_read16<ST * kGemmAStage + 1u * 4096u>(a); break;
-                    case 2: af[nxt][i] = lds_read16<ST * kGemmAStage + 2u * 4096u>(a); break;
-                    default: af[nxt][i] = lds_read16<ST * kGemmAStage + 3u * 4096u>(a); break;
-                }
-            }
+            lds_read_slices<NT, ST * kGemmAStage>(af[nxt], L.a_rd[st + 1]);
             bf[nxt][0] = dequant8(bw0[st + 1], g0);
             bf[nxt][1] = dequant8(bw1[st + 1], g1);
         }
@@ -389,47 +434,48 @@ __device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT]
     }
 }
 
-// One chunk: wait for it, read its weights, scales and step-0 activations,
-// run its MFMAs, then start chunk c + 2 into the stage chunk c - 1 used.
+// One chunk: wait for it, read its weights, scale and step-0 activations, run
+// its MFMAs, then start chunk c + 2 (into the stage chunk c - 1 used) and, at
+// the first chunk of a scale window, the next window.
 template <int G, bool SYM, int NT, int ST>
 __device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uint32_t c,
                                            f16v_t (&acc)[NT][2]) {
-    constexpr uint32_t kNW = SYM ? 4u : 6u;
-    // chunk c landed (chunk c + 1 may still be in flight); after the barrier
-    // every wave is done with stage (c + 2) % 3
-    if (L.a_wave) wait_vmcnt<4u + kNW>();
-    else wait_vmcnt<kNW>();
+    constexpr uint32_t W = gemm_window<G>();
+    constexpr uint32_t kNS = SYM ? 4u : 8u;
+    // Loads allowed in flight: chunk c + 1's (4 activation + 2 weight) and
+    // the scale window started at chunk c - 1 or c - 2, if any.
+    const bool s_recent = (c >= 1u && (c - 1u) % W == 0u) || (c >= 2u && (c - 2u) % W == 0u);
+    if (L.a_wave) {
+        if (s_recent) wait_vmcnt<6u + kNS>();
+        else wait_vmcnt<6u>();
+    } else {
+        if (s_recent) wait_vmcnt<2u + kNS>();
+        else wait_vmcnt<2u>();
+    }
     block_barrier();
     if (L.live) {
+        const uint32_t win = c / W, lane = threadIdx.x & 63u, h = lane >> 5;
+        const uint32_t wb = window_byte<G>(win), gb = group_byte<G>(c, h);
+        const uint32_t slot = (win & 1u) * kGemmSSlot;
         u32x4_t af[2][NT];
         u32x4_t bw0 = lds_read16<ST * kGemmBStage>(L.b_rd);
-        u32x4_t bw1 = lds_read16<ST * kGemmBStage + 1024u>(L.b_rd);
-        uint32_t sw0 = lds_read4<ST * kGemmSStage>(L.s_rd);
-        uint32_t sw1 = lds_read4<ST * kGemmSStage + 256u>(L.s_rd);
+        u32x4_t bw1 = lds_read16<ST * kGemmBStage + kGemmBTile>(L.b_rd);
+        uint32_t sw0 = lds_read_u16(L.s_rd + slot + (L.s_own[0] + gb) - ((L.s_own[0] + wb) & ~3u));
+        uint32_t sw1 = lds_read_u16(L.s_rd + 512u + slot + (L.s_own[1] + gb) - ((L.s_own[1] + wb) & ~3u));
         uint32_t zw0 = 0u, zw1 = 0u;
         if constexpr (!SYM) {
-            zw0 = lds_read4<kGemmBiasBase - kGemmSBase + ST * kGemmSStage>(L.s_rd);
-            zw1 = lds_read4<kGemmBiasBase - kGemmSBase + ST * kGemmSStage + 256u>(L.s_rd);
+            constexpr uint32_t zo = kGemmZBase - kGemmSBase;
+            zw0 = lds_read_u16(L.s_rd + zo + slot + (L.z_own[0] + gb) - ((L.z_own[0] + wb) & ~3u));
+            zw1 = lds_read_u16(L.s_rd + zo + 512u + slot + (L.z_own[1] + gb) - ((L.z_own[1] + wb) & ~3u));
         }
-#pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            switch (i) {
-                case 0: af[0][i] = lds_read16<ST * kGemmAStage + 0u * 4096u>(L.a_rd[0]); break;
-                case 1: af[0][i] = lds_read16<ST * kGemmAStage + 1u * 4096u>(L.a_rd[0]); break;
-                case 2: af[0][i] = lds_read16<ST * kGemmAStage + 2u * 4096u>(L.a_rd[0]); break;
-                default: af[0][i] = lds_read16<ST * kGemmAStage + 3u * 4096u>(L.a_rd[0]); break;
-            }
-        }
+        lds_read_slices<NT, ST * kGemmAStage>(af[0], L.a_rd[0]);
         lds_wait<NT>(af[0], bw0, bw1, sw0, sw1, zw0, zw1);
-        // the 16-bit value inside each loaded dword
-        const uint32_t gb = group_byte<G>(c);
-        const uint32_t sh0 = ((L.s_off[0] + gb) & 2u) * 8u, sh1 = ((L.s_off[1] + gb) & 2u) * 8u;
-        const uint32_t bh0 = ((L.b_off[0] + gb) & 2u) * 8u, bh1 = ((L.b_off[1] + gb) & 2u) * 8u;
-        const GroupScale g0 = group_scale<SYM>((uint16_t)(sw0 >> sh0), (uint16_t)(zw0 >> bh0));
-        const GroupScale g1 = group_scale<SYM>((uint16_t)(sw1 >> sh1), (uint16_t)(zw1 >> bh1));
+        const GroupScale g0 = group_scale<SYM>((uint16_t)sw0, (uint16_t)zw0);
+        const GroupScale g1 = group_scale<SYM>((uint16_t)sw1, (uint16_t)zw1);
         gemm_mma<NT, ST>(L, af, bw0, bw1, g0, g1, acc);
     }
-    gemm_issue<G, SYM, (ST + 2) % 3>(L, smem, c + 2u);
+    gemm_issue<(ST + 2) % 3>(L, smem, c + 2u);
+    if (c % W == 0u) gemm_issue_scales<G, SYM>(L, smem, c / W + 1u);
 }
 
 // MODE 0: gate/up + activation; MODE 1: down + scatter.
@@ -441,43 +487,55 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     L.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t K = MODE == 0 ? args.d : args.f;
     L.nchunks = K / kGemmKC;
+    L.nwin = (L.nchunks + gemm_window<G>() - 1u) / gemm_window<G>();
     L.blob = args.layer_base + (uint64_t)blk.local_slot * args.expert_stride;
     L.a_wave = L.wave < (uint32_t)NT;
 
-    // weight rows of this lane (each wave's rows are all live or all dead:
-    // d and f are multiples of 64)
+    // the wave's weight rows: tile t row r is row0[t] + r of sub-tensor t
     const uint32_t ngroups = K / G;
-    uint32_t n0, n1, ow0, ow1;
+    uint32_t row0[2], w_off[2], s_off[2], z_off[2];
     if (MODE == 0) {
-        n0 = n1 = (tile * 4u + L.wave) * 32u + m;
-        L.live = (tile * 4u + L.wave) * 32u < args.f;
-        const uint32_t r = L.live ? n0 : 0u;
-        ow0 = args.o.gate_w + r * (K / 2u);
-        ow1 = args.o.up_w + r * (K / 2u);
-        L.s_off[0] = args.o.gate_s + r * ngroups * 2u;
-        L.s_off[1] = args.o.up_s + r * ngroups * 2u;
-        L.b_off[0] = args.o.gate_b + r * ngroups * 2u;
-        L.b_off[1] = args.o.up_b + r * ngroups * 2u;
+        row0[0] = row0[1] = tile * 128u + 32u * L.wave;
+        L.live = row0[0] < args.f;
+        w_off[0] = args.o.gate_w, w_off[1] = args.o.up_w;
+        s_off[0] = args.o.gate_s, s_off[1] = args.o.up_s;
+        z_off[0] = args.o.gate_b, z_off[1] = args.o.up_b;
     } else {
-        n0 = (tile * 4u + L.wave) * 64u + m;
-        n1 = n0 + 32u;
-        L.live = (tile * 4u + L.wave) * 64u < args.d;
-        const uint32_t r0 = L.live ? n0 : 0u, r1 = L.live ? n1 : 0u;
-        ow0 = args.o.down_w + r0 * (K / 2u);
-        ow1 = args.o.down_w + r1 * (K / 2u);
-        L.s_off[0] = args.o.down_s + r0 * ngroups * 2u;
-        L.s_off[1] = args.o.down_s + r1 * ngroups * 2u;
-        L.b_off[0] = args.o.down_b + r0 * ngroups * 2u;
-        L.b_off[1] = args.o.down_b + r1 * ngroups * 2u;
+        row0[0] = tile * 256u + 64u * L.wave;
+        row0[1] = row0[0] + 32u;
+        L.live = row0[0] < args.d;
+        w_off[0] = w_off[1] = args.o.down_w;
+        s_off[0] = s_off[1] = args.o.down_s;
+        z_off[0] = z_off[1] = args.o.down_b;
     }
-    L.w_src[0] = L.blob + ow0 + h * 16u;
-    L.w_src[1] = L.blob + ow1 + h * 16u;
-    if (G == 32) {
+    const uint32_t n0 = row0[0] + m, n1 = row0[1] + m;  // output columns
+    if (!L.live) row0[0] = row0[1] = 0u;  // dead waves load row 0's data and drop it
+    auto srow = [&](int t, uint32_t r) { return s_off[t] + (row0[t] + r) * ngroups * 2u; };
+    auto zrow = [&](int t, uint32_t r) { return z_off[t] + (row0[t] + r) * ngroups * 2u; };
+    {
+        const uint32_t r = lane >> 1;
+        const uint32_t swzb = ((r >> 2) ^ (r >> 3)) & 1u;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            L.s_off[t] += 2u * h;
-            L.b_off[t] += 2u * h;
-        }
+        for (int t = 0; t < 2; ++t)
+            L.w_src[t] = L.blob + w_off[t] + (row0[t] + r) * (K / 2u) + 16u * ((lane & 1u) ^ swzb);
+    }
+    // scale DMA j brings rows 16j .. 16j + 15 of the wave's 64 (tile j / 2)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        L.s_ld[j] = srow(j >> 1, 16u * (j & 1) + (lane >> 2));
+        L.z_ld[j] = zrow(j >> 1, 16u * (j & 1) + (lane >> 2));
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        L.s_own[t] = srow(t, m);
+        L.z_own[t] = zrow(t, m);
+    }
+    {
+        const uint32_t nrows = MODE == 0 ? args.f : args.d;  // rows x groups is even
+        const uint32_t s_hi = s_off[0] > s_off[1] ? s_off[0] : s_off[1];
+        const uint32_t z_hi = z_off[0] > z_off[1] ? z_off[0] : z_off[1];
+        L.s_last = s_hi + nrows * ngroups * 2u - 4u;
+        L.z_last = z_hi + nrows * ngroups * 2u - 4u;
     }
 
     // activation DMA j of wave w moves rows 32w + 8j + l/8, lane l bringing
@@ -495,15 +553,17 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     const uint32_t swz = (m & 7u) ^ ((m >> 3) & 1u);
 #pragma unroll
     for (int st = 0; st < 4; ++st) L.a_rd[st] = base + m * kGemmKC * 2u + (((h * 4u + st) ^ swz) << 4);
-    L.b_rd = base + kGemmBBase + L.wave * 2048u + lane * 16u;
-    L.s_rd = base + kGemmSBase + L.wave * 512u + lane * 4u;
+    const uint32_t swzb_m = ((m >> 2) ^ (m >> 3)) & 1u;
+    L.b_rd = base + kGemmBBase + L.wave * kGemmBWave + 32u * m + 16u * (h ^ swzb_m);
+    L.s_rd = base + kGemmSBase + L.wave * kGemmSWave + 16u * m;
 
     f16v_t acc[NT][2];
 #pragma unroll
     for (int i = 0; i < NT; ++i) acc[i][0] = acc[i][1] = f16v_t{};
 
-    gemm_issue<G, SYM, 0>(L, smem, 0u);
-    gemm_issue<G, SYM, 1>(L, smem, 1u);
+    gemm_issue_scales<G, SYM>(L, smem, 0u);
+    gemm_issue<0>(L, smem, 0u);
+    gemm_issue<1>(L, smem, 1u);
     for (uint32_t c = 0;;) {
         gemm_chunk<G, SYM, NT, 0>(L, smem, c, acc);
         if (++c == L.nchunks) break;
@@ -512,11 +572,12 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
         gemm_chunk<G, SYM, NT, 2>(L, smem, c, acc);
         if (++c == L.nchunks) break;
     }
-    wait_vmcnt<0>();  // no LDS write may land after the block ends
+    wait_vmcnt<0>();  // no LDS write may land after this point
+
     if (!L.live) return;
 
     // acc[i][t][v] of lane l: row 32 i + 8 (v / 4) + 4 h + v % 4 of the block,
-    // weight row n_t (column l % 32 of tile t).
+    // weight row n_t (column m of tile t).
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
 #pragma unroll
@@ -524,10 +585,9 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
             const uint32_t mm = 32u * i + 8u * (v >> 2) + 4u * h + (v & 3);
             if (mm >= rows) continue;
             if (MODE == 0) {
-                const uint32_t dst = (blk.local_row + mm) * args.f;
                 const float gt = f16_to_f32(f32_to_f16(acc[i][0][v]));
                 const float up = f16_to_f32(f32_to_f16(acc[i][1][v]));
-                args.out[dst + n0] = f32_to_f16(gate_activation<ACT>(gt) * up);
+                args.out[(blk.local_row + mm) * args.f + n0] = f32_to_f16(gate_activation<ACT>(gt) * up);
             } else {
                 const tsg_token_expert_pair pr = args.pairs[blk.pair_start + mm];
                 const uint32_t dst = (pr.token * args.top_k + pr.rank) * args.d;
@@ -555,7 +615,7 @@ __device__ __forceinline__ uint32_t xcd_order(uint32_t pid, uint32_t total) {
 // 1-D grid of ntiles x (routed block capacity) workgroups; those past the
 // live count exit at once.
 template <int G, bool SYM, int ACT, int MODE>
-__global__ __launch_bounds__(256, 2) void moe_gemm_kernel(GemmArgs args) {
+__global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmArgs args) {
     extern __shared__ __align__(16) uint8_t smem[];  // gemm_lds_bytes(SYM)
     const uint32_t nb = args.n_blocks_device ? *args.n_blocks_device : args.n_blocks;
     const uint32_t total = nb * args.ntiles;
@@ -563,13 +623,19 @@ __global__ __launch_bounds__(256, 2) void moe_gemm_kernel(GemmArgs args) {
     const uint32_t item = xcd_order(blockIdx.x, total);
     const uint32_t yb = item / args.ntiles, tile = item - yb * args.ntiles;
     const tsg_routed_block blk = args.blocks[yb];
-    const uint32_t rows = blk.row_count < kGemmRows ? blk.row_count : kGemmRows;
-    switch ((rows + 31u) / 32u) {
-        case 0: return;
-        case 1: gemm_block<G, SYM, ACT, MODE, 1>(args, blk, rows, tile, smem); break;
-        case 2: gemm_block<G, SYM, ACT, MODE, 2>(args, blk, rows, tile, smem); break;
-        case 3: gemm_block<G, SYM, ACT, MODE, 3>(args, blk, rows, tile, smem); break;
-        default: gemm_block<G, SYM, ACT, MODE, 4>(args, blk, rows, tile, smem); break;
+    // a routed block wider than kGemmRows runs as consecutive passes
+    for (uint32_t r0 = 0; r0 < blk.row_count; r0 += kGemmRows) {
+        if (r0) block_barrier();  // every wave is done with the previous pass's LDS
+        tsg_routed_block sub = blk;
+        sub.pair_start += r0;
+        sub.local_row += r0;
+        const uint32_t rows = blk.row_count - r0 < kGemmRows ? blk.row_count - r0 : kGemmRows;
+        switch ((rows + 31u) / 32u) {
+            case 1: gemm_block<G, SYM, ACT, MODE, 1>(args, sub, rows, tile, smem); break;
+            case 2: gemm_block<G, SYM, ACT, MODE, 2>(args, sub, rows, tile, smem); break;
+            case 3: gemm_block<G, SYM, ACT, MODE, 3>(args, sub, rows, tile, smem); break;
+            default: gemm_block<G, SYM, ACT, MODE, 4>(args, sub, rows, tile, smem); break;
+        }
     }
 }
 
@@ -710,7 +776,7 @@ tsg_status check_layer_moe(const tsg_moe* moe, const tsg_layer* layer) {
 template <int G, bool SYM, int MODE>
 tsg_status launch_gemm(const tsg_moe* moe, hipStream_t s, const GemmArgs& a, uint32_t max_blocks) {
     GemmArgs args = a;
-    args.ntiles = MODE == 0 ? (a.f + 127u) / 128u : (a.d + 255u) / 256u;
+    args.ntiles = MODE == 0 ? (a.f + 127u) / 128u : (a.d + 255u) / 256u;  // 4 waves x 32 / 64 rows
     TSG_REQUIRE((uint64_t)args.ntiles * max_blocks <= 0x7FFFFFFFu, TSG_ERR_INVALID_ARGUMENT,
                 "moe_gemm: %u routed blocks x %u tiles exceed the grid", max_blocks, args.ntiles);
     const dim3 grid(args.ntiles * max_blocks);
@@ -720,7 +786,7 @@ tsg_status launch_gemm(const tsg_moe* moe, hipStream_t s, const GemmArgs& a, uin
     TSG_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int)gemm_lds_bytes(SYM)));
-    hipLaunchKernelGGL(kern, grid, dim3(256), gemm_lds_bytes(SYM), s, args);
+    hipLaunchKernelGGL(kern, grid, dim3(kGemmThreads), gemm_lds_bytes(SYM), s, args);
     return check_launch(MODE == 0 ? "moe_gemm gate/up" : "moe_gemm down");
 }
 
@@ -749,6 +815,13 @@ tsg_status fill_gemm_args(const tsg_moe* moe, const tsg_layer* layer, GemmArgs* 
                 "the grouped GEMM needs d=%u and f=%u to be multiples of %u", d, f, kGemmKC);
     TSG_REQUIRE(aligned16(act_in) && a_stride % 8 == 0, TSG_ERR_ALIGNMENT,
                 "activation rows must be 16-byte aligned");
+    // scale windows are fetched as dwords: 8-group windows (G = 32) need
+    // 4-byte aligned rows; 7-group windows (G = 64) tolerate 2-byte ones
+    const tsg_expert_offsets& o = layer->offsets;
+    TSG_REQUIRE(ctx->group_size != 32 || ((o.gate_s | o.up_s | o.down_s | o.gate_b | o.up_b |
+                                           o.down_b) % 4u) == 0,
+                TSG_ERR_ALIGNMENT,
+                "the grouped GEMM needs 4-byte aligned scale/bias sub-tensors at group size 32");
     *a = GemmArgs{};
     a->layer_base = layer->base;
     a->expert_stride = layer->expert_stride;
@@ -786,8 +859,8 @@ extern "C" tsg_status tsg_prefill_group_pairs_device(
     TSG_REQUIRE(k > 0, TSG_ERR_GROUPING_INVALID_TOP_K, "topK must be positive");
     TSG_REQUIRE(ne > 0 && ne <= kMaxExperts, TSG_ERR_GROUPING_INVALID_NUM_EXPERTS,
                 "numExperts %u not in 1..%u", ne, kMaxExperts);
-    TSG_REQUIRE(tile_rows == 32 || tile_rows == 64 || tile_rows == 128, TSG_ERR_INVALID_ARGUMENT,
-                "tile_rows must be 32, 64 or 128, got %u", tile_rows);
+    TSG_REQUIRE(tile_rows == 32 || tile_rows == 64 || tile_rows == 128 || tile_rows == 256,
+                TSG_ERR_INVALID_ARGUMENT, "tile_rows must be 32, 64, 128 or 256, got %u", tile_rows);
     TSG_REQUIRE(idx && w && sorted && offsets && counts && blocks && n_blocks && scratch,
                 TSG_ERR_INVALID_ARGUMENT, "NULL grouping operand");
     hipStream_t s = as_stream(stream);
