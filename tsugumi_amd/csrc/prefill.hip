@@ -508,7 +508,6 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
         s_off[0] = s_off[1] = args.o.down_s;
         z_off[0] = z_off[1] = args.o.down_b;
     }
-    const uint32_t n0 = row0[0] + m, n1 = row0[1] + m;  // output columns
     if (!L.live) row0[0] = row0[1] = 0u;  // dead waves load row 0's data and drop it
     auto srow = [&](int t, uint32_t r) { return s_off[t] + (row0[t] + r) * ngroups * 2u; };
     auto zrow = [&](int t, uint32_t r) { return z_off[t] + (row0[t] + r) * ngroups * 2u; };
@@ -574,42 +573,140 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     }
     wait_vmcnt<0>();  // no LDS write may land after this point
 
-    if (!L.live) return;
-
+    // Output: the block's tile goes through LDS (idle now) so
+    // that global stores are 16 bytes per lane along output rows.
     // acc[i][t][v] of lane l: row 32 i + 8 (v / 4) + 4 h + v % 4 of the block,
-    // weight row n_t (column m of tile t).
+    // weight row n_t (column m of tile t). Rows are padded by 16 bytes so the
+    // two half-waves' 2-byte writes (4 rows apart) fall in different banks.
+    constexpr uint32_t kCols = MODE == 0 ? 128u : 256u;  // columns per block
+    constexpr uint32_t kStride = kCols + 8u;             // halves per LDS row
+    static_assert(kGemmRows * kStride * 2u <= gemm_lds_bytes(true), "output tile fits the LDS");
+    uint16_t* otile = reinterpret_cast<uint16_t*>(smem);
+    block_barrier();  // every wave is done reading the rings
+    if (L.live) {
+        const uint32_t c0 = MODE == 0 ? 32u * L.wave + m : 64u * L.wave + m;
 #pragma unroll
-    for (int i = 0; i < NT; ++i) {
+        for (int i = 0; i < NT; ++i) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const uint32_t mm = 32u * i + 8u * (v >> 2) + 4u * h + (v & 3);
-            if (mm >= rows) continue;
-            if (MODE == 0) {
-                const float gt = f16_to_f32(f32_to_f16(acc[i][0][v]));
-                const float up = f16_to_f32(f32_to_f16(acc[i][1][v]));
-                args.out[(blk.local_row + mm) * args.f + n0] = f32_to_f16(gate_activation<ACT>(gt) * up);
-            } else {
-                const tsg_token_expert_pair pr = args.pairs[blk.pair_start + mm];
-                const uint32_t dst = (pr.token * args.top_k + pr.rank) * args.d;
-                args.out[dst + n0] = f32_to_f16(acc[i][0][v]);
-                args.out[dst + n1] = f32_to_f16(acc[i][1][v]);
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t mm = 32u * i + 8u * (v >> 2) + 4u * h + (v & 3);
+                if (MODE == 0) {
+                    const float gt = f16_to_f32(f32_to_f16(acc[i][0][v]));
+                    const float up = f16_to_f32(f32_to_f16(acc[i][1][v]));
+                    otile[mm * kStride + c0] = f32_to_f16(gate_activation<ACT>(gt) * up);
+                } else {
+                    otile[mm * kStride + c0] = f32_to_f16(acc[i][0][v]);
+                    otile[mm * kStride + c0 + 32u] = f32_to_f16(acc[i][1][v]);
+                }
             }
         }
     }
+    block_barrier();
+    const uint32_t col0 = MODE == 0 ? tile * 128u : tile * 256u;
+    const uint32_t ncols = MODE == 0 ? args.f : args.d;
+    const uint32_t live = ncols - col0 < kCols ? ncols - col0 : kCols;  // multiple of 64
+    constexpr uint32_t kPieces = kCols / 8u;  // 16-byte pieces per row
+    for (uint32_t p = threadIdx.x; p < rows * kPieces; p += kGemmThreads) {
+        const uint32_t r = p / kPieces, cg = p - r * kPieces;
+        if (cg * 8u >= live) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(otile + r * kStride + cg * 8u);
+        uint32_t dst;
+        if (MODE == 0) {
+            dst = (blk.local_row + r) * args.f;
+        } else {
+            const tsg_token_expert_pair pr = args.pairs[blk.pair_start + r];
+            dst = (pr.token * args.top_k + pr.rank) * args.d;
+        }
+        *reinterpret_cast<uint4*>(args.out + dst + col0 + cg * 8u) = v;
+    }
 }
 
-// Workgroups go to the 8 XCDs (each with its own L2) round-robin by linear
-// id. Work item order (routed block major, weight tile minor) is dealt out so
-// that each XCD runs one contiguous range of it: the tiles of a routed block
-// share its activation rows, and neighbouring routed blocks mostly share the
-// expert's weights, in the same L2 at about the same time. Bijective on
-// [0, total).
-__device__ __forceinline__ uint32_t xcd_order(uint32_t pid, uint32_t total) {
-    constexpr uint32_t kXcds = 8;
-    const uint32_t per = (total + kXcds - 1u) / kXcds;
-    const uint32_t tall = total - (per - 1u) * kXcds;  // XCDs that run `per` items
-    const uint32_t xcd = pid % kXcds, local = pid / kXcds;
-    return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1u) + local;
+// Work item of workgroup pid. Routed blocks are taken largest first (stable
+// in block order), so the long items start early and short ones fill the
+// tail; groups of 8 consecutive routed blocks are dealt one per XCD
+// (workgroups go to the 8 XCDs round-robin by linear id, each XCD with its
+// own L2) with their ntiles items on that XCD, tile-major, so the items of a
+// routed block share its activation rows in one L2. Blocks past
+// kSortBlocks keep block order. `scratch` is 64 words of LDS the caller does
+// not use yet. Bijective on [0, nb * ntiles).
+constexpr uint32_t kSortBlocks = 1024;
+
+__device__ __forceinline__ uint32_t size_bucket(uint32_t rows) {
+    const uint32_t b = (rows + 31u) / 32u;
+    return b < 8u ? b : 8u;
+}
+
+__device__ void gemm_work_item(const GemmArgs& args, uint32_t nb, uint32_t pid, uint32_t* scratch,
+                               uint32_t& yb, uint32_t& tile) {
+    const uint32_t T = args.ntiles, G = nb / 8u;
+    uint32_t j;
+    if (pid < 8u * T * G) {
+        const uint32_t rem = pid % (8u * T);
+        j = 8u * (pid / (8u * T)) + rem % 8u;
+        tile = rem / 8u;
+    } else {
+        const uint32_t q = pid - 8u * T * G;
+        j = 8u * G + q / T;
+        tile = q % T;
+    }
+    if (nb > kSortBlocks) {
+        yb = j;
+        return;
+    }
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+    uint32_t bq[kSortBlocks / kGemmThreads];
+#pragma unroll
+    for (uint32_t q = 0; q < kSortBlocks / kGemmThreads; ++q) {
+        const uint32_t jj = tid + kGemmThreads * q;
+        bq[q] = jj < nb ? size_bucket(args.blocks[jj].row_count) : 0u;
+    }
+    // per-wave bucket counts (buckets 0..8) -> scratch[9 * wave + bucket]
+#pragma unroll
+    for (uint32_t k = 0; k <= 8u; ++k) {
+        uint32_t c = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < kSortBlocks / kGemmThreads; ++q)
+            c += (uint32_t)__builtin_popcountll(__ballot(bq[q] == k));
+        if (lane == 0) scratch[9u * wv + k] = c;
+    }
+    __syncthreads();
+    // rank j in (bucket descending, block index) order: bucket kk, rank r in it
+    uint32_t kk = 0, r = 0, base = 0;
+    for (int k = 8; k >= 0; --k) {
+        uint32_t c = 0;
+        for (uint32_t w = 0; w < kGemmWaves; ++w) c += scratch[9u * w + (uint32_t)k];
+        if (j < base + c) {
+            kk = (uint32_t)k;
+            r = j - base;
+            break;
+        }
+        base += c;
+    }
+    __syncthreads();
+    // matches of bucket kk per (q, wave) segment, in block index order
+    uint64_t mask[kSortBlocks / kGemmThreads];
+#pragma unroll
+    for (uint32_t q = 0; q < kSortBlocks / kGemmThreads; ++q) {
+        mask[q] = __ballot(bq[q] == kk);
+        if (lane == 0) scratch[kGemmWaves * q + wv] = (uint32_t)__builtin_popcountll(mask[q]);
+    }
+    __syncthreads();
+    uint32_t acc = 0;
+    for (uint32_t q = 0; q < kSortBlocks / kGemmThreads; ++q) {
+        for (uint32_t w = 0; w < kGemmWaves; ++w) {
+            const uint32_t c = scratch[kGemmWaves * q + w];
+            if (r < acc + c) {
+                if (w == wv && ((mask[q] >> lane) & 1u) &&
+                    (uint32_t)__builtin_popcountll(mask[q] & ((1ull << lane) - 1ull)) == r - acc)
+                    scratch[63] = kGemmThreads * q + 64u * w + lane;
+                q = kSortBlocks;  // done
+                break;
+            }
+            acc += c;
+        }
+    }
+    __syncthreads();
+    yb = scratch[63];
 }
 
 // 1-D grid of ntiles x (routed block capacity) workgroups; those past the
@@ -620,8 +717,10 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmArgs args
     const uint32_t nb = args.n_blocks_device ? *args.n_blocks_device : args.n_blocks;
     const uint32_t total = nb * args.ntiles;
     if (blockIdx.x >= total) return;
-    const uint32_t item = xcd_order(blockIdx.x, total);
-    const uint32_t yb = item / args.ntiles, tile = item - yb * args.ntiles;
+    uint32_t yb, tile;
+    // the weight ring's last stage is first written after chunk 0's barrier
+    gemm_work_item(args, nb, blockIdx.x, reinterpret_cast<uint32_t*>(smem + kGemmBBase + 2u * kGemmBStage),
+                   yb, tile);
     const tsg_routed_block blk = args.blocks[yb];
     // a routed block wider than kGemmRows runs as consecutive passes
     for (uint32_t r0 = 0; r0 < blk.row_count; r0 += kGemmRows) {
@@ -815,6 +914,7 @@ tsg_status fill_gemm_args(const tsg_moe* moe, const tsg_layer* layer, GemmArgs* 
                 "the grouped GEMM needs d=%u and f=%u to be multiples of %u", d, f, kGemmKC);
     TSG_REQUIRE(aligned16(act_in) && a_stride % 8 == 0, TSG_ERR_ALIGNMENT,
                 "activation rows must be 16-byte aligned");
+    TSG_REQUIRE(aligned16(out), TSG_ERR_ALIGNMENT, "GEMM output must be 16-byte aligned");
     // scale windows are fetched as dwords: 8-group windows (G = 32) need
     // 4-byte aligned rows; 7-group windows (G = 64) tolerate 2-byte ones
     const tsg_expert_offsets& o = layer->offsets;
