@@ -113,6 +113,33 @@ __device__ __forceinline__ void load_expert_gains(const uint16_t* __restrict__ p
     }
 }
 
+// Softmax over the 8 selected slots (scores descending, unfilled = -inf) with
+// the per-expert gains, rounded to fp16 (moe.metal:330-342): lane r < 8 holds
+// slot r's score and gain and returns slot r's weight; the sum of the
+// exponentials runs in slot order. Shared by the wave and block selections so
+// both agree bit for bit.
+__device__ __forceinline__ uint16_t slot_softmax_lane(float my_s, float my_gain) {
+    const float my_exp = expf(my_s - lane_value(my_s, 0));
+    float sum_exp = lane_value(my_exp, 0);
+#pragma unroll
+    for (uint32_t r = 1; r < kTopK; ++r) sum_exp += lane_value(my_exp, r);
+    return (uint16_t)f32_to_f16(my_exp / sum_exp * my_gain);
+}
+
+// The same with the 8 slots' scores and gains held by every lane.
+__device__ __forceinline__ void topk_softmax8(const float (&top_s)[kTopK],
+                                              const float (&gain)[kTopK], uint16_t (&w)[kTopK]) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t r_l = lane & (kTopK - 1u);
+    float my_s = top_s[0], my_gain = gain[0];
+#pragma unroll
+    for (uint32_t r = 1; r < kTopK; ++r)
+        if (r_l == r) { my_s = top_s[r]; my_gain = gain[r]; }
+    const uint32_t my_w = slot_softmax_lane(my_s, my_gain);
+#pragma unroll
+    for (uint32_t r = 0; r < kTopK; ++r) w[r] = (uint16_t)__builtin_amdgcn_readlane(my_w, r);
+}
+
 __device__ __forceinline__ TopK wave_topk_softmax_regs(const float (&logit)[4], uint32_t ne,
                                                       const uint32_t (&pes)[4]) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -148,19 +175,7 @@ __device__ __forceinline__ TopK wave_topk_softmax_regs(const float (&logit)[4], 
                 if ((uint32_t)j == jj && lane == l) key[j] = 0u;
         }
     }
-    // softmax: lane r < 8 owns slot r's exponential; the sum runs in slot order
-    const uint32_t r_l = lane & (kTopK - 1u);
-    float my_s = top_s[0], my_gain = gain[0];
-#pragma unroll
-    for (uint32_t r = 1; r < kTopK; ++r)
-        if (r_l == r) { my_s = top_s[r]; my_gain = gain[r]; }
-    const float my_exp = expf(my_s - top_s[0]);
-    float sum_exp = lane_value(my_exp, 0);
-#pragma unroll
-    for (uint32_t r = 1; r < kTopK; ++r) sum_exp += lane_value(my_exp, r);
-    const uint32_t my_w = f32_to_f16(my_exp / sum_exp * my_gain);
-#pragma unroll
-    for (uint32_t r = 0; r < kTopK; ++r) t.w[r] = (uint16_t)__builtin_amdgcn_readlane(my_w, r);
+    topk_softmax8(top_s, gain, t.w);
     return t;
 }
 
@@ -511,88 +526,77 @@ __global__ __launch_bounds__(1024) void phase2_kernel(BlobSource src, tsg_expert
     phase2_body<G, SYM>(src, o, as, slot_h, asum, routing_w, res_bits, y, d, f, row, bt, true);
 }
 
-// ------------------------------------------------- in-launch rendezvous
+// ------------------------------------------------- in-launch hand-offs
 
-// The one-launch layer has two points where blocks need what others produced:
-// the router logits (for the top-8) and the phase-1 activations (for phase 2).
-// Neither uses a shared atomic counter (arrivals on one address serialize at
-// the memory-side atomic unit) nor has every block poll every other (the
-// polls then queue on the same few lines). Words travel by agent-coherent
-// stores and loads, tagged with the launch's epoch, along a shallow tree:
-//   - router: each expert's logit is posted as a (tag << 32 | bits) word;
-//     block 0 gathers them, runs the top-8 and posts (tag, weight, id) words
-//     to kSyncReplicas lines; block b reads line b % kSyncReplicas;
-//   - phase 1 done: block b posts flag b; the leader of each 16 blocks
-//     gathers its group and posts a group flag; block 0 gathers the groups
-//     and posts the go word to kSyncReplicas lines.
-// A word carries its own tag, so no reader can mistake an earlier launch's
-// words for this one's. The epoch (read at launch start, advanced by block 0
-// once every block has passed both rendezvous) makes each launch's tag new,
-// also across HIP graph replays. Polls are bounded by kSpinLimit; a block
-// that gives up sets the error word (reported by tsg_ctx_synchronize) and
-// carries on, so every wave reaches the end of the kernel.
+// The one-launch layer runs as kDecodeGroups groups of kGroupMembers blocks,
+// group g = block % 8 owning expert slot g. Workgroups go to the 8 XCDs
+// round-robin by linear id, so a group's blocks share one XCD and its L2; the
+// protocol below does not depend on that. No step waits for the whole grid,
+// and every hand-off is a 64-bit word carrying the launch's tag above its
+// payload, polled by its readers directly (no separate flag or counter):
+//   - every group computes all router logits (each block a few expert rows);
+//     every block gathers its group's logits and ranks them itself, so all
+//     blocks obtain the same selection, bit for bit;
+//   - each block posts the activations of its gate/up pairs; every block of
+//     the group reads the slot's full activation row once all have arrived;
+//   - each block posts fp32 partial down outputs of its slot; block (g, m)
+//     then reads the 8 slots' partials of its share of row range m and
+//     writes y = half(res + sum_s w_s v_s) in slot order.
+// Tags come from the epoch word read at launch start, so no reader can take
+// an earlier launch's word for this one's. Block 0 advances the epoch once
+// its combine has read partials from all 8 groups: each of those blocks had
+// read its whole group's activations, so by then all 256 blocks have read
+// the epoch. Polls are bounded by kSpinLimit; a block that gives up sets the
+// error word (reported by tsg_ctx_synchronize) and carries on, so every wave
+// reaches the end.
 constexpr uint32_t kSpinLimit = 1u << 20;
-constexpr uint32_t kSyncFanIn = 16;
 
 struct DecodeSync {
     uint32_t* epoch;
     uint32_t* error;
-    uint32_t* flags;
-    uint32_t* groups;
-    uint32_t* go;       // kSyncReplicas lines
-    uint64_t* topk;     // kSyncReplicas lines of kTopK words
-    uint64_t* logits;   // kMaxExperts words
+    uint64_t* logits;   // kMaxExperts words per group
 };
 
 __device__ __forceinline__ DecodeSync decode_sync(uint32_t* words) {
     DecodeSync s;
     s.epoch = words + kSyncEpochWord;
     s.error = words + kSyncErrorWord;
-    s.flags = words + kSyncFlagWord;
-    s.groups = words + kSyncGroupWord;
-    s.go = words + kSyncGoWord;
-    s.topk = reinterpret_cast<uint64_t*>(words + kSyncTopkWord);
     s.logits = reinterpret_cast<uint64_t*>(words + kSyncLogitWord);
     return s;
 }
 
-// One wave polls until `ready()` holds on every lane (bounded).
-template <typename F>
-__device__ __forceinline__ void wave_poll(const DecodeSync& sy, F&& ready) {
+__device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t payload) {
+    return ((uint64_t)tag << 32) | payload;
+}
+
+// One wave reads up to N tagged words per lane (word k at addr(k), for k in
+// `live`, a lane's bit mask) until each carries `tag`, handing each payload to
+// use(k, payload) once; every pass re-reads only the words still missing, so
+// words already in cost no further traffic. Bounded: after kSpinLimit passes
+// the wave sets the error word and returns.
+template <int N, typename Addr, typename Use>
+__device__ __forceinline__ void poll_tagged(const DecodeSync& sy, uint32_t tag, uint32_t live,
+                                            Addr&& addr, Use&& use) {
+    uint32_t pending = live;
     for (uint32_t spins = 0;; ++spins) {
-        if (__all(ready())) return;
+        uint64_t w[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if (pending & (1u << k)) w[k] = ld_coherent(addr(k));
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            if ((pending & (1u << k)) && (uint32_t)(w[k] >> 32) == tag) {
+                use(k, (uint32_t)w[k]);
+                pending &= ~(1u << k);
+            }
+        }
+        if (__all(pending == 0u)) return;
         if (spins > kSpinLimit) {
             if ((threadIdx.x & 63u) == 0) atomicOr(sy.error, 1u);
             return;
         }
         __builtin_amdgcn_s_sleep(1);
     }
-}
-
-// One wave: `count` packed words at `w` all equal `tag`.
-__device__ __forceinline__ void wave_wait_words(const DecodeSync& sy, const uint32_t* w,
-                                                uint32_t count, uint32_t tag) {
-    const uint32_t lane = threadIdx.x & 63u;
-    wave_poll(sy, [&] {
-        bool ok = true;
-        for (uint32_t i = lane; i < count; i += 64u) ok = ok && ld_coherent(w + i) == tag;
-        return ok;
-    });
-}
-
-// One wave: every block of the launch has posted flag == tag.
-__device__ __forceinline__ void rendezvous_all(const DecodeSync& sy, uint32_t nb, uint32_t tag) {
-    const uint32_t b = blockIdx.x, lane = threadIdx.x & 63u;
-    if (b % kSyncFanIn == 0) {
-        const uint32_t n = min(kSyncFanIn, nb - b);
-        wave_wait_words(sy, sy.flags + b, n, tag);
-        if (lane == 0) st_coherent(sy.groups + b / kSyncFanIn, tag);
-    }
-    if (b == 0) {
-        wave_wait_words(sy, sy.groups, (nb + kSyncFanIn - 1) / kSyncFanIn, tag);
-        if (lane < kSyncReplicas) st_coherent(sy.go + lane * kSyncLineWords, tag);
-    }
-    wave_wait_words(sy, sy.go + (b % kSyncReplicas) * kSyncLineWords, 1u, tag);
 }
 
 // -------------------------------------------------- fused decode layer
@@ -611,135 +615,336 @@ struct DecodeLayerArgs {
     uint32_t* out_idx;
     uint16_t* out_w;
     uint16_t* acts;
-    uint16_t* act_rep;  // kActReplicas copies of the activations
+    uint64_t* handoff;    // kDecodeGroups regions of kHandoffWords tagged words
     uint32_t* sync_words;
-    uint32_t ne, d, f, pairs_per_block, rows_per_block;
+    uint32_t ne, d, f;
+    uint32_t router_rows;  // expert rows per block: ceil(ne / kGroupMembers)
+    uint32_t pairs;        // gate/up pairs per block: ceil(f / kGroupMembers)
+    uint32_t rows;         // down rows per block: ceil(d / kGroupMembers)
+    uint32_t as_off;       // dynamic LDS: staged activation row (after x)
+    uint32_t xe_off;       // dynamic LDS: router products x * es, fp32
 };
 
-// One decode MoE layer in one launch (grid = one block per CU, all
-// co-resident): router logits (one expert row per block, the router kernel's
-// canonical order) -> rendezvous, every block runs the top-k -> prefetch of
-// its down-projection weights, gate/up + activation for its row pairs ->
-// rendezvous -> down + slot-ordered combine for its output rows. The
-// arithmetic of every phase is the separate kernels' (shared bodies), so the
-// fused and unfused paths agree bit for bit.
-template <int G, bool SYM, int ACT>
-__global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ uint32_t s_tag;
-    __shared__ uint16_t s_w[kTopK];
-    __shared__ uint32_t s_idx[kTopK];
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t nb = gridDim.x;
-    const DecodeSync sy = decode_sync(a.sync_words);
-    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-    float* xsum = reinterpret_cast<float*>(smem + lds_chunks_halves(a.d) * 2u);
-
-    uint32_t gains[4] = {0u, 0u, 0u, 0u};
-    if (blockIdx.x == 0 && wave == 0) load_expert_gains(a.pes, a.ne, gains);
-    uint32_t tag = 0;
-    if (threadIdx.x == 0) {
-        tag = ld_coherent(sy.epoch) + 1u;
-        tag = tag ? tag : 1u;
-        s_tag = tag;
+// Down row `row` of one slot on 8 lanes (lane = 8 r + j of the wave): the
+// per-slot value of phase2_body, the same chunk split and the same sum, so
+// the combine below reproduces the unfused path bit for bit.
+template <int G, bool SYM>
+__device__ __forceinline__ float slot_down_row(const uint8_t* w, const uint16_t* sc,
+                                               const uint16_t* bi, const uint16_t* as,
+                                               const float* asum, uint32_t f,
+                                               ChunkBatch<kDBatch>& bt) {
+    const uint32_t j = threadIdx.x & 7u, nchunks = f / 32u;
+    float acc[1] = {0.0f};
+    for (uint32_t base = 0; base < nchunks; base += kDLanes * kDBatch) {
+        if (base) load_batch<G, SYM, kDBatch, kDLanes>(w, sc, bi, base, j, nchunks, bt);
+        compute_batch<G, SYM, kDBatch, kDLanes, 1>(bt, base, j, nchunks, as, 0u, asum, 1u, acc);
     }
-    // router rows: wave 0 of block b takes experts b, b + nb, ...
-    if (wave == 0)
-        for (uint32_t e = blockIdx.x; e < a.ne; e += nb) {
-            const float s = router_dot(a.router_w + (uint64_t)e * a.d, a.router_hidden, a.es,
-                                       a.d, lane);
-            if (lane == 0)
-                st_coherent(sy.logits + e, ((uint64_t)tag << 32) | __float_as_uint(s));
+    return group8_sum(acc[0]);
+}
+
+// router_chunks_dot with the products x * es taken from LDS (fp32, element
+// order): the same products and the same fma order, so the same sum.
+__device__ __forceinline__ float router_dot_staged(const uint4 (&wv)[kRouterChunks],
+                                                   const float* xe, uint32_t nchunks,
+                                                   uint32_t lane) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRouterChunks; ++i) {
+        const uint32_t c = lane + 64u * i;
+        if (c >= nchunks) break;
+        const float4 p0 = *reinterpret_cast<const float4*>(xe + c * 8u);
+        const float4 p1 = *reinterpret_cast<const float4*>(xe + c * 8u + 4u);
+        const float p[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        const uint32_t wa[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            acc = __builtin_fmaf(__uint_as_float(wa[k] << 16), p[2 * k], acc);
+            acc = __builtin_fmaf(__uint_as_float(wa[k] & 0xFFFF0000u), p[2 * k + 1], acc);
         }
-    stage_act_rows<SYM>(a.x, 0u, 1u, a.d, xs, 0u, xsum);
+    }
+    acc = group16_sum(acc);
+    return (lane_value(acc, 0) + lane_value(acc, 16)) + (lane_value(acc, 32) + lane_value(acc, 48));
+}
+
+__device__ __forceinline__ uint32_t row16_max(uint32_t k) {
+    k = max(k, dpp_u32<0xB1>(k));   // quad_perm [1,0,3,2]
+    k = max(k, dpp_u32<0x4E>(k));   // quad_perm [2,3,0,1]
+    k = max(k, dpp_u32<0x141>(k));  // row_half_mirror
+    k = max(k, dpp_u32<0x140>(k));  // row_mirror
+    return k;
+}
+
+// Top-8 on one wave over the order keys of experts lane + 64 j (0 = not
+// eligible; keys of experts >= ne are 0), with the reference's rule
+// (moe.metal:281-329): descending score, ties to the lower index, -inf and
+// NaN never enter. T, the least of the maxima of the eight 16-expert groups
+// of experts 0..127, has at least 8 keys at or above it, so an expert below T
+// ranks 8th or later; the experts at or above T (the candidates, typically a
+// few dozen) are ranked among themselves by composite key (key << 32 | ~e:
+// by score, then lower expert, no two equal) and rank r < 8 takes slot r. A
+// slot whose expert is not eligible, or that no candidate reaches, keeps its
+// preset (expert 0, unfilled, -inf). `cand` holds ne4 + 1 words, `ncand` is
+// zeroed and the slots preset before the call.
+__device__ __forceinline__ void wave_select_top8(const uint32_t (&key)[4], uint32_t ne4,
+                                                 uint64_t* cand, uint32_t* ncand,
+                                                 uint32_t* slot_id, uint32_t* slot_fill,
+                                                 uint32_t* slot_key) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t m = min(row16_max(key[0]), row16_max(key[1]));
+    const auto a = __builtin_amdgcn_permlane16_swap(m, m, false, false);
+    m = min(m, min((uint32_t)a[0], (uint32_t)a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(m, m, false, false);
+    m = min(m, min((uint32_t)b[0], (uint32_t)b[1]));
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t e = lane + 64u * j;
+        if (e < ne4 && key[j] >= m) {
+            const uint32_t pos = atomicAdd(ncand, 1u);
+            cand[pos] = ((uint64_t)key[j] << 32) | (uint32_t)~e;
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // LDS ops of one wave run in order
+    const uint32_t n = *ncand;
+    if (lane == 0) cand[n] = 0u;  // pad: 0 exceeds no candidate
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    for (uint32_t i = lane; i < n; i += 64u) {
+        const uint64_t ki = cand[i];
+        uint32_t c = 0;
+        for (uint32_t q = 0; q < n; q += 2u) {
+            const ulonglong2 kk = *reinterpret_cast<const ulonglong2*>(cand + q);
+            c += kk.x > ki ? 1u : 0u;
+            c += kk.y > ki ? 1u : 0u;
+        }
+        if (c < kTopK) {
+            const uint32_t k = (uint32_t)(ki >> 32);
+            slot_id[c] = k ? ~(uint32_t)ki : 0u;
+            slot_fill[c] = k ? 1u : 0u;
+            slot_key[c] = k;
+        }
+    }
+}
+
+// One decode MoE layer in one launch (kDecodeBlocks blocks, all co-resident).
+// Per group g: router logits -> top-8 (every block) -> gate/up + activation of
+// slot g (pairs per block) -> down rows of slot g -> partials -> slot-ordered
+// combine. The arithmetic of every phase is the separate kernels' (shared
+// bodies), so the fused and unfused paths agree bit for bit. Wave roles:
+// waves < router_rows compute a router row each; wave 0 gathers the logits,
+// selects, and combines; wave w < pairs / 2 computes gate/up pairs 2w, 2w+1;
+// wave w < rows / 8 computes 8 down rows; the last wave (no down rows, so no
+// weight loads ahead of its polls) reads the slot's activations into LDS.
+template <int G, bool SYM, int ACT>
+__global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_arg) {
+    // The arguments are copied to LDS once: under SGPR pressure the compiler
+    // re-reads kernel arguments instead of spilling, and a kernarg reload in
+    // a loop costs a memory round trip each time; an LDS copy costs cycles.
+    __shared__ DecodeLayerArgs a;
+    static_assert(sizeof(DecodeLayerArgs) % 4 == 0 && sizeof(DecodeLayerArgs) <= 4 * 64, "args copy");
+    if (threadIdx.x < sizeof(DecodeLayerArgs) / 4)
+        reinterpret_cast<uint32_t*>(&a)[threadIdx.x] = reinterpret_cast<const uint32_t*>(&a_arg)[threadIdx.x];
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ uint32_t s_tag, s_ncand;
+    __shared__ uint16_t s_w[kTopK];
+    __shared__ uint32_t s_idx[kTopK], s_fill[kTopK], s_skey[kTopK];
+    __shared__ uint32_t s_gains[kMaxExperts];
+    __shared__ __align__(16) uint64_t s_cand[kMaxExperts + 2];
+    const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
+    const uint32_t grp = blockIdx.x % kDecodeGroups, mem = blockIdx.x / kDecodeGroups;
+    if (t < kTopK) {
+        s_idx[t] = 0u;
+        s_fill[t] = 0u;
+        s_skey[t] = 0u;
+    }
+    if (t == 0) s_ncand = 0u;
     __syncthreads();
-    tag = s_tag;
+    const uint32_t d = a.d, f = a.f, ne = a.ne;
+    const uint8_t* layer_base = global_ptr(a.layer_base);
+    const DecodeSync sy = decode_sync(global_ptr(a.sync_words));
+    uint64_t* handoff = global_ptr(a.handoff);
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+    float* xsum = reinterpret_cast<float*>(smem + lds_chunks_halves(d) * 2u);
+    uint16_t* as = reinterpret_cast<uint16_t*>(smem + a.as_off);
+    float* asum = reinterpret_cast<float*>(smem + a.as_off + p2_slot_halves(f) * 2u);
+    float* xe = reinterpret_cast<float*>(smem + a.xe_off);
+    uint64_t* logits = sy.logits + grp * kMaxExperts;
+    uint64_t* gacts = handoff + (size_t)grp * kHandoffWords;
+    const uint32_t nwaves = blockDim.x >> 6;
+
+    // Every load of the first phase goes out before any is waited for: the
+    // epoch, the per-expert gains, x for the gate/up dot products, x and es
+    // for the router products, and this wave's router row.
+    uint32_t epoch = 0;
+    if (t == 0) epoch = ld_coherent(sy.epoch);
+    const uint32_t gain = t < ne ? global_ptr(a.pes)[t] : 0u;
+    const uint32_t units = d / 8u;  // units <= 2 * blockDim (host-checked)
+    const bool two = units > blockDim.x;
+    const uint16_t* xg = global_ptr(a.x);
+    const uint16_t* hg = global_ptr(a.router_hidden);
+    const uint16_t* eg = global_ptr(a.es);
+    uint4 xv[2], hv[2], ev[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (i == 1 && !two) break;
+        const uint32_t q = min(t + i * blockDim.x, units - 1u) * 8u;
+        xv[i] = *reinterpret_cast<const uint4*>(xg + q);
+        hv[i] = *reinterpret_cast<const uint4*>(hg + q);
+        ev[i] = *reinterpret_cast<const uint4*>(eg + q);
+    }
+    const uint32_t er = mem * a.router_rows + wave;
+    const bool router_wave = wave < a.router_rows && er < ne;
+    uint4 rw[kRouterChunks];
+    if (router_wave) {
+        const uint16_t* w_row = global_ptr(a.router_w) + (uint64_t)er * d;
+#pragma unroll
+        for (int i = 0; i < kRouterChunks; ++i)
+            rw[i] = *reinterpret_cast<const uint4*>(w_row + min(lane + 64u * i, units - 1u) * 8u);
+    }
+    if (t < kMaxExperts) s_gains[t] = gain;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t q = t + i * blockDim.x;
+        if (q >= units) break;
+        *reinterpret_cast<uint4*>(xs + (q >> 2) * kChunkLds + (q & 3u) * 8u) = pair_permute(xv[i]);
+        const uint32_t hw[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w};
+        const uint32_t ew[4] = {ev[i].x, ev[i].y, ev[i].z, ev[i].w};
+        float p[8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            p[2 * k] = f16_to_f32((uint16_t)(hw[k] & 0xFFFFu)) * __uint_as_float(ew[k] << 16);
+            p[2 * k + 1] = f16_to_f32((uint16_t)(hw[k] >> 16)) * __uint_as_float(ew[k] & 0xFFFF0000u);
+        }
+        *reinterpret_cast<float4*>(xe + q * 8u) = make_float4(p[0], p[1], p[2], p[3]);
+        *reinterpret_cast<float4*>(xe + q * 8u + 4u) = make_float4(p[4], p[5], p[6], p[7]);
+    }
+    if (t == 0) {
+        const uint32_t tag = epoch + 1u;
+        s_tag = tag ? tag : 1u;
+    }
+    __syncthreads();
+    const uint32_t tag = s_tag;
+    if (router_wave) {
+        const float s = router_dot_staged(rw, xe, units, lane);
+        if (lane == 0) st_coherent(logits + er, tagged(tag, __float_as_uint(s)));
+    }
+    if constexpr (!SYM) staged_chunk_sums(xs, 0u, 1u, d, xsum);
+
+    // wave 0 gathers the group's logits and selects; the block waits once
+    const uint32_t ne4 = (ne + 3u) & ~3u;
     if (wave == 0) {
-        if (blockIdx.x == 0) {
-            // gather the logits, run the top-8, post it to every replica line
-            float v[4];
-            wave_poll(sy, [&] {
-                bool ok = true;
+        uint32_t key[4] = {0u, 0u, 0u, 0u};
+        uint32_t live = 0;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t e = lane + 64u * j;
-                    v[j] = -INFINITY;
-                    if (e < a.ne) {
-                        const uint64_t w = ld_coherent(sy.logits + e);
-                        v[j] = __uint_as_float((uint32_t)w);
-                        ok = ok && (uint32_t)(w >> 32) == tag;
-                    }
-                }
-                return ok;
-            });
-            const TopK t = wave_topk_softmax_regs(v, a.ne, gains);
-            const uint32_t r = lane & (kTopK - 1u);
-            uint32_t id = 0, wb = 0;
-#pragma unroll
-            for (uint32_t q = 0; q < kTopK; ++q)
-                if (r == q) { id = t.idx[q]; wb = t.w[q]; }
-            for (uint32_t q = lane / kTopK; q < kSyncReplicas; q += 64u / kTopK)
-                st_coherent(sy.topk + q * (kSyncLineWords / 2) + r,
-                            ((uint64_t)tag << 32) | (wb << 16) | id);
-            if (lane < kTopK) {
-                a.out_idx[lane] = id;
-                a.out_w[lane] = (uint16_t)wb;
+        for (uint32_t j = 0; j < 4; ++j) live |= lane + 64u * j < ne ? 1u << j : 0u;
+        poll_tagged<4>(sy, tag, live, [&](int j) { return logits + lane + 64u * j; },
+                       [&](int j, uint32_t bits) {
+                           const float v = __uint_as_float(bits);
+                           key[j] = (v == v && v != -INFINITY) ? order_key(v) : 0u;
+                       });
+        wave_select_top8(key, ne4, s_cand, &s_ncand, s_idx, s_fill, s_skey);
+    }
+    __syncthreads();
+
+    // gate/up pairs of slot grp: mem * pairs + t / 32
+    const uint32_t pl = t >> 5;
+    const uint32_t fr = mem * a.pairs + pl;
+    const bool pair_live = pl < a.pairs && fr < f;
+    const LdsBlobs src{layer_base, a.expert_stride, s_idx};
+    const bool gu_wave = 2u * wave < a.pairs;
+    ChunkBatch<kGUBatch> gbt;
+    GULane l{};
+    if (gu_wave) {
+        l = gu_lane(src, a.o, d, G, pair_live ? grp : 0u, pair_live ? fr : 0u, pair_live);
+        load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, 0u, t & 15u, d / 32u, gbt);
+    }
+    // the slot weights (needed only by the combine) while the loads fly
+    if (wave == 0) {
+        const uint32_t r = lane & (kTopK - 1u);
+        const uint32_t id = s_idx[r];
+        const float my_s = s_fill[r] ? order_key_value(s_skey[r]) : -INFINITY;
+        const uint16_t w = slot_softmax_lane(my_s, bf16_to_f32((uint16_t)s_gains[id]));
+        if (lane < kTopK) {
+            s_w[lane] = w;
+            if (blockIdx.x == 0) {
+                global_ptr(a.out_idx)[lane] = id;
+                global_ptr(a.out_w)[lane] = w;
             }
         }
-        const uint64_t* line = sy.topk + (blockIdx.x % kSyncReplicas) * (kSyncLineWords / 2);
-        uint64_t w = 0;
-        wave_poll(sy, [&] {
-            if (lane >= kTopK) return true;
-            w = ld_coherent(line + lane);
-            return (uint32_t)(w >> 32) == tag;
-        });
-        if (lane < kTopK) {
-            s_idx[lane] = (uint32_t)w & 0xFFFFu;
-            s_w[lane] = (uint16_t)(w >> 16);
+    }
+    if (gu_wave) {
+        uint16_t act;
+        if (phase1_compute<G, SYM, ACT>(l, gbt, xs, xsum, d, act)) {
+            global_ptr(a.acts)[grp * f + fr] = act;
+            st_coherent(gacts + fr, tagged(tag, act));
         }
     }
-    __syncthreads();
 
-    const LdsBlobs src{a.layer_base, a.expert_stride, s_idx};
-    const uint32_t row = blockIdx.x * a.rows_per_block + wave;
+    // this block's down rows (8 per wave) stream while the group finishes
+    const uint8_t* blob = layer_base + (uint64_t)s_idx[grp] * a.expert_stride;
+    const uint32_t rl = 8u * wave + (lane >> 3);
+    const uint32_t row = mem * a.rows + rl;
+    const bool row_live = rl < a.rows && row < d;
+    const bool down_wave = 8u * wave < a.rows;
+    const uint32_t rr = row_live ? row : 0u;
+    const uint32_t fgroups = f / G;
+    const uint8_t* dw = blob + a.o.down_w + (uint64_t)rr * (f / 2u);
+    const uint16_t* dsc = reinterpret_cast<const uint16_t*>(blob + a.o.down_s) + (uint64_t)rr * fgroups;
+    const uint16_t* dbi = reinterpret_cast<const uint16_t*>(blob + a.o.down_b) + (uint64_t)rr * fgroups;
     ChunkBatch<kDBatch> dbt;
-    uint16_t res_bits = 0;
-    const bool p2_wave = wave < a.rows_per_block;
-    if (p2_wave) phase2_prefetch<G, SYM>(src, a.o, a.residual, a.d, a.f, row, dbt, res_bits);
-    {
-        const uint32_t pair = blockIdx.x * a.pairs_per_block + (threadIdx.x >> 5);
-        const bool live = (threadIdx.x >> 5) < a.pairs_per_block && pair < kTopK * a.f;
-        const uint32_t pp = live ? pair : 0u;
-        const uint32_t slot = pp / a.f;
-        const GULane l = gu_lane(src, a.o, a.d, G, slot, pp - slot * a.f, live);
-        ChunkBatch<kGUBatch> gbt;
-        load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, 0u, threadIdx.x & 15u, a.d / 32u, gbt);
-        uint16_t v;
-        if (phase1_compute<G, SYM, ACT>(l, gbt, xs, xsum, a.d, v)) {
-            const uint32_t at = l.slot * a.f + l.fr;
-            a.acts[at] = v;
+    if (down_wave) load_batch<G, SYM, kDBatch, kDLanes>(dw, dsc, dbi, 0u, lane & 7u, f / 32u, dbt);
+
+    // once this block's gate/up work is out, the last wave reads the slot's
+    // activation row into LDS as its words arrive
+    __syncthreads();
+    if (wave == nwaves - 1u) {
+        for (uint32_t i0 = 0; i0 < f; i0 += 64u * 16u) {
+            uint32_t live = 0;
 #pragma unroll
-            for (uint32_t r = 0; r < kActReplicas; ++r)
-                st_coherent(a.act_rep + (size_t)r * kActReplicaHalves + at, v);
+            for (uint32_t k = 0; k < 16; ++k) live |= i0 + lane + 64u * k < f ? 1u << k : 0u;
+            poll_tagged<16>(sy, tag, live, [&](int k) { return gacts + i0 + lane + 64u * k; },
+                            [&](int k, uint32_t bits) {
+                                const uint32_t i = i0 + lane + 64u * k, c = i & 31u;
+                                as[(i >> 5) * kChunkLds + (c >> 3) * 8u + paired_pos(c & 7u)] =
+                                    (uint16_t)bits;
+                            });
         }
     }
-    wait_vector_memory();  // this wave's activation stores have completed
     __syncthreads();
-    if (threadIdx.x == 0) st_coherent(sy.flags + blockIdx.x, tag);
-    if (wave == 0) rendezvous_all(sy, nb, tag);
-    __syncthreads();
+    if constexpr (!SYM) {
+        staged_chunk_sums(as, 0u, 1u, f, asum);
+        __syncthreads();
+    }
+    uint64_t* parts = handoff + kMaxFusedDim;  // slot g's partials at g * kHandoffWords
+    if (down_wave) {
+        const float v = slot_down_row<G, SYM>(dw, dsc, dbi, as, asum, f, dbt);
+        if ((lane & 7u) == 0 && row_live)
+            st_coherent(parts + (size_t)grp * kHandoffWords + row, tagged(tag, __float_as_uint(v)));
+    }
 
-    const uint32_t slot_h = p2_slot_halves(a.f);
-    uint16_t* as = reinterpret_cast<uint16_t*>(smem);
-    float* asum = reinterpret_cast<float*>(smem + kTopK * slot_h * 2u);
-    stage_act_rows<SYM, 4, true>(a.act_rep + (size_t)(blockIdx.x % kActReplicas) * kActReplicaHalves,
-                                 a.f, kTopK, a.f, as, slot_h, asum);
-    __syncthreads();
-    if (p2_wave)
-        phase2_body<G, SYM>(src, a.o, as, slot_h, asum, s_w, res_bits, a.y, a.d, a.f, row,
-                            dbt, true);
-    // every block has passed both rendezvous: the next launch may use tag + 1
-    if (blockIdx.x == 0 && threadIdx.x == 0) st_coherent(sy.epoch, tag);
+    // this block's share of row range mem: y = half(res + sum_s w_s v_s) in
+    // slot order (moe.metal:678-686)
+    if (wave == 0) {
+        const uint32_t share = (a.rows + kDecodeGroups - 1u) / kDecodeGroups;
+        const uint32_t cl = grp * share + lane;
+        const uint32_t crow = mem * a.rows + cl;
+        const bool live = lane < share && cl < a.rows && crow < d;
+        const uint16_t res = global_ptr(a.residual)[live ? crow : 0u];
+        float vq[kTopK];
+        poll_tagged<kTopK>(sy, tag, live ? 0xFFu : 0u,
+                           [&](int q) { return parts + (size_t)q * kHandoffWords + crow; },
+                           [&](int q, uint32_t bits) { vq[q] = __uint_as_float(bits); });
+        if (live) {
+            float out = f16_to_f32(res);
+#pragma unroll
+            for (uint32_t q = 0; q < kTopK; ++q) {
+                const float p = f16_to_f32(s_w[q]) * vq[q];
+                out = out + p;
+            }
+            global_ptr(a.y)[crow] = f32_to_f16(out);
+        }
+        // block 0 has now seen every group's partials: the next launch may
+        // use tag + 1
+        if (blockIdx.x == 0 && lane == 0) st_coherent(sy.epoch, tag);
+    }
 }
 
 // ------------------------------------------------------------ host helpers
@@ -870,31 +1075,36 @@ tsg_status phase2_dispatch(tsg_moe* moe, hipStream_t stream, const BlobSource& s
 // once (the rendezvous need all blocks resident). Returns TSG_ERR_DECLINED
 // otherwise and the caller runs the three-kernel sequence.
 template <int G, bool SYM, int ACT>
-tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, const DecodeLayerArgs& a,
-                        const DecodeGeometry& g) {
-    const uint32_t nb = g.p1_blocks > g.p2_blocks ? g.p1_blocks : g.p2_blocks;
-    const size_t lds_a = lds_chunks_halves(a.d) * 2u + (SYM ? 0u : (a.d / 32u) * 4u);
-    const size_t lds_b = phase2_lds(a.f, SYM);
-    const size_t lds = lds_a > lds_b ? lds_a : lds_b;
+tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
+    const auto up64 = [](uint32_t v) { return (v + 63u) / 64u * 64u; };
+    uint32_t threads = 32u * a.pairs;                               // gate/up pairs
+    threads = std::max(threads, 64u * ((a.rows + 7u) / 8u + 1u));    // down rows, 8 per wave, + poll wave
+    threads = std::max(threads, 64u * a.router_rows);                // router rows
+    threads = std::max(threads, up64((a.d / 8u + 1u) / 2u));         // x in two 16-byte units
+    const uint32_t xs_bytes = lds_chunks_halves(a.d) * 2u + (SYM ? 0u : (a.d / 32u) * 4u);
+    const uint32_t as_bytes = p2_slot_halves(a.f) * 2u + (SYM ? 0u : (a.f / 32u) * 4u);
+    a.as_off = (xs_bytes + 15u) & ~15u;
+    a.xe_off = (a.as_off + as_bytes + 15u) & ~15u;
+    const size_t lds = a.xe_off + a.d * 4u;
     auto kern = decode_layer_kernel<G, SYM, ACT>;
     int per_cu = 0;
-    if (nb > kMaxFusedBlocks || a.ne > kMaxExperts || kTopK * a.f > kActReplicaHalves ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, (int)g.threads, lds) !=
+    if (threads > 1024u || a.ne > kMaxExperts || a.f > kMaxFusedDim || a.d > kMaxFusedDim ||
+        (a.rows + kDecodeGroups - 1u) / kDecodeGroups > 64u ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, (int)threads, lds) !=
             hipSuccess ||
-        (uint64_t)per_cu * (uint64_t)moe->ctx->num_cus < nb)
+        (uint64_t)per_cu * (uint64_t)moe->ctx->num_cus < kDecodeBlocks)
         return TSG_ERR_DECLINED;
-    hipLaunchKernelGGL(kern, dim3(nb), dim3(g.threads), lds, stream, a);
+    hipLaunchKernelGGL(kern, dim3(kDecodeBlocks), dim3(threads), lds, stream, a);
     return check_launch("decode_layer");
 }
 
-tsg_status fused_dispatch(tsg_moe* moe, hipStream_t stream, const DecodeLayerArgs& a,
-                          const DecodeGeometry& g) {
+tsg_status fused_dispatch(tsg_moe* moe, hipStream_t stream, const DecodeLayerArgs& a) {
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
     const bool silu = moe->activation == TSG_ACT_SILU;
 #define TSG_FU(GG, SS)                                                             \
-    return silu ? launch_fused<GG, SS, TSG_ACT_SILU>(moe, stream, a, g)            \
-                : launch_fused<GG, SS, TSG_ACT_GELU_TANH>(moe, stream, a, g)
+    return silu ? launch_fused<GG, SS, TSG_ACT_SILU>(moe, stream, a)               \
+                : launch_fused<GG, SS, TSG_ACT_GELU_TANH>(moe, stream, a)
     if (ctx->group_size == 32) {
         if (sym) TSG_FU(32, true);
         TSG_FU(32, false);
@@ -1092,7 +1302,6 @@ extern "C" tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream,
     TSG_REQUIRE(d % 8 == 0 && d <= 8u * 64u * kRouterChunks, TSG_ERR_INVALID_ARGUMENT,
                 "d=%u out of the router's range", d);
     hipStream_t s = as_stream(stream);
-    const DecodeGeometry g = decode_geometry(d, f, kTopK * f, kTargetBlocks);
     DecodeLayerArgs a{};
     a.layer_base = layer->base;
     a.expert_stride = layer->expert_stride;
@@ -1108,14 +1317,15 @@ extern "C" tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream,
     a.out_w = out_w;
     a.acts = acts;
     a.sync_words = moe->ctx->counters;
-    a.act_rep = moe->ctx->act_replicas;
+    a.handoff = reinterpret_cast<uint64_t*>(moe->ctx->act_replicas);
     a.ne = ne;
     a.d = d;
     a.f = f;
-    a.pairs_per_block = g.pairs_per_block;
-    a.rows_per_block = g.rows_per_block;
+    a.router_rows = (ne + kGroupMembers - 1u) / kGroupMembers;
+    a.pairs = (f + kGroupMembers - 1u) / kGroupMembers;
+    a.rows = (d + kGroupMembers - 1u) / kGroupMembers;
     if (!moe->unfused_decode) {
-        st = fused_dispatch(moe, s, a, g);
+        st = fused_dispatch(moe, s, a);
         if (st != TSG_ERR_DECLINED) return st;
     }
     if ((st = router_launch(moe, s, router_w, router_hidden, d, es, pes, out_idx, out_w, nullptr,

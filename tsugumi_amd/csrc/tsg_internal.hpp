@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -71,28 +72,26 @@ namespace tsg {
 constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kMaxRouterRows = 8;      // MoE.maxRouterRows (verify rows)
 constexpr uint32_t kMaxPromptRows = 4096;   // rows one router launch may route
-constexpr uint32_t kMaxCounters = 4096;
+constexpr uint32_t kMaxCounters = 8192;
 // Words of ctx->counters used by the one-launch decode layer (below them, words
 // [0, kMaxPromptRows / 16) are the router's per-row-group completion
-// counters). Each area starts on its own 128-byte line; replicated words sit
-// one per line.
-constexpr uint32_t kSyncEpochWord = 1024;                       // launch epoch
-constexpr uint32_t kSyncErrorWord = 1056;                       // rendezvous timeout
-constexpr uint32_t kMaxFusedBlocks = 1024;
-constexpr uint32_t kSyncFlagWord = 1088;                        // per block, packed
-constexpr uint32_t kSyncGroupWord = kSyncFlagWord + kMaxFusedBlocks;  // per 16 blocks, packed
-constexpr uint32_t kSyncReplicas = 16;
-// The one-launch layer's phase-1 activations are published in this many
-// copies (block b stages copy b % kActReplicas) so that no line is read by
-// every block; each copy holds up to kTopK * 4096 fp16 values.
-constexpr uint32_t kActReplicas = 8;
+// counters). Each area starts on its own 128-byte line.
+constexpr uint32_t kDecodeGroups = 8;      // one expert slot per group
+constexpr uint32_t kGroupMembers = 32;     // blocks per group
+constexpr uint32_t kDecodeBlocks = kDecodeGroups * kGroupMembers;
+constexpr uint32_t kSyncEpochWord = 1024;  // launch epoch
+constexpr uint32_t kSyncErrorWord = 1056;  // rendezvous timeout
+constexpr uint32_t kSyncLogitWord = 1088;  // tagged 64-bit logits, kMaxExperts per group
+static_assert(kSyncLogitWord + kDecodeGroups * 2 * kMaxExperts <= kMaxCounters, "sync area overflow");
+static_assert(kSyncLogitWord % 2 == 0, "64-bit words must be aligned");
+// Per-group hand-off regions of the one-launch layer (ctx->act_replicas):
+// group g's region holds kHandoffWords tagged 64-bit words, its slot's
+// activations in [0, kMaxFusedDim) and its partial down outputs above.
+constexpr uint32_t kActReplicas = kDecodeGroups;
 constexpr uint32_t kActReplicaHalves = 8u * 4096u;
-constexpr uint32_t kSyncLineWords = 32;
-constexpr uint32_t kSyncGoWord = kSyncGroupWord + 64;           // kSyncReplicas lines
-constexpr uint32_t kSyncTopkWord = kSyncGoWord + kSyncReplicas * kSyncLineWords;
-constexpr uint32_t kSyncLogitWord = kSyncTopkWord + kSyncReplicas * kSyncLineWords;
-static_assert(kSyncLogitWord + 2 * kMaxExperts <= kMaxCounters, "sync area overflow");
-static_assert(kSyncTopkWord % 2 == 0 && kSyncLogitWord % 2 == 0, "64-bit words must be aligned");
+constexpr uint32_t kHandoffWords = kActReplicaHalves / 4u;
+constexpr uint32_t kMaxFusedDim = 4096u;  // largest d and f of the one-launch layer
+static_assert(2u * kMaxFusedDim <= kHandoffWords, "hand-off region overflow");
 
 constexpr uint32_t kTopK = 8;
 
@@ -114,6 +113,16 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load16_nt(const void* p) {
     const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// A pointer read from LDS (or built from an integer) is generic: the compiler
+// emits flat instructions for it, which also count against the LDS counter.
+// Rebuilding it as a global-address-space pointer gives global loads and
+// stores with scalar bases.
+template <typename T>
+__device__ __forceinline__ T* global_ptr(T* p) {
+    typedef __attribute__((address_space(1))) T global_t;
+    return (T*)(global_t*)(uintptr_t)p;
 }
 
 // Agent-coherent accesses for the few values the blocks of one launch hand to
@@ -230,6 +239,22 @@ __device__ __forceinline__ uint4 pair_permute(uint4 v) {
     return o;
 }
 
+// The fp32 sum of each 32-element chunk of `rows` staged rows, in element
+// order, into sums[r * n/32 + c] (the affine scheme's bias term). The staged
+// rows must be visible to the block (the caller synchronises before).
+__device__ __forceinline__ void staged_chunk_sums(const uint16_t* dst, uint32_t dst_stride,
+                                                  uint32_t rows, uint32_t n, float* sums) {
+    const uint32_t cpr = n / 32u;
+    for (uint32_t q = threadIdx.x; q < rows * cpr; q += blockDim.x) {
+        const uint32_t r = q / cpr, c = q - r * cpr;
+        const uint16_t* chunk = dst + (size_t)r * dst_stride + c * kChunkLds;
+        float s = 0.0f;
+        for (uint32_t k = 0; k < 32u; ++k)
+            s += f16_to_f32(chunk[(k >> 3) * 8u + paired_pos(k & 7u)]);
+        sums[q] = s;
+    }
+}
+
 // Stage `rows` activation rows of `n` fp16 each (row r at src + r*src_stride)
 // into LDS at dst + r*dst_stride halves, padded chunk layout. Every global load
 // a thread makes in one pass is issued before any of its LDS stores
@@ -276,15 +301,7 @@ __device__ __forceinline__ void stage_act_rows(const uint16_t* __restrict__ src,
     }
     if constexpr (!SYM) {
         __syncthreads();
-        const uint32_t cpr = n / 32u;
-        for (uint32_t q = threadIdx.x; q < rows * cpr; q += blockDim.x) {
-            const uint32_t r = q / cpr, c = q - r * cpr;
-            const uint16_t* chunk = dst + (size_t)r * dst_stride + c * kChunkLds;
-            float s = 0.0f;
-            for (uint32_t k = 0; k < 32u; ++k)
-                s += f16_to_f32(chunk[(k >> 3) * 8u + paired_pos(k & 7u)]);
-            sums[q] = s;
-        }
+        staged_chunk_sums(dst, dst_stride, rows, n, sums);
     }
 }
 
