@@ -164,15 +164,25 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
 }
 
 // Eight packed nibbles (one u32, low nibble = element 0) -> four fp16 pairs in
-// "paired" order (e0,e4) (e1,e5) (e2,e6) (e3,e7). Each 16-bit half gets
-// 0x6400 | q = 1024 + q exactly; subtracting `bias` (1024, or 1032 for the
-// symmetric lattice) leaves q or q - 8, both exact in fp16.
+// "paired" order (e0,e4) (e1,e5) (e2,e6) (e3,e7), each exact: q or q - 8.
+// A low nibble of a byte lands in mantissa bits 0-3 under exponent 0x64
+// (1024 + q) and `bias` (1024, or 1032 for the symmetric lattice) is
+// subtracted; a high nibble lands in bits 4-7 (1024 + 16 q), and one fma
+// with 1/16 and -(bias - 960) = -(64 + bias - 1024) leaves the same value.
+// The masks live in registers so each extraction is one v_and_or_b32 (a VOP3
+// takes no literal here): 13 VALU ops per 8 weights with the four dot2s.
 __device__ __forceinline__ void nib8_to_pairs(uint32_t w, h2_t bias, h2_t out[4]) {
-    const uint32_t m = 0x000F000Fu, e = 0x64006400u;
-    out[0] = __builtin_bit_cast(h2_t, (w & m) | e) - bias;
-    out[1] = __builtin_bit_cast(h2_t, ((w >> 4) & m) | e) - bias;
-    out[2] = __builtin_bit_cast(h2_t, ((w >> 8) & m) | e) - bias;
-    out[3] = __builtin_bit_cast(h2_t, ((w >> 12) & m) | e) - bias;
+    uint32_t m_lo, m_hi, e;
+    asm("v_mov_b32 %0, 0x000f000f" : "=v"(m_lo));
+    asm("v_mov_b32 %0, 0x00f000f0" : "=v"(m_hi));
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(e));
+    const h2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const h2_t hi_bias = bias - h2_t{(_Float16)960.0f, (_Float16)960.0f};
+    const uint32_t w8 = w >> 8;
+    out[0] = __builtin_bit_cast(h2_t, (w & m_lo) | e) - bias;
+    out[1] = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (w & m_hi) | e), sixteenth, -hi_bias);
+    out[2] = __builtin_bit_cast(h2_t, (w8 & m_lo) | e) - bias;
+    out[3] = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (w8 & m_hi) | e), sixteenth, -hi_bias);
 }
 
 // v_dot2_f32_f16: a.x*b.x + a.y*b.y + c with fp32 accumulation.
