@@ -681,45 +681,96 @@ __device__ __forceinline__ uint32_t row16_max(uint32_t k) {
 // of experts 0..127, has at least 8 keys at or above it, so an expert below T
 // ranks 8th or later; the experts at or above T (the candidates, typically a
 // few dozen) are ranked among themselves by composite key (key << 32 | ~e:
-// by score, then lower expert, no two equal) and rank r < 8 takes slot r. A
-// slot whose expert is not eligible, or that no candidate reaches, keeps its
-// preset (expert 0, unfilled, -inf). `cand` holds ne4 + 1 words, `ncand` is
-// zeroed and the slots preset before the call.
+// by score, then lower expert, no two are equal) and rank r < 8 takes slot r.
+// Candidates are compacted into `cand` by ballot and lane counts (no atomic
+// round trip) and the list is padded with zeros (0 exceeds no candidate) to a
+// multiple of kCandBatch. Up to kCandBatch candidates (the usual case), lanes
+// 2i and 2i+1 count the list entries above candidate i, half each, and add
+// the halves; beyond that, each lane ranks its own candidates against the
+// whole list, kCandBatch keys per batch of reads. A slot whose expert is not eligible, or
+// that no candidate reaches, keeps its preset (expert 0, unfilled, -inf).
+// `cand` holds ne4 + kCandBatch words.
+constexpr uint32_t kCandBatch = 32;
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
 __device__ __forceinline__ void wave_select_top8(const uint32_t (&key)[4], uint32_t ne4,
-                                                 uint64_t* cand, uint32_t* ncand,
-                                                 uint32_t* slot_id, uint32_t* slot_fill,
-                                                 uint32_t* slot_key) {
+                                                 uint64_t* cand, uint32_t* slot_id,
+                                                 uint32_t* slot_fill, uint32_t* slot_key) {
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t m = min(row16_max(key[0]), row16_max(key[1]));
     const auto a = __builtin_amdgcn_permlane16_swap(m, m, false, false);
     m = min(m, min((uint32_t)a[0], (uint32_t)a[1]));
     const auto b = __builtin_amdgcn_permlane32_swap(m, m, false, false);
     m = min(m, min((uint32_t)b[0], (uint32_t)b[1]));
+    uint32_t pos[4], n = 0;  // n: candidates so far (uniform, counted on the VALU)
+    bool is_cand[4];
+    uint64_t ck[4];
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) {
         const uint32_t e = lane + 64u * j;
-        if (e < ne4 && key[j] >= m) {
-            const uint32_t pos = atomicAdd(ncand, 1u);
-            cand[pos] = ((uint64_t)key[j] << 32) | (uint32_t)~e;
-        }
+        is_cand[j] = e < ne4 && key[j] >= m;
+        ck[j] = ((uint64_t)key[j] << 32) | (uint32_t)~e;
+        const uint64_t mask = __ballot(is_cand[j]);
+        pos[j] = n + lanes_below(mask);
+        n += __builtin_popcount((uint32_t)mask) + __builtin_popcount((uint32_t)(mask >> 32));
+        if (is_cand[j]) cand[pos[j]] = ck[j];
     }
+    const uint32_t padded = (n + kCandBatch - 1u) / kCandBatch * kCandBatch;
+    if (n + lane < padded) cand[n + lane] = 0u;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // LDS ops of one wave run in order
-    const uint32_t n = *ncand;
-    if (lane == 0) cand[n] = 0u;  // pad: 0 exceeds no candidate
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    for (uint32_t i = lane; i < n; i += 64u) {
+    if (n <= kCandBatch) {
+        // lanes 2i and 2i+1 rank candidate i, each against half of the list
+        const uint32_t i = lane >> 1, h = (lane & 1u) * (kCandBatch / 2u);
         const uint64_t ki = cand[i];
-        uint32_t c = 0;
-        for (uint32_t q = 0; q < n; q += 2u) {
-            const ulonglong2 kk = *reinterpret_cast<const ulonglong2*>(cand + q);
-            c += kk.x > ki ? 1u : 0u;
-            c += kk.y > ki ? 1u : 0u;
+        uint64_t kq[kCandBatch / 2];
+#pragma unroll
+        for (uint32_t q = 0; q < kCandBatch / 2; q += 2u) {
+            const ulonglong2 kk = *reinterpret_cast<const ulonglong2*>(cand + h + q);
+            kq[q] = kk.x;
+            kq[q + 1] = kk.y;
         }
-        if (c < kTopK) {
+        uint32_t c = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < kCandBatch / 2; ++q) c += kq[q] > ki ? 1u : 0u;
+        c += __builtin_amdgcn_update_dpp(0u, c, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+        if ((lane & 1u) == 0 && i < n && c < kTopK) {
             const uint32_t k = (uint32_t)(ki >> 32);
             slot_id[c] = k ? ~(uint32_t)ki : 0u;
             slot_fill[c] = k ? 1u : 0u;
             slot_key[c] = k;
+        }
+        return;
+    }
+    uint32_t cnt[4] = {0u, 0u, 0u, 0u};
+    for (uint32_t q0 = 0; q0 < padded; q0 += kCandBatch) {
+        uint64_t kq[kCandBatch];
+#pragma unroll
+        for (uint32_t q = 0; q < kCandBatch; q += 2u) {
+            const ulonglong2 kk = *reinterpret_cast<const ulonglong2*>(cand + q0 + q);
+            kq[q] = kk.x;
+            kq[q + 1] = kk.y;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            if (64u * j >= ne4) break;
+            if (is_cand[j]) {
+#pragma unroll
+                for (uint32_t q = 0; q < kCandBatch; ++q) cnt[j] += kq[q] > ck[j] ? 1u : 0u;
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        if (64u * j >= ne4) break;
+        if (is_cand[j] && cnt[j] < kTopK) {
+            const uint32_t k = key[j];
+            slot_id[cnt[j]] = k ? lane + 64u * j : 0u;
+            slot_fill[cnt[j]] = k ? 1u : 0u;
+            slot_key[cnt[j]] = k;
         }
     }
 }
@@ -743,11 +794,11 @@ __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_ar
     if (threadIdx.x < sizeof(DecodeLayerArgs) / 4)
         reinterpret_cast<uint32_t*>(&a)[threadIdx.x] = reinterpret_cast<const uint32_t*>(&a_arg)[threadIdx.x];
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ uint32_t s_tag, s_ncand;
+    __shared__ uint32_t s_tag;
     __shared__ uint16_t s_w[kTopK];
     __shared__ uint32_t s_idx[kTopK], s_fill[kTopK], s_skey[kTopK];
     __shared__ uint32_t s_gains[kMaxExperts];
-    __shared__ __align__(16) uint64_t s_cand[kMaxExperts + 2];
+    __shared__ __align__(16) uint64_t s_cand[kMaxExperts + kCandBatch];
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
     const uint32_t grp = blockIdx.x % kDecodeGroups, mem = blockIdx.x / kDecodeGroups;
     if (t < kTopK) {
@@ -755,7 +806,6 @@ __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_ar
         s_fill[t] = 0u;
         s_skey[t] = 0u;
     }
-    if (t == 0) s_ncand = 0u;
     __syncthreads();
     const uint32_t d = a.d, f = a.f, ne = a.ne;
     const uint8_t* layer_base = global_ptr(a.layer_base);
@@ -840,7 +890,7 @@ __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_ar
                            const float v = __uint_as_float(bits);
                            key[j] = (v == v && v != -INFINITY) ? order_key(v) : 0u;
                        });
-        wave_select_top8(key, ne4, s_cand, &s_ncand, s_idx, s_fill, s_skey);
+        wave_select_top8(key, ne4, s_cand, s_idx, s_fill, s_skey);
     }
     __syncthreads();
 
