@@ -51,10 +51,10 @@ PREFILL_T = 2048
 PREFILL_FLOP = 2 * PREFILL_T * TOPK * 3 * F * H  # 194,884,141,056
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode_layer_kernel launch: rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE over `bench.py --traffic-probe` (13,926.84 KiB fetched, 749.09 KiB
+# WRITE_SIZE over `bench.py --traffic-probe` (16,415.92 KiB fetched, 320.09 KiB
 # written per dispatch), scaled by the counters of a plain 64 MiB device copy in
 # the same runs (fetch x 1.9990, write x 1.000).
-TRAFFIC_BYTES = 29275474
+TRAFFIC_BYTES = 33931486
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
