@@ -209,6 +209,42 @@ tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream, const tsg_layer
  * forces the three-launch form (no reference counterpart; for A/B checks). */
 tsg_status tsg_moe_set_fused_decode(tsg_moe* moe, int enabled);
 
+/* ------------------------------------------------- Qwen shared expert ----
+ * The Qwen-family MoE block's shared expert and its sigmoid gate
+ * (QwenForwardRunner.encodeSharedExpert, QwenForwardRunner.swift:1548-1578):
+ *   act       = half(silu(half(gate . x)) * half(up . x))
+ *   sharedOut = half(half(down . act) * sigmoid(w_g . x))
+ * The routed experts then add on top with residual = sharedOut
+ * (QwenForwardRunner.swift:1583-1608: tsg_moe_decode_layer's residual). An
+ * empty size returns TSG_ERR_DECLINED with nothing enqueued (the reference's
+ * encoders return false). */
+
+/* QwenKernels.encodeSiluMul (QwenKernels.swift:371-389, qwen.metal:466):
+ * out[i] = half(silu(float(gate[i])) * float(up[i])), silu(x) = x / (1 + e^-x)
+ * as x * sigmoid(x). */
+tsg_status tsg_qwen_silu_mul(tsg_ctx* ctx, tsg_stream stream, const uint16_t* gate,
+                             const uint16_t* up, uint16_t* out, uint32_t count);
+/* QwenKernels.encodeMoESharedGate (QwenKernels.swift:311-327, qwen.metal:432-455):
+ * y[i] = half(float(y[i]) * sigmoid(sum_k float(x[k]) * float(weight[k]))) in
+ * place; x fp16 [hidden], weight bf16 [hidden] (the [1, hidden] gate row). */
+tsg_status tsg_qwen_moe_shared_gate(tsg_ctx* ctx, tsg_stream stream, uint16_t* y,
+                                    const uint16_t* x, const uint16_t* weight, uint32_t hidden);
+/* QwenKernels.encodeMoESharedGateLogit (QwenKernels.swift:335-350,
+ * qwen.metal:1038-1046): y[i] = half(float(y[i]) * sigmoid(float(logit[0]))),
+ * the logit (fp16) already taken by a GEMV. */
+tsg_status tsg_qwen_moe_shared_gate_logit(tsg_ctx* ctx, tsg_stream stream, uint16_t* y,
+                                          const uint16_t* logit, uint32_t hidden);
+/* The whole shared branch of encodeSharedExpert (QwenForwardRunner.swift:1548-1578)
+ * in two launches: the three int4 projections of one expert laid out as a
+ * blob (MoEExpertOffsets, the ctx's group size and scheme; gate/up [f, d],
+ * down [d, f]), SwiGLU, and the bf16 gate row. act_scratch holds f fp16 (the
+ * activations). out fp16 [d]. Bit-identical to tsg_qmv_int4 (gate), (up),
+ * tsg_qwen_silu_mul, tsg_qmv_int4 (down), tsg_qwen_moe_shared_gate in turn. */
+tsg_status tsg_moe_shared_expert(tsg_moe* moe, tsg_stream stream, const void* blob,
+                                 const tsg_expert_offsets* offsets, const uint16_t* x,
+                                 const uint16_t* gate_weight, uint16_t* act_scratch,
+                                 uint16_t* out, uint32_t d, uint32_t f);
+
 /* ---------------------------------------------------------------- QMV ----
  * DequantInt4GEMV (Kernels/Quant/DequantInt4GEMV.swift:6-364). */
 

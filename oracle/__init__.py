@@ -104,6 +104,12 @@ def _declare(L):
     L.tsgo_gelu_tanh.restype = C.c_float
     L.tsgo_silu.argtypes = [C.c_float]
     L.tsgo_silu.restype = C.c_float
+    L.tsgo_sigmoid.argtypes = [C.c_float]
+    L.tsgo_sigmoid.restype = C.c_float
+    L.tsgo_silu_mul_f16.argtypes = [_u16p, _u16p, _u16p, C.c_int]
+    L.tsgo_shared_gate_f16.argtypes = [_u16p, _u16p, _u16p, C.c_int]
+    L.tsgo_shared_expert.argtypes = [_u8p, _u32p, _u16p, _u16p, C.c_int, C.c_int, C.c_int,
+                                     C.c_int, _u16p]
     L.tsgo_moe_run_ffn.argtypes = [_u8p, _u16p, _u16p, _u8p, _u16p, _u16p, _u8p, _u16p, _u16p,
                                    _f32p, C.c_int, C.c_int, C.c_int, C.c_int, _f32p]
     L.tsgo_moe_apply_streamed_routed.argtypes = [C.POINTER(_u8p), _u32p, _f32p, _f32p, _f32p,
@@ -273,6 +279,44 @@ def gelu_tanh(x: float) -> float:
 
 def silu(x: float) -> float:
     return float(lib().tsgo_silu(float(x)))
+
+
+def sigmoid(x: float) -> float:
+    """qwen_sigmoid (qwen.metal:33)."""
+    return float(lib().tsgo_sigmoid(float(x)))
+
+
+def silu_mul_f16(gate, up) -> np.ndarray:
+    """qwen_silu_mul (qwen.metal:466) on fp16 bits."""
+    gate = np.ascontiguousarray(gate, np.uint16)
+    up = np.ascontiguousarray(up, np.uint16)
+    out = np.empty_like(gate)
+    lib().tsgo_silu_mul_f16(_p(gate, C.c_uint16), _p(up, C.c_uint16), _p(out, C.c_uint16),
+                            gate.size)
+    return out
+
+
+def shared_gate_f16(y, x, w_bf16) -> np.ndarray:
+    """qwen_moe_shared_gate (qwen.metal:432-455): returns the gated copy of y."""
+    y = np.array(y, np.uint16, copy=True)
+    x = np.ascontiguousarray(x, np.uint16)
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    lib().tsgo_shared_gate_f16(_p(y, C.c_uint16), _p(x, C.c_uint16), _p(w, C.c_uint16), y.size)
+    return y
+
+
+def shared_expert(blob, offsets9, x, gate_w_bf16, d: int, f: int, group: int,
+                  symmetric: bool) -> np.ndarray:
+    """QwenForwardRunner.encodeSharedExpert (QwenForwardRunner.swift:1548-1578)
+    over one expert blob; returns sharedOut as fp16 bits."""
+    blob = np.ascontiguousarray(blob, np.uint8)
+    o = np.ascontiguousarray(offsets9, np.uint32)
+    x = np.ascontiguousarray(x, np.uint16)
+    w = np.ascontiguousarray(gate_w_bf16, np.uint16)
+    out = np.empty(d, np.uint16)
+    lib().tsgo_shared_expert(_p(blob, C.c_uint8), _p(o, C.c_uint32), _p(x, C.c_uint16),
+                             _p(w, C.c_uint16), d, f, group, int(symmetric), _p(out, C.c_uint16))
+    return out
 
 
 def _blob_ptr_array(blobs):

@@ -327,6 +327,63 @@ float tsgo_gelu_tanh(float x) {
 /* moe.metal:117: x / (1 + exp(-x)). */
 float tsgo_silu(float x) { return x / (1.0f + expf(-x)); }
 
+/* ------------------------------------------------ Qwen shared expert ---- */
+
+/* qwen.metal:33 (qwen_sigmoid): 1 / (1 + exp(-x)). */
+float tsgo_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* qwen.metal:466 (qwen_silu_mul): out = half(silu(float(g)) * float(u)) with
+ * silu(x) = x * sigmoid(x) (qwen.metal:34). */
+void tsgo_silu_mul_f16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int n) {
+    for (int i = 0; i < n; ++i) {
+        const float g = tsgo_f16_to_float(gate[i]);
+        out[i] = tsgo_f16_bits(g * tsgo_sigmoid(g) * tsgo_f16_to_float(up[i]));
+    }
+}
+
+/* qwen.metal:432-455 (qwen_moe_shared_gate): logit = sum_i float(x[i]) *
+ * float(w[i]); y[i] = half(float(y[i]) * sigmoid(logit)). The kernel sums in
+ * fp32 in its hardware reduction order; this sums in double. */
+void tsgo_shared_gate_f16(uint16_t* y, const uint16_t* x_f16, const uint16_t* w_bf16, int d) {
+    double logit = 0.0;
+    for (int i = 0; i < d; ++i)
+        logit += (double)tsgo_f16_to_float(x_f16[i]) * (double)tsgo_bf16_to_float(w_bf16[i]);
+    const float scale = tsgo_sigmoid((float)logit);
+    for (int i = 0; i < d; ++i) y[i] = tsgo_f16_bits(tsgo_f16_to_float(y[i]) * scale);
+}
+
+/* QwenForwardRunner.encodeSharedExpert (QwenForwardRunner.swift:1548-1578)
+ * over one expert laid out as MoEExpertOffsets (MoE.swift:4-29): each
+ * projection is DequantInt4GemvRef (fp32 rows, fp32 dot) stored as fp16 the
+ * way the GEMV stores y (DequantInt4GEMV.swift:78-121); act =
+ * qwen_silu_mul(gate, up); out = qwen_moe_shared_gate(down(act)). */
+void tsgo_shared_expert(const uint8_t* blob, const uint32_t* o, const uint16_t* x_f16,
+                        const uint16_t* gate_w_bf16, int d, int f, int group, int symmetric,
+                        uint16_t* out_f16) {
+    float* x = (float*)malloc(sizeof(float) * (size_t)d);
+    float* g = (float*)malloc(sizeof(float) * (size_t)f);
+    float* u = (float*)malloc(sizeof(float) * (size_t)f);
+    float* a = (float*)malloc(sizeof(float) * (size_t)f);
+    float* dn = (float*)malloc(sizeof(float) * (size_t)d);
+    uint16_t* g16 = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)f);
+    uint16_t* u16 = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)f);
+    uint16_t* a16 = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)f);
+    tsgo_f16_to_float_n(x_f16, x, (size_t)d);
+    tsgo_dequant_int4_gemv_ref(blob + o[0], (const uint16_t*)(blob + o[1]),
+                               symmetric ? NULL : (const uint16_t*)(blob + o[2]), x, f, d, group, g);
+    tsgo_dequant_int4_gemv_ref(blob + o[3], (const uint16_t*)(blob + o[4]),
+                               symmetric ? NULL : (const uint16_t*)(blob + o[5]), x, f, d, group, u);
+    tsgo_float_to_f16_n(g, g16, (size_t)f);
+    tsgo_float_to_f16_n(u, u16, (size_t)f);
+    tsgo_silu_mul_f16(g16, u16, a16, f);
+    tsgo_f16_to_float_n(a16, a, (size_t)f);
+    tsgo_dequant_int4_gemv_ref(blob + o[6], (const uint16_t*)(blob + o[7]),
+                               symmetric ? NULL : (const uint16_t*)(blob + o[8]), a, d, f, group, dn);
+    tsgo_float_to_f16_n(dn, out_f16, (size_t)d);
+    tsgo_shared_gate_f16(out_f16, x_f16, gate_w_bf16, d);
+    free(x); free(g); free(u); free(a); free(dn); free(g16); free(u16); free(a16);
+}
+
 static inline float gate_act(float x, int act) {
     return act == 1 ? tsgo_silu(x) : tsgo_gelu_tanh(x);
 }

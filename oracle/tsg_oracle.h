@@ -77,6 +77,13 @@ void tsgo_dequant_int4_gemv_ref(const uint8_t* packed, const uint16_t* scales,
                                 int m, int n, int group, float* y);
 float tsgo_gelu_tanh(float x);
 float tsgo_silu(float x);
+/* Qwen shared expert (qwen.metal, QwenForwardRunner.swift:1548-1578). */
+float tsgo_sigmoid(float x);
+void tsgo_silu_mul_f16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int n);
+void tsgo_shared_gate_f16(uint16_t* y, const uint16_t* x_f16, const uint16_t* w_bf16, int d);
+void tsgo_shared_expert(const uint8_t* blob, const uint32_t* offsets9, const uint16_t* x_f16,
+                        const uint16_t* gate_w_bf16, int d, int f, int group, int symmetric,
+                        uint16_t* out_f16);
 /* One expert: down(act(gate x) * up x). act: 0 = gelu_pytorch_tanh, 1 = silu.
  * NULL bias pointers mean `sym`. */
 void tsgo_moe_run_ffn(const uint8_t* gate_w, const uint16_t* gate_s, const uint16_t* gate_b,

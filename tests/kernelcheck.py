@@ -162,3 +162,20 @@ def layer_image(expert_parts, symmetric, keep_biases, stride_align=16384):
     for i, b in enumerate(blobs):
         image[i * stride:i * stride + b.size] = b
     return image, stride, offs, blobs
+
+
+def shared_expert_case(d, f, group, seed, symmetric):
+    """A Qwen shared-expert case (QwenForwardRunner.swift:1548-1578): this
+    build's own seeded draw with the harness generators (the reference's
+    harness has no shared-expert check). gate/up [f, d], down [d, f] in the
+    blob layout, x fp16, the bf16 gate row [d]."""
+    rng = oracle.seed_tree_key(seed, f"shared-expert-d{d}-f{f}-g{group}")
+    g = rng.uniforms(-0.4, 0.4, f * d).reshape(f, d)
+    u = rng.uniforms(-0.4, 0.4, f * d).reshape(f, d)
+    dn = rng.uniforms(-0.4, 0.4, d * f).reshape(d, f)
+    x_bits = oracle.f16_bits(rng.uniforms(-0.5, 0.5, d))
+    gate_w = rng.uniforms_bf16(-0.05, 0.05, d)
+    parts = [oracle.quantize_int4(m, group, symmetric) for m in (g, u, dn)]
+    blob, offs = pack_blob(parts, symmetric, keep_biases=not symmetric)
+    ref = oracle.shared_expert(blob, offs, x_bits, gate_w, d, f, group, symmetric)
+    return dict(blob=blob, offsets=offs, x_bits=x_bits, gate_w=gate_w, parts=parts, ref=ref)

@@ -28,7 +28,8 @@ from ._abi import (TSG_ACT_GELU_TANH, TSG_ACT_SILU, TSG_AFFINE, TSG_SYM, ExpertO
                    RoutedBlock, TokenExpertPair, TsgError, check, load)
 
 __all__ = [
-    "Context", "MoE", "DequantInt4GEMV", "PrefillRouter", "PrefillMoEGrouping",
+    "Context", "MoE", "DequantInt4GEMV", "QwenKernels", "encode_shared_expert",
+    "PrefillRouter", "PrefillMoEGrouping",
     "PrefillRoutedGEMMPlanner", "PrefillGroupedRoutedMoE", "PrefillMoE", "ResidentLayer",
     "ExpertOffsets", "TsgError", "PAIR_DTYPE", "BLOCK_DTYPE", "GROUP_DTYPE", "TILE_DTYPE",
     "generators", "load",
@@ -258,6 +259,36 @@ class MoE:
             self.close()
         except Exception:
             pass
+
+
+class QwenKernels:
+    """The Qwen-family shared-expert steps of QwenKernels (QwenKernels.swift)
+    and QwenForwardRunner.encodeSharedExpert (QwenForwardRunner.swift:1548-1578)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def encode_silu_mul(self, gate, up, out, count, stream=None):
+        check(self.lib.tsg_qwen_silu_mul(self.ctx.handle, _stream(stream), _ptr(gate), _ptr(up),
+                                         _ptr(out), count))
+
+    def encode_moe_shared_gate(self, y, x, weight, hidden_size, stream=None):
+        check(self.lib.tsg_qwen_moe_shared_gate(self.ctx.handle, _stream(stream), _ptr(y),
+                                                _ptr(x), _ptr(weight), hidden_size))
+
+    def encode_moe_shared_gate_logit(self, y, logit, hidden_size, stream=None):
+        check(self.lib.tsg_qwen_moe_shared_gate_logit(self.ctx.handle, _stream(stream), _ptr(y),
+                                                      _ptr(logit), hidden_size))
+
+
+def encode_shared_expert(moe: "MoE", blob, offsets, x, gate_weight, act_scratch, out, d, f,
+                         stream=None):
+    """The shared branch of QwenForwardRunner.encodeSharedExpert in two launches."""
+    o = offsets_from(offsets)
+    check(moe.lib.tsg_moe_shared_expert(moe.handle, _stream(stream), _ptr(blob), C.byref(o),
+                                        _ptr(x), _ptr(gate_weight), _ptr(act_scratch), _ptr(out),
+                                        d, f))
 
 
 class DequantInt4GEMV:

@@ -92,6 +92,10 @@ SIGNATURES = {
                                        U32]),
     "tsg_moe_set_fused_decode": (C.c_int, [P, C.c_int]),
     "tsg_qmv_int4": (C.c_int, [P, P, P, P, P, P, P, U32, U32]),
+    "tsg_qwen_silu_mul": (C.c_int, [P, P, P, P, P, U32]),
+    "tsg_qwen_moe_shared_gate": (C.c_int, [P, P, P, P, P, U32]),
+    "tsg_qwen_moe_shared_gate_logit": (C.c_int, [P, P, P, P, U32]),
+    "tsg_moe_shared_expert": (C.c_int, [P, P, P, P, P, P, P, P, U32, U32]),
     "tsg_qmv_int4_rows": (C.c_int, [P, P, P, P, P, P, U32, P, U32, U32, U32, U32]),
     "tsg_debug_dequant_f16": (C.c_int, [P, P, P, P, P, P, U32, U32]),
     "tsg_debug_gemm_dequant_f16": (C.c_int, [P, P, P, P, P, P, U32, U32]),

@@ -1,0 +1,232 @@
+// shared.hip — the Qwen-family shared expert with its sigmoid gate
+// (QwenForwardRunner.swift:1548-1578):
+//
+//   act       = half(silu(half(gate · x)) · half(up · x))
+//   sharedOut = half(half(down · act) · sigmoid(w_g · x))
+//
+// as the reference's separate steps — the three projections are the dense int4
+// GEMV (tsg_qmv_int4, DequantInt4GEMV), qwen_silu_mul (qwen.metal:466),
+// qwen_moe_shared_gate (qwen.metal:432-455) and qwen_moe_shared_gate_logit
+// (qwen.metal:1038-1046) — and fused into two launches that give the same
+// bits: gate/up rows use the GEMV's lane geometry and sum order, and the
+// gate logit is one block-wide sum shared by both forms.
+#include "gemv_lane.hpp"
+
+namespace tsg {
+namespace {
+
+constexpr uint32_t kGateThreads = 256;  // the block size gate_logit_block assumes
+
+// qwen.metal:33-34.
+__device__ __forceinline__ float qwen_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float qwen_silu(float x) { return x * qwen_sigmoid(x); }
+
+// half(silu(float(g)) * float(u)) (qwen.metal:466).
+__device__ __forceinline__ uint16_t silu_mul_h(uint16_t g, uint16_t u) {
+    return f32_to_f16(qwen_silu(f16_to_f32(g)) * f16_to_f32(u));
+}
+
+// The gate logit sum_i float(x[i]) * float(w[i]) (x fp16, w bf16) on one block
+// of kGateThreads threads: thread t accumulates i = t, t + 256, ... with fma in
+// order, each wave sums its lanes as group16_sum and then the four 16-lane rows
+// as (r0 + r1) + (r2 + r3), and the four waves add as (w0 + w1) + (w2 + w3).
+// Every thread returns the same value. `red` is 4 floats of LDS.
+__device__ float gate_logit_block(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                  uint32_t d, float* red) {
+    const uint32_t t = threadIdx.x;
+    float acc = 0.0f;
+    for (uint32_t i = t; i < d; i += kGateThreads)
+        acc = __builtin_fmaf(f16_to_f32(x[i]), bf16_to_f32(w[i]), acc);
+    acc = group16_sum(acc);
+    acc = (lane_value(acc, 0) + lane_value(acc, 16)) + (lane_value(acc, 32) + lane_value(acc, 48));
+    if ((t & 63u) == 0) red[t >> 6] = acc;
+    __syncthreads();
+    const float s = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return s;
+}
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gate,
+                                                       const uint16_t* __restrict__ up,
+                                                       uint16_t* __restrict__ out, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = silu_mul_h(gate[i], up[i]);
+}
+
+// y *= sigmoid(w_g · x) in place, one block (qwen.metal:432-455).
+__global__ __launch_bounds__(kGateThreads) void shared_gate_kernel(uint16_t* __restrict__ y,
+                                                                   const uint16_t* __restrict__ x,
+                                                                   const uint16_t* __restrict__ w,
+                                                                   uint32_t d) {
+    __shared__ float red[4];
+    const float scale = qwen_sigmoid(gate_logit_block(x, w, d, red));
+    for (uint32_t i = threadIdx.x; i < d; i += kGateThreads)
+        y[i] = f32_to_f16(f16_to_f32(y[i]) * scale);
+}
+
+// y *= sigmoid(logit[0]) in place (qwen.metal:1038-1046).
+__global__ __launch_bounds__(256) void shared_gate_logit_kernel(uint16_t* __restrict__ y,
+                                                                const uint16_t* __restrict__ logit,
+                                                                uint32_t d) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < d) y[i] = f32_to_f16(f16_to_f32(y[i]) * qwen_sigmoid(f16_to_f32(logit[0])));
+}
+
+// act[p] = half(silu(half(gate_p · x)) * half(up_p · x)). 8 rows p per block:
+// lanes 0..15 of each 32 sum the gate row, lanes 16..31 the up row, in the
+// dense GEMV's geometry (16 lanes per row, kGUBatch chunks per batch), so each
+// sum and its fp16 rounding equal tsg_qmv_int4's.
+template <int G, bool SYM>
+__global__ __launch_bounds__(256) void shared_gate_up_kernel(const uint8_t* __restrict__ blob,
+                                                             tsg_expert_offsets o,
+                                                             const uint16_t* __restrict__ x,
+                                                             uint16_t* __restrict__ act,
+                                                             uint32_t d, uint32_t f) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+    float* xsum = reinterpret_cast<float*>(smem + lds_chunks_halves(d) * 2u);
+    const uint32_t t = threadIdx.x, j = t & 15u;
+    const bool is_up = (t >> 4) & 1u;
+    const uint32_t p = blockIdx.x * 8u + (t >> 5);
+    const bool live = p < f;
+    const uint32_t pr = live ? p : 0u;
+    const uint32_t ngroups = d / G, nchunks = d / 32u;
+    const uint8_t* w = blob + (is_up ? o.up_w : o.gate_w) + (uint64_t)pr * (d / 2u);
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + (is_up ? o.up_s : o.gate_s)) +
+                         (uint64_t)pr * ngroups;
+    const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + (is_up ? o.up_b : o.gate_b)) +
+                         (uint64_t)pr * ngroups;
+    ChunkBatch<kGUBatch> bt;
+    load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, 0u, j, nchunks, bt);
+    stage_act_rows<SYM>(x, 0u, 1u, d, xs, 0u, xsum);
+    __syncthreads();
+    float acc[1] = {0.0f};
+    for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
+        if (base) load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, base, j, nchunks, bt);
+        compute_batch<G, SYM, kGUBatch, kGULanes, 1>(bt, base, j, nchunks, xs, 0u, xsum, 1u, acc);
+    }
+    const float s = group16_sum(acc[0]);
+    const float u = shfl_xor(s, 16);  // gate lanes receive the up sum
+    if (live && !is_up && j == 0) act[p] = silu_mul_h(f32_to_f16(s), f32_to_f16(u));
+}
+
+// out[r] = half(half(down_r · act) * sigmoid(w_g · x)): 16 rows per block in the
+// dense GEMV's geometry, the gate logit summed by every block the way
+// shared_gate_kernel sums it.
+template <int G, bool SYM>
+__global__ __launch_bounds__(kGateThreads) void shared_down_kernel(
+    const uint8_t* __restrict__ blob, tsg_expert_offsets o, const uint16_t* __restrict__ act,
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate_w,
+    uint16_t* __restrict__ out, uint32_t d, uint32_t f) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float red[4];
+    uint16_t* as = reinterpret_cast<uint16_t*>(smem);
+    float* asum = reinterpret_cast<float*>(smem + lds_chunks_halves(f) * 2u);
+    const uint32_t t = threadIdx.x, j = t & 15u;
+    const uint32_t row = blockIdx.x * 16u + (t >> 4);
+    const bool live = row < d;
+    const uint32_t rr = live ? row : 0u;
+    const uint32_t ngroups = f / G, nchunks = f / 32u;
+    const uint8_t* w = blob + o.down_w + (uint64_t)rr * (f / 2u);
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + o.down_s) + (uint64_t)rr * ngroups;
+    const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + o.down_b) + (uint64_t)rr * ngroups;
+    ChunkBatch<kGUBatch> bt;
+    load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, 0u, j, nchunks, bt);
+    stage_act_rows<SYM>(act, 0u, 1u, f, as, 0u, asum);
+    const float scale = qwen_sigmoid(gate_logit_block(x, gate_w, d, red));  // synchronises
+    float acc[1] = {0.0f};
+    for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
+        if (base) load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, base, j, nchunks, bt);
+        compute_batch<G, SYM, kGUBatch, kGULanes, 1>(bt, base, j, nchunks, as, 0u, asum, 1u, acc);
+    }
+    const float v = group16_sum(acc[0]);
+    if (live && j == 0) out[row] = f32_to_f16(f16_to_f32(f32_to_f16(v)) * scale);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+tsg_status check_gate_args(const tsg_ctx* ctx, const void* y, const void* a, const void* b,
+                           uint32_t n) {
+    TSG_REQUIRE(ctx, TSG_ERR_INVALID_ARGUMENT, "ctx is NULL");
+    TSG_REQUIRE(y && a && b, TSG_ERR_INVALID_ARGUMENT, "NULL operand");
+    // The reference's encoders return false (nothing encoded) for an empty size.
+    TSG_REQUIRE(n > 0, TSG_ERR_DECLINED, "empty size: nothing to encode");
+    return TSG_OK;
+}
+
+template <int G, bool SYM>
+tsg_status launch_shared(hipStream_t s, const uint8_t* blob, const tsg_expert_offsets& o,
+                         const uint16_t* x, const uint16_t* gate_w, uint16_t* act, uint16_t* out,
+                         uint32_t d, uint32_t f) {
+    const size_t lds_gu = (size_t)lds_chunks_halves(d) * 2u + (SYM ? 0u : (d / 32u) * 4u);
+    const size_t lds_dn = (size_t)lds_chunks_halves(f) * 2u + (SYM ? 0u : (f / 32u) * 4u);
+    hipLaunchKernelGGL((shared_gate_up_kernel<G, SYM>), dim3((f + 7u) / 8u), dim3(256), lds_gu, s,
+                       blob, o, x, act, d, f);
+    hipLaunchKernelGGL((shared_down_kernel<G, SYM>), dim3((d + 15u) / 16u), dim3(kGateThreads),
+                       lds_dn, s, blob, o, act, x, gate_w, out, d, f);
+    return check_launch("shared_expert");
+}
+
+}  // namespace
+}  // namespace tsg
+
+using namespace tsg;
+
+extern "C" tsg_status tsg_qwen_silu_mul(tsg_ctx* ctx, tsg_stream stream, const uint16_t* gate,
+                                        const uint16_t* up, uint16_t* out, uint32_t count) {
+    tsg_status st = check_gate_args(ctx, out, gate, up, count);
+    if (st) return st;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((count + 255u) / 256u), dim3(256), 0,
+                       as_stream(stream), gate, up, out, count);
+    return check_launch("qwen_silu_mul");
+}
+
+extern "C" tsg_status tsg_qwen_moe_shared_gate(tsg_ctx* ctx, tsg_stream stream, uint16_t* y,
+                                               const uint16_t* x, const uint16_t* weight,
+                                               uint32_t hidden) {
+    tsg_status st = check_gate_args(ctx, y, x, weight, hidden);
+    if (st) return st;
+    hipLaunchKernelGGL(shared_gate_kernel, dim3(1), dim3(kGateThreads), 0, as_stream(stream), y,
+                       x, weight, hidden);
+    return check_launch("qwen_moe_shared_gate");
+}
+
+extern "C" tsg_status tsg_qwen_moe_shared_gate_logit(tsg_ctx* ctx, tsg_stream stream,
+                                                     uint16_t* y, const uint16_t* logit,
+                                                     uint32_t hidden) {
+    tsg_status st = check_gate_args(ctx, y, logit, logit, hidden);
+    if (st) return st;
+    hipLaunchKernelGGL(shared_gate_logit_kernel, dim3((hidden + 255u) / 256u), dim3(256), 0,
+                       as_stream(stream), y, logit, hidden);
+    return check_launch("qwen_moe_shared_gate_logit");
+}
+
+extern "C" tsg_status tsg_moe_shared_expert(tsg_moe* moe, tsg_stream stream, const void* blob,
+                                            const tsg_expert_offsets* offsets, const uint16_t* x,
+                                            const uint16_t* gate_weight, uint16_t* act_scratch,
+                                            uint16_t* out, uint32_t d, uint32_t f) {
+    TSG_REQUIRE(moe && moe->ctx, TSG_ERR_INVALID_ARGUMENT, "moe is NULL");
+    TSG_REQUIRE(blob && offsets && x && gate_weight && act_scratch && out,
+                TSG_ERR_INVALID_ARGUMENT, "NULL shared-expert operand");
+    const tsg_ctx* ctx = moe->ctx;
+    const uint32_t g = ctx->group_size;
+    TSG_REQUIRE(d > 0 && f > 0 && d % g == 0 && f % g == 0, TSG_ERR_INVALID_ARGUMENT,
+                "d=%u and f=%u must be positive multiples of the group size %u", d, f, g);
+    const tsg_expert_offsets& o = *offsets;
+    const uint8_t* b = static_cast<const uint8_t*>(blob);
+    TSG_REQUIRE(aligned16(b + o.gate_w) && aligned16(b + o.up_w) && aligned16(b + o.down_w),
+                TSG_ERR_ALIGNMENT, "weight sub-tensors must start on 16 bytes");
+    TSG_REQUIRE(((o.gate_s | o.up_s | o.down_s | o.gate_b | o.up_b | o.down_b) & 1u) == 0,
+                TSG_ERR_ALIGNMENT, "scale/bias offsets must be even");
+    TSG_REQUIRE(aligned16(x) && aligned16(act_scratch), TSG_ERR_ALIGNMENT,
+                "x and act_scratch must be 16-byte aligned");
+    TSG_REQUIRE((size_t)lds_chunks_halves(d) * 2u + (d / 32u) * 4u <= 64u * 1024u,
+                TSG_ERR_UNSUPPORTED, "d=%u does not fit the LDS staging", d);
+    hipStream_t s = as_stream(stream);
+    const bool sym = ctx->scheme == TSG_SYM;
+    if (g == 32)
+        return sym ? launch_shared<32, true>(s, b, o, x, gate_weight, act_scratch, out, d, f)
+                   : launch_shared<32, false>(s, b, o, x, gate_weight, act_scratch, out, d, f);
+    return sym ? launch_shared<64, true>(s, b, o, x, gate_weight, act_scratch, out, d, f)
+               : launch_shared<64, false>(s, b, o, x, gate_weight, act_scratch, out, d, f);
+}
