@@ -319,6 +319,8 @@ def make_layer(tsg, ctx, seed, ne, d, f, group, symmetric):
 @pytest.mark.gpu
 @pytest.mark.parametrize("d,f,ne,group,scheme,act", [
     (2816, 704, 128, 32, "sym", "gelu"),
+    (2048, 512, 256, 32, "sym", "silu"),
+    (2048, 512, 256, 64, "affine", "silu"),
     (1024, 512, 64, 64, "affine", "silu"),
     (768, 256, 32, 32, "affine", "gelu"),
 ])

@@ -678,8 +678,9 @@ __device__ __forceinline__ uint32_t row16_max(uint32_t k) {
 // eligible; keys of experts >= ne are 0), with the reference's rule
 // (moe.metal:281-329): descending score, ties to the lower index, -inf and
 // NaN never enter. T, the least of the maxima of the eight 16-expert groups
-// of experts 0..127, has at least 8 keys at or above it, so an expert below T
-// ranks 8th or later; the experts at or above T (the candidates, typically a
+// of experts 0..127 (the larger of that and the same over experts 128..255
+// when there are more), has at least 8 keys at or above it, so an expert below
+// T ranks 8th or later; the experts at or above T (the candidates, typically a
 // few dozen) are ranked among themselves by composite key (key << 32 | ~e:
 // by score, then lower expert, no two are equal) and rank r < 8 takes slot r.
 // Candidates are compacted into `cand` by ballot and lane counts (no atomic
@@ -697,15 +698,22 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+// The least of the maxima of the eight 16-expert groups of keys k0 (lanes)
+// and k1 (lanes): at least 8 keys are at or above it. Every lane returns it.
+__device__ __forceinline__ uint32_t group_min_of_maxima(uint32_t k0, uint32_t k1) {
+    uint32_t m = min(row16_max(k0), row16_max(k1));
+    const auto a = __builtin_amdgcn_permlane16_swap(m, m, false, false);
+    m = min(m, min((uint32_t)a[0], (uint32_t)a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(m, m, false, false);
+    return min(m, min((uint32_t)b[0], (uint32_t)b[1]));
+}
+
 __device__ __forceinline__ void wave_select_top8(const uint32_t (&key)[4], uint32_t ne4,
                                                  uint64_t* cand, uint32_t* slot_id,
                                                  uint32_t* slot_fill, uint32_t* slot_key) {
     const uint32_t lane = threadIdx.x & 63u;
-    uint32_t m = min(row16_max(key[0]), row16_max(key[1]));
-    const auto a = __builtin_amdgcn_permlane16_swap(m, m, false, false);
-    m = min(m, min((uint32_t)a[0], (uint32_t)a[1]));
-    const auto b = __builtin_amdgcn_permlane32_swap(m, m, false, false);
-    m = min(m, min((uint32_t)b[0], (uint32_t)b[1]));
+    uint32_t m = group_min_of_maxima(key[0], key[1]);
+    if (ne4 > 128u) m = max(m, group_min_of_maxima(key[2], key[3]));
     uint32_t pos[4], n = 0;  // n: candidates so far (uniform, counted on the VALU)
     bool is_cand[4];
     uint64_t ck[4];
