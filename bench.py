@@ -439,10 +439,9 @@ def make_shared_experts(tsg, torch, n_layers, h, f, seed):
 
 
 def run_qwen(tsg, torch, args):
-    """decode M=1 (shared branch in two launches, then the
-    one-launch routed layer with residual = the shared output, as
-    QwenForwardRunner.swift:1548-1608 orders them), decode M=3 (rows path +
-    shared branch), prefill T=4096 Zipf(1.0) (grouped GEMM)."""
+    """decode M=1 (the shared branch and the routed experts on top
+    of it, QwenForwardRunner.swift:1548-1608, in one launch), decode M=3 (rows
+    path + shared branch), prefill T=4096 Zipf(1.0) (grouped GEMM)."""
     h, f, e, nl = QW_H, QW_F, QW_E, QW_LAYERS
     ctx = tsg.Context(0, group_size=GROUP, scheme="sym")
     _, stride, payload = shape_offsets(h, f)
@@ -456,7 +455,6 @@ def run_qwen(tsg, torch, args):
     xs = torch.empty(n_tok * nl * h, dtype=torch.int16, device="cuda")
     tsg.generators.f16_normal(xs, 0x7777, 1.0)
     ys = torch.empty(nl * h, dtype=torch.int16, device="cuda")
-    sout = torch.empty(nl * h, dtype=torch.int16, device="cuda")
     sact = torch.empty(f, dtype=torch.int16, device="cuda")
     idx = torch.empty(nl * TOPK, dtype=torch.int32, device="cuda")
     wts = torch.empty(nl * TOPK, dtype=torch.int16, device="cuda")
@@ -467,14 +465,12 @@ def run_qwen(tsg, torch, args):
         for k in range(n_tok):
             for l in range(nl):
                 x = xs[(k * nl + l) * h:(k * nl + l + 1) * h]
-                so = sout[l * h:(l + 1) * h]
                 blob, o, gw = shared[l]
-                tsg.encode_shared_expert(moe, blob, o, x, gw, sact, so, h, f, stream=stream)
-                moe.encode_decode_layer(layers[l], routers[l], x, ones_h, ones_e, x, so,
-                                        ys[l * h:(l + 1) * h], idx[l * TOPK:(l + 1) * TOPK],
-                                        wts[l * TOPK:(l + 1) * TOPK],
-                                        acts[l * TOPK * f:(l + 1) * TOPK * f], e, h, f,
-                                        stream=stream)
+                moe.encode_decode_layer_shared(layers[l], routers[l], x, ones_h, ones_e, x,
+                                               ys[l * h:(l + 1) * h], idx[l * TOPK:(l + 1) * TOPK],
+                                               wts[l * TOPK:(l + 1) * TOPK],
+                                               acts[l * TOPK * f:(l + 1) * TOPK * f], blob, o, gw,
+                                               sact, e, h, f, f, stream=stream)
 
     ms = time_graph(torch, stream, decode, reps=max(2, args.steps // 8))
     us1 = ms * 1000.0 / (n_tok * nl)
@@ -495,7 +491,7 @@ def run_qwen(tsg, torch, args):
             "decode_m1": {"us_per_layer": round(us1, 3),
                           "GBps": round(bytes1 / (us1 * 1e-6) / 1e9, 2),
                           "bytes_per_layer": bytes1,
-                          "launches_per_layer": 3},
+                          "launches_per_layer": 1},
             "decode_m3": {"us_per_layer": round(us3, 3), "mean_union": round(u3, 2),
                           "GBps": round(bytes3 / (us3 * 1e-6) / 1e9, 2),
                           "path": "rows path + token-major reduce + shared branch (GEMV rows, "

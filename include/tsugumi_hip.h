@@ -203,6 +203,29 @@ tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream, const tsg_layer
                                 uint16_t* out_weights, uint16_t* acts_scratch,
                                 uint32_t num_experts, uint32_t d, uint32_t f, uint32_t top_k);
 
+/* The Qwen-family layer: the shared branch of
+ * QwenForwardRunner.encodeSharedExpert (QwenForwardRunner.swift:1548-1578)
+ * and the routed experts on top of it with residual = y = sharedOut
+ * (encodeRoutedExperts, :1583-1608), as one call: y = half(sharedOut +
+ * sum_s w_s expert_s(x)), sharedOut = half(half(down . act) * sigmoid(w_g . x)),
+ * act = half(silu(half(gate . x)) * half(up . x)) over the shared expert blob
+ * (MoEExpertOffsets; the ctx's group size and scheme). No single reference
+ * call: in one launch when it fits (shared_f <= 512), its shared weights
+ * loaded while the router runs; otherwise tsg_moe_shared_expert then
+ * tsg_moe_decode_layer(residual = y). Both give the same bits. shared_acts
+ * (16-byte aligned) receives the shared_f fp16 activations. */
+tsg_status tsg_moe_decode_layer_shared(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                       const uint16_t* router_weights,
+                                       const uint16_t* router_hidden,
+                                       const uint16_t* effective_scale,
+                                       const uint16_t* per_expert_scale, const uint16_t* x,
+                                       uint16_t* y, uint32_t* out_indices, uint16_t* out_weights,
+                                       uint16_t* acts_scratch, const void* shared_blob,
+                                       const tsg_expert_offsets* shared_offsets,
+                                       const uint16_t* shared_gate_weight, uint16_t* shared_acts,
+                                       uint32_t num_experts, uint32_t d, uint32_t f,
+                                       uint32_t shared_f, uint32_t top_k);
+
 /* tsg_moe_decode_layer runs as one launch (grid barriers between router,
  * gate/up and down) whenever every block fits on the device at once, else as
  * router + phase 1 + phase 2 launches; both give identical bits. enabled = 0
@@ -226,7 +249,9 @@ tsg_status tsg_qwen_silu_mul(tsg_ctx* ctx, tsg_stream stream, const uint16_t* ga
                              const uint16_t* up, uint16_t* out, uint32_t count);
 /* QwenKernels.encodeMoESharedGate (QwenKernels.swift:311-327, qwen.metal:432-455):
  * y[i] = half(float(y[i]) * sigmoid(sum_k float(x[k]) * float(weight[k]))) in
- * place; x fp16 [hidden], weight bf16 [hidden] (the [1, hidden] gate row). */
+ * place; x fp16 [hidden], weight bf16 [hidden] (the [1, hidden] gate row),
+ * both 16-byte aligned, hidden a multiple of 8 up to 4096 (TSG_ERR_ALIGNMENT /
+ * TSG_ERR_UNSUPPORTED otherwise). */
 tsg_status tsg_qwen_moe_shared_gate(tsg_ctx* ctx, tsg_stream stream, uint16_t* y,
                                     const uint16_t* x, const uint16_t* weight, uint32_t hidden);
 /* QwenKernels.encodeMoESharedGateLogit (QwenKernels.swift:335-350,

@@ -371,3 +371,61 @@ def test_fused_decode_layer_matches_three_launches(tsg, ctx, d, f, ne, group, sc
     rel = oracle.relative_error(oracle.f16_to_float(y), ref)
     print(f"fused decode d={d} f={f} ne={ne} g{group} {scheme} {act}: rel={rel:.3e}")
     assert rel <= kc.NORTH_STAR
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d,f,ne,sf,group,scheme", [
+    (2048, 512, 256, 512, 32, "sym"),     # the Qwen3.5-MoE-35B-A3B shape
+    (1024, 512, 64, 256, 64, "affine"),
+    (1024, 256, 64, 1024, 32, "sym"),     # shared_f > 512: the two-step form
+])
+def test_decode_layer_shared_expert(tsg, ctx, d, f, ne, sf, group, scheme):
+    """The Qwen-family layer (QwenForwardRunner.swift:1548-1608): one call gives
+    the same bits as tsg_moe_shared_expert followed by the decode layer with
+    residual = the shared output, in the one-launch and three-launch forms,
+    and y is within 1e-3 of the oracle's shared branch + MoeRef."""
+    import torch
+    configure(ctx, group, scheme)
+    sym = scheme == "sym"
+    layer, buf, offs, stride = make_layer(tsg, ctx, 0x5A5 + d, ne, d, f, group, sym)
+    rw = torch.empty(ne * d, dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(rw, 0xC11 + d, 1.0 / np.sqrt(d))
+    ones_d = dev(oracle.bf16_bits(np.ones(d, np.float32)))
+    pes_bits = oracle.bf16_bits(np.ones(ne, np.float32))
+    x = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(x, 0xC12 + d, 1.0)
+    c = kc.shared_expert_case(d, sf, group, 0xC13 + d, sym)
+    sblob, sgw = dev(c["blob"]), dev(c["gate_w"])
+    moe = tsg.MoE(ctx, gate_activation="silu")
+    outs = {}
+    for fused in (True, False):
+        moe.set_fused_decode(fused)
+        y, idx, wts, acts, sacts = empty(d), empty(8, np.uint32), empty(8), empty(8 * f), empty(sf)
+        print(f"shared decode d={d} f={f} ne={ne} sf={sf} fused={fused}", flush=True)
+        moe.encode_decode_layer_shared(layer, rw, x, ones_d, dev(pes_bits), x, y, idx, wts, acts,
+                                       sblob, c["offsets"], sgw, sacts, ne, d, f, sf)
+        ctx.synchronize()
+        outs[fused] = [host(t, np.uint16 if t is not idx else np.uint32)
+                       for t in (y, idx, wts, acts, sacts)]
+    # the explicit two-call sequence
+    so, sa2 = empty(d), empty(sf)
+    tsg.encode_shared_expert(moe, sblob, c["offsets"], x, sgw, sa2, so, d, sf)
+    moe.set_fused_decode(True)
+    y2, idx2, wts2, acts2 = empty(d), empty(8, np.uint32), empty(8), empty(8 * f)
+    moe.encode_decode_layer(layer, rw, x, ones_d, dev(pes_bits), x, so, y2, idx2, wts2, acts2,
+                            ne, d, f)
+    seq = [host(t, np.uint16 if t is not idx2 else np.uint32) for t in (y2, idx2, wts2, acts2, sa2)]
+    for a_, b_, c_ in zip(outs[True], outs[False], seq):
+        assert np.array_equal(a_, b_)
+        assert np.array_equal(a_, c_)
+    y, gi, gw, _, _ = outs[True]
+    image = host(buf, np.uint8)
+    blobs = [np.ascontiguousarray(image[e * stride:(e + 1) * stride]) for e in gi]
+    xb = host(x, np.uint16)
+    shared_ref = oracle.shared_expert(c["blob"], c["offsets"], xb, c["gate_w"], d, sf, group, sym)
+    ref = oracle.moe_apply_streamed_routed(
+        blobs, np.array(offs, np.uint32), oracle.f16_to_float(xb),
+        oracle.f16_to_float(shared_ref), oracle.f16_to_float(gw), d, f, group, symmetric=sym, act=1)
+    rel = oracle.relative_error(oracle.f16_to_float(y), ref)
+    print(f"  rel={rel:.3e}")
+    assert rel <= kc.NORTH_STAR

@@ -260,6 +260,20 @@ class MoE:
         except Exception:
             pass
 
+    def encode_decode_layer_shared(self, layer: ResidentLayer, router_weights, router_hidden,
+                                   effective_scale, per_expert_scale, x, y, out_indices,
+                                   out_weights, acts_scratch, shared_blob, shared_offsets,
+                                   shared_gate_weight, shared_acts, num_experts, d, f, shared_f,
+                                   top_k=8, stream=None):
+        """The Qwen-family layer: shared branch + routed experts with
+        residual = sharedOut (QwenForwardRunner.swift:1548-1608) in one call."""
+        o = offsets_from(shared_offsets)
+        check(self.lib.tsg_moe_decode_layer_shared(
+            self.handle, _stream(stream), layer.handle, _ptr(router_weights),
+            _ptr(router_hidden), _ptr(effective_scale), _ptr(per_expert_scale), _ptr(x), _ptr(y),
+            _ptr(out_indices), _ptr(out_weights), _ptr(acts_scratch), _ptr(shared_blob),
+            C.byref(o), _ptr(shared_gate_weight), _ptr(shared_acts), num_experts, d, f,
+            shared_f, top_k))
 
 class QwenKernels:
     """The Qwen-family shared-expert steps of QwenKernels (QwenKernels.swift)

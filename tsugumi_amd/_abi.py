@@ -90,6 +90,8 @@ SIGNATURES = {
     "tsg_moe_phase2_resident": (C.c_int, [P, P, P, P, P, P, P, P, U32, U32, U32]),
     "tsg_moe_decode_layer": (C.c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, U32, U32, U32,
                                        U32]),
+    "tsg_moe_decode_layer_shared": (C.c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P,
+                                              U32, U32, U32, U32, U32]),
     "tsg_moe_set_fused_decode": (C.c_int, [P, C.c_int]),
     "tsg_qmv_int4": (C.c_int, [P, P, P, P, P, P, P, U32, U32]),
     "tsg_qwen_silu_mul": (C.c_int, [P, P, P, P, P, U32]),

@@ -17,7 +17,7 @@
 //  * phase 2: a wave owns 4 output rows x 8 slots x 2 half-rows; the 8 slot
 //    values of a row are combined in slot order in one lane, as the reference
 //    does (moe.metal:678-686).
-#include "gemv_lane.hpp"
+#include "qwen_shared.hpp"
 
 namespace tsg {
 namespace {
@@ -623,6 +623,14 @@ struct DecodeLayerArgs {
     uint32_t rows;         // down rows per block: ceil(d / kGroupMembers)
     uint32_t as_off;       // dynamic LDS: staged activation row (after x)
     uint32_t xe_off;       // dynamic LDS: router products x * es, fp32
+    // the Qwen-family shared expert (kernel flag SH): gate/up/down of one
+    // expert blob, its bf16 gate row, intermediate size <= kMaxSharedF
+    const uint8_t* sh_blob;
+    tsg_expert_offsets sh_o;
+    const uint16_t* sh_gate_w;
+    uint16_t* sh_acts;     // the shared activations, also returned to the caller
+    uint32_t sh_f;
+    uint32_t ss_off;       // dynamic LDS: staged shared activations
 };
 
 // Down row `row` of one slot on 8 lanes (lane = 8 r + j of the wave): the
@@ -792,21 +800,34 @@ __device__ __forceinline__ void wave_select_top8(const uint32_t (&key)[4], uint3
 // selects, and combines; wave w < pairs / 2 computes gate/up pairs 2w, 2w+1;
 // wave w < rows / 8 computes 8 down rows; the last wave (no down rows, so no
 // weight loads ahead of its polls) reads the slot's activations into LDS.
-template <int G, bool SYM, int ACT>
+//
+// With SH the layer also runs the Qwen-family shared branch
+// (QwenForwardRunner.swift:1548-1578) and takes its output as the residual
+// (:1583-1608), on the last wave of every block: at launch start, while the
+// router runs, it loads its block's two shared gate/up pairs (the shared
+// weights do not depend on the routing) and sums the gate logit; after the
+// top-8 it posts the two shared activations (tagged words, a 9th hand-off
+// region); it prefetches the shared down rows of the rows this block combines,
+// reads all shared activations with the slot's, and leaves
+// half(half(down . act) * sigmoid(logit)) for each of those rows in LDS for
+// the combine. Each step is the dense GEMV's lane geometry and the separate
+// kernels' arithmetic (qwen_shared.hpp), so the bits are tsg_moe_shared_expert's.
+template <int G, bool SYM, int ACT, bool SH>
 __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_arg) {
     // The arguments are copied to LDS once: under SGPR pressure the compiler
     // re-reads kernel arguments instead of spilling, and a kernarg reload in
     // a loop costs a memory round trip each time; an LDS copy costs cycles.
     __shared__ DecodeLayerArgs a;
-    static_assert(sizeof(DecodeLayerArgs) % 4 == 0 && sizeof(DecodeLayerArgs) <= 4 * 64, "args copy");
-    if (threadIdx.x < sizeof(DecodeLayerArgs) / 4)
-        reinterpret_cast<uint32_t*>(&a)[threadIdx.x] = reinterpret_cast<const uint32_t*>(&a_arg)[threadIdx.x];
+    static_assert(sizeof(DecodeLayerArgs) % 4 == 0, "args copy");
+    for (uint32_t i = threadIdx.x; i < sizeof(DecodeLayerArgs) / 4; i += blockDim.x)
+        reinterpret_cast<uint32_t*>(&a)[i] = reinterpret_cast<const uint32_t*>(&a_arg)[i];
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t s_tag;
     __shared__ uint16_t s_w[kTopK];
     __shared__ uint32_t s_idx[kTopK], s_fill[kTopK], s_skey[kTopK];
     __shared__ uint32_t s_gains[kMaxExperts];
     __shared__ __align__(16) uint64_t s_cand[kMaxExperts + kCandBatch];
+    __shared__ uint16_t s_sout[kMaxCombineRows];  // SH: shared output of the combine rows
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
     const uint32_t grp = blockIdx.x % kDecodeGroups, mem = blockIdx.x / kDecodeGroups;
     if (t < kTopK) {
@@ -827,6 +848,8 @@ __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_ar
     uint64_t* logits = sy.logits + grp * kMaxExperts;
     uint64_t* gacts = handoff + (size_t)grp * kHandoffWords;
     const uint32_t nwaves = blockDim.x >> 6;
+    const bool sh_wave = SH && wave == nwaves - 1u;
+    const uint32_t share = (a.rows + kDecodeGroups - 1u) / kDecodeGroups;  // combine rows
 
     // Every load of the first phase goes out before any is waited for: the
     // epoch, the per-expert gains, x for the gate/up dot products, x and es
@@ -885,6 +908,27 @@ __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_ar
         if (lane == 0) st_coherent(logits + er, tagged(tag, __float_as_uint(s)));
     }
     if constexpr (!SYM) staged_chunk_sums(xs, 0u, 1u, d, xsum);
+    // SH: this block's two shared gate/up pairs (lanes 0..31 pair 2b, 32..63
+    // pair 2b + 1; 16 lanes per row) and the gate logit, while the logits are
+    // gathered and ranked
+    ChunkBatch<kGUBatch> sbt;
+    GULane sl{};
+    float sh_scale = 0.0f;
+    if constexpr (SH) {
+        if (sh_wave) {
+            const uint32_t p = 2u * blockIdx.x + (lane >> 5);
+            const bool is_up = (lane >> 4) & 1u, live = p < a.sh_f;
+            const uint32_t pr = live ? p : 0u, ng = d / G;
+            const uint8_t* sb = global_ptr(a.sh_blob);
+            sl.w = sb + (is_up ? a.sh_o.up_w : a.sh_o.gate_w) + (uint64_t)pr * (d / 2u);
+            sl.s = reinterpret_cast<const uint16_t*>(sb + (is_up ? a.sh_o.up_s : a.sh_o.gate_s)) + (uint64_t)pr * ng;
+            sl.b = reinterpret_cast<const uint16_t*>(sb + (is_up ? a.sh_o.up_b : a.sh_o.gate_b)) + (uint64_t)pr * ng;
+            sl.fr = p;
+            sl.live = live;
+            load_batch<G, SYM, kGUBatch, kGULanes>(sl.w, sl.s, sl.b, 0u, lane & 15u, d / 32u, sbt);
+            sh_scale = qwen_sigmoid(gate_logit_wave(xg, global_ptr(a.sh_gate_w), d));
+        }
+    }
 
     // wave 0 gathers the group's logits and selects; the block waits once
     const uint32_t ne4 = (ne + 3u) & ~3u;
@@ -935,6 +979,42 @@ __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_ar
             st_coherent(gacts + fr, tagged(tag, act));
         }
     }
+    uint64_t* shacts = handoff + (size_t)kDecodeGroups * kHandoffWords;
+    ChunkBatch<1> sdb[kMaxCombineRows / 4];
+    if constexpr (SH) {
+        if (sh_wave) {
+            // act = half(silu(half(gate . x)) * half(up . x)) (shared_gate_up_kernel)
+            const uint32_t j = lane & 15u, nck = d / 32u;
+            float acc[1] = {0.0f};
+            for (uint32_t base = 0; base < nck; base += kGULanes * kGUBatch) {
+                if (base) load_batch<G, SYM, kGUBatch, kGULanes>(sl.w, sl.s, sl.b, base, j, nck, sbt);
+                compute_batch<G, SYM, kGUBatch, kGULanes, 1>(sbt, base, j, nck, xs, 0u, xsum, 1u, acc);
+            }
+            const float g = group16_sum(acc[0]);
+            const float u = shfl_xor(g, 16);
+            if (sl.live && ((lane >> 4) & 1u) == 0 && j == 0) {
+                const uint16_t act = silu_mul_h(f32_to_f16(g), f32_to_f16(u));
+                global_ptr(a.sh_acts)[sl.fr] = act;
+                st_coherent(shacts + sl.fr, tagged(tag, act));
+            }
+            // the shared down rows of this block's combine rows, 4 per pass
+            // (16 lanes per row, one chunk each: sh_f <= 512)
+            const uint8_t* sb = global_ptr(a.sh_blob);
+            const uint32_t fg = a.sh_f / G, fck = a.sh_f / 32u;
+#pragma unroll
+            for (uint32_t pp = 0; pp < kMaxCombineRows / 4; ++pp) {
+                if (4u * pp >= share) break;
+                const uint32_t i = 4u * pp + (lane >> 4);
+                const uint32_t cl = grp * share + i, crow = mem * a.rows + cl;
+                const uint32_t cr = (i < share && cl < a.rows && crow < d) ? crow : 0u;
+                load_batch<G, SYM, 1, kGULanes>(
+                    sb + a.sh_o.down_w + (uint64_t)cr * (a.sh_f / 2u),
+                    reinterpret_cast<const uint16_t*>(sb + a.sh_o.down_s) + (uint64_t)cr * fg,
+                    reinterpret_cast<const uint16_t*>(sb + a.sh_o.down_b) + (uint64_t)cr * fg, 0u, j,
+                    fck, sdb[pp]);
+            }
+        }
+    }
 
     // this block's down rows (8 per wave) stream while the group finishes
     const uint8_t* blob = layer_base + (uint64_t)s_idx[grp] * a.expert_stride;
@@ -965,6 +1045,42 @@ __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_ar
                                     (uint16_t)bits;
                             });
         }
+        if constexpr (SH) {
+            uint16_t* ss = reinterpret_cast<uint16_t*>(smem + a.ss_off);
+            float* ssum = reinterpret_cast<float*>(smem + a.ss_off + p2_slot_halves(a.sh_f) * 2u);
+            uint32_t live = 0;
+#pragma unroll
+            for (uint32_t k = 0; k < kMaxSharedF / 64u; ++k) live |= lane + 64u * k < a.sh_f ? 1u << k : 0u;
+            poll_tagged<kMaxSharedF / 64u>(sy, tag, live, [&](int k) { return shacts + lane + 64u * k; },
+                                           [&](int k, uint32_t bits) {
+                                               const uint32_t i = lane + 64u * k, c = i & 31u;
+                                               ss[(i >> 5) * kChunkLds + (c >> 3) * 8u + paired_pos(c & 7u)] =
+                                                   (uint16_t)bits;
+                                           });
+            const uint32_t j = lane & 15u, fck = a.sh_f / 32u;
+            if constexpr (!SYM) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // one wave: LDS in order
+                for (uint32_t q = lane; q < fck; q += 64u) {
+                    const uint16_t* chunk = ss + q * kChunkLds;
+                    float sum = 0.0f;
+                    for (uint32_t k = 0; k < 32u; ++k)
+                        sum += f16_to_f32(chunk[(k >> 3) * 8u + paired_pos(k & 7u)]);
+                    ssum[q] = sum;
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            // sharedOut of the combine rows (shared_down_kernel's arithmetic)
+#pragma unroll
+            for (uint32_t pp = 0; pp < kMaxCombineRows / 4; ++pp) {
+                if (4u * pp >= share) break;
+                float acc[1] = {0.0f};
+                compute_batch<G, SYM, 1, kGULanes, 1>(sdb[pp], 0u, j, fck, ss, 0u, ssum, 1u, acc);
+                const float v = group16_sum(acc[0]);
+                const uint32_t i = 4u * pp + (lane >> 4);
+                if (j == 0 && i < share)
+                    s_sout[i] = f32_to_f16(f16_to_f32(f32_to_f16(v)) * sh_scale);
+            }
+        }
     }
     __syncthreads();
     if constexpr (!SYM) {
@@ -981,11 +1097,12 @@ __global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_ar
     // this block's share of row range mem: y = half(res + sum_s w_s v_s) in
     // slot order (moe.metal:678-686)
     if (wave == 0) {
-        const uint32_t share = (a.rows + kDecodeGroups - 1u) / kDecodeGroups;
         const uint32_t cl = grp * share + lane;
         const uint32_t crow = mem * a.rows + cl;
         const bool live = lane < share && cl < a.rows && crow < d;
-        const uint16_t res = global_ptr(a.residual)[live ? crow : 0u];
+        uint16_t res;
+        if constexpr (SH) res = s_sout[lane < share ? lane : 0u];
+        else res = global_ptr(a.residual)[live ? crow : 0u];
         float vq[kTopK];
         poll_tagged<kTopK>(sy, tag, live ? 0xFFu : 0u,
                            [&](int q) { return parts + (size_t)q * kHandoffWords + crow; },
@@ -1132,10 +1249,11 @@ tsg_status phase2_dispatch(tsg_moe* moe, hipStream_t stream, const BlobSource& s
 // The fused one-launch decode layer, when every block fits on the device at
 // once (the rendezvous need all blocks resident). Returns TSG_ERR_DECLINED
 // otherwise and the caller runs the three-kernel sequence.
-template <int G, bool SYM, int ACT>
+template <int G, bool SYM, int ACT, bool SH>
 tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
     const auto up64 = [](uint32_t v) { return (v + 63u) / 64u * 64u; };
     uint32_t threads = 32u * a.pairs;                               // gate/up pairs
+    if (SH) threads = 64u * ((a.pairs + 1u) / 2u + 1u);             // + the shared wave
     threads = std::max(threads, 64u * ((a.rows + 7u) / 8u + 1u));    // down rows, 8 per wave, + poll wave
     threads = std::max(threads, 64u * a.router_rows);                // router rows
     threads = std::max(threads, up64((a.d / 8u + 1u) / 2u));         // x in two 16-byte units
@@ -1143,11 +1261,16 @@ tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
     const uint32_t as_bytes = p2_slot_halves(a.f) * 2u + (SYM ? 0u : (a.f / 32u) * 4u);
     a.as_off = (xs_bytes + 15u) & ~15u;
     a.xe_off = (a.as_off + as_bytes + 15u) & ~15u;
-    const size_t lds = a.xe_off + a.d * 4u;
-    auto kern = decode_layer_kernel<G, SYM, ACT>;
+    size_t lds = a.xe_off + a.d * 4u;
+    if (SH) {
+        a.ss_off = (uint32_t)((lds + 15u) & ~(size_t)15u);
+        lds = a.ss_off + p2_slot_halves(a.sh_f) * 2u + (SYM ? 0u : (a.sh_f / 32u) * 4u);
+    }
+    auto kern = decode_layer_kernel<G, SYM, ACT, SH>;
     int per_cu = 0;
     if (threads > 1024u || a.ne > kMaxExperts || a.f > kMaxFusedDim || a.d > kMaxFusedDim ||
-        (a.rows + kDecodeGroups - 1u) / kDecodeGroups > 64u ||
+        (a.rows + kDecodeGroups - 1u) / kDecodeGroups > kMaxCombineRows ||
+        (SH && (a.sh_f > kMaxSharedF || a.sh_f > 2u * kDecodeBlocks)) ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, (int)threads, lds) !=
             hipSuccess ||
         (uint64_t)per_cu * (uint64_t)moe->ctx->num_cus < kDecodeBlocks)
@@ -1156,13 +1279,14 @@ tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
     return check_launch("decode_layer");
 }
 
+template <bool SH>
 tsg_status fused_dispatch(tsg_moe* moe, hipStream_t stream, const DecodeLayerArgs& a) {
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
     const bool silu = moe->activation == TSG_ACT_SILU;
 #define TSG_FU(GG, SS)                                                             \
-    return silu ? launch_fused<GG, SS, TSG_ACT_SILU>(moe, stream, a)               \
-                : launch_fused<GG, SS, TSG_ACT_GELU_TANH>(moe, stream, a)
+    return silu ? launch_fused<GG, SS, TSG_ACT_SILU, SH>(moe, stream, a)           \
+                : launch_fused<GG, SS, TSG_ACT_GELU_TANH, SH>(moe, stream, a)
     if (ctx->group_size == 32) {
         if (sym) TSG_FU(32, true);
         TSG_FU(32, false);
@@ -1337,14 +1461,20 @@ extern "C" tsg_status tsg_moe_phase2_resident(tsg_moe* moe, tsg_stream stream,
                            f);
 }
 
-extern "C" tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream,
-                                           const tsg_layer* layer, const uint16_t* router_w,
-                                           const uint16_t* router_hidden, const uint16_t* es,
-                                           const uint16_t* pes, const uint16_t* x,
-                                           const uint16_t* residual, uint16_t* y,
-                                           uint32_t* out_idx, uint16_t* out_w,
-                                           uint16_t* acts, uint32_t ne, uint32_t d, uint32_t f,
-                                           uint32_t top_k) {
+struct SharedBranch {
+    const uint8_t* blob;
+    tsg_expert_offsets o;
+    const uint16_t* gate_w;
+    uint16_t* acts;
+    uint32_t f;
+};
+
+tsg_status decode_layer_impl(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                             const uint16_t* router_w, const uint16_t* router_hidden,
+                             const uint16_t* es, const uint16_t* pes, const uint16_t* x,
+                             const uint16_t* residual, uint16_t* y, uint32_t* out_idx,
+                             uint16_t* out_w, uint16_t* acts, uint32_t ne, uint32_t d,
+                             uint32_t f, uint32_t top_k, const SharedBranch* sh) {
     tsg_status st = check_moe(moe);
     if (st) return st;
     if ((st = check_decode_shape(moe->ctx, d, f, top_k))) return st;
@@ -1382,9 +1512,24 @@ extern "C" tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream,
     a.router_rows = (ne + kGroupMembers - 1u) / kGroupMembers;
     a.pairs = (f + kGroupMembers - 1u) / kGroupMembers;
     a.rows = (d + kGroupMembers - 1u) / kGroupMembers;
+    if (sh) {
+        a.sh_blob = sh->blob;
+        a.sh_o = sh->o;
+        a.sh_gate_w = sh->gate_w;
+        a.sh_acts = sh->acts;
+        a.sh_f = sh->f;
+    }
     if (!moe->unfused_decode) {
-        st = fused_dispatch(moe, s, a);
+        st = sh ? fused_dispatch<true>(moe, s, a) : fused_dispatch<false>(moe, s, a);
         if (st != TSG_ERR_DECLINED) return st;
+    }
+    if (sh) {
+        // the shared branch into y, then the routed experts on top of it
+        // (QwenForwardRunner.swift:1583-1608: residual = y = sharedOut)
+        if ((st = tsg_moe_shared_expert(moe, stream, sh->blob, &sh->o, x, sh->gate_w, sh->acts,
+                                        y, d, sh->f)))
+            return st;
+        residual = y;
     }
     if ((st = router_launch(moe, s, router_w, router_hidden, d, es, pes, out_idx, out_w, nullptr,
                             1, ne, d, top_k, true)))
@@ -1394,6 +1539,45 @@ extern "C" tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream,
     if ((st = phase1_dispatch(moe, s, src, layer->offsets, x, acts, d, f, top_k, false)))
         return st;
     return phase2_dispatch(moe, s, src, layer->offsets, acts, out_w, residual, y, d, f);
+}
+
+extern "C" tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream,
+                                           const tsg_layer* layer, const uint16_t* router_w,
+                                           const uint16_t* router_hidden, const uint16_t* es,
+                                           const uint16_t* pes, const uint16_t* x,
+                                           const uint16_t* residual, uint16_t* y,
+                                           uint32_t* out_idx, uint16_t* out_w,
+                                           uint16_t* acts, uint32_t ne, uint32_t d, uint32_t f,
+                                           uint32_t top_k) {
+    return decode_layer_impl(moe, stream, layer, router_w, router_hidden, es, pes, x, residual, y,
+                             out_idx, out_w, acts, ne, d, f, top_k, nullptr);
+}
+
+extern "C" tsg_status tsg_moe_decode_layer_shared(
+    tsg_moe* moe, tsg_stream stream, const tsg_layer* layer, const uint16_t* router_w,
+    const uint16_t* router_hidden, const uint16_t* es, const uint16_t* pes, const uint16_t* x,
+    uint16_t* y, uint32_t* out_idx, uint16_t* out_w, uint16_t* acts, const void* shared_blob,
+    const tsg_expert_offsets* shared_offsets, const uint16_t* shared_gate_weight,
+    uint16_t* shared_acts, uint32_t ne, uint32_t d, uint32_t f, uint32_t shared_f,
+    uint32_t top_k) {
+    TSG_REQUIRE(shared_blob && shared_offsets && shared_gate_weight && shared_acts,
+                TSG_ERR_INVALID_ARGUMENT, "NULL shared-expert operand");
+    TSG_REQUIRE(moe && moe->ctx, TSG_ERR_INVALID_ARGUMENT, "moe is NULL");
+    const uint32_t g = moe->ctx->group_size;
+    TSG_REQUIRE(shared_f > 0 && shared_f % g == 0, TSG_ERR_INVALID_ARGUMENT,
+                "shared_f=%u must be a positive multiple of the group size %u", shared_f, g);
+    const tsg_expert_offsets& o = *shared_offsets;
+    const uint8_t* b = static_cast<const uint8_t*>(shared_blob);
+    TSG_REQUIRE(aligned16(b + o.gate_w) && aligned16(b + o.up_w) && aligned16(b + o.down_w),
+                TSG_ERR_ALIGNMENT, "shared weight sub-tensors must start on 16 bytes");
+    TSG_REQUIRE(((o.gate_s | o.up_s | o.down_s | o.gate_b | o.up_b | o.down_b) & 1u) == 0,
+                TSG_ERR_ALIGNMENT, "shared scale/bias offsets must be even");
+    TSG_REQUIRE(aligned16(shared_gate_weight) && aligned16(shared_acts), TSG_ERR_ALIGNMENT,
+                "the shared gate row and shared_acts must be 16-byte aligned");
+    const SharedBranch sh{b, o, shared_gate_weight, shared_acts, shared_f};
+    // y is the residual too (the reference's sharedOut is both)
+    return decode_layer_impl(moe, stream, layer, router_w, router_hidden, es, pes, x, y, y,
+                             out_idx, out_w, acts, ne, d, f, top_k, &sh);
 }
 
 extern "C" tsg_status tsg_moe_set_fused_decode(tsg_moe* moe, int enabled) {

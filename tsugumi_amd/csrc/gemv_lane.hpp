@@ -6,7 +6,8 @@
 // A weight row of K int4 values is K/32 16-byte chunks (one g32 group, half a
 // g64 group). `LANES` lanes share a row; lane j owns chunks j, j+LANES, ...,
 // loaded KB at a time with every load of a batch issued before any use.
-// Chunks past the row end load a clamped address and enter with scale 0.
+// Chunks past the row end load a clamped address and leave the sum untouched,
+// so a row's bits do not depend on KB (how many chunk slots a lane carries).
 #pragma once
 
 #include "tsg_internal.hpp"
@@ -57,15 +58,16 @@ __device__ __forceinline__ void compute_batch(const ChunkBatch<KB>& bt, uint32_t
         const uint32_t c = base + j + LANES * i;
         const uint32_t cc = min(c, nchunks - 1u);
         const bool live = c < nchunks;
-        const float s = live ? bf16_to_f32((uint16_t)bt.s[i]) : 0.0f;
+        const float s = bf16_to_f32((uint16_t)bt.s[i]);
         float b = 0.0f;
-        if constexpr (!SYM) b = live ? bf16_to_f32((uint16_t)bt.b[i]) : 0.0f;
+        if constexpr (!SYM) b = bf16_to_f32((uint16_t)bt.b[i]);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if ((uint32_t)r >= nrows) break;
-            acc[r] = __builtin_fmaf(s, chunk_dot(bt.w[i], staged_chunk(xs + (size_t)r * row_h, cc), bias),
-                                    acc[r]);
-            if constexpr (!SYM) acc[r] = __builtin_fmaf(b, xsum[r * nchunks + cc], acc[r]);
+            float v = __builtin_fmaf(s, chunk_dot(bt.w[i], staged_chunk(xs + (size_t)r * row_h, cc), bias),
+                                     acc[r]);
+            if constexpr (!SYM) v = __builtin_fmaf(b, xsum[r * nchunks + cc], v);
+            acc[r] = live ? v : acc[r];  // a chunk past the row end leaves acc as it is
         }
     }
 }

@@ -8,40 +8,24 @@
 // GEMV (tsg_qmv_int4, DequantInt4GEMV), qwen_silu_mul (qwen.metal:466),
 // qwen_moe_shared_gate (qwen.metal:432-455) and qwen_moe_shared_gate_logit
 // (qwen.metal:1038-1046) — and fused into two launches that give the same
-// bits: gate/up rows use the GEMV's lane geometry and sum order, and the
-// gate logit is one block-wide sum shared by both forms.
-#include "gemv_lane.hpp"
+// bits: gate/up and down rows use the GEMV's lane geometry and sum order, and
+// the gate logit is gate_logit_wave (qwen_shared.hpp) everywhere.
+#include "qwen_shared.hpp"
 
 namespace tsg {
 namespace {
 
-constexpr uint32_t kGateThreads = 256;  // the block size gate_logit_block assumes
+constexpr uint32_t kGateThreads = 256;
 
-// qwen.metal:33-34.
-__device__ __forceinline__ float qwen_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
-__device__ __forceinline__ float qwen_silu(float x) { return x * qwen_sigmoid(x); }
-
-// half(silu(float(g)) * float(u)) (qwen.metal:466).
-__device__ __forceinline__ uint16_t silu_mul_h(uint16_t g, uint16_t u) {
-    return f32_to_f16(qwen_silu(f16_to_f32(g)) * f16_to_f32(u));
-}
-
-// The gate logit sum_i float(x[i]) * float(w[i]) (x fp16, w bf16) on one block
-// of kGateThreads threads: thread t accumulates i = t, t + 256, ... with fma in
-// order, each wave sums its lanes as group16_sum and then the four 16-lane rows
-// as (r0 + r1) + (r2 + r3), and the four waves add as (w0 + w1) + (w2 + w3).
-// Every thread returns the same value. `red` is 4 floats of LDS.
+// gate_logit_wave on wave 0 of the block, handed to every thread through LDS.
 __device__ float gate_logit_block(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                   uint32_t d, float* red) {
-    const uint32_t t = threadIdx.x;
-    float acc = 0.0f;
-    for (uint32_t i = t; i < d; i += kGateThreads)
-        acc = __builtin_fmaf(f16_to_f32(x[i]), bf16_to_f32(w[i]), acc);
-    acc = group16_sum(acc);
-    acc = (lane_value(acc, 0) + lane_value(acc, 16)) + (lane_value(acc, 32) + lane_value(acc, 48));
-    if ((t & 63u) == 0) red[t >> 6] = acc;
+    if (threadIdx.x < 64u) {
+        const float s = gate_logit_wave(x, w, d);
+        if (threadIdx.x == 0) red[0] = s;
+    }
     __syncthreads();
-    const float s = (red[0] + red[1]) + (red[2] + red[3]);
+    const float s = red[0];
     __syncthreads();
     return s;
 }
@@ -58,7 +42,7 @@ __global__ __launch_bounds__(kGateThreads) void shared_gate_kernel(uint16_t* __r
                                                                    const uint16_t* __restrict__ x,
                                                                    const uint16_t* __restrict__ w,
                                                                    uint32_t d) {
-    __shared__ float red[4];
+    __shared__ float red[1];
     const float scale = qwen_sigmoid(gate_logit_block(x, w, d, red));
     for (uint32_t i = threadIdx.x; i < d; i += kGateThreads)
         y[i] = f32_to_f16(f16_to_f32(y[i]) * scale);
@@ -111,7 +95,7 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(const uint8_t* __re
 }
 
 // out[r] = half(half(down_r · act) * sigmoid(w_g · x)): 16 rows per block in the
-// dense GEMV's geometry, the gate logit summed by every block the way
+// dense GEMV's geometry, the gate logit summed by every block as
 // shared_gate_kernel sums it.
 template <int G, bool SYM>
 __global__ __launch_bounds__(kGateThreads) void shared_down_kernel(
@@ -119,7 +103,7 @@ __global__ __launch_bounds__(kGateThreads) void shared_down_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate_w,
     uint16_t* __restrict__ out, uint32_t d, uint32_t f) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ float red[4];
+    __shared__ float red[1];
     uint16_t* as = reinterpret_cast<uint16_t*>(smem);
     float* asum = reinterpret_cast<float*>(smem + lds_chunks_halves(f) * 2u);
     const uint32_t t = threadIdx.x, j = t & 15u;
@@ -181,11 +165,20 @@ extern "C" tsg_status tsg_qwen_silu_mul(tsg_ctx* ctx, tsg_stream stream, const u
     return check_launch("qwen_silu_mul");
 }
 
+static tsg_status check_gate_row(const uint16_t* x, const uint16_t* w, uint32_t d) {
+    TSG_REQUIRE(d % 8u == 0 && d <= 64u * 8u * kGateUnits, TSG_ERR_UNSUPPORTED,
+                "hidden=%u: the gate sum takes a multiple of 8 up to %u", d, 64u * 8u * kGateUnits);
+    TSG_REQUIRE(aligned16(x) && aligned16(w), TSG_ERR_ALIGNMENT,
+                "x and the gate weight row must be 16-byte aligned");
+    return TSG_OK;
+}
+
 extern "C" tsg_status tsg_qwen_moe_shared_gate(tsg_ctx* ctx, tsg_stream stream, uint16_t* y,
                                                const uint16_t* x, const uint16_t* weight,
                                                uint32_t hidden) {
     tsg_status st = check_gate_args(ctx, y, x, weight, hidden);
     if (st) return st;
+    if ((st = check_gate_row(x, weight, hidden))) return st;
     hipLaunchKernelGGL(shared_gate_kernel, dim3(1), dim3(kGateThreads), 0, as_stream(stream), y,
                        x, weight, hidden);
     return check_launch("qwen_moe_shared_gate");
@@ -220,6 +213,8 @@ extern "C" tsg_status tsg_moe_shared_expert(tsg_moe* moe, tsg_stream stream, con
                 TSG_ERR_ALIGNMENT, "scale/bias offsets must be even");
     TSG_REQUIRE(aligned16(x) && aligned16(act_scratch), TSG_ERR_ALIGNMENT,
                 "x and act_scratch must be 16-byte aligned");
+    tsg_status st = check_gate_row(x, gate_weight, d);
+    if (st) return st;
     TSG_REQUIRE((size_t)lds_chunks_halves(d) * 2u + (d / 32u) * 4u <= 64u * 1024u,
                 TSG_ERR_UNSUPPORTED, "d=%u does not fit the LDS staging", d);
     hipStream_t s = as_stream(stream);

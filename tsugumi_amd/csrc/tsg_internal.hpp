@@ -86,12 +86,15 @@ static_assert(kSyncLogitWord + kDecodeGroups * 2 * kMaxExperts <= kMaxCounters, 
 static_assert(kSyncLogitWord % 2 == 0, "64-bit words must be aligned");
 // Per-group hand-off regions of the one-launch layer (ctx->act_replicas):
 // group g's region holds kHandoffWords tagged 64-bit words, its slot's
-// activations in [0, kMaxFusedDim) and its partial down outputs above.
-constexpr uint32_t kActReplicas = kDecodeGroups;
+// activations in [0, kMaxFusedDim) and its partial down outputs above; a
+// ninth region holds the shared expert's activations.
+constexpr uint32_t kActReplicas = kDecodeGroups + 1;  // + the shared expert's activations
 constexpr uint32_t kActReplicaHalves = 8u * 4096u;
 constexpr uint32_t kHandoffWords = kActReplicaHalves / 4u;
 constexpr uint32_t kMaxFusedDim = 4096u;  // largest d and f of the one-launch layer
 static_assert(2u * kMaxFusedDim <= kHandoffWords, "hand-off region overflow");
+constexpr uint32_t kMaxCombineRows = 16;  // output rows one block combines: ceil(ceil(d/32)/8)
+constexpr uint32_t kMaxSharedF = 512;     // shared-expert intermediate size of the one-launch layer
 
 constexpr uint32_t kTopK = 8;
 
