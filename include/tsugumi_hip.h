@@ -38,6 +38,8 @@ typedef enum tsg_status {
     TSG_ERR_DECLINED = 4,         /* optional path declines; caller falls back */
     TSG_ERR_HIP = 5,              /* HIP runtime error                         */
     TSG_ERR_OUT_OF_MEMORY = 6,
+    TSG_ERR_FORMAT = 7,           /* a MoEPack install fails validation        */
+    TSG_ERR_IO = 8,               /* a MoEPack file is missing or unreadable   */
     /* PrefillMoEGroupingError cases (PrefillMoEGrouping.swift:52-62) */
     TSG_ERR_GROUPING_INVALID_QUERY_COUNT = 100,
     TSG_ERR_GROUPING_INVALID_TOP_K = 101,
@@ -399,6 +401,102 @@ tsg_status tsg_prefill_moe_reduce_token_major(tsg_ctx* ctx, tsg_stream stream,
                                               const uint16_t* route_weights, uint16_t* h2,
                                               uint32_t query_count, uint32_t top_k,
                                               uint32_t d);
+
+/* ------------------------------------------------------ MoEPack install ----
+ * Reader of an installed pack's manifest.json and packed_experts/layout.json,
+ * and the layer-file upload that replaces the SSD streamer: the reference
+ * opens a layer file and preads expert blobs into slot buffers on demand
+ * (ModelExpertIO.swift:112-324); here the whole layer is resident in HBM with
+ * each blob at its logical expert index, so the kernels address expert e at
+ * base + e * expert_stride whatever the file's physical order.
+ *
+ * Validation restates ManifestReader.decode/validate (ManifestReader.swift:
+ * 182-313), MoEPackManifestCodec.validate (MoEPackManifestV1.swift:378-559),
+ * MoEPackV1StructuralValidator.validate/crossValidate
+ * (MoEPackPackedExpertsLayoutV1.swift:84-211). Failures return TSG_ERR_FORMAT
+ * (content) or TSG_ERR_IO (file system); tsg_last_error() starts with the
+ * reference's ModelError case: indexCorrupt, notAMoEPackDirectory,
+ * unsupportedVersion, unknownFlag, expertStrideNotPageAligned, missingFile,
+ * partialInstall, posixFailed. Not restated: the field-by-field comparison
+ * with a compiled ArchConfig (validateArch; the caller compares the
+ * dimensions in tsg_moepack_info) and the vision/draft geometry checks (their
+ * weights are not read here). */
+typedef struct tsg_moepack tsg_moepack;
+
+typedef struct tsg_moepack_info {
+    uint32_t num_layers;            /* manifest.numLayers                          */
+    uint32_t experts_per_layer;     /* manifest.expertsPerLayer                    */
+    uint64_t expert_stride;         /* bytes per expert blob, a multiple of 16384  */
+    uint32_t hidden_size;           /* arch.hiddenSize                             */
+    uint32_t moe_intermediate_size; /* arch.moeIntermediateSize                    */
+    uint32_t top_k;                 /* arch.topKExperts                            */
+    uint32_t version_minor;
+    uint32_t legacy_magic;          /* 1: magic "GTURBO", 0: "MOEPACK"             */
+    uint32_t has_quant;             /* 0: the manifest has no quant section        */
+    uint32_t affine_group_size;     /* quant.embedding.groupSize (32|64), 0 if none */
+    uint32_t symmetric;             /* 1: the 4-bit slots use `sym` (no biases)    */
+    uint32_t routed_weight_bits;    /* quant.routedExpert.weightBits               */
+    uint32_t shared_weight_bits;    /* quant.sharedExpert.weightBits               */
+    uint32_t router_weight_bits;    /* quant.router.weightBits (8 or 16)           */
+    uint32_t has_layout;            /* layout.json read and cross-validated        */
+    uint32_t is_gemma4;             /* arch.family absent (ManifestArch.isGemma4)  */
+    char family[32];                /* arch.family, "" when absent                 */
+} tsg_moepack_info;
+
+/* SubTensorEntry (PackedExpertsLayout.swift:4-10) plus the owning expert's
+ * physical rank. */
+typedef struct tsg_moepack_subtensor {
+    uint64_t offset, size;   /* bytes, relative to the expert blob            */
+    uint32_t dtype;          /* MoEPackFormatV1.DType: 0 U32, 1 BF16          */
+    uint32_t bits;           /* weight width from the layout, 0 when absent   */
+    uint32_t rank;           /* shape entries (the first 8 are in `shape`)    */
+    uint32_t shape[8];
+    uint32_t physical_rank;  /* ExpertEntry.physicalRank of this expert       */
+} tsg_moepack_subtensor;
+
+/* ManifestReader.load + PackedExpertsLayoutReader.load(manifest:)
+ * (ManifestReader.swift:169-180, PackedExpertsLayout.swift:60-81). Files are
+ * opened component by component without following symlinks, must be regular
+ * files, and are size-capped before reading (0 = the reference defaults:
+ * 4 MiB manifest, 64 MiB layout). The directory stays open for
+ * tsg_moepack_load_layer. */
+tsg_status tsg_moepack_open(const char* directory, uint64_t manifest_max_bytes,
+                            uint64_t layout_max_bytes, tsg_moepack** out);
+/* ManifestReader.decode(data:) and PackedExpertsLayoutReader.decode(data:
+ * manifest:) on in-memory documents; layout_json may be NULL (manifest only).
+ * A parsed pack has no layer files to load. */
+tsg_status tsg_moepack_parse(const char* manifest_json, uint64_t manifest_len,
+                             const char* layout_json, uint64_t layout_len, tsg_moepack** out);
+void tsg_moepack_close(tsg_moepack* pack);
+tsg_status tsg_moepack_get_info(const tsg_moepack* pack, tsg_moepack_info* out);
+/* Model.routedExpertOffsets(layer:) (ModelExpertIO.swift:56-84): expert 0's
+ * gate/up/down sub-tensor offsets; without `<role>_biases` the bias offset
+ * aliases `<role>_scales`. TSG_ERR_FORMAT when a role is missing. */
+tsg_status tsg_moepack_routed_offsets(const tsg_moepack* pack, uint32_t layer,
+                                      tsg_expert_offsets* out);
+/* Model.routedExpertPhysicalOffsets(layer:) (ModelExpertIO.swift:86-88):
+ * offsets[e] = byte offset of logical expert e's blob in the layer file;
+ * count must equal experts_per_layer. */
+tsg_status tsg_moepack_physical_offsets(const tsg_moepack* pack, uint32_t layer,
+                                        uint64_t* offsets, uint32_t count);
+/* PackedExpertsLayout.expert(layer:expert:).subTensors[name]
+ * (PackedExpertsLayout.swift:51-54); `expert` is the logical id. */
+tsg_status tsg_moepack_tensor(const tsg_moepack* pack, uint32_t layer, uint32_t expert,
+                              const char* name, tsg_moepack_subtensor* out);
+/* Reads packed_experts/<file> of `layer` (its size must be experts_per_layer
+ * * expert_stride) and returns a new HBM-resident tsg_layer holding logical
+ * expert e at e * expert_stride, with tsg_moepack_routed_offsets. The upload
+ * goes through two pinned staging buffers of at most 64 MiB on `stream` and
+ * has finished when this returns. The caller sets the context's group size
+ * and scheme from tsg_moepack_info. */
+tsg_status tsg_moepack_load_layer(const tsg_moepack* pack, tsg_ctx* ctx, tsg_stream stream,
+                                  uint32_t layer, tsg_layer** out);
+/* The same upload into an existing layer (tsg_layer_create or caller-owned HBM
+ * through tsg_layer_wrap, e.g. one arena for every layer). The layer must have
+ * experts_per_layer experts, the pack's stride and tsg_moepack_routed_offsets;
+ * otherwise TSG_ERR_INVALID_ARGUMENT and nothing is written. */
+tsg_status tsg_moepack_upload_layer(const tsg_moepack* pack, tsg_stream stream, uint32_t layer,
+                                    tsg_layer* dst);
 
 /* ---------------------------------------------- synthetic fixtures ------
  * Device generators for benchmark inputs (no reference counterpart; the

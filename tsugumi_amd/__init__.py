@@ -12,6 +12,7 @@ include/tsugumi_hip.h (libtsugumi_hip.so). Names follow the reference:
     PrefillGroupedRoutedMoE -> PrefillGroupedRoutedMoE (PrefillGroupedRoutedMoE.swift)
     PrefillMoE              -> PrefillMoE     (PrefillMoE.swift:11-38)
     streamed experts        -> ResidentLayer  (whole layer held in HBM)
+    ManifestReader + PackedExpertsLayoutReader -> MoEPack (install reader + layer upload)
 
 Device buffers are torch CUDA tensors (plumbing only); `stream` defaults to
 torch's current stream. Every call raises TsgError on a non-OK status; there
@@ -31,6 +32,7 @@ __all__ = [
     "Context", "MoE", "DequantInt4GEMV", "QwenKernels", "encode_shared_expert",
     "PrefillRouter", "PrefillMoEGrouping",
     "PrefillRoutedGEMMPlanner", "PrefillGroupedRoutedMoE", "PrefillMoE", "ResidentLayer",
+    "MoEPack",
     "ExpertOffsets", "TsgError", "PAIR_DTYPE", "BLOCK_DTYPE", "GROUP_DTYPE", "TILE_DTYPE",
     "generators", "load",
 ]
@@ -142,6 +144,19 @@ class ResidentLayer:
                                         dst_offset))
         self.ctx.synchronize(stream)
 
+    @classmethod
+    def _adopt(cls, ctx: Context, handle, num_experts: int, expert_stride: int, offsets):
+        """Takes ownership of a tsg_layer made by the library (MoEPack.load_layer)."""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        self.lib = ctx.lib
+        self.num_experts = num_experts
+        self.expert_stride = expert_stride
+        self.offsets = offsets_from(offsets)
+        self._keep = None
+        self.handle = handle
+        return self
+
     @property
     def device_ptr(self) -> int:
         return int(self.lib.tsg_layer_device_ptr(self.handle))
@@ -149,6 +164,107 @@ class ResidentLayer:
     def close(self) -> None:
         if getattr(self, "handle", None):
             self.lib.tsg_layer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class MoEPack:
+    """An installed MoEPack's manifest.json + packed_experts/layout.json,
+    validated as ManifestReader.load (ManifestReader.swift:169-313) and
+    PackedExpertsLayoutReader.load (PackedExpertsLayout.swift:60-115) do.
+
+    `load_layer` replaces the reference's per-expert SSD streamer
+    (ModelExpertIO.swift:112-324): the whole layer file goes to HBM, each
+    expert blob at its logical index. Errors raise TsgError with status
+    TSG_ERR_FORMAT (7) or TSG_ERR_IO (8); the message starts with the
+    reference's ModelError case name."""
+
+    def __init__(self, handle, lib):
+        self.handle = handle
+        self.lib = lib
+        info = _abi.MoEPackInfo()
+        check(lib.tsg_moepack_get_info(handle, C.byref(info)))
+        self.info = {name: (getattr(info, name).decode() if name == "family"
+                            else int(getattr(info, name)))
+                     for name, _ in _abi.MoEPackInfo._fields_}
+
+    @classmethod
+    def open(cls, directory, manifest_max_bytes: int = 0, layout_max_bytes: int = 0):
+        lib = load()
+        h = C.c_void_p()
+        check(lib.tsg_moepack_open(str(directory).encode(), manifest_max_bytes,
+                                   layout_max_bytes, C.byref(h)))
+        return cls(h, lib)
+
+    @classmethod
+    def parse(cls, manifest: bytes, layout: bytes | None = None):
+        lib = load()
+        h = C.c_void_p()
+        check(lib.tsg_moepack_parse(manifest, len(manifest), layout,
+                                    0 if layout is None else len(layout), C.byref(h)))
+        return cls(h, lib)
+
+    @property
+    def num_layers(self) -> int:
+        return self.info["num_layers"]
+
+    @property
+    def experts_per_layer(self) -> int:
+        return self.info["experts_per_layer"]
+
+    @property
+    def expert_stride(self) -> int:
+        return self.info["expert_stride"]
+
+    def routed_offsets(self, layer: int) -> ExpertOffsets:
+        """Model.routedExpertOffsets(layer:) (ModelExpertIO.swift:56-84)."""
+        o = ExpertOffsets()
+        check(self.lib.tsg_moepack_routed_offsets(self.handle, layer, C.byref(o)))
+        return o
+
+    def physical_offsets(self, layer: int) -> np.ndarray:
+        """Model.routedExpertPhysicalOffsets(layer:) (ModelExpertIO.swift:86-88)."""
+        out = np.zeros(self.experts_per_layer, np.uint64)
+        check(self.lib.tsg_moepack_physical_offsets(self.handle, layer, _np_ptr(out),
+                                                    out.size))
+        return out
+
+    def tensor(self, layer: int, expert: int, name: str) -> dict:
+        """expert(layer:expert:).subTensors[name] (PackedExpertsLayout.swift:51-54)."""
+        t = _abi.MoEPackSubTensor()
+        check(self.lib.tsg_moepack_tensor(self.handle, layer, expert, name.encode(),
+                                          C.byref(t)))
+        return {"offset": t.offset, "size": t.size, "dtype": ("U32", "BF16")[t.dtype],
+                "bits": t.bits or None, "shape": list(t.shape[:min(t.rank, 8)]),
+                "physical_rank": t.physical_rank}
+
+    def configure(self, ctx: "Context") -> None:
+        """Sets the context's affine group size and scheme from manifest.quant."""
+        if self.info["has_quant"]:
+            ctx.set_affine_group_size(self.info["affine_group_size"])
+            ctx.set_affine_scheme("sym" if self.info["symmetric"] else "affine")
+
+    def load_layer(self, ctx: "Context", layer: int, stream=None) -> ResidentLayer:
+        h = C.c_void_p()
+        check(self.lib.tsg_moepack_load_layer(self.handle, ctx.handle, _stream(stream), layer,
+                                              C.byref(h)))
+        return ResidentLayer._adopt(ctx, h, self.experts_per_layer, self.expert_stride,
+                                    self.routed_offsets(layer))
+
+    def upload_layer(self, dst: ResidentLayer, layer: int, stream=None) -> None:
+        """Uploads layer `layer` into an existing ResidentLayer of the same
+        geometry (e.g. one wrapping caller-owned HBM)."""
+        check(self.lib.tsg_moepack_upload_layer(self.handle, _stream(stream), layer,
+                                                dst.handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.tsg_moepack_close(self.handle)
             self.handle = None
 
     def __del__(self):

@@ -19,6 +19,8 @@ TSG_ERR_UNSUPPORTED = 3
 TSG_ERR_DECLINED = 4
 TSG_ERR_HIP = 5
 TSG_ERR_OUT_OF_MEMORY = 6
+TSG_ERR_FORMAT = 7
+TSG_ERR_IO = 8
 GROUPING_ERRORS = {
     100: "invalidQueryCount", 101: "invalidTopK", 102: "invalidNumExperts",
     103: "invalidTileExpertCount", 104: "pairCountMismatch", 105: "tokenOutOfRange",
@@ -55,6 +57,26 @@ class RoutedBlock(C.Structure):
     """PrefillRoutedGEMMBlock (PrefillGroupedRoutedMoE.swift:20-25), 16 bytes."""
     _fields_ = [("local_slot", C.c_uint32), ("pair_start", C.c_uint32),
                 ("row_count", C.c_uint32), ("local_row", C.c_uint32)]
+
+
+class MoEPackInfo(C.Structure):
+    """tsg_moepack_info: what a validated manifest says about the routed experts."""
+    _fields_ = [("num_layers", C.c_uint32), ("experts_per_layer", C.c_uint32),
+                ("expert_stride", C.c_uint64), ("hidden_size", C.c_uint32),
+                ("moe_intermediate_size", C.c_uint32), ("top_k", C.c_uint32),
+                ("version_minor", C.c_uint32), ("legacy_magic", C.c_uint32),
+                ("has_quant", C.c_uint32), ("affine_group_size", C.c_uint32),
+                ("symmetric", C.c_uint32), ("routed_weight_bits", C.c_uint32),
+                ("shared_weight_bits", C.c_uint32), ("router_weight_bits", C.c_uint32),
+                ("has_layout", C.c_uint32), ("is_gemma4", C.c_uint32),
+                ("family", C.c_char * 32)]
+
+
+class MoEPackSubTensor(C.Structure):
+    """SubTensorEntry (PackedExpertsLayout.swift:4-10) plus the expert's physical rank."""
+    _fields_ = [("offset", C.c_uint64), ("size", C.c_uint64), ("dtype", C.c_uint32),
+                ("bits", C.c_uint32), ("rank", C.c_uint32), ("shape", C.c_uint32 * 8),
+                ("physical_rank", C.c_uint32)]
 
 
 P = C.c_void_p
@@ -113,6 +135,15 @@ SIGNATURES = {
     "tsg_prefill_moe_down": (C.c_int, [P, P, P, P, P, P, U32, P, P, U32, U32, U32]),
     "tsg_prefill_moe_rows": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, U32, U32]),
     "tsg_prefill_moe_reduce_token_major": (C.c_int, [P, P, P, P, P, U32, U32, U32]),
+    "tsg_moepack_open": (C.c_int, [C.c_char_p, U64, U64, C.POINTER(P)]),
+    "tsg_moepack_parse": (C.c_int, [C.c_char_p, U64, C.c_char_p, U64, C.POINTER(P)]),
+    "tsg_moepack_close": (None, [P]),
+    "tsg_moepack_get_info": (C.c_int, [P, C.POINTER(MoEPackInfo)]),
+    "tsg_moepack_routed_offsets": (C.c_int, [P, U32, C.POINTER(ExpertOffsets)]),
+    "tsg_moepack_physical_offsets": (C.c_int, [P, U32, P, U32]),
+    "tsg_moepack_tensor": (C.c_int, [P, U32, U32, C.c_char_p, C.POINTER(MoEPackSubTensor)]),
+    "tsg_moepack_load_layer": (C.c_int, [P, P, P, U32, C.POINTER(P)]),
+    "tsg_moepack_upload_layer": (C.c_int, [P, P, U32, P]),
     "tsg_gen_bytes": (C.c_int, [P, U64, P, U64]),
     "tsg_gen_bf16_normal": (C.c_int, [P, U64, P, U64, C.c_float, C.c_int, C.c_float]),
     "tsg_gen_f16_normal": (C.c_int, [P, U64, P, U64, C.c_float]),

@@ -15,9 +15,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libtsugumi_hip.so")
-SOURCES = ["core.hip", "decode.hip", "qmv.hip", "shared.hip", "prefill.hip", "host_routing.cpp"]
+SOURCES = ["core.hip", "decode.hip", "qmv.hip", "shared.hip", "prefill.hip", "host_routing.cpp",
+           "moepack.cpp"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
+ROCM = os.environ.get("ROCM_PATH", os.path.dirname(os.path.dirname(os.path.realpath(HIPCC))))
 # -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32 (the
 # host pass warns that it does not know the feature; that is harmless).
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
@@ -28,8 +30,8 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(os.path.basename(src))[0] + ".o")
     cmd = [HIPCC, *FLAGS]
-    if src.endswith(".cpp"):
-        cmd += ["-x", "c++"]
+    if src.endswith(".cpp"):  # host-only C++; may call the HIP runtime API
+        cmd += ["-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include")]
     cmd += ["-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"

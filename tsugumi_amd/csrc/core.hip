@@ -50,6 +50,8 @@ extern "C" const char* tsg_status_string(tsg_status s) {
         case TSG_ERR_DECLINED: return "declined";
         case TSG_ERR_HIP: return "HIP runtime error";
         case TSG_ERR_OUT_OF_MEMORY: return "out of device memory";
+        case TSG_ERR_FORMAT: return "invalid MoEPack install";
+        case TSG_ERR_IO: return "MoEPack file missing or unreadable";
         case TSG_ERR_GROUPING_INVALID_QUERY_COUNT: return "invalidQueryCount";
         case TSG_ERR_GROUPING_INVALID_TOP_K: return "invalidTopK";
         case TSG_ERR_GROUPING_INVALID_NUM_EXPERTS: return "invalidNumExperts";
@@ -226,6 +228,17 @@ extern "C" tsg_status tsg_layer_upload(tsg_layer* layer, tsg_stream stream, cons
                                as_stream(stream)));
     return TSG_OK;
 }
+
+namespace tsg {
+// Geometry of a layer for host code outside this file (the MoEPack loader).
+void layer_geometry(const tsg_layer* layer, int* device, uint32_t* num_experts,
+                    uint64_t* expert_stride, tsg_expert_offsets* offsets) {
+    *device = layer->ctx->device;
+    *num_experts = layer->num_experts;
+    *expert_stride = layer->expert_stride;
+    *offsets = layer->offsets;
+}
+}  // namespace tsg
 
 extern "C" void* tsg_layer_device_ptr(const tsg_layer* layer) {
     return layer ? layer->base : nullptr;
