@@ -185,9 +185,11 @@ def test_rows_path_matches_decode_bitwise(tsg, ctx):
     assert e.value.status == 4
 
 
-def test_reduce_token_major_bit_exact(tsg, ctx):
-    rng = oracle.SplitMix64(0x7E)
-    t, k, d = 37, 8, 2816
+@pytest.mark.parametrize("t,k,d", [(37, 8, 2816), (5, 4, 104), (5, 3, 104), (7, 8, 100)])
+def test_reduce_token_major_bit_exact(tsg, ctx, t, k, d):
+    """16-byte vector form (d % 8 == 0, k in 1, 2, 4, 8) and the scalar form
+    (k = 3, d = 100)."""
+    rng = oracle.SplitMix64(0x7E + d)
     P = rng.uniforms_f16(-1, 1, t * k * d)
     w = rng.uniforms_f16(0, 0.3, t * k)
     h2 = empty(t * d)

@@ -98,6 +98,39 @@ def test_dequant_f16_is_bit_exact(tsg, ctx, group, scheme):
 
 
 @pytest.mark.parametrize("group", GROUPS)
+def test_affine_dequant_rounds_through_fp32(tsg, ctx, group):
+    """half(fma(q, s, b)) rounds twice, to fp32 then to fp16. With s of an odd
+    8-bit significand (e.g. 1.9921875) and q = 15, q * s needs 12 bits and
+    sits on an fp16 midpoint; a bias of +-2^-30 moves the exact sum off the
+    midpoint but not its fp32 rounding, so the fp16 tie breaks to even, where
+    a single rounding of the exact sum would not."""
+    configure(ctx, group, "affine")
+    rows, n = 16, 256
+    rng = np.random.default_rng(0xDF)
+    packed = rng.integers(0, 256, (rows, n // 2), dtype=np.uint8)
+    packed[:, ::4] = 0xFF  # q = 15 in both nibbles
+    odd = np.array([0x3FFF, 0x3F81, 0x3FC1, 0x4081, 0xBFFF, 0x3E7F], np.uint16)
+    tiny = np.array([0x3080, 0xB080, 0x2F80, 0x0001], np.uint16)  # +-2^-30, 2^-32, bf16 subnormal
+    scales = odd[rng.integers(0, odd.size, (rows, n // group))]
+    biases = tiny[rng.integers(0, tiny.size, (rows, n // group))]
+    want = oracle.dequantize_int4_f16(packed, scales, biases, n, group, False)
+    # the constructed ties: the oracle's value differs from a single rounding
+    q4 = np.stack([packed & 15, packed >> 4], axis=-1).reshape(rows, n).astype(np.float64)
+    exact = (q4 * np.repeat(oracle.bf16_to_float(scales).astype(np.float64), group, axis=1) +
+             np.repeat(oracle.bf16_to_float(biases).astype(np.float64), group, axis=1))
+    single = exact.astype(np.float16).view(np.uint16)  # one rounding of the exact sum
+    assert 0 < (single != want).sum() < want.size // 8
+    q = tsg.DequantInt4GEMV(ctx)
+    for gemm_path in (False, True):
+        out = empty(rows * n)
+        q.debug_dequant_f16(dev(packed), dev(scales), dev(biases), out, rows, n,
+                            gemm_path=gemm_path)
+        got = host(out, np.uint16).reshape(rows, n)
+        bad = np.argwhere(got != want)
+        assert bad.size == 0, f"gemm_path={gemm_path}: {len(bad)} mismatches, first {bad[:3]}"
+
+
+@pytest.mark.parametrize("group", GROUPS)
 def test_router_kernelcheck_and_canonical_order(tsg, ctx, group):
     """checkRouter(16) cases (main.swift:409-517, seed 0xD2, 4 draws): indices
     equal routerReference's; weights within fp16Reduction; logits bit-equal to

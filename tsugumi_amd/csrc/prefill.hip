@@ -122,13 +122,19 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(
 typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
 
 // Per (weight row, group) dequantisation parameters. Every weight is staged
-// as RNE_f16(fmaf(q, s, b)) with b = -8 s under sym (prefill.metal:1021-1026).
-// The nibble q is isolated inside a 16-bit half, where as an fp16 bit pattern
-// it is the subnormal q * 2^-24 (bits 0..3) or q * 2^-20 (bits 4..7); the
-// scale is pre-multiplied by 2^24 or 2^20, so v_fma_mix computes the exact
-// product q * s, adds b with fmaf's single fp32 rounding and rounds once to
-// fp16: the reference's arithmetic bit for bit (for |s| < 2^103, where s * 2^24
-// stays finite), with no per-group test.
+// as RNE_f16(fmaf(q, s, b)) with b = -8 s under sym (prefill.metal:1021-1026):
+// fmaf rounds q * s + b to fp32, the conversion rounds that to fp16. The
+// nibble q is isolated inside a 16-bit half, where as an fp16 bit pattern it
+// is the subnormal q * 2^-24 (bits 0..3) or q * 2^-20 (bits 4..7); the scale
+// is pre-multiplied by 2^24 or 2^20, so v_fma_mix forms the exact product
+// q * s (for |s| < 2^103, where s * 2^24 stays finite), with no per-group test.
+//  - sym: q * s - 8 s = (q - 8) * s has at most 12 significant bits, exact in
+//    fp32, so v_fma_mix{lo,hi}_f16, which round the exact sum once to fp16,
+//    give the reference's bits.
+//  - affine: q * s + b can need more than 24 bits (b far smaller or larger
+//    than s), and rounding it to fp32 first can land on an fp16 tie that a
+//    single rounding would not; the sum is therefore taken to fp32 with
+//    v_fma_mix_f32 and converted with its own instruction.
 struct GroupScale {
     float s_lo, s_hi, b;  // s * 2^24, s * 2^20, b
 };
@@ -146,19 +152,28 @@ __device__ __forceinline__ GroupScale group_scale(uint16_t s_bits, uint16_t b_bi
 // Eight weights (one packed u32, elements 0..7 of a K run), in element order:
 // per byte j (elements 2j, 2j+1) v_perm copies the byte into both halves, one
 // AND keeps the low nibble in the low half and the high nibble in the high
-// half, and two v_fma_mix produce the pair.
+// half, and two v_fma_mix produce the pair (sym) or two fp32 sums that one
+// conversion packs (affine).
+template <bool SYM>
 __device__ __forceinline__ h8v_t dequant8(uint32_t w, const GroupScale& g) {
     h2_t p[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t x = __builtin_amdgcn_perm(w, w, 0x0C000C00u | ((uint32_t)j << 16) | (uint32_t)j);
         const h2_t y = __builtin_bit_cast(h2_t, x & 0x00F0000Fu);
-        // the empty asm makes the low half a value of its own, so the pair
-        // becomes v_fma_mixlo_f16 + v_fma_mixhi_f16 rather than two
-        // v_fma_mix_f32 and a v_cvt_pk_f16_f32
-        _Float16 lo = (_Float16)__builtin_fmaf((float)y.x, g.s_lo, g.b);
-        asm("" : "+v"(lo));
-        p[j] = h2_t{lo, (_Float16)__builtin_fmaf((float)y.y, g.s_hi, g.b)};
+        if constexpr (SYM) {
+            // the empty asm makes the low half a value of its own, so the pair
+            // becomes v_fma_mixlo_f16 + v_fma_mixhi_f16 rather than two
+            // v_fma_mix_f32 and a v_cvt_pk_f16_f32
+            _Float16 lo = (_Float16)__builtin_fmaf((float)y.x, g.s_lo, g.b);
+            asm("" : "+v"(lo));
+            p[j] = h2_t{lo, (_Float16)__builtin_fmaf((float)y.y, g.s_hi, g.b)};
+        } else {
+            float lo = __builtin_fmaf((float)y.x, g.s_lo, g.b);
+            float hi = __builtin_fmaf((float)y.y, g.s_hi, g.b);
+            asm("" : "+v"(lo), "+v"(hi));
+            p[j] = h2_t{(_Float16)lo, (_Float16)hi};
+        }
     }
     return h8v_t{p[0].x, p[0].y, p[1].x, p[1].y, p[2].x, p[2].y, p[3].x, p[3].y};
 }
@@ -181,7 +196,7 @@ __global__ void gemm_dequant_probe_kernel(const uint8_t* __restrict__ w,
         const uint32_t g = k0 / G;
         const GroupScale gs = group_scale<SYM>(scales[r * (n / G) + g],
                                                SYM ? (uint16_t)0 : biases[r * (n / G) + g]);
-        *reinterpret_cast<uint4*>(out + r * n + k0) = __builtin_bit_cast(uint4, dequant8(v, gs));
+        *reinterpret_cast<uint4*>(out + r * n + k0) = __builtin_bit_cast(uint4, dequant8<SYM>(v, gs));
     }
 }
 
@@ -409,20 +424,20 @@ __device__ __forceinline__ void gemm_issue_scales(const GemmLane& L, uint8_t* sm
 }
 
 // The MFMA work of one chunk (stage ST) for the wave's two weight tiles.
-template <int NT, int ST>
+template <bool SYM, int NT, int ST>
 __device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT], const u32x4_t& bw0,
                                          const u32x4_t& bw1, const GroupScale& g0,
                                          const GroupScale& g1, f16v_t (&acc)[NT][2]) {
     h8v_t bf[2][2];
-    bf[0][0] = dequant8(bw0[0], g0);
-    bf[0][1] = dequant8(bw1[0], g1);
+    bf[0][0] = dequant8<SYM>(bw0[0], g0);
+    bf[0][1] = dequant8<SYM>(bw1[0], g1);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
         const int cur = st & 1, nxt = cur ^ 1;
         if (st < 3) {
             lds_read_slices<NT, ST * kGemmAStage>(af[nxt], L.a_rd[st + 1]);
-            bf[nxt][0] = dequant8(bw0[st + 1], g0);
-            bf[nxt][1] = dequant8(bw1[st + 1], g1);
+            bf[nxt][0] = dequant8<SYM>(bw0[st + 1], g0);
+            bf[nxt][1] = dequant8<SYM>(bw1[st + 1], g1);
         }
 #pragma unroll
         for (int i = 0; i < NT; ++i) {
@@ -434,9 +449,9 @@ __device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT]
     }
 }
 
-// One chunk: wait for it, read its weights, scale and step-0 activations, run
-// its MFMAs, then start chunk c + 2 (into the stage chunk c - 1 used) and, at
-// the first chunk of a scale window, the next window.
+// One chunk: wait for it, start chunk c + 2 (into the stage chunk c - 1 used)
+// and, at the first chunk of a scale window, the next window, then read its
+// weights, scale and step-0 activations and run its MFMAs.
 template <int G, bool SYM, int NT, int ST>
 __device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uint32_t c,
                                            f16v_t (&acc)[NT][2]) {
@@ -453,6 +468,12 @@ __device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uin
         else wait_vmcnt<2u>();
     }
     block_barrier();
+    // Chunk c - 1's stage and the scale window before this one are free now
+    // (every wave has passed the barrier): start chunk c + 2 and, at a
+    // window's first chunk, the next window before this chunk's MFMAs, so two
+    // chunks are in flight while one is computed.
+    gemm_issue<(ST + 2) % 3>(L, smem, c + 2u);
+    if (c % W == 0u) gemm_issue_scales<G, SYM>(L, smem, c / W + 1u);
     if (L.live) {
         const uint32_t win = c / W, lane = threadIdx.x & 63u, h = lane >> 5;
         const uint32_t wb = window_byte<G>(win), gb = group_byte<G>(c, h);
@@ -472,10 +493,8 @@ __device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uin
         lds_wait<NT>(af[0], bw0, bw1, sw0, sw1, zw0, zw1);
         const GroupScale g0 = group_scale<SYM>((uint16_t)sw0, (uint16_t)zw0);
         const GroupScale g1 = group_scale<SYM>((uint16_t)sw1, (uint16_t)zw1);
-        gemm_mma<NT, ST>(L, af, bw0, bw1, g0, g1, acc);
+        gemm_mma<SYM, NT, ST>(L, af, bw0, bw1, g0, g1, acc);
     }
-    gemm_issue<(ST + 2) % 3>(L, smem, c + 2u);
-    if (c % W == 0u) gemm_issue_scales<G, SYM>(L, smem, c / W + 1u);
 }
 
 // MODE 0: gate/up + activation; MODE 1: down + scatter.
@@ -753,6 +772,46 @@ __global__ __launch_bounds__(256) void reduce_token_major_kernel(
             acc = __builtin_fmaf(f16_to_f32(w[tok * k + r]), f16_to_f32(p[(tok * k + r) * d + j]), acc);
         h2[i] = f32_to_f16(acc);
     }
+}
+
+// The same sum, eight elements per thread: 16-byte loads of the K partial
+// rows (all in flight at once) and one 16-byte store. Per element the fma
+// order over the ranks is the scalar kernel's, so the results are identical.
+// K is a template parameter so the K loaded rows stay in registers. Needs
+// d % 8 == 0 and 16-byte aligned partials and output.
+template <uint32_t K>
+__global__ __launch_bounds__(256) void reduce_token_major_vec_kernel(
+    const uint16_t* __restrict__ p, const uint16_t* __restrict__ w, uint16_t* __restrict__ h2,
+    uint32_t t, uint32_t d) {
+    const uint32_t d8 = d / 8u;
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= t * d8) return;
+    const uint32_t tok = i / d8, j8 = i - tok * d8;
+    uint4 v[K];
+    uint16_t wr[K];
+#pragma unroll
+    for (uint32_t r = 0; r < K; ++r) {
+        const uint64_t row = (uint64_t)tok * K + r;
+        v[r] = *reinterpret_cast<const uint4*>(p + row * d + 8u * j8);
+        wr[r] = w[row];
+    }
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t r = 0; r < K; ++r) {
+        const float wf = f16_to_f32(wr[r]);
+        const uint32_t u[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc[2 * q] = __builtin_fmaf(wf, f16_to_f32((uint16_t)(u[q] & 0xFFFFu)), acc[2 * q]);
+            acc[2 * q + 1] = __builtin_fmaf(wf, f16_to_f32((uint16_t)(u[q] >> 16)), acc[2 * q + 1]);
+        }
+    }
+    uint4 o;
+    o.x = (uint32_t)f32_to_f16(acc[0]) | ((uint32_t)f32_to_f16(acc[1]) << 16);
+    o.y = (uint32_t)f32_to_f16(acc[2]) | ((uint32_t)f32_to_f16(acc[3]) << 16);
+    o.z = (uint32_t)f32_to_f16(acc[4]) | ((uint32_t)f32_to_f16(acc[5]) << 16);
+    o.w = (uint32_t)f32_to_f16(acc[6]) | ((uint32_t)f32_to_f16(acc[7]) << 16);
+    *reinterpret_cast<uint4*>(h2 + (uint64_t)tok * d + 8u * j8) = o;
 }
 
 // --------------------------------------------------------- rows path
@@ -1083,6 +1142,19 @@ extern "C" tsg_status tsg_prefill_moe_reduce_token_major(tsg_ctx* ctx, tsg_strea
     TSG_REQUIRE(d > 0, TSG_ERR_INVALID_ARGUMENT, "D must be positive");
     TSG_REQUIRE(partials && w && h2, TSG_ERR_INVALID_ARGUMENT, "NULL reduce operand");
     const uint64_t total = (uint64_t)t * d;
+    if (d % 8u == 0 && aligned16(partials) && aligned16(h2) && total / 8u < (1ull << 31)) {
+        const dim3 grid((uint32_t)((total / 8u + 255) / 256)), block(256);
+        hipStream_t hs = as_stream(stream);
+        bool launched = true;
+        switch (k) {
+            case 1: hipLaunchKernelGGL(reduce_token_major_vec_kernel<1>, grid, block, 0, hs, partials, w, h2, t, d); break;
+            case 2: hipLaunchKernelGGL(reduce_token_major_vec_kernel<2>, grid, block, 0, hs, partials, w, h2, t, d); break;
+            case 4: hipLaunchKernelGGL(reduce_token_major_vec_kernel<4>, grid, block, 0, hs, partials, w, h2, t, d); break;
+            case 8: hipLaunchKernelGGL(reduce_token_major_vec_kernel<8>, grid, block, 0, hs, partials, w, h2, t, d); break;
+            default: launched = false;
+        }
+        if (launched) return check_launch("reduce_token_major_vec");
+    }
     uint64_t grid = (total + 255) / 256;
     if (grid > 65536) grid = 65536;
     hipLaunchKernelGGL(reduce_token_major_kernel, dim3(grid), dim3(256), 0, as_stream(stream),

@@ -162,7 +162,14 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
 
 // IEEE round-to-nearest-even float -> fp16 (v_cvt_f16_f32 honours the
 // default RNE mode).
+// fp32 -> fp16, round to nearest even, of a value already rounded to fp32.
+// The empty asm keeps the compiler from folding the fma or multiply that
+// produced `f` into the conversion: v_fma_mix{lo,hi}_f16 round the exact
+// result once, straight to fp16, where the reference rounds to fp32 first
+// and then to fp16; the two differ when the fp32 rounding lands on an fp16
+// tie.
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    asm("" : "+v"(f));
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
