@@ -149,28 +149,35 @@ __device__ __forceinline__ GroupScale group_scale(uint16_t s_bits, uint16_t b_bi
     return g;
 }
 
-// Eight weights (one packed u32, elements 0..7 of a K run), in element order:
-// per byte j (elements 2j, 2j+1) v_perm copies the byte into both halves, one
-// AND keeps the low nibble in the low half and the high nibble in the high
-// half, and two v_fma_mix produce the pair (sym) or two fp32 sums that one
-// conversion packs (affine).
+// Eight weights (one packed u32, elements 0..7 of a K run), in element order.
+// Two ANDs of the word and two of the word shifted right by 8 leave every
+// nibble alone in a 16-bit half, at bits 0..3 (elements 0, 2 | 4, 6: the low
+// nibbles of bytes 0, 1 | 2, 3) or 4..7 (elements 1, 3 | 5, 7); one v_fma_mix
+// per element reads its half. 13 VALU per 8 weights under sym (the pair
+// packing folds into v_fma_mix{lo,hi}_f16), 17 under affine (fp32 sums, one
+// v_cvt_pk_f16_f32 per pair).
 template <bool SYM>
 __device__ __forceinline__ h8v_t dequant8(uint32_t w, const GroupScale& g) {
+    const uint32_t w8 = w >> 8;
+    const h2_t n0 = __builtin_bit_cast(h2_t, w & 0x000F000Fu);   // e0 | e4
+    const h2_t n1 = __builtin_bit_cast(h2_t, w & 0x00F000F0u);   // e1 | e5
+    const h2_t n2 = __builtin_bit_cast(h2_t, w8 & 0x000F000Fu);  // e2 | e6
+    const h2_t n3 = __builtin_bit_cast(h2_t, w8 & 0x00F000F0u);  // e3 | e7
+    const _Float16 lo_src[4] = {n0.x, n2.x, n0.y, n2.y};  // elements 0, 2, 4, 6
+    const _Float16 hi_src[4] = {n1.x, n3.x, n1.y, n3.y};  // elements 1, 3, 5, 7
     h2_t p[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t x = __builtin_amdgcn_perm(w, w, 0x0C000C00u | ((uint32_t)j << 16) | (uint32_t)j);
-        const h2_t y = __builtin_bit_cast(h2_t, x & 0x00F0000Fu);
         if constexpr (SYM) {
             // the empty asm makes the low half a value of its own, so the pair
             // becomes v_fma_mixlo_f16 + v_fma_mixhi_f16 rather than two
             // v_fma_mix_f32 and a v_cvt_pk_f16_f32
-            _Float16 lo = (_Float16)__builtin_fmaf((float)y.x, g.s_lo, g.b);
+            _Float16 lo = (_Float16)__builtin_fmaf((float)lo_src[j], g.s_lo, g.b);
             asm("" : "+v"(lo));
-            p[j] = h2_t{lo, (_Float16)__builtin_fmaf((float)y.y, g.s_hi, g.b)};
+            p[j] = h2_t{lo, (_Float16)__builtin_fmaf((float)hi_src[j], g.s_hi, g.b)};
         } else {
-            float lo = __builtin_fmaf((float)y.x, g.s_lo, g.b);
-            float hi = __builtin_fmaf((float)y.y, g.s_hi, g.b);
+            float lo = __builtin_fmaf((float)lo_src[j], g.s_lo, g.b);
+            float hi = __builtin_fmaf((float)hi_src[j], g.s_hi, g.b);
             asm("" : "+v"(lo), "+v"(hi));
             p[j] = h2_t{(_Float16)lo, (_Float16)hi};
         }
