@@ -116,7 +116,8 @@ def _zipf_routing(rng, t, ne, k, s):
 @pytest.mark.parametrize("t,ne,k,s,tile", [(2048, 128, 8, 1.1, 64), (2048, 128, 8, 1.1, 128),
                                            (2048, 128, 8, 1.1, 256),
                                            (301, 256, 8, 1.0, 64), (5, 128, 8, 1.1, 128),
-                                           (64, 16, 4, 0.5, 32)])
+                                           (64, 16, 4, 0.5, 32), (4096, 256, 8, 1.0, 128),
+                                           (3001, 128, 3, 1.1, 256)])
 def test_device_grouping_matches_host_sort(tsg, ctx, t, ne, k, s, tile):
     """The on-device counting sort yields exactly groupTokenExpertPairs'
     permutation (PrefillMoEGrouping.swift:141-150), offsets and counts; the

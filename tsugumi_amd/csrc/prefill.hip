@@ -23,97 +23,106 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // ------------------------------------------------------- device grouping
 
+// Exclusive prefix sum of one value per thread over a block of NT threads
+// (NT a multiple of 64, at most 1024); every thread also gets the total.
+template <uint32_t NT>
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_tot,
+                                                         uint32_t& total) {
+    constexpr uint32_t kWaves = NT / 64u;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(x, off, 64);
+        if ((int)lane >= off) x += o;
+    }
+    if (lane == 63) wave_tot[wave] = x;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < kWaves; ++w) {
+        const uint32_t c = wave_tot[w];
+        before += w < wave ? c : 0u;
+        all += c;
+    }
+    total = all;
+    return before + x - v;
+}
+
 // One block per expert e: rank_of[p] = position of pair p among the pairs of
-// expert e in (token, rank) order; counts[e] = their number.
+// expert e in (token, rank) order; counts[e] = their number. Thread i owns
+// the consecutive tokens [i * tpt, (i + 1) * tpt): it counts its matches,
+// one block scan places them, and a second pass over the same (cached)
+// indices writes the ranks.
 __global__ __launch_bounds__(1024) void group_rank_kernel(const uint32_t* __restrict__ idx,
                                                           uint32_t t, uint32_t k,
                                                           uint32_t* __restrict__ rank_of,
                                                           uint32_t* __restrict__ counts) {
     __shared__ uint32_t wave_tot[16];
-    __shared__ uint32_t carry_s;
     const uint32_t e = blockIdx.x;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    uint32_t carry = 0;
-    for (uint32_t t0 = 0; t0 < t; t0 += 1024u) {
-        const uint32_t tok = t0 + threadIdx.x;
-        uint32_t c = 0;
-        if (tok < t)
-            for (uint32_t r = 0; r < k; ++r) c += idx[(uint64_t)tok * k + r] == e ? 1u : 0u;
-        // inclusive scan of c across the block
-        uint32_t v = c;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t o = __shfl_up(v, off, 64);
-            if ((int)lane >= off) v += o;
+    const uint32_t tpt = (t + 1023u) / 1024u;
+    const uint32_t p0 = min(threadIdx.x * tpt, t) * k, p1 = min(threadIdx.x * tpt + tpt, t) * k;
+    uint32_t c = 0;
+    if (k == 8u && (reinterpret_cast<uintptr_t>(idx) & 15u) == 0) {
+        for (uint32_t p = p0; p < p1; p += 8u) {
+            const uint4 a = *reinterpret_cast<const uint4*>(idx + p);
+            const uint4 b = *reinterpret_cast<const uint4*>(idx + p + 4u);
+            c += (a.x == e) + (a.y == e) + (a.z == e) + (a.w == e) + (b.x == e) + (b.y == e) +
+                 (b.z == e) + (b.w == e);
         }
-        if (lane == 63) wave_tot[wave] = v;
-        __syncthreads();
-        if (threadIdx.x < 64) {
-            uint32_t w = threadIdx.x < 16 ? wave_tot[threadIdx.x] : 0u;
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) {
-                const uint32_t o = __shfl_up(w, off, 64);
-                if ((int)threadIdx.x >= off) w += o;
-            }
-            if (threadIdx.x < 16) wave_tot[threadIdx.x] = w;  // inclusive
-        }
-        __syncthreads();
-        const uint32_t before = carry + (wave ? wave_tot[wave - 1] : 0u) + (v - c);
-        if (c) {
-            uint32_t j = 0;
-            for (uint32_t r = 0; r < k; ++r)
-                if (idx[(uint64_t)tok * k + r] == e) rank_of[(uint64_t)tok * k + r] = before + j++;
-        }
-        if (threadIdx.x == 0) carry_s = carry + wave_tot[15];
-        __syncthreads();
-        carry = carry_s;
-        __syncthreads();
+    } else {
+        for (uint32_t p = p0; p < p1; ++p) c += idx[p] == e ? 1u : 0u;
     }
-    if (threadIdx.x == 0) counts[e] = carry;
+    uint32_t total;
+    uint32_t before = block_exclusive_scan<1024>(c, wave_tot, total);
+    if (c) {
+        for (uint32_t p = p0; p < p1; ++p)
+            if (idx[p] == e) rank_of[p] = before++;
+    }
+    if (threadIdx.x == 0) counts[e] = total;
 }
 
 // Scatter pairs to their sorted positions; block 0 also writes offsets and
 // the GEMM work list. Expert ids >= num_experts are dropped (never routed).
+// Each block scans the expert counts (ne <= 256, one per thread) for the
+// expert offsets and the first routed block of each expert.
 __global__ __launch_bounds__(256) void group_scatter_kernel(
     const uint32_t* __restrict__ idx, const uint16_t* __restrict__ w, uint32_t t, uint32_t k,
     uint32_t ne, const uint32_t* __restrict__ rank_of, const uint32_t* __restrict__ counts,
     tsg_token_expert_pair* __restrict__ sorted, uint32_t* __restrict__ offsets,
     tsg_routed_block* __restrict__ blocks, uint32_t max_blocks, uint32_t* __restrict__ n_blocks,
     uint32_t tile_rows) {
+    static_assert(kMaxExperts <= 256, "one expert per thread");
     __shared__ uint32_t off_s[kMaxExperts];
-    __shared__ uint32_t blk_s[kMaxExperts];
-    if (threadIdx.x == 0) {
-        uint32_t run = 0, brun = 0;
-        for (uint32_t e = 0; e < ne; ++e) {
-            off_s[e] = run;
-            blk_s[e] = brun;
-            run += counts[e];
-            brun += (counts[e] + tile_rows - 1) / tile_rows;
-        }
-        if (blockIdx.x == 0) *n_blocks = brun < max_blocks ? brun : max_blocks;
-    }
-    __syncthreads();
+    __shared__ uint32_t wave_tot[2][4];
+    const uint32_t e = threadIdx.x;
+    const uint32_t c = e < ne ? counts[e] : 0u;
+    const uint32_t nb = (c + tile_rows - 1u) / tile_rows;
+    uint32_t total_rows, total_blocks;
+    const uint32_t off = block_exclusive_scan<256>(c, wave_tot[0], total_rows);
+    const uint32_t boff = block_exclusive_scan<256>(nb, wave_tot[1], total_blocks);
+    if (e < ne) off_s[e] = off;
     if (blockIdx.x == 0) {
-        for (uint32_t e = threadIdx.x; e < ne; e += blockDim.x) {
-            const uint32_t c = counts[e];
-            offsets[e] = c ? off_s[e] : 0xFFFFFFFFu;
-            const uint32_t nb = (c + tile_rows - 1) / tile_rows;
+        if (e == 0) *n_blocks = total_blocks < max_blocks ? total_blocks : max_blocks;
+        if (e < ne) {
+            offsets[e] = c ? off : 0xFFFFFFFFu;
             for (uint32_t b = 0; b < nb; ++b) {
-                const uint32_t bi = blk_s[e] + b;
+                const uint32_t bi = boff + b;
                 if (bi >= max_blocks) break;
-                const uint32_t start = off_s[e] + b * tile_rows;
+                const uint32_t start = off + b * tile_rows;
                 const uint32_t rows = (c - b * tile_rows) < tile_rows ? (c - b * tile_rows) : tile_rows;
                 blocks[bi] = tsg_routed_block{e, start, rows, start};
             }
         }
     }
+    __syncthreads();
     const uint64_t n = (uint64_t)t * k;
     for (uint64_t p = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; p < n;
          p += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t e = idx[p];
-        if (e >= ne) continue;
+        const uint32_t ex = idx[p];
+        if (ex >= ne) continue;
         const uint32_t tok = (uint32_t)(p / k), r = (uint32_t)(p - (uint64_t)tok * k);
-        sorted[off_s[e] + rank_of[p]] = tsg_token_expert_pair{tok, e, r, (uint32_t)w[p]};
+        sorted[off_s[ex] + rank_of[p]] = tsg_token_expert_pair{tok, ex, r, (uint32_t)w[p]};
     }
 }
 
