@@ -343,7 +343,9 @@ tsg_status tsg_plan_routed_gemm(const tsg_moe_group* groups, uint32_t n_groups,
  * routing (indices/weights [query_count, top_k]) -> pairs sorted by
  * (expert, token, rank) (bit-identical to the host sort), per-expert offsets
  * and counts, and the GEMM's work list of <= tile_rows-row blocks with
- * local_slot = expert id and local_row = pair_start. *n_blocks (device) gets
+ * local_slot = expert id and local_row = pair_start, largest first (by
+ * ceil(rows / 32), capped at 8, then expert order): the grouped GEMMs take a
+ * list whose count is on the device in this order. *n_blocks (device) gets
  * the block count; max_blocks bounds the blocks array. tile_rows: 32, 64 (the
  * reference's block), 128 (the grouped GEMM's widest pass) or 256.
  * scratch: tsg_prefill_group_scratch_bytes(...) bytes of device memory. */

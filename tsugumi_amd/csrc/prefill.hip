@@ -85,7 +85,10 @@ __global__ __launch_bounds__(1024) void group_rank_kernel(const uint32_t* __rest
 // Scatter pairs to their sorted positions; block 0 also writes offsets and
 // the GEMM work list. Expert ids >= num_experts are dropped (never routed).
 // Each block scans the expert counts (ne <= 256, one per thread) for the
-// expert offsets and the first routed block of each expert.
+// expert offsets. The work list comes largest first: routed blocks by
+// size bucket ceil(rows / 32) (capped at 8) descending, then by (expert,
+// position in the expert), so the GEMM takes it in order (long items start
+// early, short ones fill the tail) without sorting it again.
 __global__ __launch_bounds__(256) void group_scatter_kernel(
     const uint32_t* __restrict__ idx, const uint16_t* __restrict__ w, uint32_t t, uint32_t k,
     uint32_t ne, const uint32_t* __restrict__ rank_of, const uint32_t* __restrict__ counts,
@@ -94,24 +97,37 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(
     uint32_t tile_rows) {
     static_assert(kMaxExperts <= 256, "one expert per thread");
     __shared__ uint32_t off_s[kMaxExperts];
-    __shared__ uint32_t wave_tot[2][4];
+    __shared__ uint32_t wave_tot[4];
     const uint32_t e = threadIdx.x;
     const uint32_t c = e < ne ? counts[e] : 0u;
-    const uint32_t nb = (c + tile_rows - 1u) / tile_rows;
-    uint32_t total_rows, total_blocks;
-    const uint32_t off = block_exclusive_scan<256>(c, wave_tot[0], total_rows);
-    const uint32_t boff = block_exclusive_scan<256>(nb, wave_tot[1], total_blocks);
+    uint32_t total_rows;
+    const uint32_t off = block_exclusive_scan<256>(c, wave_tot, total_rows);
     if (e < ne) off_s[e] = off;
     if (blockIdx.x == 0) {
-        if (e == 0) *n_blocks = total_blocks < max_blocks ? total_blocks : max_blocks;
+        const uint32_t full = c / tile_rows, rem = c - full * tile_rows;
+        const uint32_t bfull = min(tile_rows / 32u, 8u);
+        const uint32_t brem = rem ? min((rem + 31u) / 32u, 8u) : 0u;
+        uint32_t first_full = 0, first_rem = 0, running = 0;
+        for (uint32_t bk = 8; bk >= 1; --bk) {
+            const uint32_t n_e = (bfull == bk ? full : 0u) + (brem == bk ? 1u : 0u);
+            __syncthreads();  // the previous scan's totals are read
+            uint32_t total;
+            const uint32_t before = block_exclusive_scan<256>(n_e, wave_tot, total);
+            if (bfull == bk) first_full = running + before;
+            if (brem == bk) first_rem = running + before + (bfull == bk ? full : 0u);
+            running += total;
+        }
+        if (e == 0) *n_blocks = running < max_blocks ? running : max_blocks;
         if (e < ne) {
             offsets[e] = c ? off : 0xFFFFFFFFu;
-            for (uint32_t b = 0; b < nb; ++b) {
-                const uint32_t bi = boff + b;
-                if (bi >= max_blocks) break;
+            for (uint32_t b = 0; b < full; ++b) {
+                const uint32_t bi = first_full + b;
                 const uint32_t start = off + b * tile_rows;
-                const uint32_t rows = (c - b * tile_rows) < tile_rows ? (c - b * tile_rows) : tile_rows;
-                blocks[bi] = tsg_routed_block{e, start, rows, start};
+                if (bi < max_blocks) blocks[bi] = tsg_routed_block{e, start, tile_rows, start};
+            }
+            if (rem) {
+                const uint32_t start = off + full * tile_rows;
+                if (first_rem < max_blocks) blocks[first_rem] = tsg_routed_block{e, start, rem, start};
             }
         }
     }
@@ -164,34 +180,47 @@ __device__ __forceinline__ GroupScale group_scale(uint16_t s_bits, uint16_t b_bi
 // nibbles of bytes 0, 1 | 2, 3) or 4..7 (elements 1, 3 | 5, 7); one v_fma_mix
 // per element reads its half. 13 VALU per 8 weights under sym (the pair
 // packing folds into v_fma_mix{lo,hi}_f16), 17 under affine (fp32 sums, one
-// v_cvt_pk_f16_f32 per pair).
+// v_cvt_pk_f16_f32 per pair). Split into the extraction and four pairs so the
+// GEMM can spread the work between its MFMAs.
+struct Nibbles {
+    h2_t n0, n1, n2, n3;  // e0|e4, e1|e5, e2|e6, e3|e7
+};
+
+__device__ __forceinline__ Nibbles nibbles8(uint32_t w) {
+    const uint32_t w8 = w >> 8;
+    return Nibbles{__builtin_bit_cast(h2_t, w & 0x000F000Fu), __builtin_bit_cast(h2_t, w & 0x00F000F0u),
+                   __builtin_bit_cast(h2_t, w8 & 0x000F000Fu), __builtin_bit_cast(h2_t, w8 & 0x00F000F0u)};
+}
+
+// Pair j (elements 2j, 2j+1) of the eight.
+template <bool SYM, int J>
+__device__ __forceinline__ h2_t dequant_pair(const Nibbles& n, const GroupScale& g) {
+    const _Float16 lo_src = J == 0 ? n.n0.x : J == 1 ? n.n2.x : J == 2 ? n.n0.y : n.n2.y;
+    const _Float16 hi_src = J == 0 ? n.n1.x : J == 1 ? n.n3.x : J == 2 ? n.n1.y : n.n3.y;
+    if constexpr (SYM) {
+        // the empty asm makes the low half a value of its own, so the pair
+        // becomes v_fma_mixlo_f16 + v_fma_mixhi_f16 rather than two
+        // v_fma_mix_f32 and a v_cvt_pk_f16_f32
+        _Float16 lo = (_Float16)__builtin_fmaf((float)lo_src, g.s_lo, g.b);
+        asm("" : "+v"(lo));
+        return h2_t{lo, (_Float16)__builtin_fmaf((float)hi_src, g.s_hi, g.b)};
+    } else {
+        float lo = __builtin_fmaf((float)lo_src, g.s_lo, g.b);
+        float hi = __builtin_fmaf((float)hi_src, g.s_hi, g.b);
+        asm("" : "+v"(lo), "+v"(hi));
+        return h2_t{(_Float16)lo, (_Float16)hi};
+    }
+}
+
+__device__ __forceinline__ h8v_t pack_pairs(h2_t p0, h2_t p1, h2_t p2, h2_t p3) {
+    return h8v_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
 template <bool SYM>
 __device__ __forceinline__ h8v_t dequant8(uint32_t w, const GroupScale& g) {
-    const uint32_t w8 = w >> 8;
-    const h2_t n0 = __builtin_bit_cast(h2_t, w & 0x000F000Fu);   // e0 | e4
-    const h2_t n1 = __builtin_bit_cast(h2_t, w & 0x00F000F0u);   // e1 | e5
-    const h2_t n2 = __builtin_bit_cast(h2_t, w8 & 0x000F000Fu);  // e2 | e6
-    const h2_t n3 = __builtin_bit_cast(h2_t, w8 & 0x00F000F0u);  // e3 | e7
-    const _Float16 lo_src[4] = {n0.x, n2.x, n0.y, n2.y};  // elements 0, 2, 4, 6
-    const _Float16 hi_src[4] = {n1.x, n3.x, n1.y, n3.y};  // elements 1, 3, 5, 7
-    h2_t p[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        if constexpr (SYM) {
-            // the empty asm makes the low half a value of its own, so the pair
-            // becomes v_fma_mixlo_f16 + v_fma_mixhi_f16 rather than two
-            // v_fma_mix_f32 and a v_cvt_pk_f16_f32
-            _Float16 lo = (_Float16)__builtin_fmaf((float)lo_src[j], g.s_lo, g.b);
-            asm("" : "+v"(lo));
-            p[j] = h2_t{lo, (_Float16)__builtin_fmaf((float)hi_src[j], g.s_hi, g.b)};
-        } else {
-            float lo = __builtin_fmaf((float)lo_src[j], g.s_lo, g.b);
-            float hi = __builtin_fmaf((float)hi_src[j], g.s_hi, g.b);
-            asm("" : "+v"(lo), "+v"(hi));
-            p[j] = h2_t{(_Float16)lo, (_Float16)hi};
-        }
-    }
-    return h8v_t{p[0].x, p[0].y, p[1].x, p[1].y, p[2].x, p[2].y, p[3].x, p[3].y};
+    const Nibbles n = nibbles8(w);
+    return pack_pairs(dequant_pair<SYM, 0>(n, g), dequant_pair<SYM, 1>(n, g),
+                      dequant_pair<SYM, 2>(n, g), dequant_pair<SYM, 3>(n, g));
 }
 
 // Dump of the GEMM's staging (tsg_debug_gemm_dequant_f16): one thread per 8
@@ -439,7 +468,10 @@ __device__ __forceinline__ void gemm_issue_scales(const GemmLane& L, uint8_t* sm
     }
 }
 
-// The MFMA work of one chunk (stage ST) for the wave's two weight tiles.
+// The MFMA work of one chunk (stage ST) for the wave's two weight tiles. The
+// next step's dequantisation (10 pieces: two nibble extractions, eight
+// pairs) is spread between this step's 2 NT MFMAs, and scheduling fences keep
+// the order, so the wave issues its conversions while its own MFMAs run.
 template <bool SYM, int NT, int ST>
 __device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT], const u32x4_t& bw0,
                                          const u32x4_t& bw1, const GroupScale& g0,
@@ -450,18 +482,40 @@ __device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT]
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
         const int cur = st & 1, nxt = cur ^ 1;
-        if (st < 3) {
-            lds_read_slices<NT, ST * kGemmAStage>(af[nxt], L.a_rd[st + 1]);
-            bf[nxt][0] = dequant8<SYM>(bw0[st + 1], g0);
-            bf[nxt][1] = dequant8<SYM>(bw1[st + 1], g1);
-        }
+        if (st < 3) lds_read_slices<NT, ST * kGemmAStage>(af[nxt], L.a_rd[st + 1]);
+        Nibbles n0{}, n1{};
+        h2_t p0[4], p1[4];
+        // piece k of the next step's conversion (k < 10)
+        auto piece = [&](int k) {
+            if (st >= 3) return;
+            switch (k) {
+                case 0: n0 = nibbles8(bw0[st + 1]); break;
+                case 1: n1 = nibbles8(bw1[st + 1]); break;
+                case 2: p0[0] = dequant_pair<SYM, 0>(n0, g0); break;
+                case 3: p1[0] = dequant_pair<SYM, 0>(n1, g1); break;
+                case 4: p0[1] = dequant_pair<SYM, 1>(n0, g0); break;
+                case 5: p1[1] = dequant_pair<SYM, 1>(n1, g1); break;
+                case 6: p0[2] = dequant_pair<SYM, 2>(n0, g0); break;
+                case 7: p1[2] = dequant_pair<SYM, 2>(n1, g1); break;
+                case 8: p0[3] = dequant_pair<SYM, 3>(n0, g0); break;
+                default: p1[3] = dequant_pair<SYM, 3>(n1, g1); break;
+            }
+        };
+        constexpr int kM = 2 * NT;  // MFMAs this step
 #pragma unroll
-        for (int i = 0; i < NT; ++i) {
+        for (int q = 0; q < kM; ++q) {
+            const int i = q >> 1, t = q & 1;
             const h8v_t a8 = __builtin_bit_cast(h8v_t, af[cur][i]);
-            acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, bf[cur][0], acc[i][0], 0, 0, 0);
-            acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, bf[cur][1], acc[i][1], 0, 0, 0);
+            acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, bf[cur][t], acc[i][t], 0, 0, 0);
+#pragma unroll
+            for (int k = q * 10 / kM; k < (q + 1) * 10 / kM; ++k) piece(k);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if (st < 3) lds_wait<NT>(af[nxt]);
+        if (st < 3) {
+            bf[nxt][0] = pack_pairs(p0[0], p0[1], p0[2], p0[3]);
+            bf[nxt][1] = pack_pairs(p1[0], p1[1], p1[2], p1[3]);
+            lds_wait<NT>(af[nxt]);
+        }
     }
 }
 
@@ -617,7 +671,16 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     constexpr uint32_t kStride = kCols + 8u;             // halves per LDS row
     static_assert(kGemmRows * kStride * 2u <= gemm_lds_bytes(true), "output tile fits the LDS");
     uint16_t* otile = reinterpret_cast<uint16_t*>(smem);
+    // down: each row's destination (token * top_k + rank) * d, staged once per
+    // block (the pair loads overlap the tile conversion below)
+    uint32_t* odst = reinterpret_cast<uint32_t*>(smem + kGemmRows * kStride * 2u);
+    static_assert(kGemmRows * kStride * 2u + kGemmRows * 4u <= gemm_lds_bytes(true),
+                  "output tile and row destinations fit the LDS");
     block_barrier();  // every wave is done reading the rings
+    if (MODE == 1 && threadIdx.x < rows) {
+        const tsg_token_expert_pair pr = args.pairs[blk.pair_start + threadIdx.x];
+        odst[threadIdx.x] = (pr.token * args.top_k + pr.rank) * args.d;
+    }
     if (L.live) {
         const uint32_t c0 = MODE == 0 ? 32u * L.wave + m : 64u * L.wave + m;
 #pragma unroll
@@ -645,13 +708,7 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
         const uint32_t r = p / kPieces, cg = p - r * kPieces;
         if (cg * 8u >= live) continue;
         const uint4 v = *reinterpret_cast<const uint4*>(otile + r * kStride + cg * 8u);
-        uint32_t dst;
-        if (MODE == 0) {
-            dst = (blk.local_row + r) * args.f;
-        } else {
-            const tsg_token_expert_pair pr = args.pairs[blk.pair_start + r];
-            dst = (pr.token * args.top_k + pr.rank) * args.d;
-        }
+        const uint32_t dst = MODE == 0 ? (blk.local_row + r) * args.f : odst[r];
         *reinterpret_cast<uint4*>(args.out + dst + col0 + cg * 8u) = v;
     }
 }
@@ -662,8 +719,10 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
 // (workgroups go to the 8 XCDs round-robin by linear id, each XCD with its
 // own L2) with their ntiles items on that XCD, tile-major, so the items of a
 // routed block share its activation rows in one L2. Blocks past
-// kSortBlocks keep block order. `scratch` is 64 words of LDS the caller does
-// not use yet. Bijective on [0, nb * ntiles).
+// kSortBlocks keep block order, and so does a list whose count the device
+// wrote (tsg_prefill_group_pairs_device writes it largest first). `scratch`
+// is 64 words of LDS the caller does not use yet. Bijective on
+// [0, nb * ntiles).
 constexpr uint32_t kSortBlocks = 1024;
 
 __device__ __forceinline__ uint32_t size_bucket(uint32_t rows) {
@@ -684,7 +743,9 @@ __device__ void gemm_work_item(const GemmArgs& args, uint32_t nb, uint32_t pid, 
         j = 8u * G + q / T;
         tile = q % T;
     }
-    if (nb > kSortBlocks) {
+    if (nb > kSortBlocks || args.n_blocks_device) {
+        // too many to sort here, or a list from tsg_prefill_group_pairs_device
+        // (largest first already)
         yb = j;
         return;
     }
