@@ -225,8 +225,11 @@ __host__ __device__ __forceinline__ uint32_t paired_pos(uint32_t k) {
     return (k & 3u) * 2u + (k >> 2);
 }
 
-// gelu_pytorch_tanh with the kernels' clamp (moe.metal:105-112) or SiLU
-// (moe.metal:116-118).
+// gelu_pytorch_tanh with the kernels' clamp (moe.metal:104-111) or SiLU
+// (moe.metal:116-118). 0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)) exactly, so
+// the GELU takes one exp (v_exp_f32 on a pre-scaled argument) and one
+// reciprocal instead of a full tanhf; both are accurate to a few fp32 ulp of
+// the (1 + tanh) factor, the precision of the reference's fast-math tanh.
 template <int ACT>
 __device__ __forceinline__ float gate_activation(float x) {
     if constexpr (ACT == TSG_ACT_SILU) {
@@ -235,7 +238,7 @@ __device__ __forceinline__ float gate_activation(float x) {
         const float x3 = x * x * x;
         float inner = 0.7978845608028654f * (x + 0.044715f * x3);
         inner = fminf(fmaxf(inner, -20.0f), 20.0f);
-        return 0.5f * x * (1.0f + tanhf(inner));
+        return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * inner));
     }
 }
 
