@@ -812,8 +812,13 @@ __device__ __forceinline__ void wave_select_top8(const uint32_t (&key)[4], uint3
 // half(half(down . act) * sigmoid(logit)) for each of those rows in LDS for
 // the combine. Each step is the dense GEMV's lane geometry and the separate
 // kernels' arithmetic (qwen_shared.hpp), so the bits are tsg_moe_shared_expert's.
+// The shared-branch form keeps more state per lane; its blocks are bounded at
+// 768 threads (12 waves, 3 per SIMD) so it has 168 VGPRs instead of the 128 a
+// 1024-thread bound allows, and does not spill.
+__host__ __device__ constexpr uint32_t decode_layer_max_threads(bool sh) { return sh ? 768u : 1024u; }
+
 template <int G, bool SYM, int ACT, bool SH>
-__global__ __launch_bounds__(1024) void decode_layer_kernel(DecodeLayerArgs a_arg) {
+__global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_kernel(DecodeLayerArgs a_arg) {
     // The arguments are copied to LDS once: under SGPR pressure the compiler
     // re-reads kernel arguments instead of spilling, and a kernarg reload in
     // a loop costs a memory round trip each time; an LDS copy costs cycles.
@@ -1268,7 +1273,7 @@ tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
     }
     auto kern = decode_layer_kernel<G, SYM, ACT, SH>;
     int per_cu = 0;
-    if (threads > 1024u || a.ne > kMaxExperts || a.f > kMaxFusedDim || a.d > kMaxFusedDim ||
+    if (threads > decode_layer_max_threads(SH) || a.ne > kMaxExperts || a.f > kMaxFusedDim || a.d > kMaxFusedDim ||
         (a.rows + kDecodeGroups - 1u) / kDecodeGroups > kMaxCombineRows ||
         (SH && (a.sh_f > kMaxSharedF || a.sh_f > 2u * kDecodeBlocks)) ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, (int)threads, lds) !=
