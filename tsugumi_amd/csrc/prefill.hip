@@ -896,19 +896,25 @@ __global__ __launch_bounds__(256) void reduce_token_major_vec_kernel(
 constexpr uint32_t kRowsMax = 8;
 constexpr uint32_t kRowsBlocksPerLaunch = 64;
 
+constexpr uint32_t kRowsThreads = 512;  // 16 gate/up pairs or 64 down rows per block
+
 // The rows path's block list travels in the kernel arguments, as the
 // reference passes it with setBytes (PrefillGroupedRoutedMoE.swift:835-870).
+// lds_rows: the most rows of any block in the launch (<= kRowsMax), the rows
+// the LDS is sized for.
 struct RowsBlocks {
     tsg_routed_block b[kRowsBlocksPerLaunch];
+    uint32_t lds_rows;
 };
 
-// grid (ceil(F / 8), n_blocks), block 256: 32 lanes per f row (16 on the gate
-// row, 16 on the up row), every row of the routed block (<= 8) against one
-// weight read. Per row the arithmetic is decode phase 1's (decode.hip
+// grid (ceil(F / 16), n_blocks), block 512: 32 lanes per f row (16 on the
+// gate row, 16 on the up row), every row of the routed block (<= 8) against
+// one weight read; the block's 16 f rows share one staging of the activation
+// rows. Per row the arithmetic is decode phase 1's (decode.hip
 // phase1_compute): the same gemv_lane.hpp steps, batch and reduction, so one
 // row here is bit-identical to decode.
 template <int G, bool SYM, int ACT>
-__global__ __launch_bounds__(256) void rows_gate_up_kernel(GemmArgs args, RowsBlocks rb) {
+__global__ __launch_bounds__(kRowsThreads) void rows_gate_up_kernel(GemmArgs args, RowsBlocks rb) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t tok[kRowsMax];
     const tsg_routed_block blk = rb.b[blockIdx.y];
@@ -916,9 +922,9 @@ __global__ __launch_bounds__(256) void rows_gate_up_kernel(GemmArgs args, RowsBl
     const uint32_t d = args.d, f = args.f;
     const uint32_t row_h = lds_chunks_halves(d);
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-    float* xsum = reinterpret_cast<float*>(smem + (size_t)kRowsMax * row_h * 2u);
+    float* xsum = reinterpret_cast<float*>(smem + (size_t)rb.lds_rows * row_h * 2u);
 
-    const uint32_t fr_raw = blockIdx.x * 8u + (threadIdx.x >> 5);
+    const uint32_t fr_raw = blockIdx.x * (kRowsThreads / 32u) + (threadIdx.x >> 5);
     const uint32_t j = threadIdx.x & 15u;
     const bool is_up = (threadIdx.x >> 4) & 1u;
     const bool live = fr_raw < f;
@@ -952,11 +958,12 @@ __global__ __launch_bounds__(256) void rows_gate_up_kernel(GemmArgs args, RowsBl
     }
 }
 
-// grid (ceil(D / 8), n_blocks), block 64: 8 lanes per output row, each of the
-// block's rows against one weight read. Per row the arithmetic is decode phase
+// grid (ceil(D / 64), n_blocks), block 512: 8 lanes per output row, each of
+// the block's rows against one weight read; the block's 64 output rows share
+// one staging of the activation rows. Per row the arithmetic is decode phase
 // 2's per-slot GEMV (decode.hip phase2_body): the same gemv_lane.hpp steps.
 template <int G, bool SYM>
-__global__ __launch_bounds__(64) void rows_down_kernel(GemmArgs args, RowsBlocks rb,
+__global__ __launch_bounds__(kRowsThreads) void rows_down_kernel(GemmArgs args, RowsBlocks rb,
                                                        uint16_t* partials) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t dst[kRowsMax];
@@ -965,10 +972,10 @@ __global__ __launch_bounds__(64) void rows_down_kernel(GemmArgs args, RowsBlocks
     const uint32_t d = args.d, f = args.f;
     const uint32_t row_h = lds_chunks_halves(f);
     uint16_t* as = reinterpret_cast<uint16_t*>(smem);
-    float* asum = reinterpret_cast<float*>(smem + (size_t)kRowsMax * row_h * 2u);
+    float* asum = reinterpret_cast<float*>(smem + (size_t)rb.lds_rows * row_h * 2u);
 
     const uint32_t j = threadIdx.x & 7u;
-    const uint32_t row = blockIdx.x * 8u + (threadIdx.x >> 3);
+    const uint32_t row = blockIdx.x * (kRowsThreads / 8u) + (threadIdx.x >> 3);
     const bool live_row = row < d;
     const uint32_t rr = live_row ? row : 0u;
     const uint8_t* blob = args.layer_base + (uint64_t)blk.local_slot * args.expert_stride;
@@ -1183,19 +1190,28 @@ extern "C" tsg_status tsg_prefill_moe_rows(tsg_moe* moe, tsg_stream stream,
     for (uint32_t b0 = 0; b0 < n_blocks; b0 += kRowsBlocksPerLaunch) {
         const uint32_t nb = n_blocks - b0 < kRowsBlocksPerLaunch ? n_blocks - b0 : kRowsBlocksPerLaunch;
         RowsBlocks rb{};
-        for (uint32_t i = 0; i < nb; ++i) rb.b[i] = blocks[b0 + i];
-        const dim3 g1((f + 7) / 8, nb), g2((d + 7) / 8, nb);
-#define TSG_ROWS_LAUNCH(GG, SS)                                                                  \
-    do {                                                                                         \
-        if (moe->activation == TSG_ACT_SILU)                                                     \
-            hipLaunchKernelGGL((rows_gate_up_kernel<GG, SS, TSG_ACT_SILU>), g1, dim3(256), lds1, \
-                               s, a, rb);                                                        \
-        else                                                                                     \
-            hipLaunchKernelGGL((rows_gate_up_kernel<GG, SS, TSG_ACT_GELU_TANH>), g1, dim3(256),  \
-                               lds1, s, a, rb);                                                  \
-        if ((st = check_launch("rows gate/up"))) return st;                                     \
-        hipLaunchKernelGGL((rows_down_kernel<GG, SS>), g2, dim3(64), lds2, s, a2, rb, partials); \
-        if ((st = check_launch("rows down"))) return st;                                        \
+        rb.lds_rows = 1;
+        for (uint32_t i = 0; i < nb; ++i) {
+            rb.b[i] = blocks[b0 + i];
+            rb.lds_rows = std::max(rb.lds_rows, std::min(blocks[b0 + i].row_count, kRowsMax));
+        }
+        // LDS for the launch's widest block (the maximum checked above)
+        const size_t l1 = (size_t)rb.lds_rows * lds_chunks_halves(d) * 2u + (sym ? 0u : rb.lds_rows * (d / 32u) * 4u);
+        const size_t l2 = (size_t)rb.lds_rows * lds_chunks_halves(f) * 2u + (sym ? 0u : rb.lds_rows * (f / 32u) * 4u);
+        const dim3 g1((f + kRowsThreads / 32u - 1u) / (kRowsThreads / 32u), nb);
+        const dim3 g2((d + kRowsThreads / 8u - 1u) / (kRowsThreads / 8u), nb);
+#define TSG_ROWS_LAUNCH(GG, SS)                                                                    \
+    do {                                                                                           \
+        if (moe->activation == TSG_ACT_SILU)                                                       \
+            hipLaunchKernelGGL((rows_gate_up_kernel<GG, SS, TSG_ACT_SILU>), g1,                    \
+                               dim3(kRowsThreads), l1, s, a, rb);                                  \
+        else                                                                                       \
+            hipLaunchKernelGGL((rows_gate_up_kernel<GG, SS, TSG_ACT_GELU_TANH>), g1,               \
+                               dim3(kRowsThreads), l1, s, a, rb);                                  \
+        if ((st = check_launch("rows gate/up"))) return st;                                       \
+        hipLaunchKernelGGL((rows_down_kernel<GG, SS>), g2, dim3(kRowsThreads), l2, s, a2, rb,      \
+                           partials);                                                              \
+        if ((st = check_launch("rows down"))) return st;                                          \
     } while (0)
         if (ctx->group_size == 32) {
             if (sym) TSG_ROWS_LAUNCH(32, true);
