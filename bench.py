@@ -15,6 +15,8 @@ Workload (BASELINE.json configs[1] and [3]):
           reduce.
 
 Also reported, under "other_configs" (skipped with --no-extra-configs):
+  qmv        configs[0]: one int4 QMV, K=2816, N=704 (sym group 32), as
+             back-to-back launches in a HIP graph (launch-bound).
   verify_m5  configs[2]: Gemma speculative verify, M=5 tokens whose top-8
              sets overlap (union about 16), 30 layers, rows path + reduce.
   qwen35     configs[4]: Qwen3.5-MoE-35B-A3B-shaped layer (H=2048, 256
@@ -499,6 +501,37 @@ def run_qwen(tsg, torch, args):
             "prefill_t4096": prefill_summary(pre)}
 
 
+def run_qmv(tsg, torch, ctx):
+    """DequantInt4GEMV.encode, K=2816, N=704: 1,122,176 B per call
+    (int4 weights + bf16 scales + fp16 x and y). 256 calls per graph replay."""
+    n, m = H, F
+    w = torch.empty(m * n // 2, dtype=torch.uint8, device="cuda")
+    tsg.generators.bytes(w, 0x9A1)
+    sc = torch.empty(m * (n // GROUP), dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(sc, 0x9A2, 0.02, True, 7.0)
+    x = torch.empty(n, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(x, 0x9A3, 1.0)
+    y = torch.empty(m, dtype=torch.int16, device="cuda")
+    q = tsg.DequantInt4GEMV(ctx)
+    stream = torch.cuda.Stream()
+    calls = 256
+
+    def body():
+        for _ in range(calls):
+            q.encode(w, sc, sc, x, y, m, n, stream=stream)
+
+    ms = time_graph(torch, stream, body, reps=8)
+    us = ms * 1000.0 / calls
+    nbytes = m * n // 2 + m * (n // GROUP) * 2 + n * 2 + m * 2
+    if not bool(torch.isfinite(y.view(torch.float16).float()).all()):
+        raise RuntimeError("qmv produced non-finite outputs")
+    log(f"qmv K={n} N={m}: {us:.3f} us/call ({nbytes / (us * 1e-6) / 1e9:.1f} GB/s)")
+    return {"workload": "int4 QMV K=2816 N=704 sym g32 (configs[0]), back-to-back launches",
+            "us_per_call": round(us, 3), "bytes_per_call": nbytes,
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 2),
+            "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def run_verify(tsg, torch, ctx, args, layers):
     """Gemma verify, M=5 over a union of about 12-20 experts, 30
     layers on the rows path."""
@@ -668,7 +701,8 @@ def main():
         # the other BASELINE configs, after the headline figures (a failure here
         # is reported in its entry and does not void the headline)
         extra = {}
-        for name, fn in (("verify_m5", lambda: run_verify(tsg, torch, ctx, args, layers)),
+        for name, fn in (("qmv", lambda: run_qmv(tsg, torch, ctx)),
+                         ("verify_m5", lambda: run_verify(tsg, torch, ctx, args, layers)),
                          ("qwen35", lambda: run_qwen(tsg, torch, args))):
             try:
                 extra[name] = fn()

@@ -1,7 +1,7 @@
 // qmv.hip — dense int4 GEMV (DequantInt4GEMV.swift:6-364,
 // dequant_int4.metal:135-358) and the bit-exact dequantisation check.
 //
-// One output row per 8 lanes, 16-byte weight chunks (one g32 group, half a
+// One output row per 16 lanes, 16-byte weight chunks (one g32 group, half a
 // g64 group) streamed with all loads in flight, nibbles -> fp16 by the 0x6400
 // exponent trick, v_dot2_f32_f16 against x staged in LDS, fp32 scale fma.
 // The rows form keeps T <= 8 accumulators per lane so a weight chunk is read
@@ -26,7 +26,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint8_t* __restrict__ w,
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                        // T rows
     float* xsum = reinterpret_cast<float*>(smem + (size_t)T * row_h * 2u);  // T * n / 32
 
-    const uint32_t row = blockIdx.x * 16u + (threadIdx.x >> 4);
+    const uint32_t row = blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
     const uint32_t j = threadIdx.x & 15u;
     const bool live = row < m;
     const uint32_t rr = live ? row : 0u;
@@ -82,12 +82,15 @@ template <int G, bool SYM>
 tsg_status launch_qmv(hipStream_t s, const uint8_t* w, const uint16_t* sc, const uint16_t* bi,
                       const uint16_t* x, uint32_t xs, uint16_t* y, uint32_t ys, uint32_t t,
                       uint32_t m, uint32_t n) {
-    const dim3 grid((m + 15) / 16);
+    // 16 lanes per row; 4 rows per block (one wave) below 4096 rows so a
+    // small matrix still spreads over the CUs, 16 above
+    const uint32_t rpb = m < 4096u ? 4u : 16u;
+    const dim3 grid((m + rpb - 1u) / rpb), block(16u * rpb);
     const size_t lds_per_row = (size_t)lds_chunks_halves(n) * 2u + (SYM ? 0u : (n / 32u) * 4u);
-#define TSG_QMV_CASE(TT)                                                                   \
-    case TT:                                                                               \
-        hipLaunchKernelGGL((qmv_kernel<G, SYM, TT>), grid, dim3(256), lds_per_row * TT, s, \
-                           w, sc, bi, x, xs, y, ys, t, m, n);                              \
+#define TSG_QMV_CASE(TT)                                                               \
+    case TT:                                                                           \
+        hipLaunchKernelGGL((qmv_kernel<G, SYM, TT>), grid, block, lds_per_row * TT, s, \
+                           w, sc, bi, x, xs, y, ys, t, m, n);                          \
         break;
     switch (t) {
         TSG_QMV_CASE(1)
