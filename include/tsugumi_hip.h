@@ -281,11 +281,45 @@ tsg_status tsg_qmv_int4(tsg_ctx* ctx, tsg_stream stream, const uint8_t* weights,
                         const uint16_t* scales, const uint16_t* biases, const uint16_t* x,
                         uint16_t* y, uint32_t m, uint32_t n);
 /* encodeRows (DequantInt4GEMV.swift:130-182): t <= 8 activation rows against
- * the same weights; row r is bit-identical to encode on that row. */
+ * the same weights; row r is bit-identical to encode on that row. Also the
+ * drop-in for encodeRowsWide (:220-267), which the reference defines to give
+ * encodeRows' bits. Rows that do not fit the LDS staging together (large n)
+ * run in several launches. */
 tsg_status tsg_qmv_int4_rows(tsg_ctx* ctx, tsg_stream stream, const uint8_t* weights,
                              const uint16_t* scales, const uint16_t* biases, const uint16_t* x,
                              uint32_t x_stride_elements, uint16_t* y,
                              uint32_t y_stride_elements, uint32_t t, uint32_t m, uint32_t n);
+
+/* SharedExpertProjection (Kernels/MoE/SharedExpertInt8.swift:9-33): one int4
+ * matrix [rows, cols] with bf16 group scales (and biases; under sym the bias
+ * pointer may alias the scales and is not read). Device pointers. */
+typedef struct tsg_int4_projection {
+    const uint8_t* weights;
+    const uint16_t* scales;
+    const uint16_t* biases;
+    uint32_t rows, cols;
+} tsg_int4_projection;
+
+/* gelu_mul_fp16 (Metal/Primitives/utility.metal:7-18): out = half(gelu_tanh(
+ * float(gate)) * float(up)) over count fp16 values. TSG_ERR_DECLINED when
+ * count == 0. */
+tsg_status tsg_gelu_mul_f16(tsg_ctx* ctx, tsg_stream stream, const uint16_t* gate,
+                            const uint16_t* up, uint16_t* out, uint32_t count);
+
+/* SharedExpertInt4.encode (Kernels/MoE/SharedExpertInt4.swift:30-93): Gemma's
+ * dense int4 MLP, y = down(half(gelu(gate x) * up x)), as the reference
+ * encodes it (QMV gate, QMV up, gelu_mul_fp16, QMV down), so the result is
+ * bit-identical to those four calls. The byte lengths stand in for the
+ * MTLBuffer lengths the reference checks: a mismatch of shapes returns
+ * TSG_ERR_INVALID_ARGUMENT "dimensionMismatch: ...", a short buffer
+ * "scratchTooSmall: ..." (SharedExpertError). */
+tsg_status tsg_shared_expert_int4(tsg_ctx* ctx, tsg_stream stream, const uint16_t* x,
+                                  uint64_t x_bytes, const tsg_int4_projection* gate,
+                                  const tsg_int4_projection* up,
+                                  const tsg_int4_projection* down, uint16_t* y, uint64_t y_bytes,
+                                  uint16_t* scratch_gate, uint64_t scratch_gate_bytes,
+                                  uint16_t* scratch_up, uint64_t scratch_up_bytes,
+                                  uint16_t* scratch_act, uint64_t scratch_act_bytes);
 /* Bit-exact dequantisation check: out[r*n + k] = half(fma(q, s, b)), the
  * value the prefill GEMM stages (prefill.metal:1021-1026), rows x n.
  * tsg_debug_dequant_f16 computes it directly in fp32; tsg_debug_gemm_dequant_f16

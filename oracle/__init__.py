@@ -107,6 +107,9 @@ def _declare(L):
     L.tsgo_sigmoid.argtypes = [C.c_float]
     L.tsgo_sigmoid.restype = C.c_float
     L.tsgo_silu_mul_f16.argtypes = [_u16p, _u16p, _u16p, C.c_int]
+    L.tsgo_gelu_mul_f16.argtypes = [_u16p, _u16p, _u16p, C.c_int]
+    L.tsgo_dense_mlp_int4.argtypes = [_u8p, _u16p, _u16p, _u8p, _u16p, _u16p, _u8p, _u16p, _u16p,
+                                      _u16p, C.c_int, C.c_int, C.c_int, _u16p]
     L.tsgo_shared_gate_f16.argtypes = [_u16p, _u16p, _u16p, C.c_int]
     L.tsgo_shared_expert.argtypes = [_u8p, _u32p, _u16p, _u16p, C.c_int, C.c_int, C.c_int,
                                      C.c_int, _u16p]
@@ -293,6 +296,37 @@ def silu_mul_f16(gate, up) -> np.ndarray:
     out = np.empty_like(gate)
     lib().tsgo_silu_mul_f16(_p(gate, C.c_uint16), _p(up, C.c_uint16), _p(out, C.c_uint16),
                             gate.size)
+    return out
+
+
+def gelu_mul_f16(gate, up) -> np.ndarray:
+    """gelu_mul_fp16 (utility.metal:7-18) on fp16 bits."""
+    gate = np.ascontiguousarray(gate, np.uint16)
+    up = np.ascontiguousarray(up, np.uint16)
+    out = np.empty_like(gate)
+    lib().tsgo_gelu_mul_f16(_p(gate, C.c_uint16), _p(up, C.c_uint16), _p(out, C.c_uint16),
+                            gate.size)
+    return out
+
+
+def dense_mlp_int4(gate, up, down, x_bits, d: int, f: int, group: int,
+                   symmetric: bool) -> np.ndarray:
+    """SharedExpertInt4.encode (SharedExpertInt4.swift:30-93) over
+    DequantInt4GemvRef; gate/up/down are (packed, scales, biases) triples
+    ([f, d], [f, d], [d, f]). Returns y as fp16 bits."""
+    def ptrs(t):
+        packed, scales, biases = t
+        packed = np.ascontiguousarray(packed, np.uint8)
+        scales = np.ascontiguousarray(scales, np.uint16)
+        b = None if symmetric else _p(np.ascontiguousarray(biases, np.uint16), C.c_uint16)
+        return packed, scales, b
+    keep = [ptrs(t) for t in (gate, up, down)]
+    x_bits = np.ascontiguousarray(x_bits, np.uint16)
+    out = np.empty(d, np.uint16)
+    args = []
+    for packed, scales, b in keep:
+        args += [_p(packed, C.c_uint8), _p(scales, C.c_uint16), b]
+    lib().tsgo_dense_mlp_int4(*args, _p(x_bits, C.c_uint16), d, f, group, _p(out, C.c_uint16))
     return out
 
 

@@ -327,6 +327,41 @@ float tsgo_gelu_tanh(float x) {
 /* moe.metal:117: x / (1 + exp(-x)). */
 float tsgo_silu(float x) { return x / (1.0f + expf(-x)); }
 
+/* utility.metal:7-18 (gelu_mul_fp16): out = half(gelu_tanh(float(g)) *
+ * float(u)). The kernel's +-20 clamp changes nothing in fp32 (tanh(20)
+ * rounds to 1). */
+void tsgo_gelu_mul_f16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int n) {
+    for (int i = 0; i < n; ++i)
+        out[i] = tsgo_f16_bits(tsgo_gelu_tanh(tsgo_f16_to_float(gate[i])) * tsgo_f16_to_float(up[i]));
+}
+
+/* SharedExpertInt4.encode (Kernels/MoE/SharedExpertInt4.swift:30-93) over
+ * DequantInt4GemvRef: g = half(gate x), u = half(up x) (f rows of d),
+ * a = gelu_mul(g, u), y = half(down a) (d rows of f). Biases NULL = sym. */
+void tsgo_dense_mlp_int4(const uint8_t* gw, const uint16_t* gs, const uint16_t* gb,
+                         const uint8_t* uw, const uint16_t* us, const uint16_t* ub,
+                         const uint8_t* dw, const uint16_t* ds, const uint16_t* db,
+                         const uint16_t* x_f16, int d, int f, int group, uint16_t* y_f16) {
+    float* x = (float*)malloc(sizeof(float) * (size_t)d);
+    float* g = (float*)malloc(sizeof(float) * (size_t)f);
+    float* u = (float*)malloc(sizeof(float) * (size_t)f);
+    float* a = (float*)malloc(sizeof(float) * (size_t)f);
+    float* y = (float*)malloc(sizeof(float) * (size_t)d);
+    uint16_t* g16 = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)f);
+    uint16_t* u16 = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)f);
+    uint16_t* a16 = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)f);
+    tsgo_f16_to_float_n(x_f16, x, (size_t)d);
+    tsgo_dequant_int4_gemv_ref(gw, gs, gb, x, f, d, group, g);
+    tsgo_dequant_int4_gemv_ref(uw, us, ub, x, f, d, group, u);
+    tsgo_float_to_f16_n(g, g16, (size_t)f);
+    tsgo_float_to_f16_n(u, u16, (size_t)f);
+    tsgo_gelu_mul_f16(g16, u16, a16, f);
+    tsgo_f16_to_float_n(a16, a, (size_t)f);
+    tsgo_dequant_int4_gemv_ref(dw, ds, db, a, d, f, group, y);
+    tsgo_float_to_f16_n(y, y_f16, (size_t)d);
+    free(x); free(g); free(u); free(a); free(y); free(g16); free(u16); free(a16);
+}
+
 /* ------------------------------------------------ Qwen shared expert ---- */
 
 /* qwen.metal:33 (qwen_sigmoid): 1 / (1 + exp(-x)). */

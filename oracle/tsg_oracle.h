@@ -80,6 +80,11 @@ float tsgo_silu(float x);
 /* Qwen shared expert (qwen.metal, QwenForwardRunner.swift:1548-1578). */
 float tsgo_sigmoid(float x);
 void tsgo_silu_mul_f16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int n);
+void tsgo_gelu_mul_f16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int n);
+void tsgo_dense_mlp_int4(const uint8_t* gw, const uint16_t* gs, const uint16_t* gb,
+                         const uint8_t* uw, const uint16_t* us, const uint16_t* ub,
+                         const uint8_t* dw, const uint16_t* ds, const uint16_t* db,
+                         const uint16_t* x_f16, int d, int f, int group, uint16_t* y_f16);
 void tsgo_shared_gate_f16(uint16_t* y, const uint16_t* x_f16, const uint16_t* w_bf16, int d);
 void tsgo_shared_expert(const uint8_t* blob, const uint32_t* offsets9, const uint16_t* x_f16,
                         const uint16_t* gate_w_bf16, int d, int f, int group, int symmetric,

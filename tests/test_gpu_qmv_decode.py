@@ -462,3 +462,33 @@ def test_decode_layer_shared_expert(tsg, ctx, d, f, ne, sf, group, scheme):
     rel = oracle.relative_error(oracle.f16_to_float(y), ref)
     print(f"  rel={rel:.3e}")
     assert rel <= kc.NORTH_STAR
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,n", [(4096, 2816), (2048, 2816), (2816, 4096), (8192, 2816),
+                                 (1024, 2816), (2816, 8192)])
+def test_qmv_projection_shapes(tsg, ctx, m, n):
+    """DequantInt4GEMV's decode projection shapes (DequantInt4GEMV.swift:13-20):
+    encode against DequantInt4GemvRef within the GEMV tolerance, and 8 rows
+    through encodeRows / encodeRowsWide (split into launches that fit the LDS
+    at n = 8192) bit-equal to 8 single-row calls."""
+    configure(ctx, 32, "sym")
+    rng = np.random.default_rng(m * 7 + n)
+    packed = rng.integers(0, 256, (m, n // 2), dtype=np.uint8)
+    scales = oracle.bf16_bits((np.abs(rng.normal(0, 0.02, m * (n // 32))) / 7).astype(np.float32))
+    xs = oracle.f16_bits(rng.normal(0, 1.0, 8 * n).astype(np.float32)).reshape(8, n)
+    W, S = dev(packed), dev(scales)
+    q = tsg.DequantInt4GEMV(ctx)
+    y = empty(m)
+    print(f"qmv shape m={m} n={n}", flush=True)
+    q.encode(W, S, S, dev(np.ascontiguousarray(xs[0])), y, m, n)
+    ref = oracle.dequant_int4_gemv_ref(packed, scales, None, oracle.f16_to_float(xs[0]), n, 32)
+    rel = oracle.relative_error(oracle.f16_to_float(host(y, np.uint16)), ref)
+    assert rel <= kc.FP16_REDUCTION
+    yr = empty(8 * m)
+    q.encode_rows_wide(W, S, S, dev(xs), n, yr, m, 8, m, n)
+    rows = host(yr, np.uint16).reshape(8, m)
+    for r in (0, 3, 7):
+        y1 = empty(m)
+        q.encode(W, S, S, dev(np.ascontiguousarray(xs[r])), y1, m, n)
+        assert np.array_equal(rows[r], host(y1, np.uint16)), f"row {r}"

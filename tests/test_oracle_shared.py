@@ -3,7 +3,12 @@
 shared-expert vectors, so the checks are closed forms, special cases that fix
 each rounding point, and a composition over weights whose outputs are known
 exactly (one nonzero per row), which a transposed operand, a wrong sub-tensor
-offset or a missing fp16 rounding fails."""
+offset or a missing fp16 rounding fails. Also Gemma's dense-MLP pieces
+(gelu_mul_fp16, utility.metal:7-18; SharedExpertInt4.encode): the reference's
+literal GELU points, the odd symmetry of the tanh form, and the composition
+over the oracle's own pinned GEMV steps."""
+import math
+
 import numpy as np
 import pytest
 
@@ -93,3 +98,52 @@ def test_shared_expert_matches_dense_gemv_steps(symmetric):
     dn = oracle.f16_bits(oracle.dequant_int4_gemv_ref(dp, ds, None if symmetric else db,
                                                       oracle.f16_to_float(a16), 64, 32))
     assert np.array_equal(c["ref"], oracle.shared_gate_f16(dn, c["x_bits"], c["gate_w"]))
+
+
+# ------------------------------------------------ Gemma dense MLP pieces
+
+def test_gelu_mul_known_points():
+    """gelu_mul_fp16 (utility.metal:7-18) at the reference's literal GELU
+    points (MoEReferenceTests.swift:7-17): gelu(0) = 0,
+    gelu(1) = 0.5 (1 + tanh(0.7978845608028654 * 1.044715)), gelu(-1) < 0,
+    gelu(2) > gelu(1); with up = 1 the product rounds once to fp16."""
+    g = oracle.f16_bits(np.array([0.0, 1.0, -1.0, 2.0], np.float32))
+    one = oracle.f16_bits(np.ones(4, np.float32))
+    out = oracle.f16_to_float(oracle.gelu_mul_f16(g, one))
+    at1 = np.float16(0.5 * (1.0 + math.tanh(0.7978845608028654 * (1.0 + 0.044715))))
+    assert out[0] == 0.0
+    assert out[1] == np.float32(at1)
+    assert out[2] < 0 < out[1] < out[3]
+
+
+def test_gelu_mul_odd_symmetry():
+    """0.5 x (1 + tanh(u(x))) - 0.5 (-x) (1 + tanh(u(-x))) = x, u odd: with
+    up = 1, gelu(g) - gelu(-g) recovers g within two fp16 roundings."""
+    rng = np.random.default_rng(3)
+    g = rng.uniform(-6, 6, 512).astype(np.float16)
+    gb = g.view(np.uint16)
+    one = np.full(512, np.float16(1.0)).view(np.uint16)
+    pos = oracle.f16_to_float(oracle.gelu_mul_f16(gb, one)).astype(np.float64)
+    neg = oracle.f16_to_float(oracle.gelu_mul_f16((-g).view(np.uint16), one)).astype(np.float64)
+    err = np.abs(pos - neg - g.astype(np.float64))
+    assert np.all(err <= 2 * np.abs(g.astype(np.float64)) * 2.0 ** -11 + 2.0 ** -24)
+
+
+def test_dense_mlp_is_the_gemv_steps():
+    """SharedExpertInt4's composition over the oracle's pinned steps: GEMV gate
+    and up, fp16 rounding, gelu_mul, GEMV down, fp16 rounding."""
+    d, f, group = 128, 64, 32
+    for symmetric in (True, False):
+        rng = oracle.seed_tree_key(0x6E + int(symmetric), "dense-mlp")
+        gate = kc.quantized_rows(rng, f, d, group, symmetric)
+        up = kc.quantized_rows(rng, f, d, group, symmetric)
+        down = kc.quantized_rows(rng, d, f, group, symmetric)
+        x = rng.uniforms_f16(-1.0, 1.0, d)
+        got = oracle.dense_mlp_int4(gate, up, down, x, d, f, group, symmetric)
+        xf = oracle.f16_to_float(x)
+        b = lambda t: None if symmetric else t[2]
+        g16 = oracle.f16_bits(oracle.dequant_int4_gemv_ref(gate[0], gate[1], b(gate), xf, d, group))
+        u16 = oracle.f16_bits(oracle.dequant_int4_gemv_ref(up[0], up[1], b(up), xf, d, group))
+        a = oracle.f16_to_float(oracle.gelu_mul_f16(g16, u16))
+        want = oracle.f16_bits(oracle.dequant_int4_gemv_ref(down[0], down[1], b(down), a, f, group))
+        assert np.array_equal(got, want)

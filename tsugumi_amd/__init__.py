@@ -13,6 +13,7 @@ include/tsugumi_hip.h (libtsugumi_hip.so). Names follow the reference:
     PrefillMoE              -> PrefillMoE     (PrefillMoE.swift:11-38)
     streamed experts        -> ResidentLayer  (whole layer held in HBM)
     ManifestReader + PackedExpertsLayoutReader -> MoEPack (install reader + layer upload)
+    SharedExpertInt4        -> SharedExpertInt4 (Gemma's dense int4 MLP)
 
 Device buffers are torch CUDA tensors (plumbing only); `stream` defaults to
 torch's current stream. Every call raises TsgError on a non-OK status; there
@@ -32,7 +33,7 @@ __all__ = [
     "Context", "MoE", "DequantInt4GEMV", "QwenKernels", "encode_shared_expert",
     "PrefillRouter", "PrefillMoEGrouping",
     "PrefillRoutedGEMMPlanner", "PrefillGroupedRoutedMoE", "PrefillMoE", "ResidentLayer",
-    "MoEPack",
+    "MoEPack", "SharedExpertInt4",
     "ExpertOffsets", "TsgError", "PAIR_DTYPE", "BLOCK_DTYPE", "GROUP_DTYPE", "TILE_DTYPE",
     "generators", "load",
 ]
@@ -171,6 +172,34 @@ class ResidentLayer:
             self.close()
         except Exception:
             pass
+
+
+class SharedExpertInt4:
+    """SharedExpertInt4 (Kernels/MoE/SharedExpertInt4.swift:20-93): Gemma's
+    dense int4 MLP y = down(gelu(gate x) * up x), and gelu_mul_fp16
+    (utility.metal:7-18). Projections are (weights, scales, biases, rows,
+    cols) with torch CUDA tensors."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    @staticmethod
+    def projection(weights, scales, biases, rows: int, cols: int) -> "_abi.Int4Projection":
+        return _abi.Int4Projection(_ptr(weights), _ptr(scales),
+                                   _ptr(biases if biases is not None else scales), rows, cols)
+
+    def encode_gelu_mul(self, gate, up, out, count: int, stream=None) -> None:
+        check(self.lib.tsg_gelu_mul_f16(self.ctx.handle, _stream(stream), _ptr(gate), _ptr(up),
+                                        _ptr(out), count))
+
+    def encode(self, x, gate, up, down, y, scratch_gate, scratch_up, scratch_act,
+               stream=None) -> None:
+        nbytes = lambda t: t.numel() * t.element_size()
+        check(self.lib.tsg_shared_expert_int4(
+            self.ctx.handle, _stream(stream), _ptr(x), nbytes(x), C.byref(gate), C.byref(up),
+            C.byref(down), _ptr(y), nbytes(y), _ptr(scratch_gate), nbytes(scratch_gate),
+            _ptr(scratch_up), nbytes(scratch_up), _ptr(scratch_act), nbytes(scratch_act)))
 
 
 class MoEPack:
@@ -437,6 +466,10 @@ class DequantInt4GEMV:
         check(self.lib.tsg_qmv_int4_rows(self.ctx.handle, _stream(stream), _ptr(weights),
                                          _ptr(scales), _ptr(biases), _ptr(x), x_stride, _ptr(y),
                                          y_stride, t, m, n))
+
+    # encodeRowsWide (DequantInt4GEMV.swift:220-267) gives encodeRows' bits by
+    # definition; the same entry point serves both.
+    encode_rows_wide = encode_rows
 
     def debug_dequant_f16(self, weights, scales, biases, out, rows, n, gemm_path=False,
                           stream=None):

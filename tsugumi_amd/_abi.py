@@ -79,6 +79,13 @@ class MoEPackSubTensor(C.Structure):
                 ("physical_rank", C.c_uint32)]
 
 
+class Int4Projection(C.Structure):
+    """SharedExpertProjection (SharedExpertInt8.swift:9-33): device pointers
+    and the [rows, cols] shape of one int4 matrix."""
+    _fields_ = [("weights", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+                ("rows", C.c_uint32), ("cols", C.c_uint32)]
+
+
 P = C.c_void_p
 U32 = C.c_uint32
 U64 = C.c_uint64
@@ -117,6 +124,10 @@ SIGNATURES = {
     "tsg_moe_set_fused_decode": (C.c_int, [P, C.c_int]),
     "tsg_qmv_int4": (C.c_int, [P, P, P, P, P, P, P, U32, U32]),
     "tsg_qwen_silu_mul": (C.c_int, [P, P, P, P, P, U32]),
+    "tsg_gelu_mul_f16": (C.c_int, [P, P, P, P, P, U32]),
+    "tsg_shared_expert_int4": (C.c_int, [P, P, P, U64, C.POINTER(Int4Projection),
+                                         C.POINTER(Int4Projection), C.POINTER(Int4Projection),
+                                         P, U64, P, U64, P, U64, P, U64]),
     "tsg_qwen_moe_shared_gate": (C.c_int, [P, P, P, P, P, U32]),
     "tsg_qwen_moe_shared_gate_logit": (C.c_int, [P, P, P, P, U32]),
     "tsg_moe_shared_expert": (C.c_int, [P, P, P, P, P, P, P, P, U32, U32]),

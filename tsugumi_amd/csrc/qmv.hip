@@ -125,15 +125,26 @@ tsg_status qmv_dispatch(tsg_ctx* ctx, hipStream_t s, const uint8_t* w, const uin
                 "weights must be 16-byte aligned (got %p)", (const void*)w);
     TSG_REQUIRE(aligned16(x) && xs % 8 == 0, TSG_ERR_ALIGNMENT,
                 "x rows must be 16-byte aligned");
-    const size_t lds = (size_t)t * ((size_t)lds_chunks_halves(n) * 2u + (n / 32u) * 4u);
-    TSG_REQUIRE(lds <= 160u * 1024u, TSG_ERR_UNSUPPORTED,
-                "t=%u rows of n=%u do not fit the LDS staging", t, n);
+    // Rows are independent (each is summed exactly as on its own), so rows
+    // that do not fit the LDS staging together run in several launches.
+    const size_t per_row = (size_t)lds_chunks_halves(n) * 2u + (n / 32u) * 4u;
+    const uint32_t fit = (uint32_t)std::min<size_t>(kMaxRows, (160u * 1024u) / per_row);
+    TSG_REQUIRE(fit >= 1, TSG_ERR_UNSUPPORTED, "a row of n=%u does not fit the LDS staging", n);
     const bool sym = ctx->scheme == TSG_SYM;
-    if (ctx->group_size == 32)
-        return sym ? launch_qmv<32, true>(s, w, sc, sc, x, xs, y, ys, t, m, n)
-                   : launch_qmv<32, false>(s, w, sc, bi, x, xs, y, ys, t, m, n);
-    return sym ? launch_qmv<64, true>(s, w, sc, sc, x, xs, y, ys, t, m, n)
-               : launch_qmv<64, false>(s, w, sc, bi, x, xs, y, ys, t, m, n);
+    for (uint32_t r0 = 0; r0 < t; r0 += fit) {
+        const uint32_t tt = std::min(fit, t - r0);
+        const uint16_t* xr = x + (size_t)r0 * xs;
+        uint16_t* yr = y + (size_t)r0 * ys;
+        tsg_status st;
+        if (ctx->group_size == 32)
+            st = sym ? launch_qmv<32, true>(s, w, sc, sc, xr, xs, yr, ys, tt, m, n)
+                     : launch_qmv<32, false>(s, w, sc, bi, xr, xs, yr, ys, tt, m, n);
+        else
+            st = sym ? launch_qmv<64, true>(s, w, sc, sc, xr, xs, yr, ys, tt, m, n)
+                     : launch_qmv<64, false>(s, w, sc, bi, xr, xs, yr, ys, tt, m, n);
+        if (st) return st;
+    }
+    return TSG_OK;
 }
 
 }  // namespace
@@ -156,6 +167,43 @@ extern "C" tsg_status tsg_qmv_int4_rows(tsg_ctx* ctx, tsg_stream stream, const u
                 kMaxRows);
     return qmv_dispatch(ctx, as_stream(stream), w, scales, biases, x, x_stride, y, y_stride, t,
                         m, n);
+}
+
+// SharedExpertInt4.encode (Kernels/MoE/SharedExpertInt4.swift:30-93): the
+// dense int4 MLP y = down(gelu(gate x) * up x) as the reference encodes it:
+// QMV gate and up into fp16 scratch, gelu_mul_fp16, QMV down.
+extern "C" tsg_status tsg_shared_expert_int4(
+    tsg_ctx* ctx, tsg_stream stream, const uint16_t* x, uint64_t x_bytes,
+    const tsg_int4_projection* gate, const tsg_int4_projection* up,
+    const tsg_int4_projection* down, uint16_t* y, uint64_t y_bytes, uint16_t* scratch_gate,
+    uint64_t scratch_gate_bytes, uint16_t* scratch_up, uint64_t scratch_up_bytes,
+    uint16_t* scratch_act, uint64_t scratch_act_bytes) {
+    TSG_REQUIRE(ctx && gate && up && down, TSG_ERR_INVALID_ARGUMENT, "NULL ctx or projection");
+    if (!(gate->rows == up->rows && gate->cols == up->cols && down->rows == gate->cols &&
+          down->cols == gate->rows))
+        return fail(TSG_ERR_INVALID_ARGUMENT,
+                    "dimensionMismatch: gate=(%u,%u) up=(%u,%u) down=(%u,%u)", gate->rows,
+                    gate->cols, up->rows, up->cols, down->rows, down->cols);
+    const uint64_t required = (uint64_t)gate->rows * 2u;
+    if (scratch_gate_bytes < required || scratch_up_bytes < required || scratch_act_bytes < required)
+        return fail(TSG_ERR_INVALID_ARGUMENT,
+                    "scratchTooSmall: need %llu bytes per intermediate buffer",
+                    (unsigned long long)required);
+    if (x_bytes < (uint64_t)gate->cols * 2u)
+        return fail(TSG_ERR_INVALID_ARGUMENT, "scratchTooSmall: input range exceeds x buffer");
+    if (y_bytes < (uint64_t)down->rows * 2u)
+        return fail(TSG_ERR_INVALID_ARGUMENT, "scratchTooSmall: output range exceeds y buffer");
+    tsg_status st;
+    if ((st = tsg_qmv_int4(ctx, stream, gate->weights, gate->scales, gate->biases, x,
+                           scratch_gate, gate->rows, gate->cols)))
+        return st;
+    if ((st = tsg_qmv_int4(ctx, stream, up->weights, up->scales, up->biases, x, scratch_up,
+                           up->rows, up->cols)))
+        return st;
+    if ((st = tsg_gelu_mul_f16(ctx, stream, scratch_gate, scratch_up, scratch_act, gate->rows)))
+        return st;
+    return tsg_qmv_int4(ctx, stream, down->weights, down->scales, down->biases, scratch_act, y,
+                        down->rows, down->cols);
 }
 
 extern "C" tsg_status tsg_debug_dequant_f16(tsg_ctx* ctx, tsg_stream stream, const uint8_t* w,

@@ -37,6 +37,17 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
     if (i < n) out[i] = silu_mul_h(gate[i], up[i]);
 }
 
+// out = half(gelu_tanh(float(gate)) * float(up)) (utility.metal:7-18), the
+// Gemma shared expert's activation.
+__global__ __launch_bounds__(256) void gelu_mul_kernel(const uint16_t* __restrict__ gate,
+                                                       const uint16_t* __restrict__ up,
+                                                       uint16_t* __restrict__ out, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        out[i] = f32_to_f16(gate_activation<TSG_ACT_GELU_TANH>(f16_to_f32(gate[i])) *
+                            f16_to_f32(up[i]));
+}
+
 // y *= sigmoid(w_g · x) in place, one block (qwen.metal:432-455).
 __global__ __launch_bounds__(kGateThreads) void shared_gate_kernel(uint16_t* __restrict__ y,
                                                                    const uint16_t* __restrict__ x,
@@ -163,6 +174,15 @@ extern "C" tsg_status tsg_qwen_silu_mul(tsg_ctx* ctx, tsg_stream stream, const u
     hipLaunchKernelGGL(silu_mul_kernel, dim3((count + 255u) / 256u), dim3(256), 0,
                        as_stream(stream), gate, up, out, count);
     return check_launch("qwen_silu_mul");
+}
+
+extern "C" tsg_status tsg_gelu_mul_f16(tsg_ctx* ctx, tsg_stream stream, const uint16_t* gate,
+                                       const uint16_t* up, uint16_t* out, uint32_t count) {
+    tsg_status st = check_gate_args(ctx, out, gate, up, count);
+    if (st) return st;
+    hipLaunchKernelGGL(gelu_mul_kernel, dim3((count + 255u) / 256u), dim3(256), 0,
+                       as_stream(stream), gate, up, out, count);
+    return check_launch("gelu_mul");
 }
 
 static tsg_status check_gate_row(const uint16_t* x, const uint16_t* w, uint32_t d) {
