@@ -532,6 +532,50 @@ def run_qmv(tsg, torch, ctx):
             "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def run_tail(tsg, torch, ctx):
+    """Layer tail after the prefill MoE, T=2048, top-8, D=2816: the token-major
+    reduce then PrefillLayerTail (two launches), and the reduce-fused tail (one
+    launch, h2 kept in registers). Algorithmic bytes of the fused launch:
+    partials T*8*D*2 + route weights + h1 T*D*2 + hidden read and written
+    T*D*4 + two bf16 weight rows."""
+    t, k, d = 2048, 8, H
+    P = torch.empty(t * k * d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(P, 0x7A1, 0.5)
+    w = torch.empty(t * k, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(w, 0x7A2, 0.1)
+    h1 = torch.empty(t * d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(h1, 0x7A3, 1.0)
+    hid = torch.empty(t * d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(hid, 0x7A4, 1.0)
+    w2 = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(w2, 0x7A5, 0.1, True, 1.0)
+    w1 = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(w1, 0x7A6, 0.1, True, 1.0)
+    h2 = torch.empty(t * d, dtype=torch.int16, device="cuda")
+    pm, tail = tsg.PrefillMoE(ctx), tsg.PrefillLayerTail(ctx)
+    stream = torch.cuda.Stream()
+    calls = 16
+
+    def two():
+        for _ in range(calls):
+            pm.encode_reduce_token_major(P, w, h2, t, k, d, stream=stream)
+            tail.encode(h2, h1, hid, w2, w1, t, d, d, d, d, 1e-6, 1.0, stream=stream)
+
+    def one():
+        for _ in range(calls):
+            pm.encode_reduce_layer_tail(P, w, h1, hid, w2, w1, t, k, d, d, d, 1e-6, 1.0,
+                                        stream=stream)
+
+    us_two = time_graph(torch, stream, two, reps=4) * 1000.0 / calls
+    us_one = time_graph(torch, stream, one, reps=4) * 1000.0 / calls
+    nbytes = t * k * d * 2 + t * k * 2 + t * d * 2 + t * d * 4 + 2 * d * 2
+    log(f"reduce+tail T={t}: fused {us_one:.2f} us, reduce then tail {us_two:.2f} us")
+    return {"workload": "prefill reduce + layer tail, T=2048 top-8 D=2816 (Gemma)",
+            "us_fused": round(us_one, 3), "us_reduce_then_tail": round(us_two, 3),
+            "bytes_fused": nbytes, "GBps_fused": round(nbytes / (us_one * 1e-6) / 1e9, 2),
+            "frac_hbm_peak_fused": round(nbytes / (us_one * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def run_verify(tsg, torch, ctx, args, layers):
     """Gemma verify, M=5 over a union of about 12-20 experts, 30
     layers on the rows path."""
@@ -702,6 +746,7 @@ def main():
         # is reported in its entry and does not void the headline)
         extra = {}
         for name, fn in (("qmv", lambda: run_qmv(tsg, torch, ctx)),
+                         ("layer_tail", lambda: run_tail(tsg, torch, ctx)),
                          ("verify_m5", lambda: run_verify(tsg, torch, ctx, args, layers)),
                          ("qwen35", lambda: run_qwen(tsg, torch, args))):
             try:

@@ -438,6 +438,44 @@ tsg_status tsg_prefill_moe_reduce_token_major(tsg_ctx* ctx, tsg_stream stream,
                                               uint32_t query_count, uint32_t top_k,
                                               uint32_t d);
 
+/* ----------------------------------------------------------- layer tail ----
+ * The Gemma decoder-layer tail after the MoE FFN, per row (fp16 h2, h1,
+ * hidden; bf16 norm weights):
+ *   h12    = half(h1 + half(h2 * rms_inv(h2) * post_ffn_2))
+ *   hidden = half(half(hidden + half(h12 * rms_inv(h12) * post_ffn)) * half(layer_scalar))
+ * rms_inv(x) = 1/sqrt(sum(x^2)/D + eps). Each row's sums run in one fixed order
+ * over the element index, so all three entry points give identical bits for a
+ * row whatever its strides. hidden is updated in place.
+ *
+ * PrefillLayerTail.encode (PrefillLayerTail.swift:11-58,
+ * prefill_layer_tail_block prefill.metal:319-397). Errors: queryCount == 0,
+ * D outside 1...4096, a stride below D. */
+tsg_status tsg_prefill_layer_tail(tsg_ctx* ctx, tsg_stream stream, const uint16_t* h2,
+                                  const uint16_t* h1, uint16_t* hidden,
+                                  const uint16_t* post_ffn2_weight,
+                                  const uint16_t* post_ffn_weight, uint32_t query_count,
+                                  uint32_t d, uint32_t h2_stride_elements,
+                                  uint32_t h1_stride_elements, uint32_t hidden_stride_elements,
+                                  float eps, float layer_scalar);
+/* FusedLayerTail.encode (FusedLayerTail.swift:25-56, fused_layer_tail
+ * fused.metal:271-374): one contiguous row. D > 4096 is an error; D == 0 does
+ * nothing. */
+tsg_status tsg_fused_layer_tail(tsg_ctx* ctx, tsg_stream stream, const uint16_t* h2,
+                                const uint16_t* h1, uint16_t* hidden,
+                                const uint16_t* post_ffn2_weight, const uint16_t* post_ffn_weight,
+                                uint32_t d, float eps, float layer_scalar);
+/* PrefillMoE.encodeReduceTokenMajor followed by PrefillLayerTail.encode in one
+ * launch (PrefillMoE.swift:11-38 then PrefillLayerTail.swift:11-58): h2 is
+ * formed in registers with the reduce's per-element fma order, written to
+ * h2_out only when h2_out is not NULL (contiguous [query_count, d]). Same bits
+ * as the two entry points in sequence. */
+tsg_status tsg_prefill_moe_reduce_layer_tail(
+    tsg_ctx* ctx, tsg_stream stream, const uint16_t* route_partials,
+    const uint16_t* route_weights, uint16_t* h2_out, const uint16_t* h1, uint16_t* hidden,
+    const uint16_t* post_ffn2_weight, const uint16_t* post_ffn_weight, uint32_t query_count,
+    uint32_t top_k, uint32_t d, uint32_t h1_stride_elements, uint32_t hidden_stride_elements,
+    float eps, float layer_scalar);
+
 /* ------------------------------------------------------ MoEPack install ----
  * Reader of an installed pack's manifest.json and packed_experts/layout.json,
  * and the layer-file upload that replaces the SSD streamer: the reference

@@ -100,6 +100,9 @@ def _declare(L):
                                            C.c_int, _u16p]
     L.tsgo_dequant_int4_gemv_ref.argtypes = [_u8p, _u16p, _u16p, _f32p, C.c_int, C.c_int,
                                              C.c_int, _f32p]
+    L.tsgo_layer_tail.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16p, C.c_int, C.c_int,
+                                  C.c_int, C.c_int, C.c_int, C.c_float, C.c_float]
+    L.tsgo_layer_tail.restype = None
     L.tsgo_gelu_tanh.argtypes = [C.c_float]
     L.tsgo_gelu_tanh.restype = C.c_float
     L.tsgo_silu.argtypes = [C.c_float]
@@ -505,6 +508,21 @@ def reduce_token_major(partials_bits, route_w_bits, t, top_k, d) -> np.ndarray:
     lib().tsgo_reduce_token_major(_p(p, C.c_uint16), _p(w, C.c_uint16), t, top_k, d,
                                   _p(h2, C.c_uint16))
     return h2
+
+
+def layer_tail(h2, h1, hidden, w_post2, w_post, t, d, h2_stride, h1_stride, hidden_stride,
+               eps, layer_scalar) -> np.ndarray:
+    """prefill_layer_tail_block (prefill.metal:319-397) on fp16/bf16 bits;
+    returns the updated hidden buffer (a copy, strided like the input)."""
+    h2 = np.ascontiguousarray(h2, np.uint16)
+    h1 = np.ascontiguousarray(h1, np.uint16)
+    out = np.array(hidden, np.uint16, copy=True)
+    w2 = np.ascontiguousarray(w_post2, np.uint16)
+    w1 = np.ascontiguousarray(w_post, np.uint16)
+    lib().tsgo_layer_tail(_p(h2, C.c_uint16), _p(h1, C.c_uint16), _p(out, C.c_uint16),
+                          _p(w2, C.c_uint16), _p(w1, C.c_uint16), t, d, h2_stride, h1_stride,
+                          hidden_stride, eps, layer_scalar)
+    return out
 
 
 # ------------------------------------------------------------ harness ----

@@ -811,3 +811,54 @@ void tsgo_reduce_token_major(const uint16_t* partials, const uint16_t* route_w,
         }
     }
 }
+
+/* ---------------------------------------------------------- layer tail ----
+ * prefill_rms_block_inv (prefill.metal:117-147) with lsize = 256: lane l sums
+ * x[l], x[l+256], ... by fma, simd_sum over each 32-lane SIMD group (taken in
+ * lane order here; Metal leaves the order to the hardware), then the eight
+ * group sums in group order; rsqrt(sum / D + eps). */
+static float tail_rms_inv(const float* x, int d, float eps) {
+    float groups[8];
+    for (int g = 0; g < 8; ++g) {
+        float s = 0.0f;
+        for (int lane = 0; lane < 32; ++lane) {
+            float acc = 0.0f;
+            for (int i = g * 32 + lane; i < d; i += 256) acc = fmaf(x[i], x[i], acc);
+            s += acc;
+        }
+        groups[g] = s;
+    }
+    float sum = 0.0f;
+    for (int g = 0; g < 8; ++g) sum += groups[g];
+    return 1.0f / sqrtf(sum / (float)d + eps);
+}
+
+/* prefill_layer_tail_block (prefill.metal:319-397), row by row; the fp16
+ * stage boundaries of fused_layer_tail (fused.metal:271-374). */
+void tsgo_layer_tail(const uint16_t* h2, const uint16_t* h1, uint16_t* hidden,
+                     const uint16_t* w_post2, const uint16_t* w_post, int t, int d,
+                     int h2_stride, int h1_stride, int hidden_stride, float eps,
+                     float layer_scalar) {
+    float* x = (float*)malloc(sizeof(float) * (size_t)d);
+    float* h12 = (float*)malloc(sizeof(float) * (size_t)d);
+    const float scale = f16r(layer_scalar);
+    for (int row = 0; row < t; ++row) {
+        const uint16_t* r2 = h2 + (size_t)row * h2_stride;
+        const uint16_t* r1 = h1 + (size_t)row * h1_stride;
+        uint16_t* rh = hidden + (size_t)row * hidden_stride;
+        for (int i = 0; i < d; ++i) x[i] = tsgo_f16_to_float(r2[i]);
+        const float inv_h2 = tail_rms_inv(x, d, eps);
+        for (int i = 0; i < d; ++i) {
+            const float tmp = f16r(x[i] * inv_h2 * tsgo_bf16_to_float(w_post2[i]));
+            h12[i] = f16r(tsgo_f16_to_float(r1[i]) + tmp);
+        }
+        const float inv_h12 = tail_rms_inv(h12, d, eps);
+        for (int i = 0; i < d; ++i) {
+            const float tmp = f16r(h12[i] * inv_h12 * tsgo_bf16_to_float(w_post[i]));
+            const float sum = f16r(tsgo_f16_to_float(rh[i]) + tmp);
+            rh[i] = tsgo_f16_bits(sum * scale);
+        }
+    }
+    free(x);
+    free(h12);
+}

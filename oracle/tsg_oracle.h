@@ -160,6 +160,14 @@ void tsgo_prefill_moe_ref(const uint8_t* const* expert_blobs, const uint32_t* of
 void tsgo_reduce_token_major(const uint16_t* partials, const uint16_t* route_w,
                              int t, int top_k, int d, uint16_t* h2);
 
+/* The Gemma decoder-layer tail over strided rows, hidden updated in place
+ * (prefill_layer_tail_block prefill.metal:319-397, fused_layer_tail
+ * fused.metal:271-374). */
+void tsgo_layer_tail(const uint16_t* h2, const uint16_t* h1, uint16_t* hidden,
+                     const uint16_t* w_post2, const uint16_t* w_post, int t, int d,
+                     int h2_stride, int h1_stride, int hidden_stride, float eps,
+                     float layer_scalar);
+
 /* OpenMP thread count used by the heavy loops (1 = scalar). */
 void tsgo_set_threads(int n);
 int tsgo_get_threads(void);

@@ -33,7 +33,7 @@ __all__ = [
     "Context", "MoE", "DequantInt4GEMV", "QwenKernels", "encode_shared_expert",
     "PrefillRouter", "PrefillMoEGrouping",
     "PrefillRoutedGEMMPlanner", "PrefillGroupedRoutedMoE", "PrefillMoE", "ResidentLayer",
-    "MoEPack", "SharedExpertInt4",
+    "MoEPack", "SharedExpertInt4", "PrefillLayerTail", "FusedLayerTail",
     "ExpertOffsets", "TsgError", "PAIR_DTYPE", "BLOCK_DTYPE", "GROUP_DTYPE", "TILE_DTYPE",
     "generators", "load",
 ]
@@ -615,6 +615,48 @@ class PrefillMoE:
         check(self.lib.tsg_prefill_moe_reduce_token_major(
             self.ctx.handle, _stream(stream), _ptr(route_partials), _ptr(route_weights),
             _ptr(h2), query_count, top_k, d))
+
+    def encode_reduce_layer_tail(self, route_partials, route_weights, h1, hidden,
+                                 post_ffn2_weight, post_ffn_weight, query_count, top_k, d,
+                                 h1_stride, hidden_stride, eps, layer_scalar, h2=None,
+                                 stream=None):
+        """encodeReduceTokenMajor then PrefillLayerTail.encode in one launch;
+        h2 is written only when given."""
+        check(self.lib.tsg_prefill_moe_reduce_layer_tail(
+            self.ctx.handle, _stream(stream), _ptr(route_partials), _ptr(route_weights),
+            _ptr(h2) if h2 is not None else None, _ptr(h1), _ptr(hidden),
+            _ptr(post_ffn2_weight), _ptr(post_ffn_weight), query_count, top_k, d, h1_stride,
+            hidden_stride, eps, layer_scalar))
+
+
+class PrefillLayerTail:
+    """PrefillLayerTail.encode (PrefillLayerTail.swift:11-58): post-FFN RMSNorms,
+    residual adds and the layer scalar over query_count strided rows."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def encode(self, h2, h1, hidden, post_ffn2_weight, post_ffn_weight, query_count, d,
+               h2_stride, h1_stride, hidden_stride, eps, layer_scalar, stream=None):
+        check(self.lib.tsg_prefill_layer_tail(
+            self.ctx.handle, _stream(stream), _ptr(h2), _ptr(h1), _ptr(hidden),
+            _ptr(post_ffn2_weight), _ptr(post_ffn_weight), query_count, d, h2_stride, h1_stride,
+            hidden_stride, eps, layer_scalar))
+
+
+class FusedLayerTail:
+    """FusedLayerTail.encode (FusedLayerTail.swift:25-56): the decode form, one row."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def encode(self, h2, h1, hidden, post_ffn2_weight, post_ffn_weight, d, eps, layer_scalar,
+               stream=None):
+        check(self.lib.tsg_fused_layer_tail(
+            self.ctx.handle, _stream(stream), _ptr(h2), _ptr(h1), _ptr(hidden),
+            _ptr(post_ffn2_weight), _ptr(post_ffn_weight), d, eps, layer_scalar))
 
 
 class generators:

@@ -146,6 +146,11 @@ SIGNATURES = {
     "tsg_prefill_moe_down": (C.c_int, [P, P, P, P, P, P, U32, P, P, U32, U32, U32]),
     "tsg_prefill_moe_rows": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, U32, U32]),
     "tsg_prefill_moe_reduce_token_major": (C.c_int, [P, P, P, P, P, U32, U32, U32]),
+    "tsg_prefill_layer_tail": (C.c_int, [P, P, P, P, P, P, P, U32, U32, U32, U32, U32,
+                                         C.c_float, C.c_float]),
+    "tsg_fused_layer_tail": (C.c_int, [P, P, P, P, P, P, P, U32, C.c_float, C.c_float]),
+    "tsg_prefill_moe_reduce_layer_tail": (C.c_int, [P, P, P, P, P, P, P, P, P, U32, U32, U32,
+                                                    U32, U32, C.c_float, C.c_float]),
     "tsg_moepack_open": (C.c_int, [C.c_char_p, U64, U64, C.POINTER(P)]),
     "tsg_moepack_parse": (C.c_int, [C.c_char_p, U64, C.c_char_p, U64, C.POINTER(P)]),
     "tsg_moepack_close": (None, [P]),

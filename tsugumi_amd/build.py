@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libtsugumi_hip.so")
-SOURCES = ["core.hip", "decode.hip", "qmv.hip", "shared.hip", "prefill.hip", "host_routing.cpp",
+SOURCES = ["core.hip", "decode.hip", "qmv.hip", "shared.hip", "prefill.hip", "tail.hip",
+           "host_routing.cpp",
            "moepack.cpp"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
