@@ -576,6 +576,38 @@ def run_tail(tsg, torch, ctx):
             "frac_hbm_peak_fused": round(nbytes / (us_one * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def run_dense_qmm(tsg, torch, ctx):
+    """PrefillInt4QMM at T=2048 on two Gemma projection shapes (N x K =
+    2816 x 2816 and 4096 x 2816), sym g32 as the bench's experts: 2*T*N*K FLOP
+    per call on the dequant-to-LDS MFMA GEMM."""
+    t = 2048
+    out = {}
+    for n, k in ((2816, 2816), (4096, 2816)):
+        w = torch.empty(n * k // 2, dtype=torch.uint8, device="cuda")
+        tsg.generators.bytes(w, 0xD1 + n)
+        sc = torch.empty(n * (k // GROUP), dtype=torch.int16, device="cuda")
+        tsg.generators.bf16_normal(sc, 0xD2 + n, 0.02, True, 7.0)
+        x = torch.empty(t * k, dtype=torch.int16, device="cuda")
+        tsg.generators.f16_normal(x, 0xD3 + n, 1.0)
+        y = torch.empty(t * n, dtype=torch.int16, device="cuda")
+        q = tsg.PrefillInt4QMM(ctx)
+        stream = torch.cuda.Stream()
+        calls = 16
+
+        def body():
+            for _ in range(calls):
+                q.encode(w, sc, sc, x, y, t, n, k, stream=stream)
+
+        us = time_graph(torch, stream, body, reps=4) * 1000.0 / calls
+        if not bool(torch.isfinite(y.view(torch.float16).float()).all()):
+            raise RuntimeError("qmm produced non-finite outputs")
+        tf = 2.0 * t * n * k / (us * 1e-6) / 1e12
+        log(f"dense qmm T={t} N={n} K={k}: {us:.2f} us ({tf:.0f} TFLOP/s)")
+        out[f"{n}x{k}"] = {"us_per_call": round(us, 3), "TFLOPs": round(tf, 1),
+                           "frac_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+    return {"workload": "dense int4 projection QMM, T=2048, sym g32 (PrefillInt4QMM)", **out}
+
+
 def run_verify(tsg, torch, ctx, args, layers):
     """Gemma verify, M=5 over a union of about 12-20 experts, 30
     layers on the rows path."""
@@ -747,6 +779,7 @@ def main():
         extra = {}
         for name, fn in (("qmv", lambda: run_qmv(tsg, torch, ctx)),
                          ("layer_tail", lambda: run_tail(tsg, torch, ctx)),
+                         ("dense_qmm", lambda: run_dense_qmm(tsg, torch, ctx)),
                          ("verify_m5", lambda: run_verify(tsg, torch, ctx, args, layers)),
                          ("qwen35", lambda: run_qwen(tsg, torch, args))):
             try:

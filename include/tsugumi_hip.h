@@ -438,6 +438,20 @@ tsg_status tsg_prefill_moe_reduce_token_major(tsg_ctx* ctx, tsg_stream stream,
                                               uint32_t query_count, uint32_t top_k,
                                               uint32_t d);
 
+/* PrefillInt4QMM.encode (PrefillPrimitives.swift:75-175; the tiled kernel
+ * prefill_int4_qmm_simdgroup_f16 and MPPPrefillInt4QMM.encode,
+ * MPPPrefillInt4QMM.swift:104-158): the dense int4 projection over t tokens,
+ * y[t, n] = half(sum_k x[t, k] * half(dequant(W[n, k]))), fp32 accumulation.
+ * W is [n, k/2] bytes, scales and biases [n, k/group] bf16 (biases unused
+ * under sym). The dequant-to-LDS MFMA GEMM of the routed experts, rows taken
+ * in order. Errors: K % group != 0 (the reference's precondition). Declined
+ * with TSG_ERR_UNSUPPORTED: K or N not a multiple of 64, t*n or t*k >= 2^32,
+ * or W of 4 GiB or more. */
+tsg_status tsg_prefill_int4_qmm(tsg_ctx* ctx, tsg_stream stream, const uint8_t* weights,
+                                const uint16_t* scales, const uint16_t* biases,
+                                const uint16_t* x, uint16_t* y, uint32_t t, uint32_t n,
+                                uint32_t k);
+
 /* ----------------------------------------------------------- layer tail ----
  * The Gemma decoder-layer tail after the MoE FFN, per row (fp16 h2, h1,
  * hidden; bf16 norm weights):

@@ -510,6 +510,18 @@ def reduce_token_major(partials_bits, route_w_bits, t, top_k, d) -> np.ndarray:
     return h2
 
 
+def int4_qmm(packed, scales, biases, x_bits, t: int, n: int, k: int, group: int,
+             symmetric: bool) -> np.ndarray:
+    """PrefillInt4QMM's tiled path (prefill_int4_qmm_simdgroup_f16, the default):
+    weights staged as half(fma(q, s, b)) (prefill.metal:1021-1026), products
+    summed exactly (float64 here, fp32 MMA accumulation there), y rounded to
+    fp16. Returns [t, n] fp16 bits."""
+    w16 = dequantize_int4_f16(packed, scales, biases, k, group, symmetric).reshape(n, k)
+    w = f16_to_float(w16).astype(np.float64)
+    x = f16_to_float(np.ascontiguousarray(x_bits, np.uint16)).astype(np.float64).reshape(t, k)
+    return f16_bits((x @ w.T).astype(np.float32)).reshape(t, n)
+
+
 def layer_tail(h2, h1, hidden, w_post2, w_post, t, d, h2_stride, h1_stride, hidden_stride,
                eps, layer_scalar) -> np.ndarray:
     """prefill_layer_tail_block (prefill.metal:319-397) on fp16/bf16 bits;

@@ -33,7 +33,7 @@ __all__ = [
     "Context", "MoE", "DequantInt4GEMV", "QwenKernels", "encode_shared_expert",
     "PrefillRouter", "PrefillMoEGrouping",
     "PrefillRoutedGEMMPlanner", "PrefillGroupedRoutedMoE", "PrefillMoE", "ResidentLayer",
-    "MoEPack", "SharedExpertInt4", "PrefillLayerTail", "FusedLayerTail",
+    "MoEPack", "SharedExpertInt4", "PrefillLayerTail", "FusedLayerTail", "PrefillInt4QMM",
     "ExpertOffsets", "TsgError", "PAIR_DTYPE", "BLOCK_DTYPE", "GROUP_DTYPE", "TILE_DTYPE",
     "generators", "load",
 ]
@@ -627,6 +627,20 @@ class PrefillMoE:
             _ptr(h2) if h2 is not None else None, _ptr(h1), _ptr(hidden),
             _ptr(post_ffn2_weight), _ptr(post_ffn_weight), query_count, top_k, d, h1_stride,
             hidden_stride, eps, layer_scalar))
+
+
+class PrefillInt4QMM:
+    """PrefillInt4QMM.encode (PrefillPrimitives.swift:75-175): the dense int4
+    projection y[t, n] over t tokens on the dequant-to-LDS MFMA GEMM."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def encode(self, weights, scales, biases, x, y, t, n, k, stream=None):
+        check(self.lib.tsg_prefill_int4_qmm(
+            self.ctx.handle, _stream(stream), _ptr(weights), _ptr(scales), _ptr(biases),
+            _ptr(x), _ptr(y), t, n, k))
 
 
 class PrefillLayerTail:

@@ -146,6 +146,7 @@ SIGNATURES = {
     "tsg_prefill_moe_down": (C.c_int, [P, P, P, P, P, P, U32, P, P, U32, U32, U32]),
     "tsg_prefill_moe_rows": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, U32, U32]),
     "tsg_prefill_moe_reduce_token_major": (C.c_int, [P, P, P, P, P, U32, U32, U32]),
+    "tsg_prefill_int4_qmm": (C.c_int, [P, P, P, P, P, P, P, U32, U32, U32]),
     "tsg_prefill_layer_tail": (C.c_int, [P, P, P, P, P, P, P, U32, U32, U32, U32, U32,
                                          C.c_float, C.c_float]),
     "tsg_fused_layer_tail": (C.c_int, [P, P, P, P, P, P, P, U32, C.c_float, C.c_float]),

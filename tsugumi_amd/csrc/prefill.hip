@@ -399,14 +399,19 @@ struct GemmArgs {
     const tsg_routed_block* blocks;
     uint32_t n_blocks;
     const uint32_t* n_blocks_device;
-    uint16_t* out;              // act (gate/up) or route partials (down)
+    uint16_t* out;              // act (gate/up), route partials (down) or y (dense)
     uint32_t d, f, top_k;
+    uint32_t dense_rows;        // MODE 2: rows of x and y
+    const uint8_t* dense_s;     // MODE 2: scales (the weights are at layer_base)
+    const uint8_t* dense_b;     // MODE 2: biases (the scales again under sym)
     uint32_t ntiles;            // weight-row tiles per routed block
 };
 
 // Per-lane state of one block's GEMM.
 struct GemmLane {
     const uint8_t* blob;
+    const uint8_t* sblob;       // base of the scale offsets (the blob, or dense scales)
+    const uint8_t* zblob;       // base of the bias offsets
     const uint16_t* a_src[4];   // the lane's activation piece for DMA j (chunk 0)
     const uint8_t* w_src[2];    // the lane's weight piece per tile (chunk 0)
     uint32_t s_ld[4], z_ld[4];  // scale / bias row starts of the rows this lane loads
@@ -457,13 +462,13 @@ __device__ __forceinline__ void gemm_issue_scales(const GemmLane& L, uint8_t* sm
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t o = ((L.s_ld[j] + wb) & ~3u) + dw;
-        lds_dma4(L.blob + (o < L.s_last ? o : L.s_last), dst + j * 256u);
+        lds_dma4(L.sblob + (o < L.s_last ? o : L.s_last), dst + j * 256u);
     }
     if constexpr (!SYM) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t o = ((L.z_ld[j] + wb) & ~3u) + dw;
-            lds_dma4(L.blob + (o < L.z_last ? o : L.z_last), dst + (kGemmZBase - kGemmSBase) + j * 256u);
+            lds_dma4(L.zblob + (o < L.z_last ? o : L.z_last), dst + (kGemmZBase - kGemmSBase) + j * 256u);
         }
     }
 }
@@ -567,7 +572,8 @@ __device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uin
     }
 }
 
-// MODE 0: gate/up + activation; MODE 1: down + scatter.
+// MODE 0: gate/up + activation; MODE 1: down + scatter; MODE 2: dense
+// projection y[t, n] (the down sub-tensor's geometry, rows taken in order).
 template <int G, bool SYM, int ACT, int MODE, int NT>
 __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_routed_block& blk,
                                            uint32_t rows, uint32_t tile, uint8_t* smem) {
@@ -578,6 +584,8 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     L.nchunks = K / kGemmKC;
     L.nwin = (L.nchunks + gemm_window<G>() - 1u) / gemm_window<G>();
     L.blob = args.layer_base + (uint64_t)blk.local_slot * args.expert_stride;
+    L.sblob = MODE == 2 ? args.dense_s : L.blob;
+    L.zblob = MODE == 2 ? args.dense_b : L.blob;
     L.a_wave = L.wave < (uint32_t)NT;
 
     // the wave's weight rows: tile t row r is row0[t] + r of sub-tensor t
@@ -681,6 +689,7 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
         const tsg_token_expert_pair pr = args.pairs[blk.pair_start + threadIdx.x];
         odst[threadIdx.x] = (pr.token * args.top_k + pr.rank) * args.d;
     }
+    if (MODE == 2 && threadIdx.x < rows) odst[threadIdx.x] = (blk.local_row + threadIdx.x) * args.d;
     if (L.live) {
         const uint32_t c0 = MODE == 0 ? 32u * L.wave + m : 64u * L.wave + m;
 #pragma unroll
@@ -731,7 +740,7 @@ __device__ __forceinline__ uint32_t size_bucket(uint32_t rows) {
 }
 
 __device__ void gemm_work_item(const GemmArgs& args, uint32_t nb, uint32_t pid, uint32_t* scratch,
-                               uint32_t& yb, uint32_t& tile) {
+                               bool presorted, uint32_t& yb, uint32_t& tile) {
     const uint32_t T = args.ntiles, G = nb / 8u;
     uint32_t j;
     if (pid < 8u * T * G) {
@@ -743,7 +752,7 @@ __device__ void gemm_work_item(const GemmArgs& args, uint32_t nb, uint32_t pid, 
         j = 8u * G + q / T;
         tile = q % T;
     }
-    if (nb > kSortBlocks || args.n_blocks_device) {
+    if (presorted || nb > kSortBlocks || args.n_blocks_device) {
         // too many to sort here, or a list from tsg_prefill_group_pairs_device
         // (largest first already)
         yb = j;
@@ -816,8 +825,16 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmArgs args
     uint32_t yb, tile;
     // the weight ring's last stage is first written after chunk 0's barrier
     gemm_work_item(args, nb, blockIdx.x, reinterpret_cast<uint32_t*>(smem + kGemmBBase + 2u * kGemmBStage),
-                   yb, tile);
-    const tsg_routed_block blk = args.blocks[yb];
+                   MODE == 2, yb, tile);
+    tsg_routed_block blk;
+    if (MODE == 2) {  // dense: block yb is rows 128 yb .. of x, all full but the last
+        blk.local_slot = 0;
+        blk.pair_start = blk.local_row = yb * kGemmRows;
+        blk.row_count = args.dense_rows - blk.local_row < kGemmRows ? args.dense_rows - blk.local_row
+                                                                    : kGemmRows;
+    } else {
+        blk = args.blocks[yb];
+    }
     // a routed block wider than kGemmRows runs as consecutive passes
     for (uint32_t r0 = 0; r0 < blk.row_count; r0 += kGemmRows) {
         if (r0) block_barrier();  // every wave is done with the previous pass's LDS
@@ -1043,6 +1060,24 @@ tsg_status gemm_dispatch(const tsg_moe* moe, hipStream_t s, const GemmArgs& a, u
                : launch_gemm<64, false, MODE>(moe, s, a, max_blocks);
 }
 
+// Dense projection: blocks of 128 rows of x in order, 256 output columns per
+// workgroup (the down GEMM's tiling).
+template <int G, bool SYM>
+tsg_status launch_dense_qmm(hipStream_t s, const GemmArgs& a) {
+    GemmArgs args = a;
+    args.ntiles = (a.d + 255u) / 256u;
+    args.n_blocks = (a.dense_rows + kGemmRows - 1u) / kGemmRows;
+    TSG_REQUIRE((uint64_t)args.ntiles * args.n_blocks <= 0x7FFFFFFFu, TSG_ERR_UNSUPPORTED,
+                "qmm: %u row blocks x %u tiles exceed the grid", args.n_blocks, args.ntiles);
+    auto kern = moe_gemm_kernel<G, SYM, TSG_ACT_GELU_TANH, 2>;  // ACT unused in mode 2
+    TSG_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)gemm_lds_bytes(SYM)));
+    hipLaunchKernelGGL(kern, dim3(args.ntiles * args.n_blocks), dim3(kGemmThreads),
+                       gemm_lds_bytes(SYM), s, args);
+    return check_launch("moe_gemm dense qmm");
+}
+
 tsg_status fill_gemm_args(const tsg_moe* moe, const tsg_layer* layer, GemmArgs* a,
                           const uint16_t* act_in, uint32_t a_stride,
                           const tsg_token_expert_pair* pairs, const tsg_routed_block* blocks,
@@ -1253,6 +1288,47 @@ extern "C" tsg_status tsg_prefill_moe_reduce_token_major(tsg_ctx* ctx, tsg_strea
     hipLaunchKernelGGL(reduce_token_major_kernel, dim3(grid), dim3(256), 0, as_stream(stream),
                        partials, w, h2, t, k, d);
     return check_launch("reduce_token_major");
+}
+
+extern "C" tsg_status tsg_prefill_int4_qmm(tsg_ctx* ctx, tsg_stream stream,
+                                           const uint8_t* weights, const uint16_t* scales,
+                                           const uint16_t* biases, const uint16_t* x,
+                                           uint16_t* y, uint32_t t, uint32_t n, uint32_t k) {
+    TSG_REQUIRE(ctx, TSG_ERR_INVALID_ARGUMENT, "ctx is NULL");
+    const uint32_t g = ctx->group_size;
+    const bool sym = ctx->scheme == TSG_SYM;
+    TSG_REQUIRE(t > 0 && n > 0 && k > 0, TSG_ERR_INVALID_ARGUMENT, "t, n and k must be positive");
+    TSG_REQUIRE(k % g == 0, TSG_ERR_INVALID_ARGUMENT, "K must be a multiple of %u", g);
+    TSG_REQUIRE(weights && scales && x && y && (sym || biases), TSG_ERR_INVALID_ARGUMENT,
+                "NULL QMM operand");
+    TSG_REQUIRE(g == 32 || g == 64, TSG_ERR_UNSUPPORTED,
+                "the tiled QMM supports group sizes 32 and 64, not %u", g);
+    TSG_REQUIRE(k % kGemmKC == 0 && n % 64u == 0, TSG_ERR_UNSUPPORTED,
+                "the tiled QMM needs K=%u and N=%u to be multiples of 64", k, n);
+    TSG_REQUIRE(aligned16(weights) && aligned16(x) && aligned16(y), TSG_ERR_ALIGNMENT,
+                "weights, x and y must be 16-byte aligned");
+    TSG_REQUIRE((uint64_t)t * n < (1ull << 32) && (uint64_t)t * k < (1ull << 32),
+                TSG_ERR_UNSUPPORTED, "t*n and t*k must stay below 2^32 elements");
+    const uint16_t* b = sym ? scales : biases;
+    // scale and bias windows are fetched as dwords from the sub-tensor bases
+    TSG_REQUIRE(((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(b)) % 4u) == 0,
+                TSG_ERR_ALIGNMENT, "scales and biases must be 4-byte aligned");
+    TSG_REQUIRE((uint64_t)n * k / 2u < (1ull << 32), TSG_ERR_UNSUPPORTED,
+                "the weight matrix must stay below 4 GiB");
+    GemmArgs a{};  // all nine offsets 0: each sub-tensor has its own base
+    a.layer_base = weights;
+    a.dense_s = reinterpret_cast<const uint8_t*>(scales);
+    a.dense_b = reinterpret_cast<const uint8_t*>(b);
+    a.a = x;
+    a.a_stride = k;
+    a.out = y;
+    a.d = n;
+    a.f = k;
+    a.top_k = 1;
+    a.dense_rows = t;
+    hipStream_t hs = as_stream(stream);
+    if (g == 32) return sym ? launch_dense_qmm<32, true>(hs, a) : launch_dense_qmm<32, false>(hs, a);
+    return sym ? launch_dense_qmm<64, true>(hs, a) : launch_dense_qmm<64, false>(hs, a);
 }
 
 // The GEMM's own fp16 staging, un-paired (test hook for bit-exact dequant).
