@@ -566,12 +566,21 @@ def run_tail(tsg, torch, ctx):
             pm.encode_reduce_layer_tail(P, w, h1, hid, w2, w1, t, k, d, d, d, 1e-6, 1.0,
                                         stream=stream)
 
+    ft = tsg.FusedLayerTail(ctx)
+
+    def decode_tail():  # FusedLayerTail: one row per call, as each decode step
+        for _ in range(256):
+            ft.encode(h2, h1, hid, w2, w1, d, 1e-6, 1.0, stream=stream)
+
     us_two = time_graph(torch, stream, two, reps=4) * 1000.0 / calls
     us_one = time_graph(torch, stream, one, reps=4) * 1000.0 / calls
+    us_dec = time_graph(torch, stream, decode_tail, reps=4) * 1000.0 / 256
     nbytes = t * k * d * 2 + t * k * 2 + t * d * 2 + t * d * 4 + 2 * d * 2
-    log(f"reduce+tail T={t}: fused {us_one:.2f} us, reduce then tail {us_two:.2f} us")
+    log(f"reduce+tail T={t}: fused {us_one:.2f} us, reduce then tail {us_two:.2f} us; "
+        f"decode tail (one row) {us_dec:.2f} us")
     return {"workload": "prefill reduce + layer tail, T=2048 top-8 D=2816 (Gemma)",
             "us_fused": round(us_one, 3), "us_reduce_then_tail": round(us_two, 3),
+            "us_decode_tail_one_row": round(us_dec, 3),
             "bytes_fused": nbytes, "GBps_fused": round(nbytes / (us_one * 1e-6) / 1e9, 2),
             "frac_hbm_peak_fused": round(nbytes / (us_one * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
