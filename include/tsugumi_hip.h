@@ -113,17 +113,31 @@ tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream);
  * laid out by RepackPlanner.planLayerFile, RepackPlanner.swift:442-520) is held
  * byte-for-byte in HBM; expert e's blob starts at e * expert_stride. */
 
-/* Allocates num_experts * expert_stride bytes of HBM owned by the layer. */
+/* Allocates the layer's HBM (owned by it). `expert_stride` and `offsets` are
+ * the layer file's; sub-tensor offsets need only be 2-byte aligned, the
+ * repacker's guarantee (DequantInt4GEMV.swift:93-96). When a weight
+ * sub-tensor is off 16 bytes or a scale/bias one off 4, the HBM image is laid
+ * out anew (every sub-tensor on 256 bytes, stride rounded to 16 KiB) and
+ * tsg_layer_upload places the file's bytes there; otherwise the image is the
+ * file, num_experts * expert_stride bytes. */
 tsg_status tsg_layer_create(tsg_ctx* ctx, uint32_t num_experts, uint64_t expert_stride,
                             const tsg_expert_offsets* offsets, tsg_layer** out);
-/* Wraps caller-owned HBM holding the same image (no copy, not freed). */
+/* Wraps caller-owned HBM holding the file image as it is (no copy, not freed):
+ * weight sub-tensors must start on 16 bytes and scales/biases on 4
+ * (TSG_ERR_ALIGNMENT otherwise; use tsg_layer_create). */
 tsg_status tsg_layer_wrap(tsg_ctx* ctx, void* device_base, uint32_t num_experts,
                           uint64_t expert_stride, const tsg_expert_offsets* offsets,
                           tsg_layer** out);
-/* Copies `nbytes` of a host layer-file image to byte `dst_offset` of the layer. */
+/* Copies `nbytes` of a host layer-file image, starting at byte `dst_offset` of
+ * the FILE, into the layer (through the new layout when there is one). */
 tsg_status tsg_layer_upload(tsg_layer* layer, tsg_stream stream, const void* host_bytes,
                             uint64_t nbytes, uint64_t dst_offset);
+/* The HBM image: expert e at device_ptr + e * device_stride, sub-tensors at
+ * device_offsets (tsg_layer_get_geometry); the file's geometry unless laid
+ * out anew. No reference counterpart (the reference binds MTLBuffers). */
 void* tsg_layer_device_ptr(const tsg_layer* layer);
+tsg_status tsg_layer_get_geometry(const tsg_layer* layer, uint64_t* device_stride,
+                                  tsg_expert_offsets* device_offsets);
 void tsg_layer_destroy(tsg_layer* layer);
 
 /* ------------------------------------------------------------- decode ----

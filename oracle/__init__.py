@@ -136,7 +136,7 @@ def _declare(L):
     L.tsgo_plan_routed_gemm.restype = C.c_int
     L.tsgo_prefill_moe_ref.argtypes = [C.POINTER(_u8p), _u32p, _u16p, C.c_int, C.c_void_p,
                                        C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-                                       C.c_int, _u16p]
+                                       C.c_int, C.c_int, _u16p]
     L.tsgo_reduce_token_major.argtypes = [_u16p, _u16p, C.c_int, C.c_int, C.c_int, _u16p]
     L.tsgo_set_threads.argtypes = [C.c_int]
     L.tsgo_get_threads.restype = C.c_int
@@ -482,11 +482,13 @@ def plan_routed_gemm(groups, max_rows_per_batch):
 
 
 def prefill_moe_ref(expert_blobs, offsets9, hidden_bits, hidden_stride, sorted_pairs,
-                    top_k, d, f, group, symmetric, act=0, partials=None):
+                    top_k, d, f, group, symmetric, act=0, partials=None, rows_path=False):
     """Expert-major prefill reference with the GPU's fp16 roundings
     (TsugumiKernelCheck/PrefillMoEGEMMCheck.swift:138-173). `expert_blobs` is
     indexed by expert id. Returns fp16 bits [T*top_k, d] (rows never routed keep
-    whatever `partials` held)."""
+    whatever `partials` held). rows_path: the verify rows kernel's roundings
+    (gate and up stay fp32 into the activation, prefill.metal:1621-1628)
+    instead of the tiled GEMM's (both rounded to fp16)."""
     o = np.ascontiguousarray(offsets9, np.uint32)
     hidden_bits = np.ascontiguousarray(hidden_bits, np.uint16)
     sp = np.ascontiguousarray(sorted_pairs, PAIR_DTYPE)
@@ -496,7 +498,7 @@ def prefill_moe_ref(expert_blobs, offsets9, hidden_bits, hidden_stride, sorted_p
     arr = _blob_ptr_array(expert_blobs)
     lib().tsgo_prefill_moe_ref(arr, _p(o, C.c_uint32), _p(hidden_bits, C.c_uint16),
                                hidden_stride, sp.ctypes.data, sp.size, top_k, d, f, group,
-                               int(symmetric), act, _p(partials, C.c_uint16))
+                               int(symmetric), act, int(rows_path), _p(partials, C.c_uint16))
     return partials
 
 

@@ -745,9 +745,11 @@ void tsgo_prefill_moe_ref(const uint8_t* const* expert_blobs, const uint32_t* o,
                           const uint16_t* hidden, int hidden_stride,
                           const tsgo_pair* sorted_pairs, int n_pairs,
                           int top_k, int d, int f, int group, int symmetric, int act,
-                          uint16_t* partials) {
+                          int rows_path, uint16_t* partials) {
     /* Dequantise each distinct expert once, like the reference's per-expert
-     * loop; experts are visited in the order they appear. */
+     * loop; experts are visited in the order they appear. The threads share
+     * one expert at a time (its dequantisation, then its pairs), so a head
+     * expert with thousands of rows spreads over every thread. */
     int max_expert = -1;
     for (int i = 0; i < n_pairs; ++i)
         if ((int)sorted_pairs[i].expert > max_expert) max_expert = (int)sorted_pairs[i].expert;
@@ -761,37 +763,63 @@ void tsgo_prefill_moe_ref(const uint8_t* const* expert_blobs, const uint32_t* o,
         if (first[e] < 0) first[e] = i;
         last[e] = i;
     }
-#pragma omp parallel for num_threads(g_threads) schedule(dynamic, 1)
+    float* gate = (float*)malloc(sizeof(float) * (size_t)f * d);
+    float* up = (float*)malloc(sizeof(float) * (size_t)f * d);
+    float* down = (float*)malloc(sizeof(float) * (size_t)d * f);
     for (int e = 0; e < ne; ++e) {
         if (first[e] < 0) continue;
         const uint8_t* b = expert_blobs[e];
-        float* gate = (float*)malloc(sizeof(float) * (size_t)f * d);
-        float* up = (float*)malloc(sizeof(float) * (size_t)f * d);
-        float* down = (float*)malloc(sizeof(float) * (size_t)d * f);
-        float* x = (float*)malloc(sizeof(float) * (size_t)d);
-        float* a = (float*)malloc(sizeof(float) * (size_t)f);
-        tsgo_dequantize_int4(b + o[0], (const uint16_t*)(b + o[1]),
-                             symmetric ? NULL : (const uint16_t*)(b + o[2]), f, d, group, gate);
-        tsgo_dequantize_int4(b + o[3], (const uint16_t*)(b + o[4]),
-                             symmetric ? NULL : (const uint16_t*)(b + o[5]), f, d, group, up);
-        tsgo_dequantize_int4(b + o[6], (const uint16_t*)(b + o[7]),
-                             symmetric ? NULL : (const uint16_t*)(b + o[8]), d, f, group, down);
-        for (int i = first[e]; i <= last[e]; ++i) {
-            const tsgo_pair p = sorted_pairs[i];
-            if ((int)p.expert != e) continue;
-            const uint16_t* hrow = hidden + (size_t)p.token * hidden_stride;
-            for (int k = 0; k < d; ++k) x[k] = tsgo_f16_to_float(hrow[k]);
-            for (int row = 0; row < f; ++row) {
-                const float g = f16r(dot_f32(gate + (size_t)row * d, x, d));
-                const float u = f16r(dot_f32(up + (size_t)row * d, x, d));
-                a[row] = f16r(gate_act(g, act) * u);
-            }
-            uint16_t* dst = partials + ((size_t)p.token * top_k + p.rank) * d;
-            for (int row = 0; row < d; ++row)
-                dst[row] = tsgo_f16_bits(dot_f32(down + (size_t)row * f, a, f));
+        const uint16_t* bias[3] = {NULL, NULL, NULL};
+        if (!symmetric) {
+            bias[0] = (const uint16_t*)(b + o[2]);
+            bias[1] = (const uint16_t*)(b + o[5]);
+            bias[2] = (const uint16_t*)(b + o[8]);
         }
-        free(gate); free(up); free(down); free(x); free(a);
+        const int gs_d = f / group;
+        /* row-parallel dequantisation: the same per-row routine as
+         * tsgo_dequantize_int4 */
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+        for (int row = 0; row < f; ++row) {
+            dequant_row(b + o[0] + (size_t)row * (d / 2), (const uint16_t*)(b + o[1]) + (size_t)row * (d / group),
+                        bias[0] ? bias[0] + (size_t)row * (d / group) : NULL, d, group,
+                        gate + (size_t)row * d);
+            dequant_row(b + o[3] + (size_t)row * (d / 2), (const uint16_t*)(b + o[4]) + (size_t)row * (d / group),
+                        bias[1] ? bias[1] + (size_t)row * (d / group) : NULL, d, group,
+                        up + (size_t)row * d);
+        }
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+        for (int row = 0; row < d; ++row)
+            dequant_row(b + o[6] + (size_t)row * (f / 2), (const uint16_t*)(b + o[7]) + (size_t)row * gs_d,
+                        bias[2] ? bias[2] + (size_t)row * gs_d : NULL, f, group,
+                        down + (size_t)row * f);
+#pragma omp parallel num_threads(g_threads)
+        {
+            float* x = (float*)malloc(sizeof(float) * (size_t)d);
+            float* a = (float*)malloc(sizeof(float) * (size_t)f);
+#pragma omp for schedule(dynamic, 1)
+            for (int i = first[e]; i <= last[e]; ++i) {
+                const tsgo_pair p = sorted_pairs[i];
+                if ((int)p.expert != e) continue;
+                const uint16_t* hrow = hidden + (size_t)p.token * hidden_stride;
+                for (int k = 0; k < d; ++k) x[k] = tsgo_f16_to_float(hrow[k]);
+                for (int row = 0; row < f; ++row) {
+                    float g = dot_f32(gate + (size_t)row * d, x, d);
+                    float u = dot_f32(up + (size_t)row * d, x, d);
+                    if (!rows_path) {
+                        g = f16r(g);
+                        u = f16r(u);
+                    }
+                    a[row] = f16r(gate_act(g, act) * u);
+                }
+                uint16_t* dst = partials + ((size_t)p.token * top_k + p.rank) * d;
+                for (int row = 0; row < d; ++row)
+                    dst[row] = tsgo_f16_bits(dot_f32(down + (size_t)row * f, a, f));
+            }
+            free(x);
+            free(a);
+        }
     }
+    free(gate); free(up); free(down);
     free(first);
     free(last);
 }

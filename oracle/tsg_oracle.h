@@ -150,12 +150,16 @@ int tsgo_plan_routed_gemm(const tsgo_group* groups, int n_groups, int max_rows_p
 /* ---- prefill expert-major reference with the GPU's fp16 roundings
  *      (TsugumiKernelCheck/PrefillMoEGEMMCheck.swift:138-173) ---- */
 /* experts_blobs[e] + offsets9 give each expert's sub-tensors. Writes
- * partials[(token*top_k + rank)*d + j] as fp16 bits for every sorted pair. */
+ * partials[(token*top_k + rank)*d + j] as fp16 bits for every sorted pair.
+ * rows_path = 0: the tiled GEMM's roundings, act = half(act(half(g)) *
+ * half(u)) (PrefillMoEGEMMCheck.swift:156-165); 1: the rows path's
+ * (prefill.metal:1621-1628), act = half(act(g) * u) with g, u in fp32, as
+ * decode phase 1 (moe.metal:573). */
 void tsgo_prefill_moe_ref(const uint8_t* const* expert_blobs, const uint32_t* offsets9,
                           const uint16_t* hidden, int hidden_stride,
                           const tsgo_pair* sorted_pairs, int n_pairs,
                           int top_k, int d, int f, int group, int symmetric, int act,
-                          uint16_t* partials);
+                          int rows_path, uint16_t* partials);
 /* h2[t,d] = half(sum_r fma(w[t,r], P[(t*K+r),d])) (prefill.metal:796-817). */
 void tsgo_reduce_token_major(const uint16_t* partials, const uint16_t* route_w,
                              int t, int top_k, int d, uint16_t* h2);

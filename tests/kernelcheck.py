@@ -33,12 +33,17 @@ def int4_gemv_case(m, n, group, seed, symmetric):
     return dict(packed=packed, scales=scales, biases=biases, x_bits=x_bits, ref=ref)
 
 
-def pack_blob(parts, symmetric, keep_biases=True, align=16):
+def pack_blob(parts, symmetric, keep_biases=True, align=16, lead=0):
     """Expert blob in the packer's order gate(W,S,[B]), up, down
     (RepackPlanner.swift:442-520). Returns bytes and the 9 MoEExpertOffsets
     (bias offsets alias the scales when the bias is left out). Sub-tensors are
-    placed at `align`-byte boundaries."""
+    placed at `align`-byte boundaries after `lead` leading zero bytes (lead=2,
+    align=2 gives the 2-byte aligned sub-tensors the repacker allows,
+    DequantInt4GEMV.swift:93-96)."""
     chunks, offs, cur = [], [], 0
+    if lead:
+        chunks.append(np.zeros(lead, np.uint8))
+        cur = lead
     for (p, s, b) in parts:
         for arr, is_bias in ((p, False), (s, False), (b, True)):
             if is_bias and not keep_biases:

@@ -102,14 +102,14 @@ def expert_tensors(parts, offsets, symmetric):
 
 
 def write_pack(root, layer_parts, *, d, f, group, symmetric, physical=None, top_k=8,
-               family=None):
+               family=None, align=16, lead=0):
     """Writes an install under `root`. layer_parts[l][e] = ((Wg,Sg,Bg),
     (Wu,Su,Bu), (Wd,Sd,Bd)) of logical expert e in layer l. Returns
     (stride, offsets9, logical images: one uint8 array per layer)."""
     os.makedirs(os.path.join(root, "packed_experts"), exist_ok=True)
     n_layers, n_exp = len(layer_parts), len(layer_parts[0])
-    blobs = [[kc.pack_blob(p, symmetric, keep_biases=not symmetric) for p in layer]
-             for layer in layer_parts]
+    blobs = [[kc.pack_blob(p, symmetric, keep_biases=not symmetric, align=align, lead=lead)
+              for p in layer] for layer in layer_parts]
     offs = blobs[0][0][1]
     size = max(b.size for layer in blobs for b, _ in layer)
     stride = int((size + 16383) // 16384 * 16384)

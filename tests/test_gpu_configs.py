@@ -1,0 +1,301 @@
+"""GPU parity at BASELINE.json's configuration shapes, against the oracle:
+
+- the verify rows path with 1, 2, 4 and 8 rows per expert
+  (PrefillGroupedRoutedMoETests+Execution.swift:213-310), GeGLU and SiLU,
+  and no looser than the tiled GEMM at the production shape (:322-431);
+- Gemma verify, M = 5 tokens over a union of about 16 experts,
+  rows path + token-major reduce;
+- configs[4] decode M = 3: Qwen-shaped rows path + shared branch;
+- configs[3] at its real size (T = 2048, Zipf(1.1), Gemma) and configs[4]
+  prefill (T = 4096, Zipf(1.0), Qwen-shaped, SiLU): device grouping ->
+  gate/up GEMM -> down GEMM -> reduce, every pair of the head expert and
+  every pair of every 16th token recomputed on the CPU.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests import kernelcheck as kc
+from tests import workloads as wl
+from tests.gpu_util import dev, empty, f16_fill_bits, host
+
+pytestmark = pytest.mark.gpu
+
+NAN16 = f16_fill_bits(float("nan"))
+
+
+@pytest.fixture(scope="module")
+def tsg():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import tsugumi_amd
+    return tsugumi_amd
+
+
+@pytest.fixture(scope="module")
+def ctx(tsg):
+    return tsg.Context(0)
+
+
+def configure(ctx, group, scheme):
+    ctx.set_affine_group_size(group)
+    ctx.set_affine_scheme(scheme)
+
+
+def upload(tsg, ctx, image, ne, stride, offs):
+    layer = tsg.ResidentLayer(ctx, ne, stride, offs)
+    layer.upload(image)
+    return layer
+
+
+def rows_fixture(rows, group, sym, d=320, f=320, ne=8, seed=0x5E):
+    """streamedRowsMatchesReference's route set: token t routes to experts
+    t % 3 (rank 0) and t % 2 + 3 (rank 1); hidden (i % 17 - 8) * 0.01."""
+    pairs = []
+    for t in range(rows):
+        pairs.append((t, t % 3, 0, 0x3C00))
+        pairs.append((t, t % 2 + 3, 1, 0x3C00))
+    pairs = np.array(pairs, dtype=oracle.PAIR_DTYPE)
+    grouped = oracle.group_pairs(pairs, rows, 2, ne)
+    rng = oracle.seed_tree_key(seed, f"rows-{rows}-g{group}")
+    experts = [[kc.quantized_rows(rng, r, c, group, sym, -0.3, 0.3)
+                for (r, c) in ((f, d), (f, d), (d, f))] for _ in range(ne)]
+    hidden = oracle.f16_bits(((np.arange(rows * d) % 17) - 8).astype(np.float32) * np.float32(0.01))
+    return grouped, experts, hidden
+
+
+@pytest.mark.parametrize("rows", [1, 2, 4, 8])
+@pytest.mark.parametrize("group,scheme", [(32, "sym"), (64, "affine")])
+@pytest.mark.parametrize("act", ["gelu", "silu"])
+def test_rows_path_matches_reference(tsg, ctx, rows, group, scheme, act):
+    """The verify rows path (encodeStreamedRows) with experts holding 1..rows
+    route rows, against the expert-major CPU reference; route partials start
+    as NaN so a skipped store fails."""
+    sym = scheme == "sym"
+    configure(ctx, group, scheme)
+    d = f = 320
+    top_k = 2
+    grouped, experts, hidden = rows_fixture(rows, group, sym)
+    image, stride, offs, blobs = kc.layer_image(experts, sym, keep_biases=not sym)
+    layer = upload(tsg, ctx, image, len(experts), stride, offs)
+    sp = grouped["sorted_pairs"]
+    assert int(grouped["counts"].max()) == (rows + 1) // 2  # the widest expert holds ceil(rows/2)
+    act_id = 1 if act == "silu" else 0
+    ref = oracle.prefill_moe_ref(blobs, offs, hidden, d, sp, top_k, d, f, group, sym, act=act_id,
+                                 rows_path=True)
+    moe = tsg.MoE(ctx, gate_activation=act)
+    act_buf = empty(sp.size * f)
+    part = empty(rows * top_k * d, fill=NAN16)
+    tsg.PrefillGroupedRoutedMoE(moe).encode_streamed_rows(
+        layer, dev(hidden), d, dev(sp), wl.rows_blocks(grouped), act_buf, part, top_k, d, f)
+    got = oracle.f16_to_float(host(part, np.uint16))
+    rel = oracle.relative_error(got, oracle.f16_to_float(ref).ravel())
+    print(f"rows={rows} g{group} {scheme} {act}: rel={rel:.3e}")
+    assert rel <= kc.NORTH_STAR
+
+
+def test_rows_no_looser_than_tiled_at_production_shape(tsg, ctx):
+    """streamedRowsIsNoLooserThanTiledAtProductionShape (:322-431): D = 2816,
+    F = 704, 4 tokens x top-2 over 4 experts; the rows path (decode's
+    arithmetic) must be at least as close to the CPU reference as the tiled
+    GEMM (fp16-staged weights), and within the north-star bound."""
+    configure(ctx, 32, "sym")
+    d, f, rows, top_k, ne = 2816, 704, 4, 2, 4
+    pairs = []
+    for t in range(rows):
+        pairs.append((t, t % 2, 0, 0x3C00))
+        pairs.append((t, t % 2 + 2, 1, 0x3C00))
+    grouped = oracle.group_pairs(np.array(pairs, dtype=oracle.PAIR_DTYPE), rows, top_k, ne)
+    rng = oracle.seed_tree_key(0x6E, "rows-vs-tiled")
+    experts = [[kc.quantized_rows(rng, r, c, 32, True, -0.125, 0.125)
+                for (r, c) in ((f, d), (f, d), (d, f))] for _ in range(ne)]
+    hidden = oracle.f16_bits(((np.arange(rows * d) % 23) - 11).astype(np.float32) * np.float32(0.01))
+    image, stride, offs, blobs = kc.layer_image(experts, True, keep_biases=False)
+    layer = upload(tsg, ctx, image, ne, stride, offs)
+    sp = grouped["sorted_pairs"]
+    ref = oracle.f16_to_float(
+        oracle.prefill_moe_ref(blobs, offs, hidden, d, sp, top_k, d, f, 32, True)).ravel()
+    moe = tsg.MoE(ctx)
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    blocks = wl.rows_blocks(grouped)
+    H, P = dev(hidden), dev(sp)
+    act_buf = empty(sp.size * f)
+    rows_out = empty(rows * top_k * d, fill=NAN16)
+    g.encode_streamed_rows(layer, H, d, P, blocks, act_buf, rows_out, top_k, d, f)
+    tiled_out = empty(rows * top_k * d, fill=NAN16)
+    act2 = empty(sp.size * f)
+    B = dev(blocks)
+    g.encode_gate_up(layer, H, d, P, B, blocks.size, act2, d, f)
+    g.encode_down(layer, act2, P, B, blocks.size, tiled_out, top_k, d, f)
+    rel_rows = oracle.relative_error(oracle.f16_to_float(host(rows_out, np.uint16)), ref)
+    rel_tiled = oracle.relative_error(oracle.f16_to_float(host(tiled_out, np.uint16)), ref)
+    print(f"rows rel={rel_rows:.3e} tiled rel={rel_tiled:.3e}")
+    assert rel_rows <= rel_tiled
+    assert rel_rows <= kc.NORTH_STAR and rel_tiled <= kc.NORTH_STAR
+
+
+@pytest.fixture(scope="module")
+def gemma_layer(tsg, ctx):
+    configure(ctx, 32, "sym")
+    image, stride, offs, blobs = wl.random_sym_layer(np.random.default_rng(0x6E3A), 128, 2816, 704)
+    return upload(tsg, ctx, image, 128, stride, offs), offs, blobs
+
+
+@pytest.fixture(scope="module")
+def qwen_layer(tsg, ctx):
+    configure(ctx, 32, "sym")
+    image, stride, offs, blobs = wl.random_sym_layer(np.random.default_rng(0x9E35), 256, 2048, 512)
+    return upload(tsg, ctx, image, 256, stride, offs), offs, blobs
+
+
+def host_grouping(idx, w, m, ne):
+    """A verify step's host grouping (PrefillMoEGrouping.groupTokenExpertPairs
+    over makeTokenExpertPairs), as the runner does per block."""
+    grouped = oracle.group_pairs(oracle.make_token_expert_pairs(idx, w, m, 8), m, 8, ne)
+    return grouped["sorted_pairs"], grouped
+
+
+@pytest.mark.parametrize("seed", [0x5E5E, 0x5E5F])
+def test_verify_m5_gemma_rows_path(tsg, ctx, gemma_layer, seed):
+    """five tokens whose top-8 sets overlap (union about 16) through
+    the rows path and the token-major reduce, against the expert-major CPU
+    reference and its reduce."""
+    configure(ctx, 32, "sym")
+    layer, offs, blobs = gemma_layer
+    m, d, f, ne, k = 5, 2816, 704, 128, 8
+    rng = np.random.default_rng(seed)
+    idx, w, u = wl.verify_routing(rng, m, ne, k)
+    assert 12 <= u <= 20
+    hidden = wl.f16_normal(rng, m * d)
+    sp, grouped = host_grouping(idx, w, m, ne)
+    moe = tsg.MoE(ctx)
+    blocks = wl.rows_blocks(grouped)
+    assert blocks.size == u and int(blocks["row_count"].max()) >= 2
+    act_buf, part, h2 = empty(m * k * f), empty(m * k * d, fill=NAN16), empty(m * d)
+    tsg.PrefillGroupedRoutedMoE(moe).encode_streamed_rows(layer, dev(hidden), d, dev(sp), blocks,
+                                                          act_buf, part, k, d, f)
+    tsg.PrefillMoE(ctx).encode_reduce_token_major(part, dev(w), h2, m, k, d)
+    P = oracle.prefill_moe_ref(blobs, offs, hidden, d, sp, k, d, f, 32, True, rows_path=True)
+    ref_h2 = oracle.reduce_token_major(P, w, m, k, d)
+    rel_p = oracle.relative_error(oracle.f16_to_float(host(part, np.uint16)),
+                                  oracle.f16_to_float(P).ravel())
+    rel = oracle.relative_error(oracle.f16_to_float(host(h2, np.uint16)),
+                                oracle.f16_to_float(ref_h2).ravel())
+    print(f"verify M=5 union={u} rows/expert max={int(blocks['row_count'].max())}: "
+          f"partials rel={rel_p:.3e} h2 rel={rel:.3e}")
+    assert rel_p <= kc.NORTH_STAR and rel <= kc.NORTH_STAR
+
+
+def test_qwen_decode_m3_rows_and_shared(tsg, ctx, qwen_layer):
+    """configs[4] decode at M = 3 (MTP width 2 + 1): the routed experts on the
+    rows path (SiLU) + reduce, and the shared expert with its sigmoid gate per
+    token (QwenForwardRunner.swift:1548-1578), each against the oracle."""
+    configure(ctx, 32, "sym")
+    layer, offs, blobs = qwen_layer
+    m, d, f, ne, k = 3, 2048, 512, 256, 8
+    rng = np.random.default_rng(0x3333)
+    idx, w, u = wl.verify_routing(rng, m, ne, k, target=12)
+    hidden = wl.f16_normal(rng, m * d)
+    sp, grouped = host_grouping(idx, w, m, ne)
+    moe = tsg.MoE(ctx, gate_activation="silu")
+    blocks = wl.rows_blocks(grouped)
+    act_buf, part, h2 = empty(m * k * f), empty(m * k * d, fill=NAN16), empty(m * d)
+    X = dev(hidden)
+    tsg.PrefillGroupedRoutedMoE(moe).encode_streamed_rows(layer, X, d, dev(sp), blocks, act_buf,
+                                                          part, k, d, f)
+    tsg.PrefillMoE(ctx).encode_reduce_token_major(part, dev(w), h2, m, k, d)
+    P = oracle.prefill_moe_ref(blobs, offs, hidden, d, sp, k, d, f, 32, True, act=1,
+                               rows_path=True)
+    ref_h2 = oracle.reduce_token_major(P, w, m, k, d)
+    rel = oracle.relative_error(oracle.f16_to_float(host(h2, np.uint16)),
+                                oracle.f16_to_float(ref_h2).ravel())
+    # the shared expert (one more sym blob) and its bf16 gate row
+    srng = np.random.default_rng(0x51AE)
+    simage, _, soffs, sblobs = wl.random_sym_layer(srng, 1, d, f)
+    gate_w = oracle.bf16_bits((srng.normal(0.0, 1.0 / np.sqrt(d), d)).astype(np.float32))
+    sblob = dev(simage)
+    q, qk = tsg.DequantInt4GEMV(ctx), tsg.QwenKernels(ctx)
+    sg, su, sa, sout = empty(m * f), empty(m * f), empty(m * f), empty(m * d)
+    o = [int(v) for v in soffs]
+    q.encode_rows(sblob[o[0]:], sblob[o[1]:], sblob[o[2]:], X, d, sg, f, m, f, d)
+    q.encode_rows(sblob[o[3]:], sblob[o[4]:], sblob[o[5]:], X, d, su, f, m, f, d)
+    qk.encode_silu_mul(sg, su, sa, m * f)
+    q.encode_rows(sblob[o[6]:], sblob[o[7]:], sblob[o[8]:], sa, f, sout, d, m, d, f)
+    G = dev(gate_w)
+    for t in range(m):
+        qk.encode_moe_shared_gate(sout[t * d:(t + 1) * d], X[t * d:(t + 1) * d], G, d)
+    got_s = host(sout, np.uint16).reshape(m, d)
+    rel_s = 0.0
+    for t in range(m):
+        ref_s = oracle.shared_expert(sblobs[0], soffs, hidden[t * d:(t + 1) * d], gate_w, d, f,
+                                     32, True)
+        rel_s = max(rel_s, oracle.relative_error(oracle.f16_to_float(got_s[t]),
+                                                 oracle.f16_to_float(ref_s)))
+    print(f"qwen M=3 union={u}: routed h2 rel={rel:.3e} shared rel={rel_s:.3e}")
+    assert rel <= kc.NORTH_STAR and rel_s <= kc.NORTH_STAR
+
+
+def run_prefill_full(tsg, ctx, layer, offs, blobs, t, d, f, ne, s, act, seed):
+    """Device grouping -> gate/up -> down -> reduce at full size; the head
+    expert and every 16th token recomputed by the oracle."""
+    k = 8
+    rng = np.random.default_rng(seed)
+    idx, w = wl.zipf_routing(rng, t, ne, k, s)
+    hidden = wl.f16_normal(rng, t * d)
+    moe = tsg.MoE(ctx, gate_activation=act)
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    tile = 128
+    max_blocks = t * k // tile + ne
+    sp, off, cnt = empty(t * k * 4, np.uint32), empty(ne, np.uint32), empty(ne, np.uint32)
+    blocks, nb = empty(max_blocks * 4, np.uint32), empty(1, np.uint32)
+    scratch = empty(g.scratch_bytes(t, k, ne) // 4 + 1, np.uint32)
+    g.group_pairs_device(dev(idx), dev(w), t, k, ne, sp, off, cnt, blocks, max_blocks, nb, scratch,
+                         tile_rows=tile)
+    act_buf, partials, h2 = empty(t * k * f), empty(t * k * d, fill=NAN16), empty(t * d)
+    g.encode_gate_up(layer, dev(hidden), d, sp, blocks, max_blocks, act_buf, d, f,
+                     n_blocks_device=nb)
+    g.encode_down(layer, act_buf, sp, blocks, max_blocks, partials, k, d, f, n_blocks_device=nb)
+    tsg.PrefillMoE(ctx).encode_reduce_token_major(partials, dev(w), h2, t, k, d)
+    want = oracle.group_pairs(oracle.make_token_expert_pairs(idx, w, t, k), t, k, ne)
+    assert np.array_equal(host(sp, np.uint32).view(oracle.PAIR_DTYPE), want["sorted_pairs"])
+    sub, _, tokens, head, head_rows = wl.sampled_pairs(want["sorted_pairs"], t)
+    oracle.set_threads(16)
+    P = oracle.prefill_moe_ref(blobs, offs, hidden, d, sub, k, d, f, 32, True,
+                               act=1 if act == "silu" else 0)
+    gp = host(partials, np.uint16).reshape(t * k, d)
+    assert np.all(np.isfinite(oracle.f16_to_float(gp))), "a route partial was never written"
+    rows = sub["token"].astype(np.int64) * k + sub["rank"].astype(np.int64)
+    rel_p = oracle.relative_error(oracle.f16_to_float(gp[rows]), oracle.f16_to_float(P[rows]))
+    Ps = P.reshape(t, k, d)[tokens].reshape(-1, d)
+    ref_h2 = oracle.reduce_token_major(Ps, w[tokens], tokens.size, k, d)
+    gh = host(h2, np.uint16).reshape(t, d)[tokens]
+    rel = oracle.relative_error(oracle.f16_to_float(gh), oracle.f16_to_float(ref_h2))
+    n_blocks = int(host(nb, np.uint32)[0])
+    print(f"prefill T={t} E={ne} {act}: head expert {head} ({head_rows} rows), "
+          f"{n_blocks} routed blocks, {sub.size} pairs checked: partials rel={rel_p:.3e} "
+          f"h2 rel={rel:.3e}")
+    return rel_p, rel, head_rows
+
+
+def test_gemma_prefill_t2048_full_size(tsg, ctx, gemma_layer):
+    """configs[3] at its real size: T = 2048, top-8 Zipf(1.1) over 128 experts.
+    The head expert holds well over 1,000 rows, so it runs as many 128-row work
+    items dealt across the XCDs; all of them are checked."""
+    configure(ctx, 32, "sym")
+    layer, offs, blobs = gemma_layer
+    rel_p, rel, head_rows = run_prefill_full(tsg, ctx, layer, offs, blobs, 2048, 2816, 704, 128,
+                                             1.1, "gelu", 0x21F)
+    assert head_rows > 1000
+    assert rel_p <= kc.NORTH_STAR and rel <= kc.NORTH_STAR
+
+
+def test_qwen_prefill_t4096_silu(tsg, ctx, qwen_layer):
+    """configs[4] prefill: T = 4096, top-8 Zipf(1.0) over 256 experts of
+    H = 2048, I = 512 with SwiGLU (the routed GEMM's SiLU activation,
+    prefill.metal:78-86; QwenPrefill.swift:1020-1300)."""
+    configure(ctx, 32, "sym")
+    layer, offs, blobs = qwen_layer
+    rel_p, rel, _ = run_prefill_full(tsg, ctx, layer, offs, blobs, 4096, 2048, 512, 256, 1.0,
+                                     "silu", 0x4096)
+    assert rel_p <= kc.NORTH_STAR and rel <= kc.NORTH_STAR

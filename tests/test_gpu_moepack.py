@@ -137,3 +137,80 @@ def test_load_errors(tsg, ctx, tmp_path):
     with pytest.raises(tsg.TsgError) as e:
         pack.load_layer(ctx, 0)
     assert e.value.status == 7 and "layout says" in str(e.value)
+
+
+@pytest.mark.parametrize("scheme,group", [("affine", 64), ("sym", 32)])
+def test_two_byte_aligned_install(tsg, ctx, tmp_path, scheme, group):
+    """An install whose sub-tensors are only 2-byte aligned (the repacker's
+    guarantee, DequantInt4GEMV.swift:93-96): tsg_moepack_load_layer lays the
+    HBM image out anew (every sub-tensor on 256 bytes) and the decode layer
+    and both prefill GEMMs on it give the bits they give on the same experts
+    packed 16-byte aligned; decode matches the oracle. Wrapping caller-owned
+    HBM with such offsets is refused."""
+    import torch
+    sym = scheme == "sym"
+    d, f, ne = 512, 256, 16
+    rng = np.random.default_rng(0x2A11)
+    parts = random_parts(rng, ne, d, f, group)
+    stride2, offs2, images2 = W.write_pack(tmp_path / "a2", [parts], d=d, f=f, group=group,
+                                           symmetric=sym, align=2, lead=2)
+    assert all(int(o) % 16 == 2 for o in offs2), offs2
+    stride16, offs16, images16 = W.write_pack(tmp_path / "a16", [parts], d=d, f=f, group=group,
+                                              symmetric=sym)
+    pack = tsg.MoEPack.open(tmp_path / "a2")
+    pack.configure(ctx)
+    loaded = pack.load_layer(ctx, 0)
+    dstride, doffs = loaded.device_geometry()
+    assert dstride % 16384 == 0 and all(o % 256 == 0 for o in doffs)
+    aligned = tsg.ResidentLayer(ctx, ne, stride16, offs16)
+    aligned.upload(images16[0])
+    with pytest.raises(tsg.TsgError) as e:
+        buf = torch.zeros(ne * stride2, dtype=torch.uint8, device="cuda")
+        tsg.ResidentLayer(ctx, ne, stride2, offs2, device_tensor=buf)
+    assert e.value.status == 2
+    # decode layer
+    rw_bits = bf16_from(rng.normal(0, 1.0 / np.sqrt(d), ne * d))
+    es_bits = bf16_from(np.ones(d))
+    pes_bits = bf16_from(np.ones(ne))
+    x_bits = oracle.f16_bits(rng.normal(0, 1.0, d).astype(np.float32))
+    res_bits = oracle.f16_bits(rng.normal(0, 0.5, d).astype(np.float32))
+    rw, es, pes, x, res = (dev(a) for a in (rw_bits, es_bits, pes_bits, x_bits, res_bits))
+    moe = tsg.MoE(ctx)
+    outs = []
+    for layer in (loaded, aligned):
+        y, idx, wts, acts = empty(d), empty(8, np.uint32), empty(8), empty(8 * f)
+        moe.encode_decode_layer(layer, rw, x, es, pes, x, res, y, idx, wts, acts, ne, d, f)
+        ctx.synchronize()
+        outs.append([host(y, np.uint16), host(idx, np.uint32), host(wts, np.uint16)])
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    y, gi, gw = outs[0]
+    blobs = [np.ascontiguousarray(images16[0][e * stride16:(e + 1) * stride16]) for e in gi]
+    ref = oracle.moe_apply_streamed_routed(
+        blobs, np.array(offs16, np.uint32), oracle.f16_to_float(x_bits),
+        oracle.f16_to_float(res_bits), oracle.f16_to_float(gw), d, f, group, symmetric=sym)
+    rel = oracle.relative_error(oracle.f16_to_float(y), ref)
+    assert rel <= kc.NORTH_STAR
+    # prefill GEMMs: 24 tokens x top-8 over the 16 experts
+    t, k = 24, 8
+    idx_np = np.stack([rng.permutation(ne)[:k] for _ in range(t)]).astype(np.uint32)
+    w_np = np.full((t, k), 0x3000, np.uint16)
+    grouped = oracle.group_pairs(oracle.make_token_expert_pairs(idx_np, w_np, t, k), t, k, ne)
+    sp = grouped["sorted_pairs"]
+    blocks = np.array([(int(g_["expert"]), int(g_["pair_start"]), int(g_["pair_count"]),
+                        int(g_["pair_start"])) for g_ in grouped["groups"]],
+                      dtype=oracle.BLOCK_DTYPE)
+    hid = dev(oracle.f16_bits(rng.normal(0, 1.0, t * d).astype(np.float32)))
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    P, B = dev(sp), dev(blocks)
+    parts_out = []
+    for layer in (loaded, aligned):
+        act, partials = empty(t * k * f), empty(t * k * d)
+        g.encode_gate_up(layer, hid, d, P, B, blocks.size, act, d, f)
+        g.encode_down(layer, act, P, B, blocks.size, partials, k, d, f)
+        parts_out.append(host(partials, np.uint16))
+    assert np.array_equal(parts_out[0], parts_out[1])
+    print(f"2-byte aligned install {scheme} g{group}: decode rel={rel:.3e}, "
+          f"device stride {dstride} (file {stride2})")
+    loaded.close()
+    aligned.close()

@@ -244,3 +244,30 @@ def test_prefill_pipeline_zipf_end_to_end(tsg, ctx, tile):
 def quant(rng, rows, cols):
     return oracle.quantize_int4(rng.uniforms(-0.125, 0.125, rows * cols).reshape(rows, cols),
                                 32, True)
+
+
+def test_device_grouping_reports_expert_out_of_range(tsg, ctx):
+    """PrefillMoEGrouping.swift:52-88 throws expertOutOfRange for an expert id
+    past numExperts; the device grouping leaves that pair out and the error
+    reaches the caller at tsg_ctx_synchronize (status 107). A max_blocks too
+    small for the work list is refused before anything is enqueued."""
+    t, k, ne, tile = 16, 2, 8, 32
+    idx = np.tile(np.arange(k, dtype=np.uint32), (t, 1))
+    idx[5, 1] = ne + 3
+    w = np.full((t, k), 0x3800, np.uint16)
+    g = tsg.PrefillGroupedRoutedMoE(tsg.MoE(ctx))
+    max_blocks = t * k // tile + ne + 1
+    sp, off, cnt = empty(t * k * 4, np.uint32), empty(ne, np.uint32), empty(ne, np.uint32)
+    blocks, nb = empty(max_blocks * 4, np.uint32), empty(1, np.uint32)
+    scratch = empty(g.scratch_bytes(t, k, ne) // 4 + 1, np.uint32)
+    g.group_pairs_device(dev(idx), dev(w), t, k, ne, sp, off, cnt, blocks, max_blocks, nb, scratch,
+                         tile_rows=tile)
+    with pytest.raises(tsg.TsgError) as e:
+        ctx.synchronize()
+    assert e.value.status == 107
+    ctx.synchronize()  # reading the error cleared it
+    assert int(host(cnt, np.uint32).sum()) == t * k - 1
+    with pytest.raises(tsg.TsgError) as e:
+        g.group_pairs_device(dev(idx % ne), dev(w), t, k, ne, sp, off, cnt, blocks, 1, nb,
+                             scratch, tile_rows=tile)
+    assert e.value.status == 1

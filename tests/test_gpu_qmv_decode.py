@@ -72,6 +72,44 @@ def test_qmv_rows_bit_identical_to_single_row(tsg, ctx):
         assert np.array_equal(rows[r], host(y1, np.uint16)), f"row {r} differs"
 
 
+@pytest.mark.parametrize("offset", [2, 4, 6, 10, 14])
+@pytest.mark.parametrize("group,scheme", [(32, "sym"), (64, "affine")])
+def test_qmv_weights_at_2_aligned_offset(tsg, ctx, offset, group, scheme):
+    """gemv_weightsAt2AlignedNot4AlignedOffset (DequantInt4GEMVTests.swift:
+    114-121): the packed weights bound at a 2-aligned but not 16-aligned byte
+    offset (the resident layout, whose bf16 scale regions leave weights only
+    2-aligned, DequantInt4GEMV.swift:93-96); N = 2816 so every lane loads
+    whole 16-byte chunks. The result is the aligned call's bit for bit and
+    within the north-star bound of the oracle, for one row and for rows."""
+    import torch
+    sym = scheme == "sym"
+    configure(ctx, group, scheme)
+    m, n = 128, 2816
+    c = kc.int4_gemv_case(m, n, group, 0xC4, sym)
+    q = tsg.DequantInt4GEMV(ctx)
+    S, B, X = dev(c["scales"]), dev(c["scales"] if sym else c["biases"]), dev(c["x_bits"])
+    W = dev(c["packed"])
+    # the same bytes at byte `offset` of a 16-byte aligned allocation, with
+    # nothing past their end: the first and last chunks touch the buffer's ends
+    raw = torch.zeros(offset + c["packed"].size, dtype=torch.uint8, device="cuda")
+    raw[offset:] = W.view(torch.uint8)
+    Wo = raw[offset:]
+    y_al, y_off = empty(m), empty(m)
+    q.encode(W, S, B, X, y_al, m, n)
+    q.encode(Wo, S, B, X, y_off, m, n)
+    a, b = host(y_al, np.uint16), host(y_off, np.uint16)
+    assert np.array_equal(a, b)
+    rel = oracle.relative_error(oracle.f16_to_float(b), c["ref"])
+    assert rel <= kc.NORTH_STAR
+    t = 3
+    xs = oracle.SplitMix64(0xC4 + offset).uniforms_f16(-1, 1, t * n)
+    yr_al, yr_off = empty(t * m), empty(t * m)
+    q.encode_rows(W, S, B, dev(xs), n, yr_al, m, t, m, n)
+    q.encode_rows(Wo, S, B, dev(xs), n, yr_off, m, t, m, n)
+    assert np.array_equal(host(yr_al, np.uint16), host(yr_off, np.uint16))
+    print(f"qmv weights at +{offset} g{group} {scheme}: rel={rel:.3e}")
+
+
 @pytest.mark.parametrize("group", GROUPS)
 @pytest.mark.parametrize("scheme", SCHEMES)
 def test_dequant_f16_is_bit_exact(tsg, ctx, group, scheme):

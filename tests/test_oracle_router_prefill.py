@@ -153,3 +153,37 @@ def test_router_canonical_within_fp32_bound(oracle):
     for i in range(d):
         seq = (seq + wf[:, i].astype(np.float32) * xe[i].astype(np.float32)).astype(np.float32)
     assert not np.array_equal(seq, got)
+
+
+def test_prefill_ref_rows_path_rounding_exact(oracle):
+    """The two rounding modes of the prefill reference, pinned by exact values.
+    One sym g32 expert with every scale 1.0: gate row 0 and up row 0 have
+    weight 1 at k = 0, 1 (q = 9) and 0 elsewhere; down row 0 has weight 1 at
+    k = 0. With x0 = 8, x1 = 2^-8: g = u = 8 + 2^-8 exactly. The tiled GEMM
+    rounds both to fp16 first (8 + 2^-8 is half an ulp above 8: a tie, to
+    even, 8.0), so act = 8 * 8 = 64 (tanh-GELU(8) = 8 in fp32); the rows path
+    keeps them in fp32, so act = half((8 + 2^-8)^2) = 64.0625, one fp16 ulp
+    above 64 (prefill.metal:1621-1628). The down row copies act."""
+    d = f = 32
+    q = np.full((f, d), 8, np.int64)
+    q[0, 0] = q[0, 1] = 9
+    qd = np.full((d, f), 8, np.int64)
+    qd[0, 0] = 9
+
+    def pack(qm):
+        return (qm[:, 0::2] | (qm[:, 1::2] << 4)).astype(np.uint8)
+
+    ones = lambda rows: np.full((rows, 1), 0x3F80, np.uint16)  # bf16 1.0
+    parts = [(pack(q), ones(f), ones(f)), (pack(q), ones(f), ones(f)), (pack(qd), ones(d), ones(d))]
+    from tests import kernelcheck as kc
+    blob, offs = kc.pack_blob(parts, True, keep_biases=False)
+    x = np.zeros(d, np.float32)
+    x[0], x[1] = 8.0, 2.0 ** -8
+    hidden = oracle.f16_bits(x)
+    pairs = np.array([(0, 0, 0, 0x3C00)], dtype=oracle.PAIR_DTYPE)
+    gemm = oracle.prefill_moe_ref([blob], offs, hidden, d, pairs, 1, d, f, 32, True)
+    rows = oracle.prefill_moe_ref([blob], offs, hidden, d, pairs, 1, d, f, 32, True,
+                                  rows_path=True)
+    assert oracle.f16_to_float(gemm)[0, 0] == 64.0
+    assert oracle.f16_to_float(rows)[0, 0] == 64.0625
+    assert np.all(oracle.f16_to_float(rows)[0, 1:] == 0.0)

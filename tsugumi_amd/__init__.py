@@ -162,6 +162,13 @@ class ResidentLayer:
     def device_ptr(self) -> int:
         return int(self.lib.tsg_layer_device_ptr(self.handle))
 
+    def device_geometry(self):
+        """(stride, offsets) of the HBM image: the file's, unless the layer was
+        laid out anew for 2-byte aligned sub-tensors."""
+        stride, offs = C.c_uint64(), ExpertOffsets()
+        check(self.lib.tsg_layer_get_geometry(self.handle, C.byref(stride), C.byref(offs)))
+        return int(stride.value), [getattr(offs, n) for n, _ in ExpertOffsets._fields_]
+
     def close(self) -> None:
         if getattr(self, "handle", None):
             self.lib.tsg_layer_destroy(self.handle)

@@ -104,6 +104,7 @@ SIGNATURES = {
     "tsg_layer_wrap": (C.c_int, [P, P, U32, U64, C.POINTER(ExpertOffsets), C.POINTER(P)]),
     "tsg_layer_upload": (C.c_int, [P, P, P, U64, U64]),
     "tsg_layer_device_ptr": (P, [P]),
+    "tsg_layer_get_geometry": (C.c_int, [P, C.POINTER(U64), C.POINTER(ExpertOffsets)]),
     "tsg_layer_destroy": (None, [P]),
     "tsg_moe_create": (C.c_int, [P, U32, C.c_int, C.POINTER(P)]),
     "tsg_moe_destroy": (None, [P]),

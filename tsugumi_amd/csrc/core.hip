@@ -132,13 +132,22 @@ extern "C" tsg_status tsg_ctx_set_affine_scheme(tsg_ctx* ctx, tsg_affine_scheme 
 extern "C" tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream) {
     TSG_REQUIRE(ctx, TSG_ERR_INVALID_ARGUMENT, "ctx is NULL");
     TSG_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
-    // A fused decode launch whose grid barrier timed out has set this word;
-    // that launch's outputs are invalid.
+    // Kernels that detect an error on the device set a bit of this word (the
+    // one-launch decode layer on a hand-off timeout, the device grouping on
+    // an out-of-range expert id or an overfull work list); the outputs of the
+    // affected launches are invalid. Reading clears it.
     uint32_t err = 0;
     TSG_HIP_TRY(hipMemcpy(&err, ctx->counters + kSyncErrorWord, sizeof(err),
                           hipMemcpyDeviceToHost));
     if (err) {
         TSG_HIP_TRY(hipMemset(ctx->counters + kSyncErrorWord, 0, sizeof(err)));
+        if (err & kErrGroupExpertRange)
+            return fail(TSG_ERR_GROUPING_EXPERT_OUT_OF_RANGE,
+                        "expertOutOfRange: the device grouping met a route expert id >= "
+                        "numExperts; those pairs were not grouped");
+        if (err & kErrGroupBlocks)
+            return fail(TSG_ERR_INVALID_ARGUMENT,
+                        "the device grouping's work list exceeded max_blocks");
         return fail(TSG_ERR_HIP, "fused decode layer: a block timed out waiting for the "
                                  "others; outputs of the affected launch are invalid");
     }
@@ -150,23 +159,57 @@ extern "C" tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream) {
 static tsg_status check_offsets(const tsg_expert_offsets* o, uint64_t stride) {
     TSG_REQUIRE(o != nullptr, TSG_ERR_INVALID_ARGUMENT, "offsets is NULL");
     const uint32_t* v = &o->gate_w;
-    for (int i = 0; i < 9; ++i)
+    for (int i = 0; i < 9; ++i) {
         TSG_REQUIRE(v[i] < stride, TSG_ERR_INVALID_ARGUMENT,
                     "sub-tensor offset %u lies outside the %llu-byte expert stride", v[i],
                     (unsigned long long)stride);
-    // The GEMV/GEMM kernels read weights with 16-byte loads and scales with
-    // 2-byte loads. The reference guarantees 2-byte alignment only; the
-    // shipped sym/g32 layouts are 16-byte aligned throughout.
-    TSG_REQUIRE(o->gate_w % 16 == 0 && o->up_w % 16 == 0 && o->down_w % 16 == 0,
-                TSG_ERR_ALIGNMENT,
-                "weight sub-tensor offsets (%u, %u, %u) must be 16-byte aligned; re-lay the "
-                "expert blob out before upload",
-                o->gate_w, o->up_w, o->down_w);
-    TSG_REQUIRE(o->gate_s % 2 == 0 && o->up_s % 2 == 0 && o->down_s % 2 == 0 &&
-                    o->gate_b % 2 == 0 && o->up_b % 2 == 0 && o->down_b % 2 == 0,
-                TSG_ERR_ALIGNMENT, "scale/bias offsets must be 2-byte aligned");
-    TSG_REQUIRE(stride % 16 == 0, TSG_ERR_ALIGNMENT, "expert stride must be a multiple of 16");
+        // the reference's contract: sub-tensors on 2 bytes (DequantInt4GEMV.swift:93-96)
+        TSG_REQUIRE(v[i] % 2 == 0, TSG_ERR_ALIGNMENT,
+                    "sub-tensor offset %u is not 2-byte aligned", v[i]);
+    }
+    TSG_REQUIRE(stride % 2 == 0, TSG_ERR_ALIGNMENT, "expert stride must be even");
     return TSG_OK;
+}
+
+// Whether the kernels can read a layer file's blobs where they lie: weights
+// are read as 16-byte chunks, scale and bias windows as dwords, experts on
+// 16-byte strides. The shipped sym/g32 layouts always are; the reference
+// only promises 2-byte sub-tensors.
+static bool kernel_aligned(const tsg_expert_offsets& o, uint64_t stride) {
+    return o.gate_w % 16 == 0 && o.up_w % 16 == 0 && o.down_w % 16 == 0 &&
+           ((o.gate_s | o.up_s | o.down_s | o.gate_b | o.up_b | o.down_b) % 4) == 0 &&
+           stride % 16 == 0;
+}
+
+// A new layout of a blob whose sub-tensors are off the kernels' alignment:
+// each distinct sub-tensor offset starts a run that reaches to the next one
+// (the last to the end of the blob); runs keep their order and start on 256
+// bytes; the stride is rounded up to 16 KiB like the packer's
+// (RepackPlanner.swift:514-516). Offsets that alias (sym biases = scales)
+// keep aliasing.
+static void relayout(tsg_layer* l, const tsg_expert_offsets& fo, uint64_t fstride) {
+    const uint32_t* fv = &fo.gate_w;
+    uint64_t starts[9];
+    uint32_t n = 0;
+    for (int i = 0; i < 9; ++i) {
+        bool seen = false;
+        for (uint32_t j = 0; j < n; ++j) seen = seen || starts[j] == fv[i];
+        if (!seen) starts[n++] = fv[i];
+    }
+    std::sort(starts, starts + n);
+    uint64_t cur = 0;
+    for (uint32_t j = 0; j < n; ++j) {
+        const uint64_t end = j + 1 < n ? starts[j + 1] : fstride;
+        cur = (cur + 255u) & ~uint64_t(255u);
+        l->segments[j] = tsg_layer_segment{starts[j], end - starts[j], cur};
+        cur += end - starts[j];
+    }
+    l->n_segments = n;
+    l->expert_stride = (cur + 16383u) / 16384u * 16384u;
+    uint32_t* dv = &l->offsets.gate_w;
+    for (int i = 0; i < 9; ++i)
+        for (uint32_t j = 0; j < n; ++j)
+            if (l->segments[j].file_off == fv[i]) dv[i] = (uint32_t)l->segments[j].dev_off;
 }
 
 extern "C" tsg_status tsg_layer_create(tsg_ctx* ctx, uint32_t num_experts, uint64_t stride,
@@ -177,19 +220,24 @@ extern "C" tsg_status tsg_layer_create(tsg_ctx* ctx, uint32_t num_experts, uint6
                 "num_experts %u not in 1..%u", num_experts, kMaxExperts);
     tsg_status st = check_offsets(offsets, stride);
     if (st != TSG_OK) return st;
+    tsg_layer geo;
+    geo.file_stride = geo.expert_stride = stride;
+    geo.file_offsets = geo.offsets = *offsets;
+    if (!kernel_aligned(*offsets, stride)) relayout(&geo, *offsets, stride);
+    TSG_REQUIRE(geo.expert_stride <= 0xFFFFFFFFull, TSG_ERR_INVALID_ARGUMENT,
+                "expert stride %llu is too large", (unsigned long long)geo.expert_stride);
     TSG_HIP_TRY(hipSetDevice(ctx->device));
     void* base = nullptr;
-    hipError_t e = hipMalloc(&base, (size_t)num_experts * stride);
+    const size_t bytes = (size_t)num_experts * geo.expert_stride;
+    hipError_t e = hipMalloc(&base, bytes);
     if (e != hipSuccess)
-        return fail(TSG_ERR_OUT_OF_MEMORY, "layer of %llu bytes: %s",
-                    (unsigned long long)num_experts * stride, hipGetErrorString(e));
-    tsg_layer* l = new tsg_layer();
+        return fail(TSG_ERR_OUT_OF_MEMORY, "layer of %llu bytes: %s", (unsigned long long)bytes,
+                    hipGetErrorString(e));
+    tsg_layer* l = new tsg_layer(geo);
     l->ctx = ctx;
     l->base = static_cast<uint8_t*>(base);
     l->owned = true;
     l->num_experts = num_experts;
-    l->expert_stride = stride;
-    l->offsets = *offsets;
     *out = l;
     return TSG_OK;
 }
@@ -205,13 +253,18 @@ extern "C" tsg_status tsg_layer_wrap(tsg_ctx* ctx, void* device_base, uint32_t n
                 "layer base must be 16-byte aligned");
     tsg_status st = check_offsets(offsets, stride);
     if (st != TSG_OK) return st;
+    // caller-owned memory holds the file image as it is: it cannot be laid out anew
+    TSG_REQUIRE(kernel_aligned(*offsets, stride), TSG_ERR_ALIGNMENT,
+                "wrapped HBM is read where it lies, so weight sub-tensors must start on 16 "
+                "bytes and scales/biases on 4; tsg_layer_create + tsg_layer_upload re-lay a "
+                "2-byte aligned layout");
     tsg_layer* l = new tsg_layer();
     l->ctx = ctx;
     l->base = static_cast<uint8_t*>(device_base);
     l->owned = false;
     l->num_experts = num_experts;
-    l->expert_stride = stride;
-    l->offsets = *offsets;
+    l->expert_stride = l->file_stride = stride;
+    l->offsets = l->file_offsets = *offsets;
     *out = l;
     return TSG_OK;
 }
@@ -219,29 +272,59 @@ extern "C" tsg_status tsg_layer_wrap(tsg_ctx* ctx, void* device_base, uint32_t n
 extern "C" tsg_status tsg_layer_upload(tsg_layer* layer, tsg_stream stream, const void* host,
                                        uint64_t nbytes, uint64_t dst_offset) {
     TSG_REQUIRE(layer && host, TSG_ERR_INVALID_ARGUMENT, "NULL argument");
-    const uint64_t total = (uint64_t)layer->num_experts * layer->expert_stride;
+    const uint64_t fs = layer->file_stride;
+    const uint64_t total = (uint64_t)layer->num_experts * fs;
     TSG_REQUIRE(dst_offset <= total && nbytes <= total - dst_offset, TSG_ERR_INVALID_ARGUMENT,
                 "upload of %llu bytes at %llu exceeds the %llu-byte layer",
                 (unsigned long long)nbytes, (unsigned long long)dst_offset,
                 (unsigned long long)total);
-    TSG_HIP_TRY(hipMemcpyAsync(layer->base + dst_offset, host, nbytes, hipMemcpyHostToDevice,
-                               as_stream(stream)));
+    const hipStream_t hs = as_stream(stream);
+    if (layer->n_segments == 0) {
+        TSG_HIP_TRY(hipMemcpyAsync(layer->base + dst_offset, host, nbytes, hipMemcpyHostToDevice,
+                                   hs));
+        return TSG_OK;
+    }
+    // file bytes [dst_offset, dst_offset + nbytes) -> each run's place in the
+    // new layout; bytes outside every run (padding) are not needed
+    const uint8_t* src = static_cast<const uint8_t*>(host);
+    const uint64_t lo = dst_offset, hi = dst_offset + nbytes;
+    for (uint64_t e = lo / fs; e < layer->num_experts && e * fs < hi; ++e) {
+        for (uint32_t j = 0; j < layer->n_segments; ++j) {
+            const tsg_layer_segment& sg = layer->segments[j];
+            const uint64_t a = std::max(lo, e * fs + sg.file_off);
+            const uint64_t b = std::min(hi, e * fs + sg.file_off + sg.len);
+            if (a >= b) continue;
+            uint8_t* dst = layer->base + e * layer->expert_stride + sg.dev_off +
+                           (a - (e * fs + sg.file_off));
+            TSG_HIP_TRY(hipMemcpyAsync(dst, src + (a - lo), b - a, hipMemcpyHostToDevice, hs));
+        }
+    }
     return TSG_OK;
 }
 
 namespace tsg {
 // Geometry of a layer for host code outside this file (the MoEPack loader).
+// The layer FILE's geometry (what tsg_layer_upload takes), not the HBM image's.
 void layer_geometry(const tsg_layer* layer, int* device, uint32_t* num_experts,
                     uint64_t* expert_stride, tsg_expert_offsets* offsets) {
     *device = layer->ctx->device;
     *num_experts = layer->num_experts;
-    *expert_stride = layer->expert_stride;
-    *offsets = layer->offsets;
+    *expert_stride = layer->file_stride;
+    *offsets = layer->file_offsets;
 }
 }  // namespace tsg
 
 extern "C" void* tsg_layer_device_ptr(const tsg_layer* layer) {
     return layer ? layer->base : nullptr;
+}
+
+extern "C" tsg_status tsg_layer_get_geometry(const tsg_layer* layer, uint64_t* device_stride,
+                                             tsg_expert_offsets* device_offsets) {
+    TSG_REQUIRE(layer && device_stride && device_offsets, TSG_ERR_INVALID_ARGUMENT,
+                "NULL argument");
+    *device_stride = layer->expert_stride;
+    *device_offsets = layer->offsets;
+    return TSG_OK;
 }
 
 extern "C" void tsg_layer_destroy(tsg_layer* layer) {

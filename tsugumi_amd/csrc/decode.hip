@@ -592,7 +592,7 @@ __device__ __forceinline__ void poll_tagged(const DecodeSync& sy, uint32_t tag, 
         }
         if (__all(pending == 0u)) return;
         if (spins > kSpinLimit) {
-            if ((threadIdx.x & 63u) == 0) atomicOr(sy.error, 1u);
+            if ((threadIdx.x & 63u) == 0) atomicOr(sy.error, kErrDecodeTimeout);
             return;
         }
         __builtin_amdgcn_s_sleep(1);

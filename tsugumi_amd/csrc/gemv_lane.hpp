@@ -6,6 +6,8 @@
 // A weight row of K int4 values is K/32 16-byte chunks (one g32 group, half a
 // g64 group). `LANES` lanes share a row; lane j owns chunks j, j+LANES, ...,
 // loaded KB at a time with every load of a batch issued before any use.
+// Chunks are 16-byte aligned (WA = 16) or, for weights bound at a 2-byte
+// aligned offset, read by load16_a2 (WA = 2).
 // Chunks past the row end load a clamped address and leave the sum untouched,
 // so a row's bits do not depend on KB (how many chunk slots a lane carries).
 #pragma once
@@ -29,7 +31,7 @@ struct ChunkBatch {
     uint32_t b[KB];
 };
 
-template <int G, bool SYM, int KB, int LANES>
+template <int G, bool SYM, int KB, int LANES, int WA = 16>
 __device__ __forceinline__ void load_batch(const uint8_t* __restrict__ w_row,
                                            const uint16_t* __restrict__ s_row,
                                            const uint16_t* __restrict__ b_row, uint32_t base,
@@ -37,7 +39,7 @@ __device__ __forceinline__ void load_batch(const uint8_t* __restrict__ w_row,
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
         const uint32_t cc = min(base + j + LANES * i, nchunks - 1u);
-        bt.w[i] = load16_nt(reinterpret_cast<const uint4*>(w_row) + cc);
+        bt.w[i] = load_weights16<WA>(w_row + 16u * cc);
         bt.s[i] = s_row[cc * 32u / G];
         if constexpr (!SYM) bt.b[i] = b_row[cc * 32u / G];
     }

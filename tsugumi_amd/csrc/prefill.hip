@@ -5,15 +5,15 @@
 //   token-major sum   prefill.metal:796-817
 //   verify rows path  prefill.metal:1489-1721 (encodeStreamedRows)
 //
-// GEMM design: a 256-thread block owns one routed block (<= 64 rows of one
-// expert) x 128 weight rows. Per 32-wide K step the block gathers the 64
-// activation rows into LDS (fp16, k permuted into the "paired" order the
-// nibble conversion produces) and dequantises 128 x 32 int4 weights into LDS as
-// fp16, each value RNE(fma(q, s, b)) exactly as the reference stages it. Four
-// waves (2 x 2) each accumulate 32 x 64 of the output with
-// v_mfma_f32_32x32x16_f16 (fp32 accumulation). Gate and up share the block:
-// weight rows 0..63 are gate f0..f0+63, 64..127 up f0..f0+63, so the GeGLU
-// epilogue finds both halves in the same lane.
+// GEMM design (moe_gemm_kernel below): a work item is one routed block of up
+// to 128 rows of one expert x one column tile of the weights (128 gate+up
+// rows, or 256 down rows). Four waves each own two 32-row weight tiles and
+// dequantise them in registers, RNE_f16(fma(q, s, b)) exactly as the
+// reference stages them, against every live 32-row slice of the block's
+// activation rows held in LDS; v_mfma_f32_32x32x16_f16 accumulates in fp32.
+// Operands arrive by direct global->LDS loads in a 3-stage ring. Gate and up
+// rows of the same f share a wave, so the GeGLU/SiLU epilogue runs in
+// registers; the output tile leaves through LDS as 16-byte stores.
 #include "gemv_lane.hpp"
 
 namespace tsg {
@@ -83,7 +83,10 @@ __global__ __launch_bounds__(1024) void group_rank_kernel(const uint32_t* __rest
 }
 
 // Scatter pairs to their sorted positions; block 0 also writes offsets and
-// the GEMM work list. Expert ids >= num_experts are dropped (never routed).
+// the GEMM work list. An expert id >= num_experts is the reference's
+// expertOutOfRange (PrefillMoEGrouping.swift:52-88): its pair is left out and
+// the error word gets kErrGroupExpertRange, which tsg_ctx_synchronize reports;
+// a work list longer than max_blocks is cut there and sets kErrGroupBlocks.
 // Each block scans the expert counts (ne <= 256, one per thread) for the
 // expert offsets. The work list comes largest first: routed blocks by
 // size bucket ceil(rows / 32) (capped at 8) descending, then by (expert,
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(
     uint32_t ne, const uint32_t* __restrict__ rank_of, const uint32_t* __restrict__ counts,
     tsg_token_expert_pair* __restrict__ sorted, uint32_t* __restrict__ offsets,
     tsg_routed_block* __restrict__ blocks, uint32_t max_blocks, uint32_t* __restrict__ n_blocks,
-    uint32_t tile_rows) {
+    uint32_t tile_rows, uint32_t* __restrict__ error_word) {
     static_assert(kMaxExperts <= 256, "one expert per thread");
     __shared__ uint32_t off_s[kMaxExperts];
     __shared__ uint32_t wave_tot[4];
@@ -117,7 +120,10 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(
             if (brem == bk) first_rem = running + before + (bfull == bk ? full : 0u);
             running += total;
         }
-        if (e == 0) *n_blocks = running < max_blocks ? running : max_blocks;
+        if (e == 0) {
+            *n_blocks = running < max_blocks ? running : max_blocks;
+            if (running > max_blocks) atomicOr(error_word, kErrGroupBlocks);
+        }
         if (e < ne) {
             offsets[e] = c ? off : 0xFFFFFFFFu;
             for (uint32_t b = 0; b < full; ++b) {
@@ -136,7 +142,10 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(
     for (uint64_t p = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; p < n;
          p += (uint64_t)gridDim.x * blockDim.x) {
         const uint32_t ex = idx[p];
-        if (ex >= ne) continue;
+        if (ex >= ne) {
+            atomicOr(error_word, kErrGroupExpertRange);
+            continue;
+        }
         const uint32_t tok = (uint32_t)(p / k), r = (uint32_t)(p - (uint64_t)tok * k);
         sorted[off_s[ex] + rank_of[p]] = tsg_token_expert_pair{tok, ex, r, (uint32_t)w[p]};
     }
@@ -1141,6 +1150,13 @@ extern "C" tsg_status tsg_prefill_group_pairs_device(
                 TSG_ERR_INVALID_ARGUMENT, "tile_rows must be 32, 64, 128 or 256, got %u", tile_rows);
     TSG_REQUIRE(idx && w && sorted && offsets && counts && blocks && n_blocks && scratch,
                 TSG_ERR_INVALID_ARGUMENT, "NULL grouping operand");
+    // an expert's c pairs make ceil(c / tile_rows) <= c / tile_rows + 1 blocks
+    // of at least one row, so this many always hold the list
+    const uint64_t pairs_total = (uint64_t)t * k;
+    const uint64_t need = std::min<uint64_t>(pairs_total, (pairs_total + tile_rows - 1) / tile_rows + ne);
+    TSG_REQUIRE(max_blocks >= need, TSG_ERR_INVALID_ARGUMENT,
+                "max_blocks %u cannot hold the work list: need min(t*k, ceil(t*k/%u) + %u) = %llu",
+                max_blocks, tile_rows, ne, (unsigned long long)need);
     hipStream_t s = as_stream(stream);
     uint32_t* rank_of = static_cast<uint32_t*>(scratch);
     hipLaunchKernelGGL(group_rank_kernel, dim3(ne), dim3(1024), 0, s, idx, t, k, rank_of, counts);
@@ -1150,7 +1166,8 @@ extern "C" tsg_status tsg_prefill_group_pairs_device(
     uint64_t grid = (n + 255) / 256;
     if (grid > 1024) grid = 1024;
     hipLaunchKernelGGL(group_scatter_kernel, dim3(grid), dim3(256), 0, s, idx, w, t, k, ne,
-                       rank_of, counts, sorted, offsets, blocks, max_blocks, n_blocks, tile_rows);
+                       rank_of, counts, sorted, offsets, blocks, max_blocks, n_blocks, tile_rows,
+                       ctx->counters + kSyncErrorWord);
     return check_launch("group_scatter");
 }
 
@@ -1201,10 +1218,19 @@ extern "C" tsg_status tsg_prefill_moe_rows(tsg_moe* moe, tsg_stream stream,
     TSG_REQUIRE(blocks, TSG_ERR_INVALID_ARGUMENT, "blocks is NULL");
     // The host chooses the rows path from the grouping and it declines blocks
     // wider than its cap (PrefillGroupedRoutedMoE.swift:808-830).
-    for (uint32_t i = 0; i < n_blocks; ++i)
+    for (uint32_t i = 0; i < n_blocks; ++i) {
         if (blocks[i].row_count == 0 || blocks[i].row_count > kRowsMax)
             return fail(TSG_ERR_DECLINED, "rows path takes 1..%u rows per block, block %u has %u",
                         kRowsMax, i, blocks[i].row_count);
+        // the block list is on the host: an expert id past the layer would
+        // make the kernels read outside it
+        TSG_REQUIRE(blocks[i].local_slot < layer->num_experts, TSG_ERR_INVALID_ARGUMENT,
+                    "block %u names expert %u but the layer holds %u", i, blocks[i].local_slot,
+                    layer->num_experts);
+        TSG_REQUIRE((uint64_t)blocks[i].local_row + blocks[i].row_count <= 0xFFFFFFFFull &&
+                        (uint64_t)blocks[i].pair_start + blocks[i].row_count <= 0xFFFFFFFFull,
+                    TSG_ERR_INVALID_ARGUMENT, "block %u's rows overflow 32 bits", i);
+    }
     TSG_REQUIRE(top_k > 0 && act_scratch && partials, TSG_ERR_INVALID_ARGUMENT,
                 "NULL rows operand");
     GemmArgs a;

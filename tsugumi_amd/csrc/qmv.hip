@@ -13,7 +13,10 @@ namespace {
 
 constexpr uint32_t kMaxRows = 8;
 
-template <int G, bool SYM, int T>
+// WA: the weights' alignment, 16 or 2 (a weights pointer bound at a 2-byte
+// offset, DequantInt4GEMV.swift:93-96: every row starts at the same offset
+// modulo 16, since a row is a multiple of 16 bytes).
+template <int G, bool SYM, int T, int WA>
 __global__ __launch_bounds__(256) void qmv_kernel(const uint8_t* __restrict__ w,
                                                   const uint16_t* __restrict__ scales,
                                                   const uint16_t* __restrict__ biases,
@@ -35,14 +38,14 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint8_t* __restrict__ w,
     const uint16_t* sr = scales + (uint64_t)rr * ngroups;
     const uint16_t* br = biases + (uint64_t)rr * ngroups;
     ChunkBatch<kGUBatch> bt;
-    load_batch<G, SYM, kGUBatch, kGULanes>(wr, sr, br, 0u, j, nchunks, bt);
+    load_batch<G, SYM, kGUBatch, kGULanes, WA>(wr, sr, br, 0u, j, nchunks, bt);
     stage_act_rows<SYM>(x, x_stride, t, n, xs, row_h, xsum);
     __syncthreads();
     float acc[T];
 #pragma unroll
     for (int r = 0; r < T; ++r) acc[r] = 0.0f;
     for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
-        if (base) load_batch<G, SYM, kGUBatch, kGULanes>(wr, sr, br, base, j, nchunks, bt);
+        if (base) load_batch<G, SYM, kGUBatch, kGULanes, WA>(wr, sr, br, base, j, nchunks, bt);
         compute_batch<G, SYM, kGUBatch, kGULanes, T>(bt, base, j, nchunks, xs, row_h, xsum, t, acc);
     }
 #pragma unroll
@@ -78,7 +81,7 @@ __global__ void dequant_f16_kernel(const uint8_t* __restrict__ w,
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <int G, bool SYM>
+template <int G, bool SYM, int WA>
 tsg_status launch_qmv(hipStream_t s, const uint8_t* w, const uint16_t* sc, const uint16_t* bi,
                       const uint16_t* x, uint32_t xs, uint16_t* y, uint32_t ys, uint32_t t,
                       uint32_t m, uint32_t n) {
@@ -89,7 +92,7 @@ tsg_status launch_qmv(hipStream_t s, const uint8_t* w, const uint16_t* sc, const
     const size_t lds_per_row = (size_t)lds_chunks_halves(n) * 2u + (SYM ? 0u : (n / 32u) * 4u);
 #define TSG_QMV_CASE(TT)                                                               \
     case TT:                                                                           \
-        hipLaunchKernelGGL((qmv_kernel<G, SYM, TT>), grid, block, lds_per_row * TT, s, \
+        hipLaunchKernelGGL((qmv_kernel<G, SYM, TT, WA>), grid, block, lds_per_row * TT, s, \
                            w, sc, bi, x, xs, y, ys, t, m, n);                          \
         break;
     switch (t) {
@@ -118,11 +121,16 @@ tsg_status qmv_dispatch(tsg_ctx* ctx, hipStream_t s, const uint8_t* w, const uin
                 "N must be a multiple of %u, got %u", ctx->group_size, n);
     TSG_REQUIRE(m > 0, TSG_ERR_INVALID_ARGUMENT, "m must be positive");
     // The reference reads weights through ushort* and needs a 2-aligned
-    // weightsOffset (DequantInt4GEMV.swift:91-96); these kernels stream 16-byte
-    // chunks, so rows must start on 16 bytes: n % 32 == 0 (always, n % G == 0)
-    // and a 16-byte aligned base.
-    TSG_REQUIRE(aligned16(w), TSG_ERR_ALIGNMENT,
-                "weights must be 16-byte aligned (got %p)", (const void*)w);
+    // weightsOffset (DequantInt4GEMV.swift:91-96). Rows are n / 2 bytes, a
+    // multiple of 16 (n % 32 == 0), so every 16-byte chunk has the base's
+    // alignment: 16-byte loads when the base is 16-byte aligned, else the
+    // 2-byte-safe load (load16_a2).
+    TSG_REQUIRE((reinterpret_cast<uintptr_t>(w) & 1u) == 0, TSG_ERR_ALIGNMENT,
+                "weights need a 2-aligned offset (got %p)", (const void*)w);
+    TSG_REQUIRE((reinterpret_cast<uintptr_t>(sc) & 1u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(bi ? bi : sc) & 1u) == 0,
+                TSG_ERR_ALIGNMENT, "scales and biases must be 2-byte aligned");
+    const bool w16 = aligned16(w);
     TSG_REQUIRE(aligned16(x) && xs % 8 == 0, TSG_ERR_ALIGNMENT,
                 "x rows must be 16-byte aligned");
     // Rows are independent (each is summed exactly as on its own), so rows
@@ -136,12 +144,19 @@ tsg_status qmv_dispatch(tsg_ctx* ctx, hipStream_t s, const uint8_t* w, const uin
         const uint16_t* xr = x + (size_t)r0 * xs;
         uint16_t* yr = y + (size_t)r0 * ys;
         tsg_status st;
-        if (ctx->group_size == 32)
-            st = sym ? launch_qmv<32, true>(s, w, sc, sc, xr, xs, yr, ys, tt, m, n)
-                     : launch_qmv<32, false>(s, w, sc, bi, xr, xs, yr, ys, tt, m, n);
-        else
-            st = sym ? launch_qmv<64, true>(s, w, sc, sc, xr, xs, yr, ys, tt, m, n)
-                     : launch_qmv<64, false>(s, w, sc, bi, xr, xs, yr, ys, tt, m, n);
+#define TSG_QMV_WA(WA)                                                                 \
+    if (ctx->group_size == 32)                                                         \
+        st = sym ? launch_qmv<32, true, WA>(s, w, sc, sc, xr, xs, yr, ys, tt, m, n)    \
+                 : launch_qmv<32, false, WA>(s, w, sc, bi, xr, xs, yr, ys, tt, m, n);  \
+    else                                                                               \
+        st = sym ? launch_qmv<64, true, WA>(s, w, sc, sc, xr, xs, yr, ys, tt, m, n)    \
+                 : launch_qmv<64, false, WA>(s, w, sc, bi, xr, xs, yr, ys, tt, m, n);
+        if (w16) {
+            TSG_QMV_WA(16)
+        } else {
+            TSG_QMV_WA(2)
+        }
+#undef TSG_QMV_WA
         if (st) return st;
     }
     return TSG_OK;

@@ -58,13 +58,30 @@ struct tsg_moe {
     bool unfused_decode = false;  // tsg_moe_set_fused_decode(moe, 0)
 };
 
+// One run of bytes of an expert blob: file bytes [file_off, file_off + len)
+// of each blob live at device bytes [dev_off, dev_off + len) of that expert.
+struct tsg_layer_segment {
+    uint64_t file_off, len, dev_off;
+};
+
 struct tsg_layer {
     tsg_ctx* ctx = nullptr;
     uint8_t* base = nullptr;
     bool owned = false;
     uint32_t num_experts = 0;
+    // The HBM image the kernels read: expert e at base + e * expert_stride,
+    // sub-tensors at `offsets`.
     uint64_t expert_stride = 0;
     tsg_expert_offsets offsets{};
+    // The layer file's geometry, as the caller gives it and uploads in. Equal
+    // to the above unless a sub-tensor of the file is off the kernels'
+    // alignment (16 bytes for weights, 4 for scales and biases); then the
+    // image is laid out anew, every sub-tensor on 256 bytes, and `segments`
+    // maps file bytes to image bytes.
+    uint64_t file_stride = 0;
+    tsg_expert_offsets file_offsets{};
+    uint32_t n_segments = 0;  // 0: the image is the file
+    tsg_layer_segment segments[9]{};
 };
 
 namespace tsg {
@@ -80,7 +97,13 @@ constexpr uint32_t kDecodeGroups = 8;      // one expert slot per group
 constexpr uint32_t kGroupMembers = 32;     // blocks per group
 constexpr uint32_t kDecodeBlocks = kDecodeGroups * kGroupMembers;
 constexpr uint32_t kSyncEpochWord = 1024;  // launch epoch
-constexpr uint32_t kSyncErrorWord = 1056;  // rendezvous timeout
+constexpr uint32_t kSyncErrorWord = 1056;  // device-side error bits (kErr*), read by tsg_ctx_synchronize
+// Bits of the error word: a one-launch decode layer whose hand-off wait timed
+// out; a device grouping that met an expert id >= num_experts (its pairs are
+// not grouped); a device grouping whose work list did not fit max_blocks.
+constexpr uint32_t kErrDecodeTimeout = 1u;
+constexpr uint32_t kErrGroupExpertRange = 2u;
+constexpr uint32_t kErrGroupBlocks = 4u;
 constexpr uint32_t kSyncLogitWord = 1088;  // tagged 64-bit logits, kMaxExperts per group
 static_assert(kSyncLogitWord + kDecodeGroups * 2 * kMaxExperts <= kMaxCounters, "sync area overflow");
 static_assert(kSyncLogitWord % 2 == 0, "64-bit words must be aligned");
@@ -116,6 +139,34 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load16_nt(const void* p) {
     const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 16 bytes at an address that is only 2-byte aligned (the reference's
+// contract for packed weights, DequantInt4GEMV.swift:93-96): four dwords when
+// the address is 4-byte aligned, else a 16-bit load at each end and the three
+// aligned dwords between. No byte outside [p, p + 16) is read, so the first
+// and last chunk of a buffer stay inside it.
+__device__ __forceinline__ uint4 load16_a2(const void* ptr) {
+    const uint8_t* p = static_cast<const uint8_t*>(ptr);
+    if ((reinterpret_cast<uintptr_t>(p) & 2u) == 0) {
+        typedef uint32_t u32x4a4_t __attribute__((ext_vector_type(4), aligned(4)));
+        const u32x4a4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4a4_t*>(p));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    }
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p + 2);
+    const uint32_t a = h[0], e = h[7];
+    const uint32_t b = q[0], c = q[1], d = q[2];
+    return make_uint4(a | (b << 16), (b >> 16) | (c << 16), (c >> 16) | (d << 16),
+                      (d >> 16) | (e << 16));
+}
+
+// The weight load of the GEMV lanes: WA = 16 for 16-byte aligned chunks, 2
+// for chunks that are only 2-byte aligned.
+template <int WA>
+__device__ __forceinline__ uint4 load_weights16(const void* p) {
+    if constexpr (WA == 16) return load16_nt(p);
+    else return load16_a2(p);
 }
 
 // A pointer read from LDS (or built from an integer) is generic: the compiler
