@@ -57,6 +57,7 @@ EXPERT_BYTES = 2 * (W_GU + S_GU) + W_D + S_D  # 3,345,408
 ROUTER_BYTES = E * H * 2   # 720,896
 LAYER_BYTES = TOPK * EXPERT_BYTES + ROUTER_BYTES + H * 2 + E * 2 + 3 * H * 2  # 27,506,944
 PREFILL_T = 2048
+SUSTAIN_LAYERS = 10  # prefill layers back to back in the sustained graph
 PREFILL_FLOP = 2 * PREFILL_T * TOPK * 3 * F * H  # 194,884,141,056
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode_layer_kernel launch: rocprofv3 --pmc FETCH_SIZE and
@@ -140,18 +141,25 @@ def run_decode(tsg, torch, ctx, args, layers, routers):
         for l in range(LAYERS):
             layer(k, l)
 
-    # one graph = n_inputs tokens (each a 30-layer pass from its own input)
-    with torch.cuda.stream(stream):
-        for k in range(n_inputs):
-            one_token(k)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for k in range(n_inputs):
-            one_token(k)
-    torch.cuda.synchronize()
+    # one graph = n_inputs tokens (each a 30-layer pass from its own input);
+    # a second graph holds the steps % n_inputs tokens left over, so exactly
+    # `steps` tokens are timed
+    def capture(n_tok):
+        with torch.cuda.stream(stream):
+            for k in range(n_tok):
+                one_token(k)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for k in range(n_tok):
+                one_token(k)
+        torch.cuda.synchronize()
+        return g
+
+    graph = capture(n_inputs)
+    full, rem = divmod(args.steps, n_inputs)
+    graph_rem = capture(rem) if rem else None
     replays_w = max(1, (args.warmup + n_inputs - 1) // n_inputs)
-    replays = max(1, (args.steps + n_inputs - 1) // n_inputs)
     # CUDAGraph.replay() launches on the current stream: make it `stream`, the
     # stream the events are recorded on.
     with torch.cuda.stream(stream):
@@ -162,13 +170,16 @@ def run_decode(tsg, torch, ctx, args, layers, routers):
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
         start.record(stream)
-        for _ in range(replays):
+        for _ in range(full):
             graph.replay()
+        if graph_rem is not None:
+            graph_rem.replay()
         stop.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(stop)
-    tokens = replays * n_inputs
+    tokens = args.steps
+    replays = max(1, full)
     us_per_layer = ms * 1000.0 / (tokens * LAYERS)
     log(f"decode: {tokens} tokens x {LAYERS} layers in {ms:.3f} ms (wall {wall*1e3:.1f} ms): "
         f"{us_per_layer:.3f} us/layer")
@@ -227,14 +238,18 @@ def zipf_routing(t, ne, k, s, seed):
     return idx, w
 
 
-def run_prefill(tsg, torch, ctx, args, layer):
-    return run_prefill_shape(tsg, torch, ctx, args, layer, PREFILL_T, H, F, E, 1.1, "gelu")
+def run_prefill(tsg, torch, ctx, args, layers):
+    return run_prefill_shape(tsg, torch, ctx, args, layers[0], PREFILL_T, H, F, E, 1.1, "gelu",
+                             layers=layers)
 
 
-def run_prefill_shape(tsg, torch, ctx, args, layer, t, h, f, e, zipf_s, act):
+def run_prefill_shape(tsg, torch, ctx, args, layer, t, h, f, e, zipf_s, act, layers=None):
     """One prefill MoE layer of t tokens, top-8 Zipf(zipf_s) routing over e
     experts of shape (h, f): device grouping -> gate/up GEMM + activation ->
-    down GEMM -> token-major reduce."""
+    down GEMM -> token-major reduce. The per-kernel split comes from HIP
+    events around each kernel of single layers; the sustained figures from a
+    HIP graph of SUSTAIN_LAYERS layers back to back (each with its own weights
+    from `layers` when given), replayed: GEMMs alone, and the whole layer."""
     moe = tsg.MoE(ctx, gate_activation=act)
     g = tsg.PrefillGroupedRoutedMoE(moe)
     red = tsg.PrefillMoE(ctx)
@@ -290,14 +305,44 @@ def run_prefill_shape(tsg, torch, ctx, args, layer, t, h, f, e, zipf_s, act):
         torch.cuda.synchronize()
         totals += [ev[i].elapsed_time(ev[i + 1]) for i in range(4)]
     per = totals / reps  # ms
-    total_ms = float(per.sum())
-    gemm_ms = float(per[1] + per[2])
-    log(f"prefill T={t}: group {per[0]*1e3:.1f} us, gate/up {per[1]*1e3:.1f} us, down "
-        f"{per[2]*1e3:.1f} us, reduce {per[3]*1e3:.1f} us")
     nblocks = int(nb.cpu()[0])
+    # outputs of the measured work: every routed row written, finite
+    out_ok = bool(torch.isfinite(h2.view(torch.float16).float()).all()) and \
+        bool(torch.isfinite(partials.view(torch.float16).float()).all())
+    if not out_ok:
+        raise RuntimeError(f"prefill T={t} produced non-finite outputs")
+    # sustained: SUSTAIN_LAYERS layers back to back in one graph
+    lays = [layer] * SUSTAIN_LAYERS if not layers else \
+        [layers[i % len(layers)] for i in range(SUSTAIN_LAYERS)]
+
+    def gemms():
+        for L in lays:
+            g.encode_gate_up(L, hidden, h, sp, blocks, max_blocks, act_buf, h, f,
+                             n_blocks_device=nb, stream=stream)
+            g.encode_down(L, act_buf, sp, blocks, max_blocks, partials, k, h, f,
+                          n_blocks_device=nb, stream=stream)
+
+    def whole():
+        for L in lays:
+            g.group_pairs_device(idx, w, t, k, e, sp, off, cnt, blocks, max_blocks, nb, scratch,
+                                 tile_rows=tile_rows, stream=stream)
+            g.encode_gate_up(L, hidden, h, sp, blocks, max_blocks, act_buf, h, f,
+                             n_blocks_device=nb, stream=stream)
+            g.encode_down(L, act_buf, sp, blocks, max_blocks, partials, k, h, f,
+                          n_blocks_device=nb, stream=stream)
+            red.encode_reduce_token_major(partials, w, h2, t, k, h, stream=stream)
+
+    gemm_ms = time_graph(torch, stream, gemms, reps=2) / SUSTAIN_LAYERS
+    total_ms = time_graph(torch, stream, whole, reps=2) / SUSTAIN_LAYERS
+    if not bool(torch.isfinite(h2.view(torch.float16).float()).all()):
+        raise RuntimeError(f"prefill T={t} produced non-finite outputs")
+    log(f"prefill T={t}: single layers: group {per[0]*1e3:.1f} us, gate/up {per[1]*1e3:.1f} us, "
+        f"down {per[2]*1e3:.1f} us, reduce {per[3]*1e3:.1f} us; sustained over "
+        f"{SUSTAIN_LAYERS} layers: GEMMs {gemm_ms*1e3:.1f} us, layer {total_ms*1e3:.1f} us")
     return dict(us_per_layer=total_ms * 1e3, gemm_us=gemm_ms * 1e3,
                 gate_up_us=float(per[1]) * 1e3, down_us=float(per[2]) * 1e3,
                 group_us=float(per[0]) * 1e3, reduce_us=float(per[3]) * 1e3,
+                burst_gemm_us=float(per[1] + per[2]) * 1e3,
                 gemm_tflops=flop / (gemm_ms * 1e-3) / 1e12,
                 layer_tflops=flop / (total_ms * 1e-3) / 1e12, blocks=nblocks, flop=flop)
 
@@ -487,7 +532,8 @@ def run_qwen(tsg, torch, args):
     us3, u3 = run_rows_path(tsg, torch, ctx, moe, layers, nl, 3, h, f, e, 0x3333, shared=shared)
     bytes3 = u3 * payload + payload
     log(f"qwen decode M=3: {us3:.3f} us/layer over a mean union of {u3:.1f} experts")
-    pre = run_prefill_shape(tsg, torch, ctx, args, layers[0], QW_T, h, f, e, 1.0, "silu")
+    pre = run_prefill_shape(tsg, torch, ctx, args, layers[0], QW_T, h, f, e, 1.0, "silu",
+                            layers=layers)
     return {"workload": "qwen3.5-moe-35b-a3b-shaped layer (configs[4]): H=2048, 256 experts "
                         "I=512 top-8 SwiGLU + shared expert I=512 with sigmoid gate, 40 layers",
             "decode_m1": {"us_per_layer": round(us1, 3),
@@ -634,49 +680,186 @@ def run_verify(tsg, torch, ctx, args, layers):
             "path": "rows path (encodeStreamedRows) + token-major reduce, routing precomputed"}
 
 
+def attainable_gemm(torch):
+    """The attainable dense fp16 GEMM rate on this GPU (torch.matmul ->
+    hipBLASLt, fp16 in, fp32 accumulate): a square 8192^3 GEMM, and the
+    prefill layer's gate/up work as one dense GEMM (16,384 rows x 1,408
+    columns x K 2,816), the second denominator of the prefill fraction."""
+    out = {}
+    for name, (m, n, k) in (("square_8192", (8192, 8192, 8192)),
+                            ("layer_gate_up_dense", (PREFILL_T * TOPK, 2 * F, H))):
+        a = torch.randn(m, k, dtype=torch.float16, device="cuda")
+        b = torch.randn(k, n, dtype=torch.float16, device="cuda")
+        stream = torch.cuda.Stream()
+        c = torch.empty(m, n, dtype=torch.float16, device="cuda")
+
+        def body():
+            for _ in range(10):
+                torch.matmul(a, b, out=c)
+
+        ms = time_graph(torch, stream, body, reps=4) / 10
+        out[name] = {"shape_mnk": [m, n, k], "us": round(ms * 1e3, 2),
+                     "TFLOPs": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1)}
+    log(f"attainable fp16 GEMM (torch.matmul): {out}")
+    return out
+
+
 def prefill_summary(pre):
     return {"us_per_layer": round(pre["us_per_layer"], 2),
-            "gemm_us": round(pre["gemm_us"], 2), "gate_up_us": round(pre["gate_up_us"], 2),
+            "gemm_us": round(pre["gemm_us"], 2),
+            "gemm_measure": f"sustained: {SUSTAIN_LAYERS} layers back to back in a HIP graph, "
+                            f"each with its own weights",
+            "burst_gemm_us": round(pre["burst_gemm_us"], 2),
+            "gate_up_us": round(pre["gate_up_us"], 2),
             "down_us": round(pre["down_us"], 2), "group_us": round(pre["group_us"], 2),
             "reduce_us": round(pre["reduce_us"], 2),
+            "split_measure": "single layers, HIP events around each kernel",
             "gemm_TFLOPs": round(pre["gemm_tflops"], 2),
             "frac_mfma_peak": round(pre["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
             "layer_TFLOPs": round(pre["layer_tflops"], 2),
             "flop_per_layer": pre["flop"], "routed_blocks": pre["blocks"]}
 
 
-def cpu_baseline(torch, dec, bufs, routers, offs, stride, budget_s=12.0):
-    """The reference's CPU path for the same math, restated in C (oracle):
-    routerReference + MoeRef.applyStreamedRouted per layer, on the host cores,
-    over the first layers of the decode chain with their real inputs."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# One GPU's share of the box's host cores: worker pools on the GPU box are
+# sized to it whatever nproc reports.
+CPU_SHARE = 16
+
+
+def cpu_baseline(torch, dec, bufs, routers, offs, stride, budget_s=10.0):
+    """The reference's CPU path for the same math, restated in C (oracle,
+    the timed build: -O3 -march=native for this host, vectorizable dot
+    products like vDSP_dotpr's):
+      decode  routerReference + MoeRef.applyStreamedRouted per layer
+              (main.swift:384-402, Reference/MoE/Moe.swift:16-123) over the
+              decode chain's layers with their real inputs and routing;
+      prefill the expert-major reference of PrefillMoEGEMMCheck.swift:138-173
+              on a sample of config 4's tokens (all 8 of each token's pairs,
+              its experts dequantised once), in TFLOP/s of the GEMM work.
+    Timed on CPU_SHARE threads (one GPU's share of this host) and on one."""
     import oracle
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(threads, 16))
-    oracle.set_threads(threads)
+    path = oracle.use_timed_build()
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(nproc, CPU_SHARE))
     idx = dec["idx"].cpu().numpy().reshape(LAYERS, TOPK)
-    done, elapsed = 0, 0.0
     es = np.ones(H, np.float32)
     pes = np.ones(E, np.float32)
+    layer_in = []
     for l in range(LAYERS):
         x_bits = dec["xs"][l].cpu().numpy().view(np.uint16)
         rw = oracle.bf16_to_float(routers[l].cpu().numpy().view(np.uint16)).reshape(E, H)
-        experts = idx[l]
-        blobs = [bufs[l][int(e) * stride:(int(e) + 1) * stride].cpu().numpy() for e in experts]
-        x = oracle.f16_to_float(x_bits)
+        blobs = [bufs[l][int(e) * stride:(int(e) + 1) * stride].cpu().numpy() for e in idx[l]]
+        layer_in.append((oracle.f16_to_float(x_bits), rw, blobs))
+
+    def decode_us(n_threads, budget):
+        oracle.set_threads(n_threads)
+        done, elapsed = 0, 0.0
+        while elapsed < budget and done < 4 * LAYERS:
+            x, rw, blobs = layer_in[done % LAYERS]
+            t0 = time.perf_counter()
+            _, rwts = oracle.router_reference(rw, x * es, TOPK, pes)
+            oracle.moe_apply_streamed_routed(blobs, np.array(offs, np.uint32), x, x, rwts, H, F,
+                                             GROUP, True)
+            elapsed += time.perf_counter() - t0
+            done += 1
+        return elapsed * 1e6 / done, done
+
+    us_n, n_n = decode_us(threads, budget_s)
+    us_1, n_1 = decode_us(1, budget_s / 2)
+    # prefill: config 4's routing and inputs, every pair of a sample of tokens
+    t_all = PREFILL_T
+    idx_p, w_p = zipf_routing(t_all, E, TOPK, 1.1, 0x21F)
+    image = bufs[0].cpu().numpy()
+    blobs_all = [image[e * stride:(e + 1) * stride] for e in range(E)]
+    hid = np.random.default_rng(0x33).normal(0, 1, t_all * H).astype(np.float32)
+    hid_bits = oracle.f16_bits(hid)
+
+    def prefill_rate(n_threads, tokens):
+        oracle.set_threads(n_threads)
+        sel = np.arange(tokens, dtype=np.int64)
+        pairs = oracle.make_token_expert_pairs(idx_p[sel].astype(np.uint32),
+                                               w_p[sel].view(np.uint16), tokens, TOPK)
+        sp = oracle.group_pairs(pairs, tokens, TOPK, E)["sorted_pairs"]
         t0 = time.perf_counter()
-        ri, rwts = oracle.router_reference(rw, x * es, TOPK, pes)
-        oracle.moe_apply_streamed_routed(blobs, np.array(offs, np.uint32), x, x, rwts, H, F,
-                                         GROUP, True)
-        elapsed += time.perf_counter() - t0
-        done += 1
-        if elapsed > budget_s:
-            break
-    us = elapsed * 1e6 / done
-    return dict(value=round(LAYER_BYTES / (us * 1e-6) / 1e9, 3), unit="GB/s", cores=threads,
+        oracle.prefill_moe_ref(blobs_all, np.array(offs, np.uint32), hid_bits[:tokens * H], H, sp,
+                               TOPK, H, F, GROUP, True)
+        el = time.perf_counter() - t0
+        flop = 2.0 * sp.size * 3 * F * H
+        return flop / el / 1e12, el, sp.size, len(set(sp["expert"].tolist()))
+
+    pre_n = prefill_rate(threads, 64)
+    pre_1 = prefill_rate(1, 8)
+    return dict(value=round(LAYER_BYTES / (us_n * 1e-6) / 1e9, 3), unit="GB/s", cores=threads,
                 kind="port",
-                sample=f"{done} decode layers (router + 8 experts, H=2816 F=704 sym g32) "
-                       f"through the C restatement of routerReference + MoeRef, "
-                       f"{us:.0f} us/layer on {threads} threads")
+                sample=f"{n_n} decode layers (router + 8 experts, H=2816 F=704 sym g32) through "
+                       f"the C restatement of routerReference + MoeRef, {us_n:.0f} us/layer on "
+                       f"{threads} threads ({n_1} layers, {us_1:.0f} us/layer on 1 thread)",
+                us_per_layer=round(us_n, 1), one_thread_us_per_layer=round(us_1, 1),
+                one_thread_value=round(LAYER_BYTES / (us_1 * 1e-6) / 1e9, 3),
+                nproc=nproc, cpu_model=_cpu_model(),
+                build=os.path.basename(path) + " (gcc -O3 -march=native -ffp-contract=off)",
+                prefill={"unit": "TFLOP/s", "value": round(pre_n[0], 5),
+                         "one_thread_value": round(pre_1[0], 5),
+                         "sample": f"config 4, first 64 tokens: {pre_n[2]} pairs over "
+                                   f"{pre_n[3]} experts, {pre_n[1]:.2f} s on {threads} threads; "
+                                   f"first 8 tokens ({pre_1[2]} pairs) {pre_1[1]:.2f} s on 1 "
+                                   f"thread; expert-major with fp16 roundings "
+                                   f"(PrefillMoEGEMMCheck.swift:138-173)"})
+
+
+def run_floors(tsg, torch, layers, reps=8):
+    """Two floors of a one-launch decode layer of this shape (measurement
+    kernels of libtsugumi_floors.so), each as 120 launches back to back in a
+    HIP graph (4 tokens x 30 layers, fresh random expert ids per launch):
+    an empty kernel with the layer's grid, block and LDS (the launch-to-launch
+    period), and a kernel of the same grid that only streams the 8 routed
+    experts' 26,763,264 payload bytes with 16-byte loads (the time to move the
+    expert bytes once the routing is known)."""
+    import ctypes as C
+    lib = C.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "tsugumi_amd",
+                              "libtsugumi_floors.so"))
+    lib.tsg_floor_empty.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p]
+    lib.tsg_floor_stream.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32,
+                                     C.c_uint32, C.c_uint32, C.c_void_p]
+    _, stride = gemma_offsets()
+    sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+    rng = np.random.default_rng(0xF1)
+    ids = [(rng.permutation(E)[:TOPK]).astype(np.uint32) for _ in range(4 * LAYERS)]
+    blocks, threads, lds = 256, 768, 20480
+
+    def empty():
+        for _ in range(4 * LAYERS):
+            if lib.tsg_floor_empty(stream.cuda_stream, blocks, threads, lds, sink.data_ptr()):
+                raise RuntimeError("floor_empty launch failed")
+
+    def stream_all():
+        for i in range(4 * LAYERS):
+            if lib.tsg_floor_stream(stream.cuda_stream, layers[i % LAYERS].device_ptr, stride,
+                                    ids[i].ctypes.data, EXPERT_BYTES, blocks, 1024,
+                                    sink.data_ptr()):
+                raise RuntimeError("floor_stream launch failed")
+
+    us_empty = time_graph(torch, stream, empty, reps=reps) * 1000.0 / (4 * LAYERS)
+    us_stream = time_graph(torch, stream, stream_all, reps=reps) * 1000.0 / (4 * LAYERS)
+    nbytes = TOPK * EXPERT_BYTES
+    log(f"floors: empty launch {us_empty:.3f} us, 8-expert stream {us_stream:.3f} us "
+        f"({nbytes / (us_stream * 1e-6) / 1e9:.1f} GB/s)")
+    return {"empty_launch_us": round(us_empty, 3), "expert_stream_us": round(us_stream, 3),
+            "expert_stream_bytes": nbytes,
+            "expert_stream_GBps": round(nbytes / (us_stream * 1e-6) / 1e9, 1),
+            "grid": f"{blocks} blocks x {threads} threads, {lds} B dynamic LDS (empty); "
+                    f"{blocks} x 1024 (stream)"}
 
 
 COPY_BYTES = 64 << 20
@@ -724,6 +907,8 @@ def main():
                     help="run only the prefill layer (for profiling) and print its figures")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the copy + one-token dispatches for rocprofv3 --pmc and exit")
+    ap.add_argument("--floors", action="store_true",
+                    help="time the decode layer's floors (empty launch, expert stream) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -740,13 +925,16 @@ def main():
     if args.traffic_probe:
         traffic_probe(tsg, torch, ctx, layers, routers)
         return
+    if args.floors:
+        print(json.dumps({"floors": run_floors(tsg, torch, layers)}), flush=True)
+        return
     if args.prefill_only:
-        pre = run_prefill(tsg, torch, ctx, args, layers[0])
+        pre = run_prefill(tsg, torch, ctx, args, layers)
         print(json.dumps({"prefill_gemm_us": round(pre["gemm_us"], 2),
                           "gemm_TFLOPs": round(pre["gemm_tflops"], 2)}), flush=True)
         return
     dec = run_decode(tsg, torch, ctx, args, layers, routers)
-    pre = None if args.no_prefill else run_prefill(tsg, torch, ctx, args, layers[0])
+    pre = None if args.no_prefill else run_prefill(tsg, torch, ctx, args, layers)
     gbs = LAYER_BYTES / (dec["us_per_layer"] * 1e-6) / 1e9
     k_gbs = LAYER_BYTES / (dec["kernel_us"] * 1e-6) / 1e9
     out = {
@@ -782,6 +970,17 @@ def main():
     }
     if pre is not None:
         out["prefill"] = prefill_summary(pre)
+        try:
+            att = attainable_gemm(torch)
+            out["prefill"]["attainable_fp16_gemm"] = att
+            out["prefill"]["frac_attainable_square"] = round(
+                pre["gemm_tflops"] / att["square_8192"]["TFLOPs"], 4)
+        except Exception as exc:  # noqa: BLE001 - reported, not hidden
+            log(f"attainable GEMM failed: {exc}")
+    try:
+        out["decode"]["floors"] = run_floors(tsg, torch, layers)
+    except Exception as exc:  # noqa: BLE001 - reported, not hidden
+        log(f"floors failed: {exc}")
     if not args.no_extra_configs:
         # the other BASELINE configs, after the headline figures (a failure here
         # is reported in its entry and does not void the headline)

@@ -59,6 +59,19 @@ def lib():
     return _lib
 
 
+def use_timed_build() -> str:
+    """Switches this process to liboracle_timed.so (`make timed`: -O3
+    -march=native for the CPU it runs on, dot products in eight interleaved
+    partial sums), the copy bench.py times as the CPU baseline. It is never
+    used as a checker. Returns its path."""
+    global _lib
+    subprocess.run(["make", "-s", "-C", _HERE, "timed"], check=True)
+    path = os.path.join(_HERE, "liboracle_timed.so")
+    _lib = C.CDLL(path)
+    _declare(_lib)
+    return path
+
+
 _u8p = C.POINTER(C.c_uint8)
 _u16p = C.POINTER(C.c_uint16)
 _u32p = C.POINTER(C.c_uint32)

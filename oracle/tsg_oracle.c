@@ -289,14 +289,26 @@ void tsgo_dequantize_int4_f16(const uint8_t* packed, const uint16_t* scales,
 /* ------------------------------------------------------------------------ */
 
 /* vDSP_dotpr's internal order is unspecified (Accelerate is closed); this
- * restatement sums left to right in fp32. */
+ * restatement sums left to right in fp32. The timed build (TSGO_TIMED_DOT,
+ * the CPU baseline only, never a checker) keeps eight interleaved partial
+ * sums added pairwise at the end, an order a compiler can vectorize the way
+ * vDSP is vectorized. */
 static inline float dot_f32(const float* a, const float* b, int n) {
+#ifdef TSGO_TIMED_DOT
+    float part[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    int i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int k = 0; k < 8; ++k) part[k] = part[k] + a[i + k] * b[i + k];
+    for (; i < n; ++i) part[i & 7] = part[i & 7] + a[i] * b[i];
+    return ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+#else
     float acc = 0.0f;
     for (int i = 0; i < n; ++i) {
         const float p = a[i] * b[i];
         acc = acc + p;
     }
     return acc;
+#endif
 }
 
 void tsgo_dequant_int4_gemv_ref(const uint8_t* packed, const uint16_t* scales,

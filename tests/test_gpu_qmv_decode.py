@@ -88,7 +88,7 @@ def test_qmv_weights_at_2_aligned_offset(tsg, ctx, offset, group, scheme):
     c = kc.int4_gemv_case(m, n, group, 0xC4, sym)
     q = tsg.DequantInt4GEMV(ctx)
     S, B, X = dev(c["scales"]), dev(c["scales"] if sym else c["biases"]), dev(c["x_bits"])
-    W = dev(c["packed"])
+    W = dev(c["packed"]).reshape(-1)
     # the same bytes at byte `offset` of a 16-byte aligned allocation, with
     # nothing past their end: the first and last chunks touch the buffer's ends
     raw = torch.zeros(offset + c["packed"].size, dtype=torch.uint8, device="cuda")
@@ -218,6 +218,83 @@ def test_router_rows_bit_identical_to_single(tsg, ctx):
     assert e.value.status == 4  # declined, like the reference's `false`
 
 
+def _tie_router(kind):
+    """Router rows for the tie cases at the reference's shape (16 experts,
+    D = 128; RouterTopKTests.swift:46-68): row e = pattern * gain_e in bf16,
+    hidden uniform(0.5, 1.5), effective and per-expert scales 1.
+    'exact': the reference's gains 0.5 and 0.5 * (1 + 1e-4) for experts 7
+    and 8, their bf16 rows made identical (the two gains' rows round to bf16
+    differently in a few places), so 7 and 8 tie exactly and the lower index
+    wins.
+    'near': expert 8 = expert 7 with one element one bf16 ulp larger, where
+    hidden is smallest: the logits differ by about 1e-5 relative.
+    'all': every row identical, so the top 8 are experts 0..7."""
+    ne, d = 16, 128
+    rng = oracle.SplitMix64(0x71E0F4A)
+    pattern = rng.uniforms(0.2, 1.0, d)
+    hidden = rng.uniforms_f16(0.5, 1.5, d)
+    gains = np.zeros(ne, np.float32)
+    for e in range(7):
+        gains[e] = 1.0 - e * 0.05
+    gains[7] = 0.5
+    gains[8] = 0.5 * (1.0 + 1e-4)
+    for e in range(9, ne):
+        gains[e] = 0.4 - (e - 9) * 0.02
+    if kind == "all":
+        gains[:] = 0.7
+    w = oracle.bf16_bits((pattern[None, :] * gains[:, None]).astype(np.float32))
+    if kind in ("exact", "near"):
+        w[8] = w[7]  # bf16 rounding of the two gains' rows can differ in places
+    if kind == "near":
+        w[8, int(np.argmin(oracle.f16_to_float(hidden)))] += 1
+    return w.ravel(), hidden, ne, d
+
+
+@pytest.mark.parametrize("kind", ["exact", "near", "all"])
+def test_router_ties_on_gpu(tsg, ctx, kind):
+    """Exact and near ties in bf16 router logits (RouterTopKTests.swift:46-68,
+    the bf16 form of its int8 case): the router kernel and the one-launch
+    decode layer's top-8 both select what the kernel rule (descending, ties
+    to the lower index) gives on the canonical-order logits, and on an exact
+    tie that is the lower expert. Reported: the fp64 8th/9th margin."""
+    configure(ctx, 32, "sym")
+    w_bits, hidden, ne, d = _tie_router(kind)
+    es = oracle.bf16_bits(np.ones(d, np.float32))
+    pes = oracle.bf16_bits(np.ones(ne, np.float32))
+    canon = oracle.router_logits_canonical(w_bits, hidden, d, es, 1, ne, d)
+    ci, cw = oracle.topk_softmax(canon[0], 8, np.ones(ne, np.float32))
+    if kind == "exact":
+        assert canon[0][7] == canon[0][8]
+        assert list(ci) == list(range(8))
+    if kind == "all":
+        assert list(ci) == list(range(8))
+    l64 = oracle.bf16_to_float(w_bits).reshape(ne, d).astype(np.float64) @ \
+        oracle.f16_to_float(hidden).astype(np.float64)
+    srt = np.sort(l64)[::-1]
+    print(f"router tie '{kind}': fp64 8th/9th margin {srt[7] - srt[8]:.3e}, selected {list(ci)}")
+    moe = tsg.MoE(ctx)
+    W, X, ES, PES = dev(w_bits), dev(hidden), dev(es), dev(pes)
+    idx, wts = empty(8, np.uint32), empty(8)
+    moe.encode_router_gemma4_bf16(W, X, ES, PES, idx, wts, ne, d)
+    assert list(host(idx, np.uint32)) == list(ci)
+    # the one-launch layer's own top-8 (random experts of d = 128, f = 64)
+    f = 64
+    rng = oracle.SplitMix64(0x7E)
+    parts = [[oracle.quantize_int4(rng.uniforms(-0.3, 0.3, r * c_).reshape(r, c_), 32, True)
+              for (r, c_) in ((f, d), (f, d), (d, f))] for _ in range(ne)]
+    image, stride, offs, _ = kc.layer_image(parts, True, keep_biases=False)
+    layer = tsg.ResidentLayer(ctx, ne, stride, offs)
+    layer.upload(image)
+    for fused in (True, False):
+        moe.set_fused_decode(fused)
+        y, li, lw, acts = empty(d), empty(8, np.uint32), empty(8), empty(8 * f)
+        moe.encode_decode_layer(layer, W, X, ES, PES, X, X, y, li, lw, acts, ne, d, f)
+        ctx.synchronize()
+        assert list(host(li, np.uint32)) == list(ci), f"fused={fused}"
+        assert np.array_equal(host(lw, np.uint16), host(wts, np.uint16))
+    moe.set_fused_decode(True)
+
+
 def _routed_blobs(case):
     return [dev(b) for b in case["blobs"]]
 
@@ -313,6 +390,41 @@ def make_gemma_layer(tsg, ctx, seed, ne=128, d=2816, f=704):
     return layer, buf, offs, stride
 
 
+def test_fresh_context_ignores_earlier_contexts_handoff_words(tsg):
+    """A context's first one-launch layers must not take hand-off words left in
+    recycled device memory by an earlier context (their tags repeat: every
+    context's epoch starts at 0). Contexts are made and dropped in turn, each
+    running the fused layer on different inputs, and every launch must equal
+    the three-launch form bit for bit."""
+    import torch
+    d, f, ne = 1024, 512, 64
+    outs = []
+    for round_ in range(3):
+        c = tsg.Context(0, group_size=32, scheme="sym")
+        layer, _, _, _ = make_gemma_layer(tsg, c, 0x5EED, ne=ne, d=d, f=f)
+        rw = torch.empty(ne * d, dtype=torch.int16, device="cuda")
+        tsg.generators.bf16_normal(rw, 0xB00 + round_, 1.0 / np.sqrt(d))
+        ones_d = dev(np.full(d, 0x3F80, np.uint16))
+        ones_e = dev(np.full(ne, 0x3F80, np.uint16))
+        for k in range(3):
+            x = torch.empty(d, dtype=torch.int16, device="cuda")
+            tsg.generators.f16_normal(x, 0xC00 + 16 * round_ + k, 1.0)
+            ys = []
+            for fused in (True, False):
+                moe = tsg.MoE(c)
+                moe.set_fused_decode(fused)
+                y, idx, wts, acts = empty(d), empty(8, np.uint32), empty(8), empty(8 * f)
+                moe.encode_decode_layer(layer, rw, x, ones_d, ones_e, x, x, y, idx, wts, acts, ne,
+                                        d, f)
+                c.synchronize()
+                ys.append(host(y, np.uint16))
+            assert np.array_equal(ys[0], ys[1]), f"context {round_}, launch {k}"
+            outs.append(ys[0])
+        layer.close()
+        c.close()
+    assert len({o.tobytes() for o in outs}) == len(outs)
+
+
 def test_resident_decode_layer_gemma_shape(tsg, ctx):
     """One Gemma-4-26B-A4B-shaped decode MoE layer (config 2): router over
     128 bf16 rows -> top-8 -> gate/up + GeGLU -> down + combine, all device
@@ -332,6 +444,7 @@ def test_resident_decode_layer_gemma_shape(tsg, ctx):
     moe = tsg.MoE(ctx)
     y, idx, wts, acts = empty(d), empty(8, np.uint32), empty(8), empty(8 * f)
     moe.encode_decode_layer(layer, rw, x, ones_d, ones_e, x, x, y, idx, wts, acts, ne, d, f)
+    ctx.synchronize()  # reports a one-launch hand-off timeout
     gi, gw = host(idx, np.uint32), host(wts, np.uint16)
     xb, rwb = host(x, np.uint16), host(rw, np.uint16)
     canon = oracle.router_logits_canonical(rwb, xb, d, np.full(d, 0x3F80, np.uint16), 1, ne, d)

@@ -2,6 +2,8 @@
 
 Each source compiles to an object in tsugumi_amd/_build/ (in parallel), then
 one link. `python -m tsugumi_amd.build` or tsugumi_amd.build.build().
+libtsugumi_floors.so (csrc/floors.hip) holds the measurement kernels of
+`bench.py --floors`; it is not part of the drop-in library.
 """
 from __future__ import annotations
 
@@ -15,9 +17,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libtsugumi_hip.so")
+FLOORS_LIB = os.path.join(HERE, "libtsugumi_floors.so")
 SOURCES = ["core.hip", "decode.hip", "qmv.hip", "shared.hip", "prefill.hip", "tail.hip",
            "host_routing.cpp",
            "moepack.cpp"]
+FLOORS_SOURCES = ["floors.hip"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ROCM = os.environ.get("ROCM_PATH", os.path.dirname(os.path.dirname(os.path.realpath(HIPCC))))
@@ -44,18 +48,24 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
+def _link(objs, lib: str) -> None:
+    tmp = lib + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = SOURCES + FLOORS_SOURCES
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = dict(zip(srcs, ex.map(_compile, srcs)))
+    _link([objs[s] for s in SOURCES], LIB)
+    _link([objs[s] for s in FLOORS_SOURCES], FLOORS_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {FLOORS_LIB}")
     return LIB
 
 

@@ -91,6 +91,12 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
     if (e == hipSuccess)
         e = hipMalloc(&ctx->act_replicas, sizeof(uint16_t) * kActReplicas * kActReplicaHalves);
     if (e == hipSuccess) e = hipMemset(ctx->counters, 0, sizeof(uint32_t) * kMaxCounters);
+    // The one-launch decode layer's hand-off words carry the launch's tag
+    // (epoch + 1, never 0) and the epoch starts at 0 here: words left by an
+    // earlier context in recycled memory would carry tags this context will
+    // issue again, so the regions start at tag 0.
+    if (e == hipSuccess)
+        e = hipMemset(ctx->act_replicas, 0, sizeof(uint16_t) * kActReplicas * kActReplicaHalves);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         (void)hipFree(ctx->counters);

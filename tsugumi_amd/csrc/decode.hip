@@ -397,10 +397,7 @@ __device__ __forceinline__ bool phase1_compute(const GULane& l, ChunkBatch<kGUBa
     const bool is_up = (threadIdx.x >> 4) & 1u;
     const uint32_t nchunks = d / 32u;
     float acc[1] = {0.0f};
-    for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
-        if (base) load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, base, j, nchunks, bt);
-        compute_batch<G, SYM, kGUBatch, kGULanes, 1>(bt, base, j, nchunks, xs, 0u, xsum, 1u, acc);
-    }
+    gemv_batches<G, SYM, kGUBatch, kGULanes, 1>(l.w, l.s, l.b, j, nchunks, bt, xs, 0u, xsum, 1u, acc);
     acc[0] = group16_sum(acc[0]);
     const float up = shfl_xor(acc[0], 16);  // gate lanes receive the up sum
     out = f32_to_f16(gate_activation<ACT>(acc[0]) * up);
@@ -427,11 +424,9 @@ __device__ __forceinline__ void phase2_body(const Src& src, const tsg_expert_off
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + o.down_s) + (uint64_t)rr * ngroups;
     const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + o.down_b) + (uint64_t)rr * ngroups;
     float acc[1] = {0.0f};
-    for (uint32_t base = 0; base < nchunks; base += kDLanes * kDBatch) {
-        if (base || !preloaded) load_batch<G, SYM, kDBatch, kDLanes>(w, sc, bi, base, j, nchunks, bt);
-        compute_batch<G, SYM, kDBatch, kDLanes, 1>(bt, base, j, nchunks, as + slot * slot_h, 0u,
-                                                   asum + slot * nchunks, 1u, acc);
-    }
+    if (!preloaded) load_batch<G, SYM, kDBatch, kDLanes>(w, sc, bi, 0u, j, nchunks, bt);
+    gemv_batches<G, SYM, kDBatch, kDLanes, 1>(w, sc, bi, j, nchunks, bt, as + slot * slot_h, 0u,
+                                              asum + slot * nchunks, 1u, acc);
     acc[0] = group8_sum(acc[0]);
     float vals[kTopK];
 #pragma unroll
@@ -618,7 +613,7 @@ struct DecodeLayerArgs {
     uint64_t* handoff;    // kDecodeGroups regions of kHandoffWords tagged words
     uint32_t* sync_words;
     uint32_t ne, d, f;
-    uint32_t router_rows;  // expert rows per block: ceil(ne / kGroupMembers)
+    uint32_t router_rows;  // expert rows per block: ceil(ne / kDecodeBlocks), one per wave
     uint32_t pairs;        // gate/up pairs per block: ceil(f / kGroupMembers)
     uint32_t rows;         // down rows per block: ceil(d / kGroupMembers)
     uint32_t as_off;       // dynamic LDS: staged activation row (after x)
@@ -643,10 +638,7 @@ __device__ __forceinline__ float slot_down_row(const uint8_t* w, const uint16_t*
                                                ChunkBatch<kDBatch>& bt) {
     const uint32_t j = threadIdx.x & 7u, nchunks = f / 32u;
     float acc[1] = {0.0f};
-    for (uint32_t base = 0; base < nchunks; base += kDLanes * kDBatch) {
-        if (base) load_batch<G, SYM, kDBatch, kDLanes>(w, sc, bi, base, j, nchunks, bt);
-        compute_batch<G, SYM, kDBatch, kDLanes, 1>(bt, base, j, nchunks, as, 0u, asum, 1u, acc);
-    }
+    gemv_batches<G, SYM, kDBatch, kDLanes, 1>(w, sc, bi, j, nchunks, bt, as, 0u, asum, 1u, acc);
     return group8_sum(acc[0]);
 }
 
@@ -850,19 +842,33 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     uint16_t* as = reinterpret_cast<uint16_t*>(smem + a.as_off);
     float* asum = reinterpret_cast<float*>(smem + a.as_off + p2_slot_halves(f) * 2u);
     float* xe = reinterpret_cast<float*>(smem + a.xe_off);
+    // expert row e's logit is computed once, by block e % kDecodeBlocks
+    // (wave e / kDecodeBlocks), and posted to all kDecodeGroups regions; each
+    // group polls its own copy, so 32 blocks, not 256, read each word
     uint64_t* logits = sy.logits + grp * kMaxExperts;
     uint64_t* gacts = handoff + (size_t)grp * kHandoffWords;
     const uint32_t nwaves = blockDim.x >> 6;
     const bool sh_wave = SH && wave == nwaves - 1u;
     const uint32_t share = (a.rows + kDecodeGroups - 1u) / kDecodeGroups;  // combine rows
 
-    // Every load of the first phase goes out before any is waited for: the
-    // epoch, the per-expert gains, x for the gate/up dot products, x and es
-    // for the router products, and this wave's router row.
+    // Every load of the first phase goes out before any is waited for: this
+    // wave's router row first (the routing waits on it), the epoch, the
+    // per-expert gains, x for the gate/up dot products, and x and es for the
+    // router products.
+    const uint32_t units = d / 8u;  // units <= 2 * blockDim (host-checked)
+    const uint32_t er = blockIdx.x + kDecodeBlocks * wave;
+    const bool router_wave = wave < a.router_rows && er < ne;
+    const bool router_block = blockIdx.x < ne;  // holds at least one router row
+    uint4 rw[kRouterChunks];
+    if (router_wave) {
+        const uint16_t* w_row = global_ptr(a.router_w) + (uint64_t)er * d;
+#pragma unroll
+        for (int i = 0; i < kRouterChunks; ++i)
+            rw[i] = *reinterpret_cast<const uint4*>(w_row + min(lane + 64u * i, units - 1u) * 8u);
+    }
     uint32_t epoch = 0;
     if (t == 0) epoch = ld_coherent(sy.epoch);
     const uint32_t gain = t < ne ? global_ptr(a.pes)[t] : 0u;
-    const uint32_t units = d / 8u;  // units <= 2 * blockDim (host-checked)
     const bool two = units > blockDim.x;
     const uint16_t* xg = global_ptr(a.x);
     const uint16_t* hg = global_ptr(a.router_hidden);
@@ -873,17 +879,10 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
         if (i == 1 && !two) break;
         const uint32_t q = min(t + i * blockDim.x, units - 1u) * 8u;
         xv[i] = *reinterpret_cast<const uint4*>(xg + q);
-        hv[i] = *reinterpret_cast<const uint4*>(hg + q);
-        ev[i] = *reinterpret_cast<const uint4*>(eg + q);
-    }
-    const uint32_t er = mem * a.router_rows + wave;
-    const bool router_wave = wave < a.router_rows && er < ne;
-    uint4 rw[kRouterChunks];
-    if (router_wave) {
-        const uint16_t* w_row = global_ptr(a.router_w) + (uint64_t)er * d;
-#pragma unroll
-        for (int i = 0; i < kRouterChunks; ++i)
-            rw[i] = *reinterpret_cast<const uint4*>(w_row + min(lane + 64u * i, units - 1u) * 8u);
+        if (router_block) {
+            hv[i] = *reinterpret_cast<const uint4*>(hg + q);
+            ev[i] = *reinterpret_cast<const uint4*>(eg + q);
+        }
     }
     if (t < kMaxExperts) s_gains[t] = gain;
 #pragma unroll
@@ -891,6 +890,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
         const uint32_t q = t + i * blockDim.x;
         if (q >= units) break;
         *reinterpret_cast<uint4*>(xs + (q >> 2) * kChunkLds + (q & 3u) * 8u) = pair_permute(xv[i]);
+        if (!router_block) continue;
         const uint32_t hw[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w};
         const uint32_t ew[4] = {ev[i].x, ev[i].y, ev[i].z, ev[i].w};
         float p[8];
@@ -910,7 +910,8 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     const uint32_t tag = s_tag;
     if (router_wave) {
         const float s = router_dot_staged(rw, xe, units, lane);
-        if (lane == 0) st_coherent(logits + er, tagged(tag, __float_as_uint(s)));
+        if (lane < kDecodeGroups)
+            st_coherent(sy.logits + lane * kMaxExperts + er, tagged(tag, __float_as_uint(s)));
     }
     if constexpr (!SYM) staged_chunk_sums(xs, 0u, 1u, d, xsum);
     // SH: this block's two shared gate/up pairs (lanes 0..31 pair 2b, 32..63
@@ -957,31 +958,47 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     const bool pair_live = pl < a.pairs && fr < f;
     const LdsBlobs src{layer_base, a.expert_stride, s_idx};
     const bool gu_wave = 2u * wave < a.pairs;
-    ChunkBatch<kGUBatch> gbt;
-    GULane l{};
+    uint16_t s_wout = 0;  // wave 0: lane r's slot weight
+    // this block's down rows (8 per wave), requested once the wave's gate/up
+    // work is done: issued with the gate/up rows they share the memory
+    // system with the gate/up stream and with the activation hand-off's
+    // polls, and measured slower (the hand-off, not the down stream, is on
+    // the critical path)
+    const uint8_t* blob = layer_base + (uint64_t)s_idx[grp] * a.expert_stride;
+    const uint32_t rl = 8u * wave + (lane >> 3);
+    const uint32_t row = mem * a.rows + rl;
+    const bool row_live = rl < a.rows && row < d;
+    const bool down_wave = 8u * wave < a.rows;
+    const uint32_t rr = row_live ? row : 0u;
+    const uint32_t fgroups = f / G;
+    const uint8_t* dw = blob + a.o.down_w + (uint64_t)rr * (f / 2u);
+    const uint16_t* dsc = reinterpret_cast<const uint16_t*>(blob + a.o.down_s) + (uint64_t)rr * fgroups;
+    const uint16_t* dbi = reinterpret_cast<const uint16_t*>(blob + a.o.down_b) + (uint64_t)rr * fgroups;
+    ChunkBatch<kDBatch> dbt;
+    // Loads, the slot weights and the dot products in one straight-line
+    // region per wave (wave 0 is always a gate/up wave: pairs >= 1), so the
+    // waits before each chunk's dot product count only the loads after it.
     if (gu_wave) {
-        l = gu_lane(src, a.o, d, G, pair_live ? grp : 0u, pair_live ? fr : 0u, pair_live);
+        ChunkBatch<kGUBatch> gbt;
+        const GULane l = gu_lane(src, a.o, d, G, pair_live ? grp : 0u, pair_live ? fr : 0u, pair_live);
         load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, 0u, t & 15u, d / 32u, gbt);
-    }
-    // the slot weights (needed only by the combine) while the loads fly
-    if (wave == 0) {
-        const uint32_t r = lane & (kTopK - 1u);
-        const uint32_t id = s_idx[r];
-        const float my_s = s_fill[r] ? order_key_value(s_skey[r]) : -INFINITY;
-        const uint16_t w = slot_softmax_lane(my_s, bf16_to_f32((uint16_t)s_gains[id]));
-        if (lane < kTopK) {
-            s_w[lane] = w;
-            if (blockIdx.x == 0) {
-                global_ptr(a.out_idx)[lane] = id;
-                global_ptr(a.out_w)[lane] = w;
-            }
+        // the slot weights (needed only by the combine) while the loads fly
+        if (wave == 0) {
+            const uint32_t r = lane & (kTopK - 1u);
+            const uint32_t id = s_idx[r];
+            const float my_s = s_fill[r] ? order_key_value(s_skey[r]) : -INFINITY;
+            const uint16_t w = slot_softmax_lane(my_s, bf16_to_f32((uint16_t)s_gains[id]));
+            if (lane < kTopK) s_w[lane] = w;
+            s_wout = w;
         }
-    }
-    if (gu_wave) {
         uint16_t act;
         if (phase1_compute<G, SYM, ACT>(l, gbt, xs, xsum, d, act)) {
             global_ptr(a.acts)[grp * f + fr] = act;
             st_coherent(gacts + fr, tagged(tag, act));
+        }
+        if (wave == 0 && blockIdx.x == 0 && lane < kTopK) {
+            global_ptr(a.out_idx)[lane] = s_idx[lane];
+            global_ptr(a.out_w)[lane] = s_wout;
         }
     }
     uint64_t* shacts = handoff + (size_t)kDecodeGroups * kHandoffWords;
@@ -991,10 +1008,8 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
             // act = half(silu(half(gate . x)) * half(up . x)) (shared_gate_up_kernel)
             const uint32_t j = lane & 15u, nck = d / 32u;
             float acc[1] = {0.0f};
-            for (uint32_t base = 0; base < nck; base += kGULanes * kGUBatch) {
-                if (base) load_batch<G, SYM, kGUBatch, kGULanes>(sl.w, sl.s, sl.b, base, j, nck, sbt);
-                compute_batch<G, SYM, kGUBatch, kGULanes, 1>(sbt, base, j, nck, xs, 0u, xsum, 1u, acc);
-            }
+            gemv_batches<G, SYM, kGUBatch, kGULanes, 1>(sl.w, sl.s, sl.b, j, nck, sbt, xs, 0u, xsum, 1u,
+                                                        acc);
             const float g = group16_sum(acc[0]);
             const float u = shfl_xor(g, 16);
             if (sl.live && ((lane >> 4) & 1u) == 0 && j == 0) {
@@ -1021,18 +1036,6 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
         }
     }
 
-    // this block's down rows (8 per wave) stream while the group finishes
-    const uint8_t* blob = layer_base + (uint64_t)s_idx[grp] * a.expert_stride;
-    const uint32_t rl = 8u * wave + (lane >> 3);
-    const uint32_t row = mem * a.rows + rl;
-    const bool row_live = rl < a.rows && row < d;
-    const bool down_wave = 8u * wave < a.rows;
-    const uint32_t rr = row_live ? row : 0u;
-    const uint32_t fgroups = f / G;
-    const uint8_t* dw = blob + a.o.down_w + (uint64_t)rr * (f / 2u);
-    const uint16_t* dsc = reinterpret_cast<const uint16_t*>(blob + a.o.down_s) + (uint64_t)rr * fgroups;
-    const uint16_t* dbi = reinterpret_cast<const uint16_t*>(blob + a.o.down_b) + (uint64_t)rr * fgroups;
-    ChunkBatch<kDBatch> dbt;
     if (down_wave) load_batch<G, SYM, kDBatch, kDLanes>(dw, dsc, dbi, 0u, lane & 7u, f / 32u, dbt);
 
     // once this block's gate/up work is out, the last wave reads the slot's
@@ -1514,7 +1517,7 @@ tsg_status decode_layer_impl(tsg_moe* moe, tsg_stream stream, const tsg_layer* l
     a.ne = ne;
     a.d = d;
     a.f = f;
-    a.router_rows = (ne + kGroupMembers - 1u) / kGroupMembers;
+    a.router_rows = (ne + kDecodeBlocks - 1u) / kDecodeBlocks;
     a.pairs = (f + kGroupMembers - 1u) / kGroupMembers;
     a.rows = (d + kGroupMembers - 1u) / kGroupMembers;
     if (sh) {

@@ -36,12 +36,20 @@ __device__ __forceinline__ void load_batch(const uint8_t* __restrict__ w_row,
                                            const uint16_t* __restrict__ s_row,
                                            const uint16_t* __restrict__ b_row, uint32_t base,
                                            uint32_t j, uint32_t nchunks, ChunkBatch<KB>& bt) {
+    // scales (and biases) first, then the chunks in the order compute_batch
+    // uses them: loads return in issue order, so chunk i is usable once the
+    // loads after it are the only ones outstanding, and the dot products of
+    // early chunks run while later chunks are still in flight
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+        const uint32_t cc = min(base + j + LANES * i, nchunks - 1u);
+        bt.s[i] = s_row[cc * 32u / G];
+        if constexpr (!SYM) bt.b[i] = b_row[cc * 32u / G];
+    }
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
         const uint32_t cc = min(base + j + LANES * i, nchunks - 1u);
         bt.w[i] = load_weights16<WA>(w_row + 16u * cc);
-        bt.s[i] = s_row[cc * 32u / G];
-        if constexpr (!SYM) bt.b[i] = b_row[cc * 32u / G];
     }
 }
 
@@ -71,6 +79,25 @@ __device__ __forceinline__ void compute_batch(const ChunkBatch<KB>& bt, uint32_t
             if constexpr (!SYM) v = __builtin_fmaf(b, xsum[r * nchunks + cc], v);
             acc[r] = live ? v : acc[r];  // a chunk past the row end leaves acc as it is
         }
+    }
+}
+
+// A whole row segment: the first batch, already requested into `bt` by the
+// caller with load_batch (so its loads can go out early), then the rest
+// batch by batch. The first batch sits outside the loop so the compiler's
+// waits before its chunks count only the loads issued after each (inside a
+// loop they are merged with the back edge's and wait for every load).
+template <int G, bool SYM, int KB, int LANES, int R, int WA = 16>
+__device__ __forceinline__ void gemv_batches(const uint8_t* __restrict__ w_row,
+                                             const uint16_t* __restrict__ s_row,
+                                             const uint16_t* __restrict__ b_row, uint32_t j,
+                                             uint32_t nchunks, ChunkBatch<KB>& bt,
+                                             const uint16_t* xs, uint32_t row_h,
+                                             const float* xsum, uint32_t nrows, float* acc) {
+    compute_batch<G, SYM, KB, LANES, R>(bt, 0u, j, nchunks, xs, row_h, xsum, nrows, acc);
+    for (uint32_t base = LANES * KB; base < nchunks; base += LANES * KB) {
+        load_batch<G, SYM, KB, LANES, WA>(w_row, s_row, b_row, base, j, nchunks, bt);
+        compute_batch<G, SYM, KB, LANES, R>(bt, base, j, nchunks, xs, row_h, xsum, nrows, acc);
     }
 }
 

@@ -969,11 +969,8 @@ __global__ __launch_bounds__(kRowsThreads) void rows_gate_up_kernel(GemmArgs arg
     float acc[kRowsMax];
 #pragma unroll
     for (uint32_t r = 0; r < kRowsMax; ++r) acc[r] = 0.0f;
-    for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
-        if (base) load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, base, j, nchunks, bt);
-        compute_batch<G, SYM, kGUBatch, kGULanes, kRowsMax>(bt, base, j, nchunks, xs, row_h, xsum,
-                                                            rows, acc);
-    }
+    gemv_batches<G, SYM, kGUBatch, kGULanes, kRowsMax>(w, sc, bi, j, nchunks, bt, xs, row_h, xsum,
+                                                       rows, acc);
 #pragma unroll
     for (uint32_t r = 0; r < kRowsMax; ++r) {
         acc[r] = group16_sum(acc[r]);
@@ -1020,11 +1017,8 @@ __global__ __launch_bounds__(kRowsThreads) void rows_down_kernel(GemmArgs args, 
     float acc[kRowsMax];
 #pragma unroll
     for (uint32_t r = 0; r < kRowsMax; ++r) acc[r] = 0.0f;
-    for (uint32_t base = 0; base < nchunks; base += kDLanes * kDBatch) {
-        if (base) load_batch<G, SYM, kDBatch, kDLanes>(w, sc, bi, base, j, nchunks, bt);
-        compute_batch<G, SYM, kDBatch, kDLanes, kRowsMax>(bt, base, j, nchunks, as, row_h, asum,
-                                                          rows, acc);
-    }
+    gemv_batches<G, SYM, kDBatch, kDLanes, kRowsMax>(w, sc, bi, j, nchunks, bt, as, row_h, asum, rows,
+                                                     acc);
 #pragma unroll
     for (uint32_t r = 0; r < kRowsMax; ++r) {
         acc[r] = group8_sum(acc[r]);

@@ -44,10 +44,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint8_t* __restrict__ w,
     float acc[T];
 #pragma unroll
     for (int r = 0; r < T; ++r) acc[r] = 0.0f;
-    for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
-        if (base) load_batch<G, SYM, kGUBatch, kGULanes, WA>(wr, sr, br, base, j, nchunks, bt);
-        compute_batch<G, SYM, kGUBatch, kGULanes, T>(bt, base, j, nchunks, xs, row_h, xsum, t, acc);
-    }
+    gemv_batches<G, SYM, kGUBatch, kGULanes, T, WA>(wr, sr, br, j, nchunks, bt, xs, row_h, xsum, t, acc);
 #pragma unroll
     for (int r = 0; r < T; ++r) {
         acc[r] = group16_sum(acc[r]);

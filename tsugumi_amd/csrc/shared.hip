@@ -96,10 +96,7 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(const uint8_t* __re
     stage_act_rows<SYM>(x, 0u, 1u, d, xs, 0u, xsum);
     __syncthreads();
     float acc[1] = {0.0f};
-    for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
-        if (base) load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, base, j, nchunks, bt);
-        compute_batch<G, SYM, kGUBatch, kGULanes, 1>(bt, base, j, nchunks, xs, 0u, xsum, 1u, acc);
-    }
+    gemv_batches<G, SYM, kGUBatch, kGULanes, 1>(w, sc, bi, j, nchunks, bt, xs, 0u, xsum, 1u, acc);
     const float s = group16_sum(acc[0]);
     const float u = shfl_xor(s, 16);  // gate lanes receive the up sum
     if (live && !is_up && j == 0) act[p] = silu_mul_h(f32_to_f16(s), f32_to_f16(u));
@@ -130,10 +127,7 @@ __global__ __launch_bounds__(kGateThreads) void shared_down_kernel(
     stage_act_rows<SYM>(act, 0u, 1u, f, as, 0u, asum);
     const float scale = qwen_sigmoid(gate_logit_block(x, gate_w, d, red));  // synchronises
     float acc[1] = {0.0f};
-    for (uint32_t base = 0; base < nchunks; base += kGULanes * kGUBatch) {
-        if (base) load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, base, j, nchunks, bt);
-        compute_batch<G, SYM, kGUBatch, kGULanes, 1>(bt, base, j, nchunks, as, 0u, asum, 1u, acc);
-    }
+    gemv_batches<G, SYM, kGUBatch, kGULanes, 1>(w, sc, bi, j, nchunks, bt, as, 0u, asum, 1u, acc);
     const float v = group16_sum(acc[0]);
     if (live && j == 0) out[row] = f32_to_f16(f16_to_f32(f32_to_f16(v)) * scale);
 }
