@@ -61,10 +61,10 @@ SUSTAIN_LAYERS = 10  # prefill layers back to back in the sustained graph
 PREFILL_FLOP = 2 * PREFILL_T * TOPK * 3 * F * H  # 194,884,141,056
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode_layer_kernel launch: rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE over `bench.py --traffic-probe` (16,415.92 KiB fetched, 320.09 KiB
+# WRITE_SIZE over `bench.py --traffic-probe` (13,956.06 KiB fetched, 320.09 KiB
 # written per dispatch), scaled by the counters of a plain 64 MiB device copy in
-# the same runs (fetch x 1.9990, write x 1.000).
-TRAFFIC_BYTES = 33931486
+# the same runs (fetch x 1.9991, write x 1.000).
+TRAFFIC_BYTES = 28896551
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
@@ -836,7 +836,7 @@ def run_floors(tsg, torch, layers, reps=8):
     stream = torch.cuda.Stream()
     rng = np.random.default_rng(0xF1)
     ids = [(rng.permutation(E)[:TOPK]).astype(np.uint32) for _ in range(4 * LAYERS)]
-    blocks, threads, lds = 256, 768, 20480
+    blocks, threads, lds = 256, 704, 20080  # decode_layer_kernel's launch at this shape
 
     def empty():
         for _ in range(4 * LAYERS):
