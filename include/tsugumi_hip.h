@@ -407,6 +407,24 @@ tsg_status tsg_prefill_group_pairs_device(tsg_ctx* ctx, tsg_stream stream,
                                           uint32_t* counts, tsg_routed_block* blocks,
                                           uint32_t max_blocks, uint32_t* n_blocks,
                                           void* scratch);
+/* tsg_prefill_group_pairs_device without the scratch argument: no counterpart
+ * in the reference. For callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc):
+ * it calls no allocating routine; the pairs' ranks live in a 256 KiB
+ * file-scope device array, one per GPU, held until the process ends. Same
+ * arguments, checks and results as tsg_prefill_group_pairs_device; also
+ * TSG_ERR_UNSUPPORTED when query_count * top_k exceeds 65536 pairs. Every
+ * call on one GPU uses that GPU's array: calls that overlap on one GPU (two
+ * streams, two host threads) race and must be serialised by the caller. */
+tsg_status tsg_prefill_group_pairs_device_noalloc(tsg_ctx* ctx, tsg_stream stream,
+                                                  const uint32_t* indices,
+                                                  const uint16_t* weights,
+                                                  uint32_t query_count, uint32_t top_k,
+                                                  uint32_t num_experts, uint32_t tile_rows,
+                                                  tsg_token_expert_pair* sorted,
+                                                  uint32_t* offsets, uint32_t* counts,
+                                                  tsg_routed_block* blocks,
+                                                  uint32_t max_blocks, uint32_t* n_blocks);
 
 /* encodeStreamedTiled mode 0 + gelu_mul (PrefillGroupedRoutedMoE.swift:931-1051,
  * prefill.metal:3664-3864, 1081-1092) on a resident layer: for every block,

@@ -589,6 +589,17 @@ class PrefillGroupedRoutedMoE:
             num_experts, tile_rows, _ptr(sorted_pairs), _ptr(offsets), _ptr(counts),
             _ptr(blocks), max_blocks, _ptr(n_blocks), _ptr(scratch)))
 
+    def group_pairs_device_noalloc(self, indices, weights, query_count, top_k, num_experts,
+                                   sorted_pairs, offsets, counts, blocks, max_blocks, n_blocks,
+                                   tile_rows=64, stream=None):
+        """group_pairs_device with the library's file-scope rank scratch (no
+        workspace, no allocation; at most 65536 pairs; calls on one GPU must
+        not overlap)."""
+        check(self.lib.tsg_prefill_group_pairs_device_noalloc(
+            self.ctx.handle, _stream(stream), _ptr(indices), _ptr(weights), query_count, top_k,
+            num_experts, tile_rows, _ptr(sorted_pairs), _ptr(offsets), _ptr(counts),
+            _ptr(blocks), max_blocks, _ptr(n_blocks)))
+
     def encode_gate_up(self, layer, hidden, hidden_stride, sorted_pairs, blocks, n_blocks, act,
                        d, f, n_blocks_device=None, stream=None):
         check(self.lib.tsg_prefill_moe_gate_up(

@@ -143,6 +143,8 @@ SIGNATURES = {
     "tsg_prefill_group_scratch_bytes": (C.c_size_t, [U32, U32, U32]),
     "tsg_prefill_group_pairs_device": (C.c_int, [P, P, P, P, U32, U32, U32, U32, P, P, P, P,
                                                  U32, P, P]),
+    "tsg_prefill_group_pairs_device_noalloc": (C.c_int, [P, P, P, P, U32, U32, U32, U32, P, P,
+                                                         P, P, U32, P]),
     "tsg_prefill_moe_gate_up": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, U32]),
     "tsg_prefill_moe_down": (C.c_int, [P, P, P, P, P, P, U32, P, P, U32, U32, U32]),
     "tsg_prefill_moe_rows": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, U32, U32]),

@@ -98,11 +98,14 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
     if (e == hipSuccess)
         e = hipMemset(ctx->act_replicas, 0, sizeof(uint16_t) * kActReplicas * kActReplicaHalves);
     if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
+    // this device's address of the no-alloc grouping scratch (device current)
+    const tsg_status st = e == hipSuccess ? group_noalloc_setup(ctx) : TSG_OK;
+    if (e != hipSuccess || st != TSG_OK) {
         (void)hipFree(ctx->counters);
         (void)hipFree(ctx->logits);
         (void)hipFree(ctx->act_replicas);
         delete ctx;
+        if (st != TSG_OK) return st;
         return fail(TSG_ERR_OUT_OF_MEMORY, "context scratch: %s", hipGetErrorString(e));
     }
     *out = ctx;

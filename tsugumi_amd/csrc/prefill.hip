@@ -1130,20 +1130,34 @@ extern "C" size_t tsg_prefill_group_scratch_bytes(uint32_t query_count, uint32_t
     return (size_t)query_count * top_k * sizeof(uint32_t);
 }
 
-extern "C" tsg_status tsg_prefill_group_pairs_device(
-    tsg_ctx* ctx, tsg_stream stream, const uint32_t* idx, const uint16_t* w, uint32_t t,
-    uint32_t k, uint32_t ne, uint32_t tile_rows, tsg_token_expert_pair* sorted,
-    uint32_t* offsets, uint32_t* counts, tsg_routed_block* blocks, uint32_t max_blocks,
-    uint32_t* n_blocks, void* scratch) {
-    TSG_REQUIRE(ctx, TSG_ERR_INVALID_ARGUMENT, "ctx is NULL");
-    TSG_REQUIRE(t > 0, TSG_ERR_GROUPING_INVALID_QUERY_COUNT, "queryCount must be positive");
-    TSG_REQUIRE(k > 0, TSG_ERR_GROUPING_INVALID_TOP_K, "topK must be positive");
-    TSG_REQUIRE(ne > 0 && ne <= kMaxExperts, TSG_ERR_GROUPING_INVALID_NUM_EXPERTS,
-                "numExperts %u not in 1..%u", ne, kMaxExperts);
-    TSG_REQUIRE(tile_rows == 32 || tile_rows == 64 || tile_rows == 128 || tile_rows == 256,
-                TSG_ERR_INVALID_ARGUMENT, "tile_rows must be 32, 64, 128 or 256, got %u", tile_rows);
-    TSG_REQUIRE(idx && w && sorted && offsets && counts && blocks && n_blocks && scratch,
-                TSG_ERR_INVALID_ARGUMENT, "NULL grouping operand");
+// Scratch of tsg_prefill_group_pairs_device_noalloc: the rank of each pair
+// among its expert's pairs, one word per pair, for up to kNoAllocPairs pairs
+// (256 KiB). A file-scope device array, so that entry point allocates
+// nothing: each GPU the library runs on holds its own copy until the process
+// ends. Host code passes the per-device address that
+// tsg::group_noalloc_setup looks up, never the array's name.
+static __device__ __align__(256) uint32_t noalloc_rank_scratch[kNoAllocPairs];
+
+namespace tsg {
+
+tsg_status group_noalloc_setup(tsg_ctx* ctx) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_rank_scratch));
+    TSG_REQUIRE(e == hipSuccess && p != nullptr, TSG_ERR_HIP,
+                "device %d: address of the no-alloc grouping scratch: %s", ctx->device,
+                hipGetErrorString(e));
+    ctx->group_rank_scratch = static_cast<uint32_t*>(p);
+    return TSG_OK;
+}
+
+namespace {
+
+// The device grouping of both entry points; rank_of holds t * k words.
+tsg_status group_pairs_device(tsg_ctx* ctx, hipStream_t s, const uint32_t* idx,
+                              const uint16_t* w, uint32_t t, uint32_t k, uint32_t ne,
+                              uint32_t tile_rows, tsg_token_expert_pair* sorted,
+                              uint32_t* offsets, uint32_t* counts, tsg_routed_block* blocks,
+                              uint32_t max_blocks, uint32_t* n_blocks, uint32_t* rank_of) {
     // an expert's c pairs make ceil(c / tile_rows) <= c / tile_rows + 1 blocks
     // of at least one row, so this many always hold the list
     const uint64_t pairs_total = (uint64_t)t * k;
@@ -1151,8 +1165,6 @@ extern "C" tsg_status tsg_prefill_group_pairs_device(
     TSG_REQUIRE(max_blocks >= need, TSG_ERR_INVALID_ARGUMENT,
                 "max_blocks %u cannot hold the work list: need min(t*k, ceil(t*k/%u) + %u) = %llu",
                 max_blocks, tile_rows, ne, (unsigned long long)need);
-    hipStream_t s = as_stream(stream);
-    uint32_t* rank_of = static_cast<uint32_t*>(scratch);
     hipLaunchKernelGGL(group_rank_kernel, dim3(ne), dim3(1024), 0, s, idx, t, k, rank_of, counts);
     tsg_status st = check_launch("group_rank");
     if (st) return st;
@@ -1163,6 +1175,52 @@ extern "C" tsg_status tsg_prefill_group_pairs_device(
                        rank_of, counts, sorted, offsets, blocks, max_blocks, n_blocks, tile_rows,
                        ctx->counters + kSyncErrorWord);
     return check_launch("group_scatter");
+}
+
+tsg_status check_group_args(const tsg_ctx* ctx, uint32_t t, uint32_t k, uint32_t ne,
+                            uint32_t tile_rows) {
+    TSG_REQUIRE(ctx, TSG_ERR_INVALID_ARGUMENT, "ctx is NULL");
+    TSG_REQUIRE(t > 0, TSG_ERR_GROUPING_INVALID_QUERY_COUNT, "queryCount must be positive");
+    TSG_REQUIRE(k > 0, TSG_ERR_GROUPING_INVALID_TOP_K, "topK must be positive");
+    TSG_REQUIRE(ne > 0 && ne <= kMaxExperts, TSG_ERR_GROUPING_INVALID_NUM_EXPERTS,
+                "numExperts %u not in 1..%u", ne, kMaxExperts);
+    TSG_REQUIRE(tile_rows == 32 || tile_rows == 64 || tile_rows == 128 || tile_rows == 256,
+                TSG_ERR_INVALID_ARGUMENT, "tile_rows must be 32, 64, 128 or 256, got %u", tile_rows);
+    return TSG_OK;
+}
+
+}  // namespace
+}  // namespace tsg
+
+extern "C" tsg_status tsg_prefill_group_pairs_device(
+    tsg_ctx* ctx, tsg_stream stream, const uint32_t* idx, const uint16_t* w, uint32_t t,
+    uint32_t k, uint32_t ne, uint32_t tile_rows, tsg_token_expert_pair* sorted,
+    uint32_t* offsets, uint32_t* counts, tsg_routed_block* blocks, uint32_t max_blocks,
+    uint32_t* n_blocks, void* scratch) {
+    tsg_status st = check_group_args(ctx, t, k, ne, tile_rows);
+    if (st) return st;
+    TSG_REQUIRE(idx && w && sorted && offsets && counts && blocks && n_blocks && scratch,
+                TSG_ERR_INVALID_ARGUMENT, "NULL grouping operand");
+    return group_pairs_device(ctx, as_stream(stream), idx, w, t, k, ne, tile_rows, sorted, offsets,
+                              counts, blocks, max_blocks, n_blocks, static_cast<uint32_t*>(scratch));
+}
+
+extern "C" tsg_status tsg_prefill_group_pairs_device_noalloc(
+    tsg_ctx* ctx, tsg_stream stream, const uint32_t* idx, const uint16_t* w, uint32_t t,
+    uint32_t k, uint32_t ne, uint32_t tile_rows, tsg_token_expert_pair* sorted,
+    uint32_t* offsets, uint32_t* counts, tsg_routed_block* blocks, uint32_t max_blocks,
+    uint32_t* n_blocks) {
+    tsg_status st = check_group_args(ctx, t, k, ne, tile_rows);
+    if (st) return st;
+    TSG_REQUIRE(idx && w && sorted && offsets && counts && blocks && n_blocks,
+                TSG_ERR_INVALID_ARGUMENT, "NULL grouping operand");
+    TSG_REQUIRE((uint64_t)t * k <= kNoAllocPairs, TSG_ERR_UNSUPPORTED,
+                "t*k = %llu pairs exceed the no-alloc grouping scratch (%u pairs); use "
+                "tsg_prefill_group_pairs_device with a workspace",
+                (unsigned long long)t * k, kNoAllocPairs);
+    TSG_REQUIRE(ctx->group_rank_scratch, TSG_ERR_HIP, "context has no no-alloc grouping scratch");
+    return group_pairs_device(ctx, as_stream(stream), idx, w, t, k, ne, tile_rows, sorted, offsets,
+                              counts, blocks, max_blocks, n_blocks, ctx->group_rank_scratch);
 }
 
 extern "C" tsg_status tsg_prefill_moe_gate_up(tsg_moe* moe, tsg_stream stream,

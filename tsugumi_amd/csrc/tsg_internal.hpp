@@ -48,6 +48,9 @@ struct tsg_ctx {
     uint32_t* counters = nullptr;        // kMaxCounters
     float* logits = nullptr;             // kMaxPromptRows * kMaxExperts
     uint16_t* act_replicas = nullptr;    // kActReplicas * kActReplicaHalves
+    // this device's copy of the no-alloc grouping scratch (a file-scope device
+    // array of prefill.hip, not owned: never freed)
+    uint32_t* group_rank_scratch = nullptr;
     int num_cus = 256;
 };
 
@@ -120,6 +123,13 @@ constexpr uint32_t kMaxCombineRows = 16;  // output rows one block combines: cei
 constexpr uint32_t kMaxSharedF = 512;     // shared-expert intermediate size of the one-launch layer
 
 constexpr uint32_t kTopK = 8;
+
+// Pairs (t * k) tsg_prefill_group_pairs_device_noalloc takes: its file-scope
+// rank scratch holds one word per pair.
+constexpr uint32_t kNoAllocPairs = 65536;
+// Looks up this device's address of that scratch (the device current);
+// tsg_ctx_create calls it.
+tsg_status group_noalloc_setup(tsg_ctx* ctx);
 
 inline hipStream_t as_stream(tsg_stream s) { return reinterpret_cast<hipStream_t>(s); }
 
