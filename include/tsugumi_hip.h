@@ -285,6 +285,17 @@ tsg_status tsg_moe_shared_expert(tsg_moe* moe, tsg_stream stream, const void* bl
                                  const tsg_expert_offsets* offsets, const uint16_t* x,
                                  const uint16_t* gate_weight, uint16_t* act_scratch,
                                  uint16_t* out, uint32_t d, uint32_t f);
+/* The same for row_count <= 8 token rows (x + r * x_stride, x_stride a
+ * multiple of 8 elements), the shared branch of a multi-token decode step
+ * (MTP verify; encodeSharedExpert per row, QwenForwardRunner.swift:1548-1578)
+ * in two launches, each weight read once for all rows: act_scratch [rows, f],
+ * out [rows, d]; row r is bit-identical to tsg_moe_shared_expert on x_r.
+ * Returns TSG_ERR_DECLINED for row_count 0 or > 8. */
+tsg_status tsg_moe_shared_expert_rows(tsg_moe* moe, tsg_stream stream, const void* blob,
+                                      const tsg_expert_offsets* offsets, const uint16_t* x,
+                                      uint32_t x_stride, const uint16_t* gate_weight,
+                                      uint16_t* act_scratch, uint16_t* out, uint32_t row_count,
+                                      uint32_t d, uint32_t f);
 
 /* ---------------------------------------------------------------- QMV ----
  * DequantInt4GEMV (Kernels/Quant/DequantInt4GEMV.swift:6-364). */
@@ -462,6 +473,23 @@ tsg_status tsg_prefill_moe_rows(tsg_moe* moe, tsg_stream stream, const tsg_layer
                                 const tsg_routed_block* blocks, uint32_t n_blocks,
                                 uint16_t* act_scratch, uint16_t* route_partials,
                                 uint32_t top_k, uint32_t d, uint32_t f);
+/* encodeStreamedRows with the block list left on the device, where
+ * tsg_prefill_group_pairs_device (any tile_rows >= the token count) writes it:
+ * the verify block's grouping (RealForwardRunner.swift:2116-2151) without a
+ * host round trip. blocks holds max_blocks entries (<= 65535), the first
+ * *n_blocks_device of them live; each live block gives exactly
+ * tsg_prefill_moe_rows' results for it. A live block with no rows, more than
+ * 8, or an expert past the layer is skipped and tsg_ctx_synchronize reports
+ * TSG_ERR_INVALID_ARGUMENT (the host form declines such a list up front).
+ * No counterpart entry in the reference, which reads the grouping back to the
+ * host. */
+tsg_status tsg_prefill_moe_rows_device(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                       const uint16_t* hidden, uint32_t hidden_stride,
+                                       const tsg_token_expert_pair* sorted_pairs,
+                                       const tsg_routed_block* blocks, uint32_t max_blocks,
+                                       const uint32_t* n_blocks_device, uint16_t* act_scratch,
+                                       uint16_t* route_partials, uint32_t top_k, uint32_t d,
+                                       uint32_t f);
 /* PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38):
  * h2[t,d] = half(sum_{r<top_k} fma(w[t,r], P[(t*top_k + r), d])). */
 tsg_status tsg_prefill_moe_reduce_token_major(tsg_ctx* ctx, tsg_stream stream,

@@ -236,6 +236,141 @@ def test_qwen_decode_m3_rows_and_shared(tsg, ctx, qwen_layer):
     assert rel <= kc.NORTH_STAR and rel_s <= kc.NORTH_STAR
 
 
+def device_verify_layer(tsg, ctx, moe, layer, rng, m, d, f, ne, spread=0.35):
+    """A verify step's routed MoE with nothing on the host: the router rows
+    (M tokens whose hidden states share a common part, so their top-8 sets
+    overlap), the device grouping, the device-list rows path and the
+    token-major reduce. Returns the device buffers and the inputs."""
+    k = 8
+    x0 = rng.normal(0.0, 1.0, d)
+    hidden = oracle.f16_bits((x0[None, :] + spread * rng.normal(0.0, 1.0, (m, d)))
+                             .astype(np.float32)).ravel()
+    rw = oracle.bf16_bits(rng.normal(0.0, 1.0 / np.sqrt(d), ne * d).astype(np.float32))
+    ones_d = np.full(d, 0x3F80, np.uint16)
+    ones_e = np.full(ne, 0x3F80, np.uint16)
+    X = dev(hidden)
+    idx, wts = empty(m * k, np.uint32), empty(m * k)
+    moe.encode_router_gemma4_bf16_rows(dev(rw), X, d, dev(ones_d), dev(ones_e), idx, wts, m, ne,
+                                       d)
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    max_blocks = m * k
+    sp, off, cnt = empty(m * k * 4, np.uint32), empty(ne, np.uint32), empty(ne, np.uint32)
+    blocks, nb = empty(max_blocks * 4, np.uint32), empty(1, np.uint32)
+    g.group_pairs_device_noalloc(idx, wts, m, k, ne, sp, off, cnt, blocks, max_blocks, nb,
+                                 tile_rows=32)
+    act_buf, part, h2 = empty(m * k * f), empty(m * k * d, fill=NAN16), empty(m * d)
+    g.encode_streamed_rows_device(layer, X, d, sp, blocks, max_blocks, nb, act_buf, part, k, d, f)
+    tsg.PrefillMoE(ctx).encode_reduce_token_major(part, wts, h2, m, k, d)
+    ctx.synchronize()
+    return dict(hidden=hidden, X=X, idx=host(idx, np.uint32).reshape(m, k).copy(),
+                w=host(wts, np.uint16).reshape(m, k).copy(), sp=sp, part=part, h2=h2,
+                n=int(host(nb, np.uint32)[0]))
+
+
+@pytest.mark.parametrize("shape", ["gemma-m5", "qwen-m3"])
+def test_verify_whole_layer_on_device(tsg, ctx, gemma_layer, qwen_layer, shape):
+    """configs[2] and configs[4] M=3 as whole layers on the device (router
+    rows, device grouping, device-list rows path, reduce): the same partials
+    and outputs, bit for bit, as the host-list path run on the routing the
+    device chose, which the oracle checks."""
+    configure(ctx, 32, "sym")
+    if shape == "gemma-m5":
+        (layer, offs, blobs), m, d, f, ne, act = gemma_layer, 5, 2816, 704, 128, "gelu"
+    else:
+        (layer, offs, blobs), m, d, f, ne, act = qwen_layer, 3, 2048, 512, 256, "silu"
+    k = 8
+    moe = tsg.MoE(ctx, gate_activation=act)
+    r = device_verify_layer(tsg, ctx, moe, layer, np.random.default_rng(0xD1CE + m), m, d, f, ne)
+    sp_h, grouped = host_grouping(r["idx"], r["w"], m, ne)
+    assert np.array_equal(host(r["sp"], np.uint32)[:m * k * 4].view(oracle.PAIR_DTYPE), sp_h)
+    blocks = wl.rows_blocks(grouped)
+    assert r["n"] == blocks.size and 8 < blocks.size < m * k  # the top-8 sets overlap
+    act2, part2, h22 = empty(m * k * f), empty(m * k * d, fill=NAN16), empty(m * d)
+    tsg.PrefillGroupedRoutedMoE(moe).encode_streamed_rows(layer, r["X"], d, dev(sp_h), blocks,
+                                                          act2, part2, k, d, f)
+    tsg.PrefillMoE(ctx).encode_reduce_token_major(part2, dev(r["w"]), h22, m, k, d)
+    assert np.array_equal(host(r["part"], np.uint16), host(part2, np.uint16))
+    assert np.array_equal(host(r["h2"], np.uint16), host(h22, np.uint16))
+    P = oracle.prefill_moe_ref(blobs, offs, r["hidden"], d, sp_h, k, d, f, 32, True,
+                               act=1 if act == "silu" else 0, rows_path=True)
+    ref_h2 = oracle.reduce_token_major(P, r["w"], m, k, d)
+    rel = oracle.relative_error(oracle.f16_to_float(host(r["h2"], np.uint16)),
+                                oracle.f16_to_float(ref_h2).ravel())
+    print(f"{shape}: union={blocks.size} h2 rel={rel:.3e}")
+    assert rel <= kc.NORTH_STAR
+
+
+def test_rows_device_list_skips_and_reports(tsg, ctx, gemma_layer):
+    """Blocks past the device count are not run; a live block the rows path
+    cannot take (9 rows) is skipped and reported at synchronisation."""
+    configure(ctx, 32, "sym")
+    layer, offs, blobs = gemma_layer
+    d, f, k = 2816, 704, 8
+    moe = tsg.MoE(ctx)
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    pairs = np.zeros(16, oracle.PAIR_DTYPE)
+    pairs["token"] = np.arange(16) // 8
+    pairs["rank"] = np.arange(16) % 8
+    pairs["expert"] = 3
+    bl = np.zeros(2, oracle.BLOCK_DTYPE)
+    bl["local_slot"] = 3
+    bl["pair_start"] = bl["local_row"] = [0, 2]
+    bl["row_count"] = [2, 9]
+    X = dev(wl.f16_normal(np.random.default_rng(1), 16 * d))
+    act_buf, part = empty(16 * f), empty(16 * d, fill=NAN16)
+    # count 0: nothing runs
+    g.encode_streamed_rows_device(layer, X, d, dev(pairs), dev(bl), 2, dev(np.zeros(1, np.uint32)),
+                                  act_buf, part, k, d, f)
+    ctx.synchronize()
+    assert np.all(host(part, np.uint16) == np.uint16(NAN16 & 0xFFFF))
+    # count 2: block 0 runs, block 1 (9 rows) is skipped and reported
+    g.encode_streamed_rows_device(layer, X, d, dev(pairs), dev(bl), 2, dev(np.full(1, 2, np.uint32)),
+                                  act_buf, part, k, d, f)
+    with pytest.raises(tsg.TsgError) as e:
+        ctx.synchronize()
+    assert e.value.status == 1
+    got = host(part, np.uint16).reshape(16, d)
+    assert np.all(got[2:] == np.uint16(NAN16 & 0xFFFF))
+    assert not np.any(np.isnan(oracle.f16_to_float(got[:2])))
+
+
+@pytest.mark.parametrize("rows,scheme", [(3, "sym"), (8, "sym"), (5, "affine")])
+def test_shared_expert_rows_matches_one_row_form(tsg, ctx, rows, scheme):
+    """tsg_moe_shared_expert_rows: row r equals tsg_moe_shared_expert on x_r
+    bit for bit (configs[4]'s shared expert, d=2048, f=512), and the oracle."""
+    configure(ctx, 32, scheme)
+    d, f = 2048, 512
+    rng = np.random.default_rng(0x5A + rows)
+    if scheme == "sym":
+        image, _, soffs, sblobs = wl.random_sym_layer(rng, 1, d, f)
+    else:
+        krng = oracle.seed_tree_key(0x5A, f"shared-rows-{rows}")
+        experts = [[kc.quantized_rows(krng, r, c, 32, False, -0.3, 0.3)
+                    for (r, c) in ((f, d), (f, d), (d, f))]]
+        image, _, soffs, sblobs = kc.layer_image(experts, False, keep_biases=True)
+    gate_w = oracle.bf16_bits((rng.normal(0.0, 1.0 / np.sqrt(d), d)).astype(np.float32))
+    stride = d + 8  # a token stride other than d
+    xs = np.zeros(rows * stride, np.uint16)
+    for r in range(rows):
+        xs[r * stride:r * stride + d] = wl.f16_normal(rng, d)
+    moe = tsg.MoE(ctx, gate_activation="silu")
+    blob, X, G = dev(image), dev(xs), dev(gate_w)
+    sact, sout = empty(rows * f), empty(rows * d)
+    tsg.encode_shared_expert_rows(moe, blob, soffs, X, stride, G, sact, sout, rows, d, f)
+    got = host(sout, np.uint16).reshape(rows, d).copy()
+    for r in range(rows):
+        a1, o1 = empty(f), empty(d)
+        tsg.encode_shared_expert(moe, blob, soffs, X[r * stride:], G, a1, o1, d, f)
+        assert np.array_equal(got[r], host(o1, np.uint16)), r
+        ref = oracle.shared_expert(sblobs[0], soffs, xs[r * stride:r * stride + d], gate_w, d, f,
+                                   32, scheme == "sym")
+        rel = oracle.relative_error(oracle.f16_to_float(got[r]), oracle.f16_to_float(ref))
+        assert rel <= kc.NORTH_STAR, (r, rel)
+    with pytest.raises(tsg.TsgError) as e:
+        tsg.encode_shared_expert_rows(moe, blob, soffs, X, stride, G, sact, sout, 9, d, f)
+    assert e.value.status == 4
+
+
 def run_prefill_full(tsg, ctx, layer, offs, blobs, t, d, f, ne, s, act, seed):
     """Device grouping -> gate/up -> down -> reduce at full size; the head
     expert and every 16th token recomputed by the oracle."""

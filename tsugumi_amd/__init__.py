@@ -457,6 +457,16 @@ def encode_shared_expert(moe: "MoE", blob, offsets, x, gate_weight, act_scratch,
                                         d, f))
 
 
+def encode_shared_expert_rows(moe: "MoE", blob, offsets, x, x_stride, gate_weight, act_scratch,
+                              out, rows, d, f, stream=None):
+    """encode_shared_expert for rows <= 8 token rows (x + r * x_stride), each
+    weight read once; row r gives encode_shared_expert's bits on x_r."""
+    o = offsets_from(offsets)
+    check(moe.lib.tsg_moe_shared_expert_rows(moe.handle, _stream(stream), _ptr(blob),
+                                             C.byref(o), _ptr(x), x_stride, _ptr(gate_weight),
+                                             _ptr(act_scratch), _ptr(out), rows, d, f))
+
+
 class DequantInt4GEMV:
     """DequantInt4GEMV (DequantInt4GEMV.swift:6-364)."""
 
@@ -611,6 +621,16 @@ class PrefillGroupedRoutedMoE:
         check(self.lib.tsg_prefill_moe_down(
             self.moe.handle, _stream(stream), layer.handle, _ptr(act), _ptr(sorted_pairs),
             _ptr(blocks), n_blocks, _ptr(n_blocks_device), _ptr(route_partials), top_k, d, f))
+
+    def encode_streamed_rows_device(self, layer, hidden, hidden_stride, sorted_pairs, blocks,
+                                    max_blocks, n_blocks_device, act_scratch, route_partials,
+                                    top_k, d, f, stream=None):
+        """encode_streamed_rows with the block list (and its count) on the
+        device, as group_pairs_device writes them."""
+        check(self.lib.tsg_prefill_moe_rows_device(
+            self.moe.handle, _stream(stream), layer.handle, _ptr(hidden), hidden_stride,
+            _ptr(sorted_pairs), _ptr(blocks), max_blocks, _ptr(n_blocks_device),
+            _ptr(act_scratch), _ptr(route_partials), top_k, d, f))
 
     def encode_streamed_rows(self, layer, hidden, hidden_stride, sorted_pairs, host_blocks,
                              act_scratch, route_partials, top_k, d, f, stream=None):

@@ -132,6 +132,7 @@ SIGNATURES = {
     "tsg_qwen_moe_shared_gate": (C.c_int, [P, P, P, P, P, U32]),
     "tsg_qwen_moe_shared_gate_logit": (C.c_int, [P, P, P, P, U32]),
     "tsg_moe_shared_expert": (C.c_int, [P, P, P, P, P, P, P, P, U32, U32]),
+    "tsg_moe_shared_expert_rows": (C.c_int, [P, P, P, P, P, U32, P, P, P, U32, U32, U32]),
     "tsg_qmv_int4_rows": (C.c_int, [P, P, P, P, P, P, U32, P, U32, U32, U32, U32]),
     "tsg_debug_dequant_f16": (C.c_int, [P, P, P, P, P, P, U32, U32]),
     "tsg_debug_gemm_dequant_f16": (C.c_int, [P, P, P, P, P, P, U32, U32]),
@@ -148,6 +149,8 @@ SIGNATURES = {
     "tsg_prefill_moe_gate_up": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, U32]),
     "tsg_prefill_moe_down": (C.c_int, [P, P, P, P, P, P, U32, P, P, U32, U32, U32]),
     "tsg_prefill_moe_rows": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, U32, U32]),
+    "tsg_prefill_moe_rows_device": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, P, U32, U32,
+                                              U32]),
     "tsg_prefill_moe_reduce_token_major": (C.c_int, [P, P, P, P, P, U32, U32, U32]),
     "tsg_prefill_int4_qmm": (C.c_int, [P, P, P, P, P, P, P, U32, U32, U32]),
     "tsg_prefill_layer_tail": (C.c_int, [P, P, P, P, P, P, P, U32, U32, U32, U32, U32,

@@ -143,8 +143,9 @@ extern "C" tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream) {
     TSG_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
     // Kernels that detect an error on the device set a bit of this word (the
     // one-launch decode layer on a hand-off timeout, the device grouping on
-    // an out-of-range expert id or an overfull work list); the outputs of the
-    // affected launches are invalid. Reading clears it.
+    // an out-of-range expert id or an overfull work list, the device-list rows
+    // path on a block it cannot take); the outputs of the affected launches
+    // are invalid. Reading clears it.
     uint32_t err = 0;
     TSG_HIP_TRY(hipMemcpy(&err, ctx->counters + kSyncErrorWord, sizeof(err),
                           hipMemcpyDeviceToHost));
@@ -157,6 +158,10 @@ extern "C" tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream) {
         if (err & kErrGroupBlocks)
             return fail(TSG_ERR_INVALID_ARGUMENT,
                         "the device grouping's work list exceeded max_blocks");
+        if (err & kErrRowsBlock)
+            return fail(TSG_ERR_INVALID_ARGUMENT,
+                        "rows path: a device block had no rows, more than 8, or an expert past "
+                        "the layer; it was skipped");
         return fail(TSG_ERR_HIP, "fused decode layer: a block timed out waiting for the "
                                  "others; outputs of the affected launch are invalid");
     }

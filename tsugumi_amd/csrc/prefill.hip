@@ -414,6 +414,8 @@ struct GemmArgs {
     const uint8_t* dense_s;     // MODE 2: scales (the weights are at layer_base)
     const uint8_t* dense_b;     // MODE 2: biases (the scales again under sym)
     uint32_t ntiles;            // weight-row tiles per routed block
+    uint32_t num_experts;       // experts of the layer (device block lists are checked)
+    uint32_t* error;            // the context's device error word
 };
 
 // Per-lane state of one block's GEMM.
@@ -940,15 +942,15 @@ struct RowsBlocks {
 // phase1_compute): the same gemv_lane.hpp steps, batch and reduction, so one
 // row here is bit-identical to decode.
 template <int G, bool SYM, int ACT>
-__global__ __launch_bounds__(kRowsThreads) void rows_gate_up_kernel(GemmArgs args, RowsBlocks rb) {
+__device__ __forceinline__ void rows_gate_up_body(const GemmArgs& args, const tsg_routed_block& blk,
+                                                  uint32_t lds_rows) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t tok[kRowsMax];
-    const tsg_routed_block blk = rb.b[blockIdx.y];
     const uint32_t rows = blk.row_count < kRowsMax ? blk.row_count : kRowsMax;
     const uint32_t d = args.d, f = args.f;
     const uint32_t row_h = lds_chunks_halves(d);
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-    float* xsum = reinterpret_cast<float*>(smem + (size_t)rb.lds_rows * row_h * 2u);
+    float* xsum = reinterpret_cast<float*>(smem + (size_t)lds_rows * row_h * 2u);
 
     const uint32_t fr_raw = blockIdx.x * (kRowsThreads / 32u) + (threadIdx.x >> 5);
     const uint32_t j = threadIdx.x & 15u;
@@ -986,16 +988,15 @@ __global__ __launch_bounds__(kRowsThreads) void rows_gate_up_kernel(GemmArgs arg
 // one staging of the activation rows. Per row the arithmetic is decode phase
 // 2's per-slot GEMV (decode.hip phase2_body): the same gemv_lane.hpp steps.
 template <int G, bool SYM>
-__global__ __launch_bounds__(kRowsThreads) void rows_down_kernel(GemmArgs args, RowsBlocks rb,
-                                                       uint16_t* partials) {
+__device__ __forceinline__ void rows_down_body(const GemmArgs& args, const tsg_routed_block& blk,
+                                               uint32_t lds_rows, uint16_t* partials) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t dst[kRowsMax];
-    const tsg_routed_block blk = rb.b[blockIdx.y];
     const uint32_t rows = blk.row_count < kRowsMax ? blk.row_count : kRowsMax;
     const uint32_t d = args.d, f = args.f;
     const uint32_t row_h = lds_chunks_halves(f);
     uint16_t* as = reinterpret_cast<uint16_t*>(smem);
-    float* asum = reinterpret_cast<float*>(smem + (size_t)rb.lds_rows * row_h * 2u);
+    float* asum = reinterpret_cast<float*>(smem + (size_t)lds_rows * row_h * 2u);
 
     const uint32_t j = threadIdx.x & 7u;
     const uint32_t row = blockIdx.x * (kRowsThreads / 8u) + (threadIdx.x >> 3);
@@ -1025,6 +1026,46 @@ __global__ __launch_bounds__(kRowsThreads) void rows_down_kernel(GemmArgs args, 
     }
     if (live_row && j == 0)
         for (uint32_t r = 0; r < rows; ++r) partials[dst[r] + row] = f32_to_f16(acc[r]);
+}
+
+template <int G, bool SYM, int ACT>
+__global__ __launch_bounds__(kRowsThreads) void rows_gate_up_kernel(GemmArgs args, RowsBlocks rb) {
+    rows_gate_up_body<G, SYM, ACT>(args, rb.b[blockIdx.y], rb.lds_rows);
+}
+
+template <int G, bool SYM>
+__global__ __launch_bounds__(kRowsThreads) void rows_down_kernel(GemmArgs args, RowsBlocks rb,
+                                                                 uint16_t* partials) {
+    rows_down_body<G, SYM>(args, rb.b[blockIdx.y], rb.lds_rows, partials);
+}
+
+// The device-list forms: the block list and its count were written on the
+// device (tsg_prefill_group_pairs_device), the grid covers the list's
+// capacity and blocks past the count exit. A block the rows path cannot take
+// (no rows, more than kRowsMax, an expert past the layer) is skipped and sets
+// kErrRowsBlock, which tsg_ctx_synchronize reports.
+__device__ __forceinline__ bool rows_device_block(const GemmArgs& args, tsg_routed_block& blk) {
+    const uint32_t n = min(*args.n_blocks_device, args.n_blocks);
+    if (blockIdx.y >= n) return false;
+    blk = args.blocks[blockIdx.y];
+    if (blk.row_count == 0 || blk.row_count > kRowsMax || blk.local_slot >= args.num_experts) {
+        if (threadIdx.x == 0 && blockIdx.x == 0) atomicOr(args.error, kErrRowsBlock);
+        return false;
+    }
+    return true;
+}
+
+template <int G, bool SYM, int ACT>
+__global__ __launch_bounds__(kRowsThreads) void rows_gate_up_dev_kernel(GemmArgs args) {
+    tsg_routed_block blk;
+    if (rows_device_block(args, blk)) rows_gate_up_body<G, SYM, ACT>(args, blk, kRowsMax);
+}
+
+template <int G, bool SYM>
+__global__ __launch_bounds__(kRowsThreads) void rows_down_dev_kernel(GemmArgs args,
+                                                                     uint16_t* partials) {
+    tsg_routed_block blk;
+    if (rows_device_block(args, blk)) rows_down_body<G, SYM>(args, blk, kRowsMax, partials);
 }
 
 // ------------------------------------------------------------ host side
@@ -1117,6 +1158,8 @@ tsg_status fill_gemm_args(const tsg_moe* moe, const tsg_layer* layer, GemmArgs* 
     a->d = d;
     a->f = f;
     a->top_k = top_k;
+    a->num_experts = layer->num_experts;
+    a->error = ctx->counters + kSyncErrorWord;
     return TSG_OK;
 }
 
@@ -1336,6 +1379,61 @@ extern "C" tsg_status tsg_prefill_moe_rows(tsg_moe* moe, tsg_stream stream,
 #undef TSG_ROWS_LAUNCH
     }
     return TSG_OK;
+}
+
+extern "C" tsg_status tsg_prefill_moe_rows_device(tsg_moe* moe, tsg_stream stream,
+                                                  const tsg_layer* layer, const uint16_t* hidden,
+                                                  uint32_t hidden_stride,
+                                                  const tsg_token_expert_pair* pairs,
+                                                  const tsg_routed_block* blocks,
+                                                  uint32_t max_blocks,
+                                                  const uint32_t* n_blocks_device,
+                                                  uint16_t* act_scratch, uint16_t* partials,
+                                                  uint32_t top_k, uint32_t d, uint32_t f) {
+    tsg_status st = check_layer_moe(moe, layer);
+    if (st) return st;
+    TSG_REQUIRE(n_blocks_device && top_k > 0 && act_scratch && partials, TSG_ERR_INVALID_ARGUMENT,
+                "NULL rows operand");
+    TSG_REQUIRE(max_blocks > 0 && max_blocks <= 65535u, TSG_ERR_INVALID_ARGUMENT,
+                "max_blocks must be in 1..65535, got %u", max_blocks);
+    GemmArgs a;
+    if ((st = fill_gemm_args(moe, layer, &a, hidden, hidden_stride, pairs, blocks, max_blocks,
+                             n_blocks_device, act_scratch, d, f, top_k)))
+        return st;
+    TSG_REQUIRE(aligned16(act_scratch), TSG_ERR_ALIGNMENT, "act_scratch must be 16-byte aligned");
+    const tsg_ctx* ctx = moe->ctx;
+    const bool sym = ctx->scheme == TSG_SYM;
+    // LDS for the widest block the rows path takes
+    const size_t l1 = (size_t)kRowsMax * lds_chunks_halves(d) * 2u + (sym ? 0u : kRowsMax * (d / 32u) * 4u);
+    const size_t l2 = (size_t)kRowsMax * lds_chunks_halves(f) * 2u + (sym ? 0u : kRowsMax * (f / 32u) * 4u);
+    TSG_REQUIRE(l1 <= 64u * 1024u && l2 <= 64u * 1024u, TSG_ERR_UNSUPPORTED,
+                "d=%u / f=%u do not fit the rows path's LDS staging", d, f);
+    hipStream_t s = as_stream(stream);
+    GemmArgs a2 = a;
+    a2.a = act_scratch;
+    a2.a_stride = f;
+    const dim3 g1((f + kRowsThreads / 32u - 1u) / (kRowsThreads / 32u), max_blocks);
+    const dim3 g2((d + kRowsThreads / 8u - 1u) / (kRowsThreads / 8u), max_blocks);
+#define TSG_ROWS_DEV(GG, SS)                                                                       \
+    do {                                                                                           \
+        if (moe->activation == TSG_ACT_SILU)                                                       \
+            hipLaunchKernelGGL((rows_gate_up_dev_kernel<GG, SS, TSG_ACT_SILU>), g1,                \
+                               dim3(kRowsThreads), l1, s, a);                                      \
+        else                                                                                       \
+            hipLaunchKernelGGL((rows_gate_up_dev_kernel<GG, SS, TSG_ACT_GELU_TANH>), g1,           \
+                               dim3(kRowsThreads), l1, s, a);                                      \
+        if ((st = check_launch("rows gate/up (device list)"))) return st;                         \
+        hipLaunchKernelGGL((rows_down_dev_kernel<GG, SS>), g2, dim3(kRowsThreads), l2, s, a2,      \
+                           partials);                                                              \
+        return check_launch("rows down (device list)");                                           \
+    } while (0)
+    if (ctx->group_size == 32) {
+        if (sym) TSG_ROWS_DEV(32, true);
+        TSG_ROWS_DEV(32, false);
+    }
+    if (sym) TSG_ROWS_DEV(64, true);
+    TSG_ROWS_DEV(64, false);
+#undef TSG_ROWS_DEV
 }
 
 extern "C" tsg_status tsg_prefill_moe_reduce_token_major(tsg_ctx* ctx, tsg_stream stream,

@@ -103,10 +103,13 @@ constexpr uint32_t kSyncEpochWord = 1024;  // launch epoch
 constexpr uint32_t kSyncErrorWord = 1056;  // device-side error bits (kErr*), read by tsg_ctx_synchronize
 // Bits of the error word: a one-launch decode layer whose hand-off wait timed
 // out; a device grouping that met an expert id >= num_experts (its pairs are
-// not grouped); a device grouping whose work list did not fit max_blocks.
+// not grouped); a device grouping whose work list did not fit max_blocks; a
+// device-list rows-path block with no rows, more than 8, or an expert past
+// the layer (skipped).
 constexpr uint32_t kErrDecodeTimeout = 1u;
 constexpr uint32_t kErrGroupExpertRange = 2u;
 constexpr uint32_t kErrGroupBlocks = 4u;
+constexpr uint32_t kErrRowsBlock = 8u;  // a device-list rows-path block it cannot take
 constexpr uint32_t kSyncLogitWord = 1088;  // tagged 64-bit logits, kMaxExperts per group
 static_assert(kSyncLogitWord + kDecodeGroups * 2 * kMaxExperts <= kMaxCounters, "sync area overflow");
 static_assert(kSyncLogitWord % 2 == 0, "64-bit words must be aligned");
