@@ -466,6 +466,73 @@ def run_rows_path(tsg, torch, ctx, moe, layers, n_layers, m, h, f, ne, seed, sha
     return ms * 1000.0 / n_layers, float(np.mean(unions))
 
 
+def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, ne, seed,
+                     shared=None):
+    """M tokens through n_layers whole layers with nothing on the host: the
+    router rows (RealForwardRunner.swift:1826-1872), the device grouping
+    (:2116-2151, tsg_prefill_group_pairs_device_noalloc), the rows path over the
+    device block list and the token-major reduce; `shared` (Qwen) adds the
+    shared expert over the M rows (two launches). The M hidden states of a layer
+    share a common part (x0 + 0.35 N(0,1)), so their top-8 sets overlap (a
+    union of about 12-20). Returns us per layer, the mean union and the
+    launches per layer."""
+    k = TOPK
+    rng = np.random.default_rng(seed)
+    hid = np.empty((n_layers, m, h), np.float32)
+    for l in range(n_layers):
+        hid[l] = rng.normal(0.0, 1.0, h)[None, :] + 0.35 * rng.normal(0.0, 1.0, (m, h))
+    hidden = torch.from_numpy(hid.astype(np.float16).view(np.int16).ravel().copy()).cuda()
+    ones_h = torch.full((h,), 0x3F80, dtype=torch.int16, device="cuda")
+    ones_e = torch.full((ne,), 0x3F80, dtype=torch.int16, device="cuda")
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    red = tsg.PrefillMoE(ctx)
+    max_blocks = m * k
+    idx = torch.empty(n_layers * m * k, dtype=torch.int32, device="cuda")
+    wts = torch.empty(n_layers * m * k, dtype=torch.int16, device="cuda")
+    sp = torch.empty(m * k * 4, dtype=torch.int32, device="cuda")
+    off = torch.empty(ne, dtype=torch.int32, device="cuda")
+    cnt = torch.empty(ne, dtype=torch.int32, device="cuda")
+    blocks = torch.empty(max_blocks * 4, dtype=torch.int32, device="cuda")
+    nbs = torch.empty(n_layers, dtype=torch.int32, device="cuda")
+    act = torch.empty(m * k * f, dtype=torch.int16, device="cuda")
+    part = torch.empty(m * k * h, dtype=torch.int16, device="cuda")
+    h2 = torch.empty(n_layers * m * h, dtype=torch.int16, device="cuda")
+    if shared is not None:
+        sact = torch.empty(m * f, dtype=torch.int16, device="cuda")
+        sout = torch.empty(n_layers * m * h, dtype=torch.int16, device="cuda")
+    stream = torch.cuda.Stream()
+
+    def body():
+        for l in range(n_layers):
+            x = hidden[l * m * h:(l + 1) * m * h]
+            il, wl = idx[l * m * k:(l + 1) * m * k], wts[l * m * k:(l + 1) * m * k]
+            nb = nbs[l:l + 1]
+            moe.encode_router_gemma4_bf16_rows(routers[l], x, h, ones_h, ones_e, il, wl, m, ne,
+                                               h, stream=stream)
+            g.group_pairs_device_noalloc(il, wl, m, k, ne, sp, off, cnt, blocks, max_blocks, nb,
+                                         tile_rows=32, stream=stream)
+            g.encode_streamed_rows_device(layers[l], x, h, sp, blocks, max_blocks, nb, act, part,
+                                          k, h, f, stream=stream)
+            red.encode_reduce_token_major(part, wl, h2[l * m * h:(l + 1) * m * h], m, k, h,
+                                          stream=stream)
+            if shared is not None:
+                blob, o, gw = shared[l]
+                tsg.encode_shared_expert_rows(moe, blob, o, x, h, gw, sact,
+                                              sout[l * m * h:(l + 1) * m * h], m, h, f,
+                                              stream=stream)
+
+    ms = time_graph(torch, stream, body, reps=8)
+    ctx.synchronize()
+    out = h2.view(torch.float16).float()
+    if not bool(torch.isfinite(out).all()):
+        raise RuntimeError("verify layer produced non-finite outputs")
+    if shared is not None and not bool(torch.isfinite(sout.view(torch.float16).float()).all()):
+        raise RuntimeError("shared expert rows produced non-finite outputs")
+    unions = nbs.cpu().numpy()
+    launches = 1 + 2 + 2 + 1 + (2 if shared is not None else 0)
+    return ms * 1000.0 / n_layers, float(np.mean(unions)), launches
+
+
 def make_shared_experts(tsg, torch, n_layers, h, f, seed):
     """One shared expert (sym g32, the routed experts' generators) and a bf16
     gate row N(0, 1/sqrt(h)) per layer."""
@@ -529,9 +596,11 @@ def run_qwen(tsg, torch, args):
         raise RuntimeError("qwen decode routing collapsed")
     bytes1 = TOPK * payload + payload + e * h * 2 + h * 2 + 6 * h * 2
     log(f"qwen decode M=1: {us1:.3f} us/layer ({bytes1 / (us1 * 1e-6) / 1e9:.1f} GB/s)")
-    us3, u3 = run_rows_path(tsg, torch, ctx, moe, layers, nl, 3, h, f, e, 0x3333, shared=shared)
-    bytes3 = u3 * payload + payload
-    log(f"qwen decode M=3: {us3:.3f} us/layer over a mean union of {u3:.1f} experts")
+    us3, u3, nl3 = run_verify_layer(tsg, torch, ctx, moe, layers, routers, nl, 3, h, f, e,
+                                    0x3333, shared=shared)
+    bytes3 = u3 * payload + payload + e * h * 2 + h * 2
+    log(f"qwen decode M=3 whole layer: {us3:.3f} us/layer over a mean union of {u3:.1f} "
+        f"experts ({bytes3 / (us3 * 1e-6) / 1e9:.1f} GB/s)")
     pre = run_prefill_shape(tsg, torch, ctx, args, layers[0], QW_T, h, f, e, 1.0, "silu",
                             layers=layers)
     return {"workload": "qwen3.5-moe-35b-a3b-shaped layer (configs[4]): H=2048, 256 experts "
@@ -542,8 +611,10 @@ def run_qwen(tsg, torch, args):
                           "launches_per_layer": 1},
             "decode_m3": {"us_per_layer": round(us3, 3), "mean_union": round(u3, 2),
                           "GBps": round(bytes3 / (us3 * 1e-6) / 1e9, 2),
-                          "path": "rows path + token-major reduce + shared branch (GEMV rows, "
-                                  "SiLU-mul, 3 gates)"},
+                          "bytes_per_layer": int(bytes3), "launches_per_layer": nl3,
+                          "path": "whole layer on the device: router rows, device grouping, "
+                                  "rows path over the device block list, reduce, shared expert "
+                                  "over the 3 rows (2 launches)"},
             "prefill_t4096": prefill_summary(pre)}
 
 
@@ -663,21 +734,29 @@ def run_dense_qmm(tsg, torch, ctx):
     return {"workload": "dense int4 projection QMM, T=2048, sym g32 (PrefillInt4QMM)", **out}
 
 
-def run_verify(tsg, torch, ctx, args, layers):
+def run_verify(tsg, torch, ctx, args, layers, routers):
     """Gemma verify, M=5 over a union of about 12-20 experts, 30
-    layers on the rows path."""
+    layers: the whole layer (router rows, device grouping, rows path, reduce),
+    and the rows path alone with the routing precomputed."""
     moe = tsg.MoE(ctx)
-    us, u = run_rows_path(tsg, torch, ctx, moe, layers, LAYERS, 5, H, F, E, 0x5E5E)
+    us, u, nl = run_verify_layer(tsg, torch, ctx, moe, layers, routers, LAYERS, 5, H, F, E,
+                                 0x5E5E)
+    us0, u0 = run_rows_path(tsg, torch, ctx, moe, layers, LAYERS, 5, H, F, E, 0x5E5E)
     _, _, payload = shape_offsets(H, F)
-    b = u * payload
-    log(f"verify M=5: {us:.3f} us/layer over a mean union of {u:.1f} experts "
-        f"({b / (us * 1e-6) / 1e9:.1f} GB/s)")
+    b = u * payload + ROUTER_BYTES
+    log(f"verify M=5 whole layer: {us:.3f} us/layer over a mean union of {u:.1f} experts "
+        f"({b / (us * 1e-6) / 1e9:.1f} GB/s); rows path alone {us0:.3f} us")
     return {"workload": "gemma4-26b-a4b verify, M=5 (draft 4 + 1), union ~12-20, 30 layers "
                         "(configs[2])",
             "us_per_layer": round(us, 3), "mean_union": round(u, 2),
+            "bytes_per_layer": int(b),
             "GBps": round(b / (us * 1e-6) / 1e9, 2),
             "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "path": "rows path (encodeStreamedRows) + token-major reduce, routing precomputed"}
+            "launches_per_layer": nl,
+            "path": "whole layer on the device: router rows, device grouping (no-alloc), rows "
+                    "path over the device block list, token-major reduce",
+            "rows_path_only": {"us_per_layer": round(us0, 3), "mean_union": round(u0, 2),
+                               "path": "rows path + reduce, routing precomputed on the host"}}
 
 
 def attainable_gemm(torch):
@@ -988,7 +1067,7 @@ def main():
         for name, fn in (("qmv", lambda: run_qmv(tsg, torch, ctx)),
                          ("layer_tail", lambda: run_tail(tsg, torch, ctx)),
                          ("dense_qmm", lambda: run_dense_qmm(tsg, torch, ctx)),
-                         ("verify_m5", lambda: run_verify(tsg, torch, ctx, args, layers)),
+                         ("verify_m5", lambda: run_verify(tsg, torch, ctx, args, layers, routers)),
                          ("qwen35", lambda: run_qwen(tsg, torch, args))):
             try:
                 extra[name] = fn()
