@@ -213,6 +213,36 @@ def run_decode(tsg, torch, ctx, args, layers, routers):
                 kernel_us=k_us, idx=idx, xs=last, wts=wts)
 
 
+def routing_margins(torch, dec, routers):
+    """The fp64 margin between the 8th and 9th router logits of the last timed
+    token of every layer (RouterTopKTests.swift:46-68 pins ties; this shows
+    how far the measured routing is from one): logits W x in fp64 from the
+    same bf16 weights and fp16 inputs (effective scale 1), the fp32
+    accumulation's worst-case error n u sum|w x| beside it, and whether the
+    GPU's top-8 set is the fp64 one."""
+    idx = dec["idx"].view(LAYERS, TOPK).cpu().numpy()
+    margins, ratios, same = [], [], 0
+    for l in range(LAYERS):
+        w = routers[l].cpu().numpy().view(np.uint16).astype(np.uint32) << 16
+        w = w.view(np.float32).astype(np.float64).reshape(E, H)
+        x = dec["xs"][l].cpu().numpy().view(np.float16).astype(np.float64)
+        logits = w @ x
+        order = np.argsort(-logits, kind="stable")
+        m = float(logits[order[7]] - logits[order[8]])
+        bound = H * 2.0 ** -24 * float(np.max(np.abs(w) @ np.abs(x)))
+        margins.append(m)
+        ratios.append(m / bound)
+        same += int(set(order[:TOPK].tolist()) == set(idx[l].tolist()))
+    out = {"min_margin": round(min(margins), 6), "median_margin": round(float(np.median(margins)), 6),
+           "min_margin_over_fp32_bound": round(min(ratios), 2), "layers": LAYERS,
+           "gpu_top8_equals_fp64_top8": same,
+           "note": "8th minus 9th logit in fp64 for the last timed token of each layer; the "
+                   "bound is n * 2^-24 * max_e sum_i |w_ei x_i| (n = 2816)"}
+    log(f"routing margins: min {out['min_margin']:.4g} (x{out['min_margin_over_fp32_bound']} "
+        f"the fp32 bound), fp64 top-8 = GPU top-8 on {same}/{LAYERS} layers")
+    return out
+
+
 def check_decode_outputs(torch, ys, idx):
     """The measured work must be the claimed work: finite outputs and routing
     that spreads over many experts (a collapsed routing reads one expert)."""
@@ -469,9 +499,9 @@ def run_rows_path(tsg, torch, ctx, moe, layers, n_layers, m, h, f, ne, seed, sha
 def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, ne, seed,
                      shared=None):
     """M tokens through n_layers whole layers with nothing on the host: the
-    router rows (RealForwardRunner.swift:1826-1872), the device grouping
-    (:2116-2151, tsg_prefill_group_pairs_device_noalloc), the rows path over the
-    device block list and the token-major reduce; `shared` (Qwen) adds the
+    router rows (RealForwardRunner.swift:1826-1872) and the grouping of their
+    pairs (:2116-2151) in one launch, the rows path over the device block
+    list and the token-major reduce; `shared` (Qwen) adds the
     shared expert over the M rows (two launches). The M hidden states of a layer
     share a common part (x0 + 0.35 N(0,1)), so their top-8 sets overlap (a
     union of about 12-20). Returns us per layer, the mean union and the
@@ -507,10 +537,9 @@ def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, n
             x = hidden[l * m * h:(l + 1) * m * h]
             il, wl = idx[l * m * k:(l + 1) * m * k], wts[l * m * k:(l + 1) * m * k]
             nb = nbs[l:l + 1]
-            moe.encode_router_gemma4_bf16_rows(routers[l], x, h, ones_h, ones_e, il, wl, m, ne,
-                                               h, stream=stream)
-            g.group_pairs_device_noalloc(il, wl, m, k, ne, sp, off, cnt, blocks, max_blocks, nb,
-                                         tile_rows=32, stream=stream)
+            moe.encode_router_gemma4_bf16_rows_grouped(routers[l], x, h, ones_h, ones_e, il, wl,
+                                                       m, ne, h, sp, off, cnt, blocks,
+                                                       max_blocks, nb, stream=stream)
             g.encode_streamed_rows_device(layers[l], x, h, sp, blocks, max_blocks, nb, act, part,
                                           k, h, f, stream=stream)
             red.encode_reduce_token_major(part, wl, h2[l * m * h:(l + 1) * m * h], m, k, h,
@@ -529,7 +558,7 @@ def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, n
     if shared is not None and not bool(torch.isfinite(sout.view(torch.float16).float()).all()):
         raise RuntimeError("shared expert rows produced non-finite outputs")
     unions = nbs.cpu().numpy()
-    launches = 1 + 2 + 2 + 1 + (2 if shared is not None else 0)
+    launches = 1 + 2 + 1 + (2 if shared is not None else 0)
     return ms * 1000.0 / n_layers, float(np.mean(unions)), launches
 
 
@@ -612,9 +641,9 @@ def run_qwen(tsg, torch, args):
             "decode_m3": {"us_per_layer": round(us3, 3), "mean_union": round(u3, 2),
                           "GBps": round(bytes3 / (us3 * 1e-6) / 1e9, 2),
                           "bytes_per_layer": int(bytes3), "launches_per_layer": nl3,
-                          "path": "whole layer on the device: router rows, device grouping, "
-                                  "rows path over the device block list, reduce, shared expert "
-                                  "over the 3 rows (2 launches)"},
+                          "path": "whole layer on the device: router rows + grouping (one "
+                                  "launch), rows path over the device block list, reduce, shared "
+                                  "expert over the 3 rows (2 launches)"},
             "prefill_t4096": prefill_summary(pre)}
 
 
@@ -753,7 +782,7 @@ def run_verify(tsg, torch, ctx, args, layers, routers):
             "GBps": round(b / (us * 1e-6) / 1e9, 2),
             "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "launches_per_layer": nl,
-            "path": "whole layer on the device: router rows, device grouping (no-alloc), rows "
+            "path": "whole layer on the device: router rows + grouping (one launch), rows "
                     "path over the device block list, token-major reduce",
             "rows_path_only": {"us_per_layer": round(us0, 3), "mean_union": round(u0, 2),
                                "path": "rows path + reduce, routing precomputed on the host"}}
@@ -815,7 +844,7 @@ def _cpu_model() -> str:
 CPU_SHARE = 16
 
 
-def cpu_baseline(torch, dec, bufs, routers, offs, stride, budget_s=10.0):
+def cpu_baseline(torch, dec, bufs, routers, offs, stride, budget_s=6.0):
     """The reference's CPU path for the same math, restated in C (oracle,
     the timed build: -O3 -march=native for this host, vectorizable dot
     products like vDSP_dotpr's):
@@ -843,7 +872,7 @@ def cpu_baseline(torch, dec, bufs, routers, offs, stride, budget_s=10.0):
     def decode_us(n_threads, budget):
         oracle.set_threads(n_threads)
         done, elapsed = 0, 0.0
-        while elapsed < budget and done < 4 * LAYERS:
+        while elapsed < budget and done < 100 * LAYERS:
             x, rw, blobs = layer_in[done % LAYERS]
             t0 = time.perf_counter()
             _, rwts = oracle.router_reference(rw, x * es, TOPK, pes)
@@ -854,7 +883,7 @@ def cpu_baseline(torch, dec, bufs, routers, offs, stride, budget_s=10.0):
         return elapsed * 1e6 / done, done
 
     us_n, n_n = decode_us(threads, budget_s)
-    us_1, n_1 = decode_us(1, budget_s / 2)
+    us_1, n_1 = decode_us(1, budget_s * 5 / 6)
     # prefill: config 4's routing and inputs, every pair of a sample of tokens
     t_all = PREFILL_T
     idx_p, w_p = zipf_routing(t_all, E, TOPK, 1.1, 0x21F)
@@ -876,8 +905,8 @@ def cpu_baseline(torch, dec, bufs, routers, offs, stride, budget_s=10.0):
         flop = 2.0 * sp.size * 3 * F * H
         return flop / el / 1e12, el, sp.size, len(set(sp["expert"].tolist()))
 
-    pre_n = prefill_rate(threads, 64)
-    pre_1 = prefill_rate(1, 8)
+    pre_n = prefill_rate(threads, 512)
+    pre_1 = prefill_rate(1, 64)
     return dict(value=round(LAYER_BYTES / (us_n * 1e-6) / 1e9, 3), unit="GB/s", cores=threads,
                 kind="port",
                 sample=f"{n_n} decode layers (router + 8 experts, H=2816 F=704 sym g32) through "
@@ -889,9 +918,9 @@ def cpu_baseline(torch, dec, bufs, routers, offs, stride, budget_s=10.0):
                 build=os.path.basename(path) + " (gcc -O3 -march=native -ffp-contract=off)",
                 prefill={"unit": "TFLOP/s", "value": round(pre_n[0], 5),
                          "one_thread_value": round(pre_1[0], 5),
-                         "sample": f"config 4, first 64 tokens: {pre_n[2]} pairs over "
+                         "sample": f"config 4, first 512 tokens: {pre_n[2]} pairs over "
                                    f"{pre_n[3]} experts, {pre_n[1]:.2f} s on {threads} threads; "
-                                   f"first 8 tokens ({pre_1[2]} pairs) {pre_1[1]:.2f} s on 1 "
+                                   f"first 64 tokens ({pre_1[2]} pairs) {pre_1[1]:.2f} s on 1 "
                                    f"thread; expert-major with fp16 roundings "
                                    f"(PrefillMoEGEMMCheck.swift:138-173)"})
 
@@ -915,7 +944,7 @@ def run_floors(tsg, torch, layers, reps=8):
     stream = torch.cuda.Stream()
     rng = np.random.default_rng(0xF1)
     ids = [(rng.permutation(E)[:TOPK]).astype(np.uint32) for _ in range(4 * LAYERS)]
-    blocks, threads, lds = 256, 704, 20080  # decode_layer_kernel's launch at this shape
+    blocks, threads, lds = 256, 768, 20080  # decode_layer_kernel's launch at this shape
 
     def empty():
         for _ in range(4 * LAYERS):
@@ -988,6 +1017,8 @@ def main():
                     help="run the copy + one-token dispatches for rocprofv3 --pmc and exit")
     ap.add_argument("--floors", action="store_true",
                     help="time the decode layer's floors (empty launch, expert stream) and exit")
+    ap.add_argument("--verify-only", action="store_true",
+                    help="run only the verify M=5 figures (configs[2], for profiling) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -1006,6 +1037,10 @@ def main():
         return
     if args.floors:
         print(json.dumps({"floors": run_floors(tsg, torch, layers)}), flush=True)
+        return
+    if args.verify_only:
+        print(json.dumps({"verify_m5": run_verify(tsg, torch, ctx, args, layers, routers)}),
+              flush=True)
         return
     if args.prefill_only:
         pre = run_prefill(tsg, torch, ctx, args, layers)
@@ -1038,7 +1073,8 @@ def main():
                    "group": GROUP, "scheme": "sym", "layers": LAYERS,
                    "bytes_per_layer": LAYER_BYTES},
         "decode": {"us_per_layer": round(dec["us_per_layer"], 3), "GBps": round(gbs, 2),
-                   "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)},
+                   "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                   "routing_margin": routing_margins(torch, dec, routers)},
         "roofline": {"bound": "hbm",
                      "kernel": "decode_layer_kernel (router, top-8, gate/up+GeGLU, "
                                "down+combine in one launch)",

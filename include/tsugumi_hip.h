@@ -167,6 +167,23 @@ tsg_status tsg_moe_router_bf16_rows(tsg_moe* moe, tsg_stream stream, const uint1
                                     const uint16_t* per_expert_scale, uint32_t* out_indices,
                                     uint16_t* out_weights, uint32_t row_count,
                                     uint32_t num_experts, uint32_t d, uint32_t top_k);
+/* encodeRouterGemma4BF16Rows followed by the device grouping of its pairs
+ * (tsg_prefill_group_pairs_device, any tile_rows >= 8) in one launch: the
+ * verify block's routing and grouping (RealForwardRunner.swift:1826-1872,
+ * 2116-2151) with nothing read back to the host. Every output equals the two
+ * calls' bit for bit: out_indices/out_weights [row_count, 8]; sorted
+ * [row_count * 8], offsets and counts [num_experts], blocks (one per expert
+ * present, in expert order, local_row = pair_start) and *n_blocks on the
+ * device. max_blocks >= min(row_count * 8, num_experts); row_count * d * 2 <=
+ * 64 KiB. Returns TSG_ERR_DECLINED for row_count 0 or > 8. No counterpart
+ * entry in the reference, which groups on the host. */
+tsg_status tsg_moe_router_bf16_rows_grouped(
+    tsg_moe* moe, tsg_stream stream, const uint16_t* weights, const uint16_t* hidden,
+    uint32_t hidden_stride_elements, const uint16_t* effective_scale,
+    const uint16_t* per_expert_scale, uint32_t* out_indices, uint16_t* out_weights,
+    uint32_t row_count, uint32_t num_experts, uint32_t d, uint32_t top_k,
+    tsg_token_expert_pair* sorted, uint32_t* offsets, uint32_t* counts,
+    tsg_routed_block* blocks, uint32_t max_blocks, uint32_t* n_blocks);
 /* encodeRouterLogitsBF16 (MoE.swift:316-345): the GEMV alone. */
 tsg_status tsg_moe_router_logits_bf16(tsg_moe* moe, tsg_stream stream, const uint16_t* weights,
                                       const uint16_t* hidden, const uint16_t* effective_scale,

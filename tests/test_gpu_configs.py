@@ -300,6 +300,55 @@ def test_verify_whole_layer_on_device(tsg, ctx, gemma_layer, qwen_layer, shape):
     assert rel <= kc.NORTH_STAR
 
 
+@pytest.mark.parametrize("m,ne,d", [(5, 128, 2816), (3, 256, 2048), (1, 128, 2816),
+                                    (8, 128, 2816)])
+def test_router_rows_grouped_matches_router_then_grouping(tsg, ctx, m, ne, d):
+    """tsg_moe_router_bf16_rows_grouped gives the rows router's indices and
+    weights and the device grouping's sorted pairs, offsets, counts and block
+    list, bit for bit (random effective and per-expert scales)."""
+    k = 8
+    rng = np.random.default_rng(0x6A0 + m * 7 + ne)
+    x0 = rng.normal(0.0, 1.0, d)
+    hidden = oracle.f16_bits((x0[None, :] + 0.35 * rng.normal(0.0, 1.0, (m, d)))
+                             .astype(np.float32)).ravel()
+    rw = oracle.bf16_bits(rng.normal(0.0, 1.0 / np.sqrt(d), ne * d).astype(np.float32))
+    es = oracle.bf16_bits((1.0 + 0.1 * rng.normal(0.0, 1.0, d)).astype(np.float32))
+    pes = oracle.bf16_bits((0.5 + np.abs(rng.normal(0.0, 1.0, ne))).astype(np.float32))
+    RW, X, ES, PES = dev(rw), dev(hidden), dev(es), dev(pes)
+    moe = tsg.MoE(ctx)
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    max_blocks = m * k
+
+    def outs():
+        return dict(idx=empty(m * k, np.uint32, fill=-1), w=empty(m * k, fill=-1),
+                    sp=empty(m * k * 4, np.uint32, fill=-1), off=empty(ne, np.uint32, fill=-1),
+                    cnt=empty(ne, np.uint32, fill=-1), bl=empty(max_blocks * 4, np.uint32, fill=-1),
+                    nb=empty(1, np.uint32, fill=-1))
+
+    a = outs()
+    moe.encode_router_gemma4_bf16_rows(RW, X, d, ES, PES, a["idx"], a["w"], m, ne, d)
+    scratch = empty(g.scratch_bytes(m, k, ne) // 4 + 1, np.uint32)
+    g.group_pairs_device(a["idx"], a["w"], m, k, ne, a["sp"], a["off"], a["cnt"], a["bl"],
+                         max_blocks, a["nb"], scratch, tile_rows=32)
+    b = outs()
+    moe.encode_router_gemma4_bf16_rows_grouped(RW, X, d, ES, PES, b["idx"], b["w"], m, ne, d,
+                                               b["sp"], b["off"], b["cnt"], b["bl"], max_blocks,
+                                               b["nb"])
+    ctx.synchronize()
+    n = int(host(a["nb"], np.uint32)[0])
+    assert n == int(host(b["nb"], np.uint32)[0]) and 8 <= n <= m * k
+    for key in ("idx", "w", "sp", "off", "cnt"):
+        dt = np.uint16 if key == "w" else np.uint32
+        assert np.array_equal(host(a[key], dt), host(b[key], dt)), key
+    assert np.array_equal(host(a["bl"], np.uint32)[:4 * n], host(b["bl"], np.uint32)[:4 * n])
+    # the one-row router on each row gives the same indices
+    for r in range(m):
+        i1, w1 = empty(k, np.uint32), empty(k)
+        moe.encode_router_gemma4_bf16(RW, X[r * d:], ES, PES, i1, w1, ne, d)
+        assert np.array_equal(host(i1, np.uint32), host(b["idx"], np.uint32)[r * k:(r + 1) * k])
+        assert np.array_equal(host(w1, np.uint16), host(b["w"], np.uint16)[r * k:(r + 1) * k])
+
+
 def test_rows_device_list_skips_and_reports(tsg, ctx, gemma_layer):
     """Blocks past the device count are not run; a live block the rows path
     cannot take (9 rows) is skipped and reported at synchronisation."""

@@ -347,6 +347,19 @@ class MoE:
             _ptr(effective_scale), _ptr(per_expert_scale), _ptr(out_indices),
             _ptr(out_weights), row_count, num_experts, d, top_k))
 
+    def encode_router_gemma4_bf16_rows_grouped(self, weights, hidden, hidden_stride_elements,
+                                               effective_scale, per_expert_scale, out_indices,
+                                               out_weights, row_count, num_experts, d,
+                                               sorted_pairs, offsets, counts, blocks, max_blocks,
+                                               n_blocks, top_k=8, stream=None):
+        """encode_router_gemma4_bf16_rows + the device grouping of its pairs
+        in one launch (the outputs of both, bit for bit)."""
+        check(self.lib.tsg_moe_router_bf16_rows_grouped(
+            self.handle, _stream(stream), _ptr(weights), _ptr(hidden), hidden_stride_elements,
+            _ptr(effective_scale), _ptr(per_expert_scale), _ptr(out_indices), _ptr(out_weights),
+            row_count, num_experts, d, top_k, _ptr(sorted_pairs), _ptr(offsets), _ptr(counts),
+            _ptr(blocks), max_blocks, _ptr(n_blocks)))
+
     def encode_router_logits_bf16(self, weights, hidden, effective_scale, out_logits,
                                   num_experts, d, stream=None):
         check(self.lib.tsg_moe_router_logits_bf16(

@@ -110,6 +110,8 @@ SIGNATURES = {
     "tsg_moe_destroy": (None, [P]),
     "tsg_moe_router_bf16": (C.c_int, [P, P, P, P, P, P, P, P, U32, U32, U32]),
     "tsg_moe_router_bf16_rows": (C.c_int, [P, P, P, P, U32, P, P, P, P, U32, U32, U32, U32]),
+    "tsg_moe_router_bf16_rows_grouped": (C.c_int, [P, P, P, P, U32, P, P, P, P, U32, U32, U32,
+                                                   U32, P, P, P, P, U32, P]),
     "tsg_moe_router_logits_bf16": (C.c_int, [P, P, P, P, P, P, U32, U32]),
     "tsg_moe_phase1": (C.c_int, [P, P, P, C.POINTER(ExpertOffsets), P, P, U32, U32, U32]),
     "tsg_moe_phase1_subset": (C.c_int, [P, P, P, C.POINTER(ExpertOffsets), P, P, P, U32,

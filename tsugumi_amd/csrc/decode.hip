@@ -252,76 +252,6 @@ __device__ __forceinline__ float router_dot(const uint16_t* __restrict__ w_row,
     return router_chunks_dot(wv, xv, ev, nchunks, lane);
 }
 
-// One expert row against up to kRouterRows activation rows in the canonical
-// order: lane l sums chunks l, l+64, ... (elements in order, acc = fma(w,
-// x*es, acc)); each 16-lane row then sums as group16_sum does (pairs, pairs of
-// pairs, mirrored quads, mirrored 8s) and the four row sums add as
-// (r0 + r1) + (r2 + r3). Every lane ends with the full sum. Loads for all chunks are issued before
-// any arithmetic; out-of-range chunks load a clamped address and contribute
-// nothing.
-template <bool SELECT>
-__global__ __launch_bounds__(256) void router_kernel(
-    const uint16_t* __restrict__ w, const uint16_t* __restrict__ hidden, uint32_t hidden_stride,
-    const uint16_t* __restrict__ es, const uint16_t* __restrict__ pes,
-    float* __restrict__ logits, uint32_t logits_stride, uint32_t* __restrict__ counters,
-    uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w, uint32_t ne, uint32_t d,
-    uint32_t rows, uint32_t top_k) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t e = blockIdx.x * kRouterWaves + wave;
-    const uint32_t r0 = blockIdx.y * kRouterRows;
-    const uint32_t nr = min(kRouterRows, rows - r0);
-    const uint32_t nchunks = d / 8u;
-    uint32_t gains[4] = {0u, 0u, 0u, 0u};
-    if constexpr (SELECT) load_expert_gains(pes, ne, gains);
-    if (e < ne) {
-        const uint16_t* wr = w + (uint64_t)e * d;
-        uint4 wv[kRouterChunks], ev[kRouterChunks], xv[kRouterChunks];
-#pragma unroll
-        for (int i = 0; i < kRouterChunks; ++i) {
-            const uint32_t cc = min(lane + 64u * i, nchunks - 1u);
-            wv[i] = *reinterpret_cast<const uint4*>(wr + cc * 8u);
-            ev[i] = *reinterpret_cast<const uint4*>(es + cc * 8u);
-            xv[i] = *reinterpret_cast<const uint4*>(hidden + (uint64_t)r0 * hidden_stride + cc * 8u);
-        }
-        for (uint32_t r = 0; r < nr; ++r) {
-            // next row's activations go out before this row's arithmetic
-            uint4 xn[kRouterChunks];
-            const uint32_t rn = (r + 1 < nr) ? r + 1 : r;
-            const uint16_t* xnext = hidden + (uint64_t)(r0 + rn) * hidden_stride;
-#pragma unroll
-            for (int i = 0; i < kRouterChunks; ++i) {
-                const uint32_t cc = min(lane + 64u * i, nchunks - 1u);
-                xn[i] = *reinterpret_cast<const uint4*>(xnext + cc * 8u);
-            }
-            const float acc = router_chunks_dot(wv, xv, ev, nchunks, lane);
-#pragma unroll
-            for (int i = 0; i < kRouterChunks; ++i) xv[i] = xn[i];
-            if (lane == 0)
-                st_coherent(reinterpret_cast<uint32_t*>(logits) + (uint64_t)(r0 + r) * logits_stride + e,
-                            __float_as_uint(acc));
-        }
-    }
-    if constexpr (SELECT) {
-        // logits travel by agent-coherent stores/loads: completing this
-        // block's stores before it counts itself is all the last block needs
-        __shared__ uint32_t is_last;
-        wait_vector_memory();
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const uint32_t done = atomicAdd(&counters[blockIdx.y], 1u);
-            is_last = (done == gridDim.x - 1u) ? 1u : 0u;
-        }
-        __syncthreads();
-        if (is_last) {
-            for (uint32_t r = wave; r < nr; r += kRouterWaves)
-                wave_topk_softmax(logits + (uint64_t)(r0 + r) * logits_stride, ne, gains,
-                                  out_idx + (uint64_t)(r0 + r) * kTopK,
-                                  out_w + (uint64_t)(r0 + r) * kTopK);
-            if (threadIdx.x == 0) atomicExch(&counters[blockIdx.y], 0u);
-        }
-    }
-}
-
 // ------------------------------------------------------- phase geometry
 
 // Phase 1: a block owns `pairs` (slot, f) row pairs, 32 lanes each (16 on the
@@ -783,6 +713,271 @@ __device__ __forceinline__ void wave_select_top8(const uint32_t (&key)[4], uint3
     }
 }
 
+// Outputs of the grouping the rows router can append (GROUP): those of
+// tsg_prefill_group_pairs_device for the routed rows.
+struct RouterGroupOut {
+    tsg_token_expert_pair* sorted;
+    uint32_t* offsets;
+    uint32_t* counts;
+    tsg_routed_block* blocks;
+    uint32_t* n_blocks;
+};
+
+// The grouping of the rows' n = rows * 8 pairs (token-major pair p = 8 t + r
+// with expert pe[p], weight bits pw[p], in LDS; n <= 64) on one block, the
+// device grouping's results: pairs stably sorted by expert, per-expert
+// counts and exclusive offsets (0xFFFFFFFF for an expert with no pairs), and
+// one routed block per expert present (an expert's <= 8 rows fit any tile),
+// in expert order, which is the device grouping's largest-first order when
+// every block is in the first size bucket. A counting sort: an LDS
+// histogram, one scan over the experts (counts and presence packed in one
+// word), and each pair's place = its expert's offset + the earlier tokens
+// that chose the expert (a token's 8 experts are distinct; per-token expert
+// bit masks in LDS). Every thread of the block calls it; it synchronises
+// through LDS only and stores its results last.
+constexpr uint32_t kGroupPairs = kMaxRouterRows * kTopK;  // 64
+constexpr uint32_t kMaskWords = kMaxExperts / 32u;        // 8
+
+struct RouterGroupLds {
+    uint32_t cnt[kMaxExperts], off[kMaxExperts];
+    uint32_t mask[kMaxRouterRows * kMaskWords];
+    uint32_t wave_tot[kMaxExperts / 64u];
+};
+
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (uint32_t d = 1; d < 64u; d <<= 1) {
+        const uint32_t u = __shfl_up(v, d);
+        v += lane >= d ? u : 0u;
+    }
+    return v;
+}
+
+__device__ void group_router_rows(const uint32_t* pe, const uint32_t* pw, uint32_t n,
+                                  uint32_t ne, RouterGroupLds& L, const RouterGroupOut& g) {
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    if (t < kMaxExperts) L.cnt[t] = 0u;
+    if (t < kMaxRouterRows * kMaskWords) L.mask[t] = 0u;
+    lds_barrier();
+    const bool my_pair = t < n;
+    const uint32_t my_e = my_pair ? pe[t] : 0u, my_w = my_pair ? pw[t] : 0u;
+    const uint32_t tok = t / kTopK;
+    if (my_pair) {
+        atomicAdd(&L.cnt[my_e], 1u);
+        atomicOr(&L.mask[tok * kMaskWords + (my_e >> 5)], 1u << (my_e & 31u));
+    }
+    lds_barrier();
+    // offsets (low half) and block indices (high half) of the experts
+    const uint32_t c = t < ne ? L.cnt[t] : 0u;
+    const uint32_t packed = c | ((c ? 1u : 0u) << 16);
+    const uint32_t incl = t < kMaxExperts ? wave_inclusive_scan(packed) : 0u;
+    if (t < kMaxExperts && lane == 63u) L.wave_tot[wave] = incl;
+    lds_barrier();
+    uint32_t base = 0, total = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < kMaxExperts / 64u; ++w) {
+        base += w < wave ? L.wave_tot[w] : 0u;
+        total += L.wave_tot[w];
+    }
+    const uint32_t excl = base + incl - packed;
+    const uint32_t off = excl & 0xFFFFu, bidx = excl >> 16;
+    if (t < ne) L.off[t] = off;
+    lds_barrier();
+    uint32_t pos = 0;
+    if (my_pair) {
+        uint32_t rank = 0;
+        for (uint32_t u = 0; u < tok; ++u)
+            rank += (L.mask[u * kMaskWords + (my_e >> 5)] >> (my_e & 31u)) & 1u;
+        pos = L.off[my_e] + rank;
+    }
+    // every LDS read is done: the results leave
+    if (my_pair) {
+        tsg_token_expert_pair pr;
+        pr.token = tok;
+        pr.expert = my_e;
+        pr.rank = t % kTopK;
+        pr.weight_bits = my_w;
+        g.sorted[pos] = pr;
+    }
+    if (t < ne) {
+        g.counts[t] = c;
+        g.offsets[t] = c ? off : 0xFFFFFFFFu;  // the device grouping's mark of an absent expert
+        if (c) {
+            tsg_routed_block b;
+            b.local_slot = t;
+            b.pair_start = off;
+            b.row_count = c;
+            b.local_row = off;
+            g.blocks[bidx] = b;
+        }
+    }
+    if (t == 0) g.n_blocks[0] = total >> 16;
+}
+
+// One expert row against up to kRouterRows activation rows in the canonical
+// order: lane l sums chunks l, l+64, ... (elements in order, acc = fma(w,
+// x*es, acc)); each 16-lane row then sums as group16_sum does (pairs, pairs of
+// pairs, mirrored quads, mirrored 8s) and the four row sums add as
+// (r0 + r1) + (r2 + r3). Every lane ends with the full sum. Loads for all
+// chunks are issued before any arithmetic; out-of-range chunks load a clamped
+// address and contribute nothing.
+//  - one row or a prompt's rows: block b holds experts 4b .. 4b + 3, one per
+//    wave, each wave taking the rows in turn (the next row's activations
+//    requested before this row's sums); the last block ranks each row on one
+//    wave (wave_topk_softmax).
+//  - STAGE (2..8 rows, or GROUP): block e holds expert e and copies the rows
+//    to LDS once, after its weight row is requested; wave w takes rows w,
+//    w + 4. The last block ranks each row on one wave with the candidate
+//    top-8 and the slot softmax of the one-launch layer (wave_select_top8,
+//    slot_softmax_lane; the same indices and weights). Same sums as the
+//    unstaged form.
+//  - GROUP (with STAGE): the last block then groups the rows' pairs
+//    (group_router_rows).
+constexpr uint32_t kStageWaves = 8;  // the staged form: one wave per row
+static_assert(kMaxRouterRows <= kStageWaves, "one row per wave");
+
+template <bool SELECT, bool STAGE, bool GROUP>
+__global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kernel(
+    const uint16_t* __restrict__ w, const uint16_t* __restrict__ hidden, uint32_t hidden_stride,
+    const uint16_t* __restrict__ es, const uint16_t* __restrict__ pes,
+    float* __restrict__ logits, uint32_t logits_stride, uint32_t* __restrict__ counters,
+    uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w, uint32_t ne, uint32_t d,
+    uint32_t rows, uint32_t top_k, RouterGroupOut grp) {
+    static_assert(!GROUP || (SELECT && STAGE), "the grouping follows a staged selection");
+    static_assert(!STAGE || SELECT, "the staged form selects");
+    extern __shared__ __align__(16) uint4 xrows[];  // STAGE: the block's rows, d / 8 units each
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t e = STAGE ? blockIdx.x : blockIdx.x * kRouterWaves + wave;
+    const uint32_t r0 = blockIdx.y * kRouterRows;
+    const uint32_t nr = min(kRouterRows, rows - r0);
+    const uint32_t nchunks = d / 8u;
+    uint32_t gains[4] = {0u, 0u, 0u, 0u};
+    if constexpr (SELECT && !STAGE) load_expert_gains(pes, ne, gains);
+    // STAGE: thread t's expert gain, for the last block (requested early)
+    const uint32_t my_gain = (STAGE && threadIdx.x < ne) ? pes[threadIdx.x] : 0u;
+    uint4 wv[kRouterChunks], ev[kRouterChunks], xv[kRouterChunks];
+    if (e < ne) {
+        const uint16_t* wr = w + (uint64_t)e * d;
+#pragma unroll
+        for (int i = 0; i < kRouterChunks; ++i) {
+            const uint32_t cc = min(lane + 64u * i, nchunks - 1u);
+            wv[i] = *reinterpret_cast<const uint4*>(wr + cc * 8u);
+            ev[i] = *reinterpret_cast<const uint4*>(es + cc * 8u);
+            if constexpr (!STAGE)
+                xv[i] = *reinterpret_cast<const uint4*>(hidden + (uint64_t)r0 * hidden_stride + cc * 8u);
+        }
+    }
+    if constexpr (STAGE) {
+        for (uint32_t q = threadIdx.x; q < nr * nchunks; q += blockDim.x) {
+            const uint32_t r = q / nchunks, c = q - r * nchunks;
+            xrows[q] = *reinterpret_cast<const uint4*>(hidden + (uint64_t)(r0 + r) * hidden_stride + c * 8u);
+        }
+        __syncthreads();
+        for (uint32_t r = wave; r < nr; r += kStageWaves) {
+#pragma unroll
+            for (int i = 0; i < kRouterChunks; ++i)
+                xv[i] = xrows[r * nchunks + min(lane + 64u * i, nchunks - 1u)];
+            const float acc = router_chunks_dot(wv, xv, ev, nchunks, lane);
+            if (lane == 0)
+                st_coherent(reinterpret_cast<uint32_t*>(logits) + (uint64_t)(r0 + r) * logits_stride + e,
+                            __float_as_uint(acc));
+        }
+    } else if (e < ne) {
+        for (uint32_t r = 0; r < nr; ++r) {
+            // next row's activations go out before this row's arithmetic
+            uint4 xn[kRouterChunks];
+            const uint32_t rn = (r + 1 < nr) ? r + 1 : r;
+            const uint16_t* xnext = hidden + (uint64_t)(r0 + rn) * hidden_stride;
+#pragma unroll
+            for (int i = 0; i < kRouterChunks; ++i) {
+                const uint32_t cc = min(lane + 64u * i, nchunks - 1u);
+                xn[i] = *reinterpret_cast<const uint4*>(xnext + cc * 8u);
+            }
+            const float acc = router_chunks_dot(wv, xv, ev, nchunks, lane);
+#pragma unroll
+            for (int i = 0; i < kRouterChunks; ++i) xv[i] = xn[i];
+            if (lane == 0)
+                st_coherent(reinterpret_cast<uint32_t*>(logits) + (uint64_t)(r0 + r) * logits_stride + e,
+                            __float_as_uint(acc));
+        }
+    }
+    if constexpr (SELECT) {
+        // logits travel by agent-coherent stores/loads: completing this
+        // block's stores before it counts itself is all the last block needs
+        __shared__ uint32_t is_last;
+        wait_vector_memory();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const uint32_t done = atomicAdd(&counters[blockIdx.y], 1u);
+            is_last = (done == gridDim.x - 1u) ? 1u : 0u;
+        }
+        __syncthreads();
+        if (is_last) {
+            if constexpr (STAGE) {
+                __shared__ uint32_t s_gain[kMaxExperts];
+                __shared__ __align__(16) uint64_t s_cand[kStageWaves][kMaxExperts + kCandBatch];
+                __shared__ uint32_t s_sid[kStageWaves][kTopK], s_sfill[kStageWaves][kTopK];
+                __shared__ uint32_t s_skey[kStageWaves][kTopK];
+                __shared__ uint32_t s_pe[kGroupPairs], s_pw[kGroupPairs];
+                static_assert(kMaxExperts <= 64u * kStageWaves, "one gain per thread");
+                const uint32_t t = threadIdx.x;
+                if (t < kMaxExperts) s_gain[t] = my_gain;
+                lds_barrier();
+                const uint32_t ne4 = (ne + 3u) & ~3u;
+                const uint32_t r = wave;  // one row per wave
+                if (r < nr) {
+                    uint32_t key[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t ej = lane + 64u * j;
+                        const float v = ej < ne ? __uint_as_float(ld_coherent(
+                                                      reinterpret_cast<const uint32_t*>(logits) +
+                                                      (uint64_t)(r0 + r) * logits_stride + ej))
+                                                : -INFINITY;
+                        key[j] = (v == v && v != -INFINITY) ? order_key(v) : 0u;
+                    }
+                    if (lane < kTopK) {
+                        s_sid[wave][lane] = 0u;
+                        s_sfill[wave][lane] = 0u;
+                        s_skey[wave][lane] = 0u;
+                    }
+                    wave_select_top8(key, ne4, s_cand[wave], s_sid[wave], s_sfill[wave],
+                                     s_skey[wave]);
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // one wave: LDS in order
+                    const uint32_t sl = lane & (kTopK - 1u);
+                    const uint32_t id = s_sid[wave][sl];
+                    const float my_s = s_sfill[wave][sl] ? order_key_value(s_skey[wave][sl]) : -INFINITY;
+                    const uint16_t wb = slot_softmax_lane(my_s, bf16_to_f32((uint16_t)s_gain[id]));
+                    if (lane < kTopK) {
+                        s_pe[r * kTopK + lane] = id;
+                        s_pw[r * kTopK + lane] = wb;
+                    }
+                }
+                // the results leave after all the LDS work (a wave's next LDS
+                // read would wait for its global stores in flight)
+                lds_barrier();
+                const bool my_pair = t < nr * kTopK;
+                const uint32_t my_id = my_pair ? s_pe[t] : 0u, my_wb = my_pair ? s_pw[t] : 0u;
+                if constexpr (GROUP) {
+                    __shared__ RouterGroupLds gl;
+                    group_router_rows(s_pe, s_pw, nr * kTopK, ne, gl, grp);
+                }
+                if (my_pair) {
+                    out_idx[(uint64_t)r0 * kTopK + t] = my_id;
+                    out_w[(uint64_t)r0 * kTopK + t] = (uint16_t)my_wb;
+                }
+            } else {
+                for (uint32_t r = wave; r < nr; r += kRouterWaves)
+                    wave_topk_softmax(logits + (uint64_t)(r0 + r) * logits_stride, ne, gains,
+                                      out_idx + (uint64_t)(r0 + r) * kTopK,
+                                      out_w + (uint64_t)(r0 + r) * kTopK);
+            }
+            if (threadIdx.x == 0) atomicExch(&counters[blockIdx.y], 0u);
+        }
+    }
+}
+
 // One decode MoE layer in one launch (kDecodeBlocks blocks, all co-resident).
 // Per group g: router logits -> top-8 (every block) -> gate/up + activation of
 // slot g (pairs per block) -> down rows of slot g -> partials -> slot-ordered
@@ -1153,7 +1348,7 @@ tsg_status router_launch(tsg_moe* moe, hipStream_t stream, const uint16_t* w,
                          const uint16_t* hidden, uint32_t stride, const uint16_t* es,
                          const uint16_t* pes, uint32_t* out_idx, uint16_t* out_w,
                          float* logits_out, uint32_t rows, uint32_t ne, uint32_t d,
-                         uint32_t top_k, bool select) {
+                         uint32_t top_k, bool select, const RouterGroupOut* group = nullptr) {
     TSG_REQUIRE(ne > 0 && ne <= kMaxExperts, TSG_ERR_INVALID_ARGUMENT,
                 "numExperts %u not in 1..%u", ne, kMaxExperts);
     TSG_REQUIRE(d > 0 && d % 8 == 0 && d <= 8u * 64u * kRouterChunks, TSG_ERR_INVALID_ARGUMENT,
@@ -1167,18 +1362,39 @@ tsg_status router_launch(tsg_moe* moe, hipStream_t stream, const uint16_t* w,
                 "rows=%u not in 1..%u", rows, kMaxPromptRows);
     tsg_ctx* ctx = moe->ctx;
     const dim3 grid((ne + kRouterWaves - 1) / kRouterWaves, (rows + kRouterRows - 1) / kRouterRows);
+    // a few rows of one y-block are staged in LDS (same sums, no per-row
+    // round trip to memory); the one-row and prompt-sized forms are not
+    const size_t stage = (size_t)rows * d * 2u;
+    const bool staged = select && (rows > 1 || group) && rows <= kMaxRouterRows &&
+                        stage <= 64u * 1024u;
+    TSG_REQUIRE(!group || staged, TSG_ERR_UNSUPPORTED,
+                "the grouped router takes 1..%u rows of at most %zu bytes", kMaxRouterRows,
+                (size_t)64u * 1024u);
+    const dim3 sgrid(ne, 1);  // staged: one expert per block
     if (select) {
         TSG_REQUIRE(top_k == kTopK, TSG_ERR_INVALID_ARGUMENT, "topK must be %u, got %u", kTopK,
                     top_k);
         TSG_REQUIRE(pes && out_idx && out_w, TSG_ERR_INVALID_ARGUMENT, "NULL router output");
-        hipLaunchKernelGGL(router_kernel<true>, grid, dim3(256), 0, stream, w, hidden, stride, es,
-                           pes, ctx->logits, kMaxExperts, ctx->counters, out_idx, out_w, ne, d,
-                           rows, top_k);
+        if (staged) {
+            auto kern = group ? router_kernel<true, true, true> : router_kernel<true, true, false>;
+            // the staged rows take up to 64 KiB of dynamic LDS (idempotent)
+            TSG_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            64 * 1024));
+            hipLaunchKernelGGL(kern, sgrid, dim3(64u * kStageWaves), stage, stream, w, hidden,
+                               stride, es, pes,
+                               ctx->logits, kMaxExperts, ctx->counters, out_idx, out_w, ne, d,
+                               rows, top_k, group ? *group : RouterGroupOut{});
+        }
+        else
+            hipLaunchKernelGGL((router_kernel<true, false, false>), grid, dim3(256), 0, stream, w,
+                               hidden, stride, es, pes, ctx->logits, kMaxExperts, ctx->counters,
+                               out_idx, out_w, ne, d, rows, top_k, RouterGroupOut{});
     } else {
         TSG_REQUIRE(logits_out, TSG_ERR_INVALID_ARGUMENT, "out_logits is NULL");
-        hipLaunchKernelGGL(router_kernel<false>, grid, dim3(256), 0, stream, w, hidden, stride,
-                           es, pes, logits_out, ne, ctx->counters, out_idx, out_w, ne, d, rows,
-                           top_k);
+        hipLaunchKernelGGL((router_kernel<false, false, false>), grid, dim3(256), 0, stream, w,
+                           hidden, stride, es, pes, logits_out, ne, ctx->counters, out_idx, out_w,
+                           ne, d, rows, top_k, RouterGroupOut{});
     }
     return check_launch("router");
 }
@@ -1385,6 +1601,28 @@ extern "C" tsg_status tsg_moe_router_bf16_rows(tsg_moe* moe, tsg_stream stream,
                     rows);
     return router_launch(moe, as_stream(stream), w, hidden, stride, es, pes, out_idx, out_w,
                          nullptr, rows, ne, d, top_k, true);
+}
+
+extern "C" tsg_status tsg_moe_router_bf16_rows_grouped(
+    tsg_moe* moe, tsg_stream stream, const uint16_t* w, const uint16_t* hidden, uint32_t stride,
+    const uint16_t* es, const uint16_t* pes, uint32_t* out_idx, uint16_t* out_w, uint32_t rows,
+    uint32_t ne, uint32_t d, uint32_t top_k, tsg_token_expert_pair* sorted, uint32_t* offsets,
+    uint32_t* counts, tsg_routed_block* blocks, uint32_t max_blocks, uint32_t* n_blocks) {
+    tsg_status st = check_moe(moe);
+    if (st) return st;
+    TSG_REQUIRE(top_k == kTopK, TSG_ERR_INVALID_ARGUMENT, "topK must be %u, got %u", kTopK, top_k);
+    TSG_REQUIRE(ne <= kMaxExperts, TSG_ERR_INVALID_ARGUMENT, "numExperts %u > %u", ne, kMaxExperts);
+    if (rows == 0 || rows > kMaxRouterRows)
+        return fail(TSG_ERR_DECLINED, "rows router takes 1..%u rows, got %u", kMaxRouterRows,
+                    rows);
+    TSG_REQUIRE(sorted && offsets && counts && blocks && n_blocks, TSG_ERR_INVALID_ARGUMENT,
+                "NULL grouping output");
+    TSG_REQUIRE(max_blocks >= std::min(rows * kTopK, ne), TSG_ERR_INVALID_ARGUMENT,
+                "max_blocks %u cannot hold the work list: need min(rows*8, numExperts) = %u",
+                max_blocks, std::min(rows * kTopK, ne));
+    const RouterGroupOut g{sorted, offsets, counts, blocks, n_blocks};
+    return router_launch(moe, as_stream(stream), w, hidden, stride, es, pes, out_idx, out_w,
+                         nullptr, rows, ne, d, top_k, true, &g);
 }
 
 extern "C" tsg_status tsg_moe_router_logits_bf16(tsg_moe* moe, tsg_stream stream,

@@ -210,6 +210,14 @@ __device__ __forceinline__ uint4 ld_coherent16(const void* p) {
     const uint64_t lo = ld_coherent(q), hi = ld_coherent(q + 1);
     return make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
 }
+// Workgroup barrier for data exchanged through LDS only: this wave's LDS
+// operations complete, then s_barrier. Unlike __syncthreads() it does not
+// wait for the wave's outstanding global stores (its release fence would).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 // Blocks until this wave's outstanding vector memory operations (coherent
 // stores included) have completed; also a compiler barrier.
 __device__ __forceinline__ void wait_vector_memory() {
