@@ -71,13 +71,22 @@ __device__ __forceinline__ void compute_batch(const ChunkBatch<KB>& bt, uint32_t
         const float s = bf16_to_f32((uint16_t)bt.s[i]);
         float b = 0.0f;
         if constexpr (!SYM) b = bf16_to_f32((uint16_t)bt.b[i]);
+        if constexpr (R == 1) {
+            float v = __builtin_fmaf(s, chunk_dot(bt.w[i], staged_chunk(xs, cc), bias), acc[0]);
+            if constexpr (!SYM) v = __builtin_fmaf(b, xsum[cc], v);
+            acc[0] = live ? v : acc[0];  // a chunk past the row end leaves acc as it is
+        } else {
+            // several rows: the chunk's weights are unpacked once for all of them
+            h2_t q[16];
+            chunk_pairs(bt.w[i], bias, q);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if ((uint32_t)r >= nrows) break;
-            float v = __builtin_fmaf(s, chunk_dot(bt.w[i], staged_chunk(xs + (size_t)r * row_h, cc), bias),
-                                     acc[r]);
-            if constexpr (!SYM) v = __builtin_fmaf(b, xsum[r * nchunks + cc], v);
-            acc[r] = live ? v : acc[r];  // a chunk past the row end leaves acc as it is
+            for (int r = 0; r < R; ++r) {
+                if ((uint32_t)r >= nrows) break;
+                float v = __builtin_fmaf(s, chunk_dot_pairs(q, staged_chunk(xs + (size_t)r * row_h, cc)),
+                                         acc[r]);
+                if constexpr (!SYM) v = __builtin_fmaf(b, xsum[r * nchunks + cc], v);
+                acc[r] = live ? v : acc[r];
+            }
         }
     }
 }

@@ -292,6 +292,22 @@ __device__ __forceinline__ float chunk_dot(uint4 w, const h2_t* xp, h2_t bias) {
     return acc;
 }
 
+// The same in two steps, for a chunk used against several activation rows:
+// its 16 pairs once (chunk_pairs), then chunk_dot's dot2 sequence per row
+// (chunk_dot_pairs), which gives chunk_dot's bits.
+__device__ __forceinline__ void chunk_pairs(uint4 w, h2_t bias, h2_t (&q)[16]) {
+    nib8_to_pairs(w.x, bias, q);
+    nib8_to_pairs(w.y, bias, q + 4);
+    nib8_to_pairs(w.z, bias, q + 8);
+    nib8_to_pairs(w.w, bias, q + 12);
+}
+__device__ __forceinline__ float chunk_dot_pairs(const h2_t (&q)[16], const h2_t* xp) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = dot2(q[i], xp[i], acc);
+    return acc;
+}
+
 // Position of element k (0..7) of an 8-element block in paired order.
 __host__ __device__ __forceinline__ uint32_t paired_pos(uint32_t k) {
     return (k & 3u) * 2u + (k >> 2);
