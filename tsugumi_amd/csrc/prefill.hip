@@ -543,23 +543,31 @@ __device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uin
                                            f16v_t (&acc)[NT][2]) {
     constexpr uint32_t W = gemm_window<G>();
     constexpr uint32_t kNS = SYM ? 4u : 8u;
-    // Loads allowed in flight: chunk c + 1's (4 activation + 2 weight) and
-    // the scale window started at chunk c - 1 or c - 2, if any.
-    const bool s_recent = (c >= 1u && (c - 1u) % W == 0u) || (c >= 2u && (c - 2u) % W == 0u);
-    if (L.a_wave) {
-        if (s_recent) wait_vmcnt<6u + kNS>();
-        else wait_vmcnt<6u>();
+    // Loads allowed in flight: chunk c + 1's (4 activation + 2 weight), if
+    // there is one, and the scale window started at chunk c - 1 or c - 2, if
+    // any (nothing past the last chunk or window is requested).
+    const bool next = c + 1u < L.nchunks;
+    const bool s_recent = (c >= 1u && (c - 1u) % W == 0u && (c - 1u) / W + 1u < L.nwin) ||
+                          (c >= 2u && (c - 2u) % W == 0u && (c - 2u) / W + 1u < L.nwin);
+    if (next) {
+        if (L.a_wave) {
+            if (s_recent) wait_vmcnt<6u + kNS>();
+            else wait_vmcnt<6u>();
+        } else {
+            if (s_recent) wait_vmcnt<2u + kNS>();
+            else wait_vmcnt<2u>();
+        }
     } else {
-        if (s_recent) wait_vmcnt<2u + kNS>();
-        else wait_vmcnt<2u>();
+        if (s_recent) wait_vmcnt<kNS>();
+        else wait_vmcnt<0u>();
     }
     block_barrier();
     // Chunk c - 1's stage and the scale window before this one are free now
     // (every wave has passed the barrier): start chunk c + 2 and, at a
     // window's first chunk, the next window before this chunk's MFMAs, so two
     // chunks are in flight while one is computed.
-    gemm_issue<(ST + 2) % 3>(L, smem, c + 2u);
-    if (c % W == 0u) gemm_issue_scales<G, SYM>(L, smem, c / W + 1u);
+    if (c + 2u < L.nchunks) gemm_issue<(ST + 2) % 3>(L, smem, c + 2u);
+    if (c % W == 0u && c / W + 1u < L.nwin) gemm_issue_scales<G, SYM>(L, smem, c / W + 1u);
     if (L.live) {
         const uint32_t win = c / W, lane = threadIdx.x & 63u, h = lane >> 5;
         const uint32_t wb = window_byte<G>(win), gb = group_byte<G>(c, h);
@@ -670,7 +678,7 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
 
     gemm_issue_scales<G, SYM>(L, smem, 0u);
     gemm_issue<0>(L, smem, 0u);
-    gemm_issue<1>(L, smem, 1u);
+    if (L.nchunks > 1u) gemm_issue<1>(L, smem, 1u);
     for (uint32_t c = 0;;) {
         gemm_chunk<G, SYM, NT, 0>(L, smem, c, acc);
         if (++c == L.nchunks) break;
