@@ -277,6 +277,23 @@ def test_router_ties_on_gpu(tsg, ctx, kind):
     idx, wts = empty(8, np.uint32), empty(8)
     moe.encode_router_gemma4_bf16(W, X, ES, PES, idx, wts, ne, d)
     assert list(host(idx, np.uint32)) == list(ci)
+    # the staged rows router and its grouped form (candidate top-8 per row):
+    # three copies of the row give the one-row call's indices and weights
+    m = 3
+    Xr = dev(np.tile(hidden, m))
+    ri, rw_ = empty(8 * m, np.uint32), empty(8 * m)
+    moe.encode_router_gemma4_bf16_rows(W, Xr, d, ES, PES, ri, rw_, m, ne, d)
+    gi, gw = empty(8 * m, np.uint32), empty(8 * m)
+    sp, off, cnt = empty(8 * m * 4, np.uint32), empty(ne, np.uint32), empty(ne, np.uint32)
+    bl, nb = empty(8 * m * 4, np.uint32), empty(1, np.uint32)
+    moe.encode_router_gemma4_bf16_rows_grouped(W, Xr, d, ES, PES, gi, gw, m, ne, d, sp, off,
+                                               cnt, bl, 8 * m, nb)
+    ctx.synchronize()
+    for got_i, got_w in ((ri, rw_), (gi, gw)):
+        assert list(host(got_i, np.uint32)) == list(ci) * m
+        assert np.array_equal(host(got_w, np.uint16), np.tile(host(wts, np.uint16), m))
+    assert int(host(nb, np.uint32)[0]) == 8
+    assert list(host(cnt, np.uint32)[list(ci)]) == [m] * 8
     # the one-launch layer's own top-8 (random experts of d = 128, f = 64)
     f = 64
     rng = oracle.SplitMix64(0x7E)
