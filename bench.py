@@ -183,6 +183,7 @@ def run_decode(tsg, torch, ctx, args, layers, routers):
     us_per_layer = ms * 1000.0 / (tokens * LAYERS)
     log(f"decode: {tokens} tokens x {LAYERS} layers in {ms:.3f} ms (wall {wall*1e3:.1f} ms): "
         f"{us_per_layer:.3f} us/layer")
+    ctx.synchronize()  # raises if a launch's hand-off wait timed out (its outputs are invalid)
     check_decode_outputs(torch, ys, idx)
     # dominant kernel: the one-launch decode layer alone, 4 tokens x 30 layers
     # per graph, timed on the stream the launches go to.
@@ -203,6 +204,7 @@ def run_decode(tsg, torch, ctx, args, layers, routers):
     torch.cuda.synchronize()
     k_us = start.elapsed_time(stop) * 1000.0 / (reps * k_reps * LAYERS)
     log(f"decode_layer_kernel alone: {k_us:.3f} us/launch")
+    ctx.synchronize()
     check_decode_outputs(torch, ys, idx)
     # the graph's last token is the last one executed: its inputs and routing
     last = [x_of(n_inputs - 1, l) for l in range(LAYERS)]
@@ -616,6 +618,7 @@ def run_qwen(tsg, torch, args):
                                                sact, e, h, f, f, stream=stream)
 
     ms = time_graph(torch, stream, decode, reps=max(2, args.steps // 8))
+    ctx.synchronize()  # raises if a launch's hand-off wait timed out
     us1 = ms * 1000.0 / (n_tok * nl)
     y = ys.view(torch.float16).float()
     if not bool(torch.isfinite(y).all()):
