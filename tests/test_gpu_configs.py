@@ -349,6 +349,35 @@ def test_router_rows_grouped_matches_router_then_grouping(tsg, ctx, m, ne, d):
         assert np.array_equal(host(w1, np.uint16), host(b["w"], np.uint16)[r * k:(r + 1) * k])
 
 
+def test_verify_entry_points_reject_bad_arguments(tsg, ctx, gemma_layer):
+    """Host-side checks of the verify entry points, before any launch: the
+    grouped router declines 0 or more than 8 rows and refuses a block list too
+    short for min(rows * 8, experts); the device-list rows path refuses an empty
+    or oversized capacity and a missing count."""
+    configure(ctx, 32, "sym")
+    layer, _, _ = gemma_layer
+    d, f, ne, k = 2816, 704, 128, 8
+    moe = tsg.MoE(ctx)
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    rw, x = empty(ne * d), empty(8 * d)
+    es, pes = empty(d, fill=0x3F80), empty(ne, fill=0x3F80)
+    idx, w = empty(9 * k, np.uint32), empty(9 * k)
+    sp, off, cnt = empty(9 * k * 4, np.uint32), empty(ne, np.uint32), empty(ne, np.uint32)
+    bl, nb = empty(9 * k * 4, np.uint32), empty(1, np.uint32)
+    for rows, max_blocks, status in ((0, 8, 4), (9, 72, 4), (5, 39, 1)):
+        with pytest.raises(tsg.TsgError) as e:
+            moe.encode_router_gemma4_bf16_rows_grouped(rw, x, d, es, pes, idx, w, rows, ne, d,
+                                                       sp, off, cnt, bl, max_blocks, nb)
+        assert e.value.status == status, (rows, max_blocks)
+    act, part = empty(8 * k * f), empty(8 * k * d)
+    for max_blocks, count in ((0, nb), (65536, nb), (8, None)):
+        with pytest.raises(tsg.TsgError) as e:
+            g.encode_streamed_rows_device(layer, x, d, sp, bl, max_blocks, count, act, part, k,
+                                          d, f)
+        assert e.value.status == 1, max_blocks
+    ctx.synchronize()
+
+
 def test_rows_device_list_skips_and_reports(tsg, ctx, gemma_layer):
     """Blocks past the device count are not run; a live block the rows path
     cannot take (9 rows) is skipped and reported at synchronisation."""
