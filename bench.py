@@ -279,9 +279,11 @@ def run_prefill_shape(tsg, torch, ctx, args, layer, t, h, f, e, zipf_s, act, lay
     """One prefill MoE layer of t tokens, top-8 Zipf(zipf_s) routing over e
     experts of shape (h, f): device grouping -> gate/up GEMM + activation ->
     down GEMM -> token-major reduce. The per-kernel split comes from HIP
-    events around each kernel of single layers; the sustained figures from a
-    HIP graph of SUSTAIN_LAYERS layers back to back (each with its own weights
-    from `layers` when given), replayed: GEMMs alone, and the whole layer."""
+    events around each kernel of single layers run as two GEMM launches; the
+    sustained figures from a HIP graph of SUSTAIN_LAYERS layers back to back
+    (each with its own weights from `layers` when given), replayed: the GEMMs
+    as one fused persistent launch (and, for comparison, as two launches),
+    and the whole layer with the fused launch."""
     moe = tsg.MoE(ctx, gate_activation=act)
     g = tsg.PrefillGroupedRoutedMoE(moe)
     red = tsg.PrefillMoE(ctx)
@@ -343,35 +345,51 @@ def run_prefill_shape(tsg, torch, ctx, args, layer, t, h, f, e, zipf_s, act, lay
         bool(torch.isfinite(partials.view(torch.float16).float()).all())
     if not out_ok:
         raise RuntimeError(f"prefill T={t} produced non-finite outputs")
+    # the fused persistent launch (tsg_prefill_moe_gate_up_down) gives the two
+    # GEMMs' bits: checked here on the measured inputs
+    want = partials.clone()
+    partials.fill_(0)
+    with torch.cuda.stream(stream):
+        g.encode_gate_up_down(layer, hidden, h, sp, blocks, max_blocks, act_buf, partials, k, h, f,
+                              n_blocks_device=nb, stream=stream)
+    ctx.synchronize(stream)
+    if not torch.equal(want, partials):
+        raise RuntimeError(f"prefill T={t}: the fused GEMM differs from the two GEMMs")
     # sustained: SUSTAIN_LAYERS layers back to back in one graph
     lays = [layer] * SUSTAIN_LAYERS if not layers else \
         [layers[i % len(layers)] for i in range(SUSTAIN_LAYERS)]
 
-    def gemms():
+    def gemms_two():
         for L in lays:
             g.encode_gate_up(L, hidden, h, sp, blocks, max_blocks, act_buf, h, f,
                              n_blocks_device=nb, stream=stream)
             g.encode_down(L, act_buf, sp, blocks, max_blocks, partials, k, h, f,
                           n_blocks_device=nb, stream=stream)
+
+    def gemms():
+        for L in lays:
+            g.encode_gate_up_down(L, hidden, h, sp, blocks, max_blocks, act_buf, partials, k, h,
+                                  f, n_blocks_device=nb, stream=stream)
 
     def whole():
         for L in lays:
             g.group_pairs_device(idx, w, t, k, e, sp, off, cnt, blocks, max_blocks, nb, scratch,
                                  tile_rows=tile_rows, stream=stream)
-            g.encode_gate_up(L, hidden, h, sp, blocks, max_blocks, act_buf, h, f,
-                             n_blocks_device=nb, stream=stream)
-            g.encode_down(L, act_buf, sp, blocks, max_blocks, partials, k, h, f,
-                          n_blocks_device=nb, stream=stream)
+            g.encode_gate_up_down(L, hidden, h, sp, blocks, max_blocks, act_buf, partials, k, h,
+                                  f, n_blocks_device=nb, stream=stream)
             red.encode_reduce_token_major(partials, w, h2, t, k, h, stream=stream)
 
+    two_ms = time_graph(torch, stream, gemms_two, reps=2) / SUSTAIN_LAYERS
     gemm_ms = time_graph(torch, stream, gemms, reps=2) / SUSTAIN_LAYERS
     total_ms = time_graph(torch, stream, whole, reps=2) / SUSTAIN_LAYERS
+    ctx.synchronize(stream)  # a fused launch's schedule error would surface here
     if not bool(torch.isfinite(h2.view(torch.float16).float()).all()):
         raise RuntimeError(f"prefill T={t} produced non-finite outputs")
     log(f"prefill T={t}: single layers: group {per[0]*1e3:.1f} us, gate/up {per[1]*1e3:.1f} us, "
         f"down {per[2]*1e3:.1f} us, reduce {per[3]*1e3:.1f} us; sustained over "
-        f"{SUSTAIN_LAYERS} layers: GEMMs {gemm_ms*1e3:.1f} us, layer {total_ms*1e3:.1f} us")
-    return dict(us_per_layer=total_ms * 1e3, gemm_us=gemm_ms * 1e3,
+        f"{SUSTAIN_LAYERS} layers: fused GEMMs {gemm_ms*1e3:.1f} us (two launches "
+        f"{two_ms*1e3:.1f} us), layer {total_ms*1e3:.1f} us")
+    return dict(us_per_layer=total_ms * 1e3, gemm_us=gemm_ms * 1e3, two_launch_gemm_us=two_ms * 1e3,
                 gate_up_us=float(per[1]) * 1e3, down_us=float(per[2]) * 1e3,
                 group_us=float(per[0]) * 1e3, reduce_us=float(per[3]) * 1e3,
                 burst_gemm_us=float(per[1] + per[2]) * 1e3,
@@ -818,13 +836,17 @@ def attainable_gemm(torch):
 def prefill_summary(pre):
     return {"us_per_layer": round(pre["us_per_layer"], 2),
             "gemm_us": round(pre["gemm_us"], 2),
+            "gemm_kernel": "moe_gemm_fused_kernel: gate/up + GeGLU and down in one persistent "
+                           "launch (tsg_prefill_moe_gate_up_down)",
             "gemm_measure": f"sustained: {SUSTAIN_LAYERS} layers back to back in a HIP graph, "
                             f"each with its own weights",
+            "two_launch_gemm_us": round(pre["two_launch_gemm_us"], 2),
             "burst_gemm_us": round(pre["burst_gemm_us"], 2),
             "gate_up_us": round(pre["gate_up_us"], 2),
             "down_us": round(pre["down_us"], 2), "group_us": round(pre["group_us"], 2),
             "reduce_us": round(pre["reduce_us"], 2),
-            "split_measure": "single layers, HIP events around each kernel",
+            "split_measure": "single layers, HIP events around each kernel of the two-launch "
+                             "form (moe_gemm_kernel gate/up, then down)",
             "gemm_TFLOPs": round(pre["gemm_tflops"], 2),
             "frac_mfma_peak": round(pre["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
             "layer_TFLOPs": round(pre["layer_tflops"], 2),

@@ -477,6 +477,24 @@ tsg_status tsg_prefill_moe_down(tsg_moe* moe, tsg_stream stream, const tsg_layer
                                 const tsg_routed_block* blocks, uint32_t n_blocks,
                                 const uint32_t* n_blocks_device, uint16_t* route_partials,
                                 uint32_t top_k, uint32_t d, uint32_t f);
+/* encodeStreamedTiled modes 0 and 1 (PrefillGroupedRoutedMoE.swift:931-1051,
+ * the two encodes the reference issues back to back) in one persistent
+ * launch: exactly tsg_prefill_moe_gate_up followed by tsg_prefill_moe_down on
+ * the same arguments (bit-identical act and route_partials), with the down
+ * tiles of a block starting as soon as that block's gate/up tiles are done.
+ * The reference has no single call for the pair; a caller that issues the two
+ * encodes back to back replaces them with this one. act must be 128-byte
+ * aligned (TSG_ERR_ALIGNMENT); at most 65536 blocks. The schedule words live
+ * in the context: fused launches on one context must not overlap (one stream
+ * or ordered streams). A wait that times out or a schedule left undrained is
+ * reported by tsg_ctx_synchronize (TSG_ERR_HIP). */
+tsg_status tsg_prefill_moe_gate_up_down(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                        const uint16_t* hidden, uint32_t hidden_stride_elements,
+                                        const tsg_token_expert_pair* sorted_pairs,
+                                        const tsg_routed_block* blocks, uint32_t n_blocks,
+                                        const uint32_t* n_blocks_device, uint16_t* act,
+                                        uint16_t* route_partials, uint32_t top_k, uint32_t d,
+                                        uint32_t f);
 /* encodeStreamedRows (PrefillGroupedRoutedMoE.swift:793-917,
  * prefill.metal:1489-1721): verify-width blocks (row_count <= 8), decode's
  * per-row arithmetic with each weight read once per block; writes act rows

@@ -512,3 +512,76 @@ def test_qwen_prefill_t4096_silu(tsg, ctx, qwen_layer):
     rel_p, rel, _ = run_prefill_full(tsg, ctx, layer, offs, blobs, 4096, 2048, 512, 256, 1.0,
                                      "silu", 0x4096)
     assert rel_p <= kc.NORTH_STAR and rel <= kc.NORTH_STAR
+
+
+def run_fused_vs_two_launches(tsg, ctx, layer, t, d, f, ne, s, act, seed, tile=128,
+                              device_list=True):
+    """tsg_prefill_moe_gate_up_down against tsg_prefill_moe_gate_up then
+    tsg_prefill_moe_down on the same grouping: act and route partials equal
+    bit for bit."""
+    k = 8
+    rng = np.random.default_rng(seed)
+    idx, w = wl.zipf_routing(rng, t, ne, k, s)
+    hidden = dev(wl.f16_normal(rng, t * d))
+    moe = tsg.MoE(ctx, gate_activation=act)
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    max_blocks = -(-t * k // tile) + ne
+    sp, off, cnt = empty(t * k * 4, np.uint32), empty(ne, np.uint32), empty(ne, np.uint32)
+    blocks, nb = empty(max_blocks * 4, np.uint32), empty(1, np.uint32)
+    scratch = empty(g.scratch_bytes(t, k, ne) // 4 + 1, np.uint32)
+    g.group_pairs_device(dev(idx), dev(w), t, k, ne, sp, off, cnt, blocks, max_blocks, nb, scratch,
+                         tile_rows=tile)
+    n_blocks = int(host(nb, np.uint32)[0])
+    kw = dict(n_blocks_device=nb) if device_list else {}
+    nlist = max_blocks if device_list else n_blocks
+    a2, p2 = empty(t * k * f, fill=NAN16), empty(t * k * d, fill=NAN16)
+    g.encode_gate_up(layer, hidden, d, sp, blocks, nlist, a2, d, f, **kw)
+    g.encode_down(layer, a2, sp, blocks, nlist, p2, k, d, f, **kw)
+    want_a, want_p = host(a2, np.uint16), host(p2, np.uint16)
+    for rep in range(2):  # the second launch runs on the schedule the first left
+        a1, p1 = empty(t * k * f, fill=NAN16), empty(t * k * d, fill=NAN16)
+        g.encode_gate_up_down(layer, hidden, d, sp, blocks, nlist, a1, p1, k, d, f, **kw)
+        ctx.synchronize()
+        assert np.array_equal(host(a1, np.uint16), want_a), f"act differs (launch {rep})"
+        assert np.array_equal(host(p1, np.uint16), want_p), f"partials differ (launch {rep})"
+    print(f"fused T={t} E={ne} {act}: {n_blocks} routed blocks, act and partials bitwise equal")
+    return n_blocks
+
+
+@pytest.mark.parametrize("shape", ["gemma-t2048", "qwen-t4096", "gemma-t5", "gemma-t301-host"])
+def test_fused_gate_up_down_matches_two_launches(tsg, ctx, gemma_layer, qwen_layer, shape):
+    """The fused persistent GEMM equals the two grouped GEMMs bit for bit at
+    configs[3] and configs[4]'s prefill sizes, at a verify-sized chunk (fewer
+    routed blocks than XCDs) and with a host-counted block list; two launches
+    in a row check that each leaves its schedule reset."""
+    configure(ctx, 32, "sym")
+    if shape == "gemma-t2048":
+        run_fused_vs_two_launches(tsg, ctx, gemma_layer[0], 2048, 2816, 704, 128, 1.1, "gelu",
+                                  0xF05E)
+    elif shape == "qwen-t4096":
+        run_fused_vs_two_launches(tsg, ctx, qwen_layer[0], 4096, 2048, 512, 256, 1.0, "silu",
+                                  0xF06E)
+    elif shape == "gemma-t5":
+        nb = run_fused_vs_two_launches(tsg, ctx, gemma_layer[0], 5, 2816, 704, 128, 1.1, "gelu",
+                                       0xF07E)
+        assert nb < 40
+    else:
+        run_fused_vs_two_launches(tsg, ctx, gemma_layer[0], 301, 2816, 704, 128, 1.0, "gelu",
+                                  0xF08E, tile=64, device_list=False)
+
+
+def test_fused_gate_up_down_rejects_unaligned_act(tsg, ctx, gemma_layer):
+    """The fused launch needs whole cache lines per activation row; an act
+    buffer off a 128-byte boundary is refused before anything is enqueued."""
+    configure(ctx, 32, "sym")
+    layer = gemma_layer[0]
+    g = tsg.PrefillGroupedRoutedMoE(tsg.MoE(ctx))
+    d, f, t, k = 2816, 704, 4, 8
+    pairs = np.zeros(t * k * 4, np.uint32)
+    blocks = np.array([(0, 0, 4, 0)], dtype=oracle.BLOCK_DTYPE).view(np.uint32)
+    act = empty(t * k * f + 64)
+    with pytest.raises(tsg.TsgError) as e:
+        g.encode_gate_up_down(layer, empty(t * d), d, dev(pairs), dev(blocks), 1, act[8:],
+                              empty(t * k * d), k, d, f)
+    assert e.value.status == 2  # TSG_ERR_ALIGNMENT
+    ctx.synchronize()

@@ -89,6 +89,14 @@ def test_prefill_moe_gemm_kernelcheck(tsg, ctx, group, scheme):
     P, B = dev(c["pairs"]), dev(c["blocks"])
     g.encode_gate_up(layer, dev(c["hidden"]), d, P, B, c["blocks"].size, act, d, f)
     g.encode_down(layer, act, P, B, c["blocks"].size, partials, K, d, f)
+    # the fused persistent launch gives the two launches' bits
+    act1 = empty(rows * f)
+    partials1 = empty(T * K * d, fill=f16_fill_bits(float("nan")))
+    g.encode_gate_up_down(layer, dev(c["hidden"]), d, P, B, c["blocks"].size, act1, partials1, K,
+                          d, f)
+    ctx.synchronize()
+    assert np.array_equal(host(act1, np.uint16), host(act, np.uint16))
+    assert np.array_equal(host(partials1, np.uint16), host(partials, np.uint16))
     got = oracle.f16_to_float(host(partials, np.uint16))
     exp = oracle.f16_to_float(expected).ravel()
     assert not np.any(np.isnan(got)), "a route partial was never written"

@@ -635,6 +635,16 @@ class PrefillGroupedRoutedMoE:
             self.moe.handle, _stream(stream), layer.handle, _ptr(act), _ptr(sorted_pairs),
             _ptr(blocks), n_blocks, _ptr(n_blocks_device), _ptr(route_partials), top_k, d, f))
 
+    def encode_gate_up_down(self, layer, hidden, hidden_stride, sorted_pairs, blocks, n_blocks,
+                            act, route_partials, top_k, d, f, n_blocks_device=None,
+                            stream=None):
+        """encode_gate_up then encode_down in one persistent launch (same
+        results; act 128-byte aligned)."""
+        check(self.lib.tsg_prefill_moe_gate_up_down(
+            self.moe.handle, _stream(stream), layer.handle, _ptr(hidden), hidden_stride,
+            _ptr(sorted_pairs), _ptr(blocks), n_blocks, _ptr(n_blocks_device), _ptr(act),
+            _ptr(route_partials), top_k, d, f))
+
     def encode_streamed_rows_device(self, layer, hidden, hidden_stride, sorted_pairs, blocks,
                                     max_blocks, n_blocks_device, act_scratch, route_partials,
                                     top_k, d, f, stream=None):

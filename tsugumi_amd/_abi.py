@@ -150,6 +150,8 @@ SIGNATURES = {
                                                          P, P, U32, P]),
     "tsg_prefill_moe_gate_up": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, U32]),
     "tsg_prefill_moe_down": (C.c_int, [P, P, P, P, P, P, U32, P, P, U32, U32, U32]),
+    "tsg_prefill_moe_gate_up_down": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, P, U32, U32,
+                                               U32]),
     "tsg_prefill_moe_rows": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, U32, U32]),
     "tsg_prefill_moe_rows_device": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, P, U32, U32,
                                               U32]),

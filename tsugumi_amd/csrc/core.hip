@@ -85,11 +85,17 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
     TSG_REQUIRE(ctx != nullptr, TSG_ERR_OUT_OF_MEMORY, "host allocation failed");
     ctx->device = device;
     ctx->num_cus = prop.multiProcessorCount;
+    int n_xcc = 1;
+    if (hipDeviceGetAttribute(&n_xcc, hipDeviceAttributeNumberOfXccs, device) != hipSuccess)
+        n_xcc = 1;
+    ctx->gemm_queues = n_xcc >= 8 ? 8u : n_xcc >= 4 ? 4u : n_xcc >= 2 ? 2u : 1u;
     hipError_t e = hipMalloc(&ctx->counters, sizeof(uint32_t) * kMaxCounters);
     if (e == hipSuccess)
         e = hipMalloc(&ctx->logits, sizeof(float) * kMaxPromptRows * kMaxExperts);
     if (e == hipSuccess)
         e = hipMalloc(&ctx->act_replicas, sizeof(uint16_t) * kActReplicas * kActReplicaHalves);
+    if (e == hipSuccess) e = hipMalloc(&ctx->gemm_sched, sizeof(uint32_t) * kGemmSchedWords);
+    if (e == hipSuccess) e = hipMemset(ctx->gemm_sched, 0, sizeof(uint32_t) * kGemmSchedWords);
     if (e == hipSuccess) e = hipMemset(ctx->counters, 0, sizeof(uint32_t) * kMaxCounters);
     // The one-launch decode layer's hand-off words carry the launch's tag
     // (epoch + 1, never 0) and the epoch starts at 0 here: words left by an
@@ -104,6 +110,7 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
         (void)hipFree(ctx->counters);
         (void)hipFree(ctx->logits);
         (void)hipFree(ctx->act_replicas);
+        (void)hipFree(ctx->gemm_sched);
         delete ctx;
         if (st != TSG_OK) return st;
         return fail(TSG_ERR_OUT_OF_MEMORY, "context scratch: %s", hipGetErrorString(e));
@@ -119,6 +126,7 @@ extern "C" void tsg_ctx_destroy(tsg_ctx* ctx) {
     (void)hipFree(ctx->counters);
     (void)hipFree(ctx->logits);
     (void)hipFree(ctx->act_replicas);
+    (void)hipFree(ctx->gemm_sched);
     delete ctx;
 }
 
@@ -162,6 +170,10 @@ extern "C" tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream) {
             return fail(TSG_ERR_INVALID_ARGUMENT,
                         "rows path: a device block had no rows, more than 8, or an expert past "
                         "the layer; it was skipped");
+        if (err & kErrGemmWait)
+            return fail(TSG_ERR_HIP, "fused grouped GEMM: a down item timed out waiting for its "
+                                     "block's gate/up tiles, or an XCD queue was not drained; "
+                                     "the layer's outputs are invalid");
         return fail(TSG_ERR_HIP, "fused decode layer: a block timed out waiting for the "
                                  "others; outputs of the affected launch are invalid");
     }

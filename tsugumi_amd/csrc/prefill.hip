@@ -833,6 +833,26 @@ __device__ void gemm_work_item(const GemmArgs& args, uint32_t nb, uint32_t pid, 
     yb = scratch[63];
 }
 
+// One work item: column tile `tile` of routed block blk; a block wider than
+// kGemmRows runs as consecutive passes.
+template <int G, bool SYM, int ACT, int MODE>
+__device__ __forceinline__ void gemm_item(const GemmArgs& args, const tsg_routed_block& blk,
+                                          uint32_t tile, uint8_t* smem) {
+    for (uint32_t r0 = 0; r0 < blk.row_count; r0 += kGemmRows) {
+        if (r0) block_barrier();  // every wave is done with the previous pass's LDS
+        tsg_routed_block sub = blk;
+        sub.pair_start += r0;
+        sub.local_row += r0;
+        const uint32_t rows = blk.row_count - r0 < kGemmRows ? blk.row_count - r0 : kGemmRows;
+        switch ((rows + 31u) / 32u) {
+            case 1: gemm_block<G, SYM, ACT, MODE, 1>(args, sub, rows, tile, smem); break;
+            case 2: gemm_block<G, SYM, ACT, MODE, 2>(args, sub, rows, tile, smem); break;
+            case 3: gemm_block<G, SYM, ACT, MODE, 3>(args, sub, rows, tile, smem); break;
+            default: gemm_block<G, SYM, ACT, MODE, 4>(args, sub, rows, tile, smem); break;
+        }
+    }
+}
+
 // 1-D grid of ntiles x (routed block capacity) workgroups; those past the
 // live count exit at once.
 template <int G, bool SYM, int ACT, int MODE>
@@ -854,19 +874,102 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmArgs args
     } else {
         blk = args.blocks[yb];
     }
-    // a routed block wider than kGemmRows runs as consecutive passes
-    for (uint32_t r0 = 0; r0 < blk.row_count; r0 += kGemmRows) {
-        if (r0) block_barrier();  // every wave is done with the previous pass's LDS
-        tsg_routed_block sub = blk;
-        sub.pair_start += r0;
-        sub.local_row += r0;
-        const uint32_t rows = blk.row_count - r0 < kGemmRows ? blk.row_count - r0 : kGemmRows;
-        switch ((rows + 31u) / 32u) {
-            case 1: gemm_block<G, SYM, ACT, MODE, 1>(args, sub, rows, tile, smem); break;
-            case 2: gemm_block<G, SYM, ACT, MODE, 2>(args, sub, rows, tile, smem); break;
-            case 3: gemm_block<G, SYM, ACT, MODE, 3>(args, sub, rows, tile, smem); break;
-            default: gemm_block<G, SYM, ACT, MODE, 4>(args, sub, rows, tile, smem); break;
+    gemm_item<G, SYM, ACT, MODE>(args, blk, tile, smem);
+}
+
+// The gate/up and down GEMMs of one layer in one persistent launch. With Q
+// queues (the device's XCDs), routed block b of the list (largest first as
+// the device grouping writes it) belongs to queue b % Q; each queue holds its blocks' work items, all
+// gate/up items (block by block, largest first) before any down item. A
+// workgroup takes items from queue XCC_ID % Q (the XCD it runs on, a hardware
+// register), so every item of a block runs on one XCD and the activations
+// pass between its gate/up and down items through that XCD's L2: a gate/up
+// item's stores complete (vmcnt), then it counts itself in done[b]; a down
+// item of b waits until done[b] holds all gate/up tiles of b. The L1 of a CU
+// is invalidated at launch, and an activation row is whole 128-byte lines
+// (f % 64 == 0, a 128-byte aligned buffer), so a CU's L1 holds no line of b's
+// activations from before b's gate/up items wrote them: a line it holds was
+// loaded by a down item of its own block, after the block's gate/up items.
+// No wait can block the gate/up items (they wait on nothing, and a down item
+// is taken only after every gate/up item of its queue was), and each wait is
+// bounded (kErrGemmWait on a timeout). The last workgroup to leave resets the
+// queues and counters for the next launch, and reports a queue no workgroup
+// drained (kErrGemmWait). Down items fill the gate/up tail, and there is no
+// launch between the two GEMMs. Launches that share a context's schedule
+// words must not overlap (one stream, or ordered streams).
+struct FusedSched {
+    uint32_t* next;    // kXcds queue heads
+    uint32_t* exited;  // workgroups that have left
+    uint32_t* done;    // gate/up tiles finished, per routed block (cap entries)
+    uint32_t cap;
+    uint32_t queues;   // 1, 2, 4 or 8
+};
+constexpr uint32_t kXcds = 8;
+constexpr uint32_t kFusedSpinLimit = 1u << 18;
+
+template <int G, bool SYM, int ACT>
+__global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_fused_kernel(GemmArgs gu, GemmArgs dn,
+                                                                         FusedSched sc) {
+    extern __shared__ __align__(16) uint8_t smem[];  // gemm_lds_bytes(SYM)
+    // The item index travels through the weight ring's last stage, which an
+    // item first writes after its first barrier (every wave has read the
+    // index by then). No static LDS: two sym workgroups fill a CU's 160 KiB.
+    uint32_t* word = reinterpret_cast<uint32_t*>(smem + kGemmBBase + 2u * kGemmBStage);
+    const uint32_t nb_dev = gu.n_blocks_device ? *gu.n_blocks_device : gu.n_blocks;
+    const uint32_t nb = nb_dev < sc.cap ? nb_dev : sc.cap;
+    const uint32_t Q = sc.queues;
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= Q - 1u;
+    const uint32_t T0 = gu.ntiles, T1 = dn.ntiles;
+    const uint32_t nbx = nb > xcc ? (nb - xcc + Q - 1u) / Q : 0u;
+    const uint32_t n_gu = nbx * T0, n_all = nbx * (T0 + T1);
+    if (threadIdx.x == 0) word[0] = atomicAdd(&sc.next[xcc], 1u);
+    __syncthreads();
+    uint32_t item = word[0];
+    while (item < n_all) {
+        // the next item is taken now; its index arrives while this one runs
+        uint32_t next = 0;
+        if (threadIdx.x == 0) next = atomicAdd(&sc.next[xcc], 1u);
+        if (item < n_gu) {
+            const uint32_t yb = xcc + Q * (item / T0), tile = item % T0;
+            gemm_item<G, SYM, ACT, 0>(gu, gu.blocks[yb], tile, smem);
+            wait_vmcnt<0>();  // this wave's activation stores are in the L2
+            __syncthreads();
+            if (threadIdx.x == 0) atomicAdd(&sc.done[yb], 1u);
+        } else {
+            const uint32_t j = item - n_gu, yb = xcc + Q * (j / T1), tile = j % T1;
+            if (threadIdx.x == 0) {
+                for (uint32_t spins = 0; ld_coherent(&sc.done[yb]) < T0; ++spins) {
+                    if (spins > kFusedSpinLimit) {
+                        atomicOr(gu.error, kErrGemmWait);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            }
+            __syncthreads();
+            gemm_item<G, SYM, ACT, 1>(dn, dn.blocks[yb], tile, smem);
         }
+        __syncthreads();  // the item's LDS is free
+        if (threadIdx.x == 0) word[0] = next;
+        __syncthreads();
+        item = word[0];
+    }
+    if (threadIdx.x == 0) word[1] = atomicAdd(sc.exited, 1u) == gridDim.x - 1u ? 1u : 0u;
+    __syncthreads();
+    if (word[1]) {
+        // every other workgroup has left: nobody reads the schedule any more
+        // (agent-coherent stores: the counters live at the memory side, where
+        // the other XCDs' atomics of the next launch find them)
+        for (uint32_t i = threadIdx.x; i < nb; i += blockDim.x) st_coherent(sc.done + i, 0u);
+        if (threadIdx.x < Q) {
+            const uint32_t x = threadIdx.x;
+            const uint32_t nx = nb > x ? (nb - x + Q - 1u) / Q : 0u;
+            if (ld_coherent(sc.next + x) < nx * (T0 + T1)) atomicOr(gu.error, kErrGemmWait);
+            st_coherent(sc.next + x, 0u);
+        }
+        if (threadIdx.x == 0) st_coherent(sc.exited, 0u);
     }
 }
 
@@ -1101,6 +1204,29 @@ tsg_status launch_gemm(const tsg_moe* moe, hipStream_t s, const GemmArgs& a, uin
     return check_launch(MODE == 0 ? "moe_gemm gate/up" : "moe_gemm down");
 }
 
+template <int G, bool SYM>
+tsg_status launch_fused(const tsg_moe* moe, hipStream_t s, GemmArgs gu, GemmArgs dn,
+                        uint32_t max_blocks) {
+    gu.ntiles = (gu.f + 127u) / 128u;
+    dn.ntiles = (dn.d + 255u) / 256u;
+    const tsg_ctx* ctx = moe->ctx;
+    FusedSched sc;
+    sc.next = ctx->gemm_sched;
+    sc.exited = ctx->gemm_sched + kXcds;
+    sc.done = ctx->gemm_sched + 16u;
+    sc.cap = max_blocks;
+    sc.queues = ctx->gemm_queues;
+    auto kern = moe->activation == TSG_ACT_SILU ? moe_gemm_fused_kernel<G, SYM, TSG_ACT_SILU>
+                                                : moe_gemm_fused_kernel<G, SYM, TSG_ACT_GELU_TANH>;
+    TSG_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)gemm_lds_bytes(SYM)));
+    // two workgroups per CU (the GEMM's occupancy), every one of them resident
+    const dim3 grid(2u * (uint32_t)ctx->num_cus);
+    hipLaunchKernelGGL(kern, grid, dim3(kGemmThreads), gemm_lds_bytes(SYM), s, gu, dn, sc);
+    return check_launch("moe_gemm fused gate/up + down");
+}
+
 template <int MODE>
 tsg_status gemm_dispatch(const tsg_moe* moe, hipStream_t s, const GemmArgs& a, uint32_t max_blocks) {
     const tsg_ctx* ctx = moe->ctx;
@@ -1289,6 +1415,36 @@ extern "C" tsg_status tsg_prefill_moe_gate_up(tsg_moe* moe, tsg_stream stream,
                              n_dev, act, d, f, kTopK)))
         return st;
     return gemm_dispatch<0>(moe, as_stream(stream), a, n_blocks);
+}
+
+extern "C" tsg_status tsg_prefill_moe_gate_up_down(
+    tsg_moe* moe, tsg_stream stream, const tsg_layer* layer, const uint16_t* hidden,
+    uint32_t hidden_stride, const tsg_token_expert_pair* pairs, const tsg_routed_block* blocks,
+    uint32_t n_blocks, const uint32_t* n_dev, uint16_t* act, uint16_t* partials, uint32_t top_k,
+    uint32_t d, uint32_t f) {
+    tsg_status st = check_layer_moe(moe, layer);
+    if (st) return st;
+    TSG_REQUIRE(top_k > 0, TSG_ERR_INVALID_ARGUMENT, "topK must be positive");
+    if (n_blocks == 0) return TSG_OK;
+    TSG_REQUIRE(n_blocks <= kGemmSchedBlocks, TSG_ERR_UNSUPPORTED,
+                "the fused GEMM takes up to %u routed blocks, got %u", kGemmSchedBlocks, n_blocks);
+    TSG_REQUIRE(((uintptr_t)act & 127u) == 0, TSG_ERR_ALIGNMENT,
+                "the fused GEMM's activation buffer must be 128-byte aligned");
+    GemmArgs gu, dn;
+    if ((st = fill_gemm_args(moe, layer, &gu, hidden, hidden_stride, pairs, blocks, n_blocks, n_dev,
+                             act, d, f, kTopK)))
+        return st;
+    if ((st = fill_gemm_args(moe, layer, &dn, act, f, pairs, blocks, n_blocks, n_dev, partials, d,
+                             f, top_k)))
+        return st;
+    const tsg_ctx* ctx = moe->ctx;
+    const bool sym = ctx->scheme == TSG_SYM;
+    hipStream_t s = as_stream(stream);
+    if (ctx->group_size == 32)
+        return sym ? launch_fused<32, true>(moe, s, gu, dn, n_blocks)
+                   : launch_fused<32, false>(moe, s, gu, dn, n_blocks);
+    return sym ? launch_fused<64, true>(moe, s, gu, dn, n_blocks)
+               : launch_fused<64, false>(moe, s, gu, dn, n_blocks);
 }
 
 extern "C" tsg_status tsg_prefill_moe_down(tsg_moe* moe, tsg_stream stream,

@@ -51,7 +51,13 @@ struct tsg_ctx {
     // this device's copy of the no-alloc grouping scratch (a file-scope device
     // array of prefill.hip, not owned: never freed)
     uint32_t* group_rank_scratch = nullptr;
+    // the fused grouped GEMM's schedule (queue heads, exit count, per-block
+    // gate/up counts; zeroed once, left zeroed by each launch)
+    uint32_t* gemm_sched = nullptr;     // kGemmSchedWords
     int num_cus = 256;
+    // the fused GEMM's queue count: the device's XCDs (8 on an MI355X in its
+    // one-partition mode), rounded down to a power of two, at most 8
+    uint32_t gemm_queues = 8;
 };
 
 struct tsg_moe {
@@ -93,6 +99,8 @@ constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kMaxRouterRows = 8;      // MoE.maxRouterRows (verify rows)
 constexpr uint32_t kMaxPromptRows = 4096;   // rows one router launch may route
 constexpr uint32_t kMaxCounters = 8192;
+constexpr uint32_t kGemmSchedBlocks = 65536;             // routed blocks the fused GEMM takes
+constexpr uint32_t kGemmSchedWords = 16u + kGemmSchedBlocks;
 // Words of ctx->counters used by the one-launch decode layer (below them, words
 // [0, kMaxPromptRows / 16) are the router's per-row-group completion
 // counters). Each area starts on its own 128-byte line.
@@ -105,11 +113,13 @@ constexpr uint32_t kSyncErrorWord = 1056;  // device-side error bits (kErr*), re
 // out; a device grouping that met an expert id >= num_experts (its pairs are
 // not grouped); a device grouping whose work list did not fit max_blocks; a
 // device-list rows-path block with no rows, more than 8, or an expert past
-// the layer (skipped).
+// the layer (skipped); the fused grouped GEMM's down item that waited too long
+// for its block's gate/up tiles, or an XCD queue no workgroup drained.
 constexpr uint32_t kErrDecodeTimeout = 1u;
 constexpr uint32_t kErrGroupExpertRange = 2u;
 constexpr uint32_t kErrGroupBlocks = 4u;
 constexpr uint32_t kErrRowsBlock = 8u;  // a device-list rows-path block it cannot take
+constexpr uint32_t kErrGemmWait = 16u;  // the fused GEMM: a wait timed out or a queue not drained
 constexpr uint32_t kSyncLogitWord = 1088;  // tagged 64-bit logits, kMaxExperts per group
 static_assert(kSyncLogitWord + kDecodeGroups * 2 * kMaxExperts <= kMaxCounters, "sync area overflow");
 static_assert(kSyncLogitWord % 2 == 0, "64-bit words must be aligned");
