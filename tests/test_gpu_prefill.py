@@ -6,6 +6,7 @@ import pytest
 
 import oracle
 from tests import kernelcheck as kc
+from tests import workloads as wl
 from tests.gpu_util import dev, empty, f16_fill_bits, host
 
 pytestmark = pytest.mark.gpu
@@ -279,3 +280,42 @@ def test_device_grouping_reports_expert_out_of_range(tsg, ctx):
         g.group_pairs_device(dev(idx % ne), dev(w), t, k, ne, sp, off, cnt, blocks, 1, nb,
                              scratch, tile_rows=tile)
     assert e.value.status == 1
+
+
+@pytest.mark.parametrize("group,scheme", [(32, "sym"), (64, "affine")])
+def test_gate_up_half_tile_equals_full_tile(tsg, ctx, group, scheme):
+    """F = 704 ends in a 64-column tile, which runs gate and up on separate
+    waves; F = 768 covers the same columns with full tiles. A layer whose
+    first 704 gate/up rows are the F = 768 layer's gives the same activations
+    there, bit for bit, at every block height (1-128 rows)."""
+    sym = scheme == "sym"
+    configure(ctx, group, scheme)
+    d, ne, t, k = 512, 4, 96, 2
+    rng = oracle.SplitMix64(0x4A1F)
+    g = rng.uniforms(-0.125, 0.125, 768 * d).reshape(768, d)
+    u = rng.uniforms(-0.125, 0.125, 768 * d).reshape(768, d)
+    layers = {}
+    for f in (704, 768):
+        parts = []
+        for e in range(ne):
+            ge, ue = g * (1.0 + 0.1 * e), u * (1.0 - 0.05 * e)
+            dn = rng.uniforms(-0.125, 0.125, d * f).reshape(d, f)
+            parts.append([oracle.quantize_int4(m, group, sym) for m in (ge[:f], ue[:f], dn)])
+        layers[f] = _upload_layer(tsg, ctx, parts, sym)[0]
+    # expert e gets 1, 31, 64 and 96 rows: every slice count
+    idx = np.zeros((t, k), np.uint32)
+    for tok in range(t):
+        idx[tok] = (3, 2) if tok < 64 else (3, 1) if tok < 95 else (3, 0)
+    w = np.full((t, k), 0x3800, np.uint16)
+    grouped = oracle.group_pairs(oracle.make_token_expert_pairs(idx, w, t, k), t, k, ne)
+    blocks = wl.rows_blocks(grouped)  # one block per expert
+    hidden = dev(rng.uniforms_f16(-1, 1, t * d))
+    g_moe = tsg.PrefillGroupedRoutedMoE(tsg.MoE(ctx))
+    P, B = dev(grouped["sorted_pairs"]), dev(blocks)
+    out = {}
+    for f in (704, 768):
+        act = empty(t * k * f, fill=f16_fill_bits(float("nan")))
+        g_moe.encode_gate_up(layers[f], hidden, d, P, B, blocks.size, act, d, f)
+        out[f] = host(act, np.uint16).reshape(t * k, f)
+    assert sorted(blocks["row_count"].tolist()) == [1, 31, 64, 96]
+    assert np.array_equal(out[704], out[768][:, :704])

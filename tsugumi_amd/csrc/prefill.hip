@@ -488,22 +488,36 @@ __device__ __forceinline__ void gemm_issue_scales(const GemmLane& L, uint8_t* sm
 // next step's dequantisation (10 pieces: two nibble extractions, eight
 // pairs) is spread between this step's 2 NT MFMAs, and scheduling fences keep
 // the order, so the wave issues its conversions while its own MFMAs run.
-template <bool SYM, int NT, int ST>
+// HALF: the wave runs one tile (bw0, g0) into acc[.][0]: NT MFMAs and 5
+// pieces per step.
+template <bool SYM, int NT, int ST, bool HALF>
 __device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT], const u32x4_t& bw0,
                                          const u32x4_t& bw1, const GroupScale& g0,
                                          const GroupScale& g1, f16v_t (&acc)[NT][2]) {
+    constexpr int kT = HALF ? 1 : 2;       // tiles per wave
+    constexpr int kP = HALF ? 5 : 10;      // conversion pieces per step
     h8v_t bf[2][2];
     bf[0][0] = dequant8<SYM>(bw0[0], g0);
-    bf[0][1] = dequant8<SYM>(bw1[0], g1);
+    if constexpr (!HALF) bf[0][1] = dequant8<SYM>(bw1[0], g1);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
         const int cur = st & 1, nxt = cur ^ 1;
         if (st < 3) lds_read_slices<NT, ST * kGemmAStage>(af[nxt], L.a_rd[st + 1]);
         Nibbles n0{}, n1{};
         h2_t p0[4], p1[4];
-        // piece k of the next step's conversion (k < 10)
+        // piece k of the next step's conversion (k < kP)
         auto piece = [&](int k) {
             if (st >= 3) return;
+            if constexpr (HALF) {
+                switch (k) {
+                    case 0: n0 = nibbles8(bw0[st + 1]); break;
+                    case 1: p0[0] = dequant_pair<SYM, 0>(n0, g0); break;
+                    case 2: p0[1] = dequant_pair<SYM, 1>(n0, g0); break;
+                    case 3: p0[2] = dequant_pair<SYM, 2>(n0, g0); break;
+                    default: p0[3] = dequant_pair<SYM, 3>(n0, g0); break;
+                }
+                return;
+            }
             switch (k) {
                 case 0: n0 = nibbles8(bw0[st + 1]); break;
                 case 1: n1 = nibbles8(bw1[st + 1]); break;
@@ -517,19 +531,19 @@ __device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT]
                 default: p1[3] = dequant_pair<SYM, 3>(n1, g1); break;
             }
         };
-        constexpr int kM = 2 * NT;  // MFMAs this step
+        constexpr int kM = kT * NT;  // MFMAs this step
 #pragma unroll
         for (int q = 0; q < kM; ++q) {
-            const int i = q >> 1, t = q & 1;
+            const int i = q / kT, t = q % kT;
             const h8v_t a8 = __builtin_bit_cast(h8v_t, af[cur][i]);
             acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, bf[cur][t], acc[i][t], 0, 0, 0);
 #pragma unroll
-            for (int k = q * 10 / kM; k < (q + 1) * 10 / kM; ++k) piece(k);
+            for (int k = q * kP / kM; k < (q + 1) * kP / kM; ++k) piece(k);
             __builtin_amdgcn_sched_barrier(0);
         }
         if (st < 3) {
             bf[nxt][0] = pack_pairs(p0[0], p0[1], p0[2], p0[3]);
-            bf[nxt][1] = pack_pairs(p1[0], p1[1], p1[2], p1[3]);
+            if constexpr (!HALF) bf[nxt][1] = pack_pairs(p1[0], p1[1], p1[2], p1[3]);
             lds_wait<NT>(af[nxt]);
         }
     }
@@ -538,7 +552,7 @@ __device__ __forceinline__ void gemm_mma(const GemmLane& L, u32x4_t (&af)[2][NT]
 // One chunk: wait for it, start chunk c + 2 (into the stage chunk c - 1 used)
 // and, at the first chunk of a scale window, the next window, then read its
 // weights, scale and step-0 activations and run its MFMAs.
-template <int G, bool SYM, int NT, int ST>
+template <int G, bool SYM, int NT, int ST, bool HALF>
 __device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uint32_t c,
                                            f16v_t (&acc)[NT][2]) {
     constexpr uint32_t W = gemm_window<G>();
@@ -574,28 +588,35 @@ __device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uin
         const uint32_t slot = (win & 1u) * kGemmSSlot;
         u32x4_t af[2][NT];
         u32x4_t bw0 = lds_read16<ST * kGemmBStage>(L.b_rd);
-        u32x4_t bw1 = lds_read16<ST * kGemmBStage + kGemmBTile>(L.b_rd);
+        u32x4_t bw1 = HALF ? bw0 : lds_read16<ST * kGemmBStage + kGemmBTile>(L.b_rd);
         uint32_t sw0 = lds_read_u16(L.s_rd + slot + (L.s_own[0] + gb) - ((L.s_own[0] + wb) & ~3u));
-        uint32_t sw1 = lds_read_u16(L.s_rd + 512u + slot + (L.s_own[1] + gb) - ((L.s_own[1] + wb) & ~3u));
+        uint32_t sw1 = HALF ? sw0 : lds_read_u16(L.s_rd + 512u + slot + (L.s_own[1] + gb) - ((L.s_own[1] + wb) & ~3u));
         uint32_t zw0 = 0u, zw1 = 0u;
         if constexpr (!SYM) {
             constexpr uint32_t zo = kGemmZBase - kGemmSBase;
             zw0 = lds_read_u16(L.s_rd + zo + slot + (L.z_own[0] + gb) - ((L.z_own[0] + wb) & ~3u));
-            zw1 = lds_read_u16(L.s_rd + zo + 512u + slot + (L.z_own[1] + gb) - ((L.z_own[1] + wb) & ~3u));
+            zw1 = HALF ? zw0 : lds_read_u16(L.s_rd + zo + 512u + slot + (L.z_own[1] + gb) - ((L.z_own[1] + wb) & ~3u));
         }
         lds_read_slices<NT, ST * kGemmAStage>(af[0], L.a_rd[0]);
         lds_wait<NT>(af[0], bw0, bw1, sw0, sw1, zw0, zw1);
         const GroupScale g0 = group_scale<SYM>((uint16_t)sw0, (uint16_t)zw0);
         const GroupScale g1 = group_scale<SYM>((uint16_t)sw1, (uint16_t)zw1);
-        gemm_mma<SYM, NT, ST>(L, af, bw0, bw1, g0, g1, acc);
+        gemm_mma<SYM, NT, ST, HALF>(L, af, bw0, bw1, g0, g1, acc);
     }
 }
 
 // MODE 0: gate/up + activation; MODE 1: down + scatter; MODE 2: dense
 // projection y[t, n] (the down sub-tensor's geometry, rows taken in order).
-template <int G, bool SYM, int ACT, int MODE, int NT>
+// HALF (gate/up only, a column tile with 64 live columns): waves 0-1 run the
+// gate rows of columns 0-31 and 32-63 and waves 2-3 the up rows of the same
+// columns, one weight tile each instead of two tiles on two waves with two
+// idle; the up accumulators reach waves 0-1 through the LDS before the
+// activation. Every accumulator sees the same MFMA sequence as in a full
+// tile, so the results are identical.
+template <int G, bool SYM, int ACT, int MODE, int NT, bool HALF>
 __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_routed_block& blk,
                                            uint32_t rows, uint32_t tile, uint8_t* smem) {
+    static_assert(!HALF || MODE == 0, "only the gate/up GEMM has half tiles");
     const uint32_t lane = threadIdx.x & 63u, h = lane >> 5, m = lane & 31u;
     GemmLane L;
     L.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -611,7 +632,7 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     const uint32_t ngroups = K / G;
     uint32_t row0[2], w_off[2], s_off[2], z_off[2];
     if (MODE == 0) {
-        row0[0] = row0[1] = tile * 128u + 32u * L.wave;
+        row0[0] = row0[1] = tile * 128u + 32u * (HALF ? (L.wave & 1u) : L.wave);
         L.live = row0[0] < args.f;
         w_off[0] = args.o.gate_w, w_off[1] = args.o.up_w;
         s_off[0] = args.o.gate_s, s_off[1] = args.o.up_s;
@@ -671,20 +692,34 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     const uint32_t swzb_m = ((m >> 2) ^ (m >> 3)) & 1u;
     L.b_rd = base + kGemmBBase + L.wave * kGemmBWave + 32u * m + 16u * (h ^ swzb_m);
     L.s_rd = base + kGemmSBase + L.wave * kGemmSWave + 16u * m;
+    if (HALF && L.wave >= 2u) {  // waves 2-3 read their up tile in the tile-0 slots
+        L.b_rd += kGemmBTile;
+        L.s_rd += 512u;
+        L.s_own[0] = L.s_own[1];
+        L.z_own[0] = L.z_own[1];
+    }
 
     f16v_t acc[NT][2];
 #pragma unroll
     for (int i = 0; i < NT; ++i) acc[i][0] = acc[i][1] = f16v_t{};
 
+    // down: this thread's row destination (token * top_k + rank) * d, loaded
+    // now so that its latency hides behind the K loop (it is the oldest load,
+    // so the loop's counted waits retire it first)
+    uint32_t row_dst = 0u;
+    if (MODE == 1 && threadIdx.x < rows) {
+        const tsg_token_expert_pair pr = args.pairs[blk.pair_start + threadIdx.x];
+        row_dst = (pr.token * args.top_k + pr.rank) * args.d;
+    }
     gemm_issue_scales<G, SYM>(L, smem, 0u);
     gemm_issue<0>(L, smem, 0u);
     if (L.nchunks > 1u) gemm_issue<1>(L, smem, 1u);
     for (uint32_t c = 0;;) {
-        gemm_chunk<G, SYM, NT, 0>(L, smem, c, acc);
+        gemm_chunk<G, SYM, NT, 0, HALF>(L, smem, c, acc);
         if (++c == L.nchunks) break;
-        gemm_chunk<G, SYM, NT, 1>(L, smem, c, acc);
+        gemm_chunk<G, SYM, NT, 1, HALF>(L, smem, c, acc);
         if (++c == L.nchunks) break;
-        gemm_chunk<G, SYM, NT, 2>(L, smem, c, acc);
+        gemm_chunk<G, SYM, NT, 2, HALF>(L, smem, c, acc);
         if (++c == L.nchunks) break;
     }
     wait_vmcnt<0>();  // no LDS write may land after this point
@@ -698,18 +733,34 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     constexpr uint32_t kStride = kCols + 8u;             // halves per LDS row
     static_assert(kGemmRows * kStride * 2u <= gemm_lds_bytes(true), "output tile fits the LDS");
     uint16_t* otile = reinterpret_cast<uint16_t*>(smem);
-    // down: each row's destination (token * top_k + rank) * d, staged once per
-    // block (the pair loads overlap the tile conversion below)
+    // down: each row's destination, staged once per block
     uint32_t* odst = reinterpret_cast<uint32_t*>(smem + kGemmRows * kStride * 2u);
     static_assert(kGemmRows * kStride * 2u + kGemmRows * 4u <= gemm_lds_bytes(true),
                   "output tile and row destinations fit the LDS");
     block_barrier();  // every wave is done reading the rings
-    if (MODE == 1 && threadIdx.x < rows) {
-        const tsg_token_expert_pair pr = args.pairs[blk.pair_start + threadIdx.x];
-        odst[threadIdx.x] = (pr.token * args.top_k + pr.rank) * args.d;
-    }
+    if (MODE == 1 && threadIdx.x < rows) odst[threadIdx.x] = row_dst;
     if (MODE == 2 && threadIdx.x < rows) odst[threadIdx.x] = (blk.local_row + threadIdx.x) * args.d;
-    if (L.live) {
+    if constexpr (HALF) {
+        // waves 2-3 hand their up accumulators to waves 0-1, past the tile
+        constexpr uint32_t kXch = kGemmRows * kStride * 2u;
+        static_assert(kXch + 2u * NT * 16u * 64u * 4u <= gemm_lds_bytes(true), "exchange fits");
+        float* xch = reinterpret_cast<float*>(smem + kXch);
+        const uint32_t pair = L.wave & 1u;
+        if (L.wave >= 2u) {
+#pragma unroll
+            for (int i = 0; i < NT; ++i)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) xch[((pair * NT + i) * 16u + v) * 64u + lane] = acc[i][0][v];
+        }
+        lds_barrier();
+        if (L.wave < 2u) {
+#pragma unroll
+            for (int i = 0; i < NT; ++i)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][1][v] = xch[((pair * NT + i) * 16u + v) * 64u + lane];
+        }
+    }
+    if (L.live && (!HALF || L.wave < 2u)) {
         const uint32_t c0 = MODE == 0 ? 32u * L.wave + m : 64u * L.wave + m;
 #pragma unroll
         for (int i = 0; i < NT; ++i) {
@@ -844,11 +895,23 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& args, const tsg_routed
         sub.pair_start += r0;
         sub.local_row += r0;
         const uint32_t rows = blk.row_count - r0 < kGemmRows ? blk.row_count - r0 : kGemmRows;
-        switch ((rows + 31u) / 32u) {
-            case 1: gemm_block<G, SYM, ACT, MODE, 1>(args, sub, rows, tile, smem); break;
-            case 2: gemm_block<G, SYM, ACT, MODE, 2>(args, sub, rows, tile, smem); break;
-            case 3: gemm_block<G, SYM, ACT, MODE, 3>(args, sub, rows, tile, smem); break;
-            default: gemm_block<G, SYM, ACT, MODE, 4>(args, sub, rows, tile, smem); break;
+        // gate/up column tiles hold 128 columns, the last one 64 when F is an
+        // odd multiple of 64
+        const bool half = MODE == 0 && args.f - tile * 128u <= 64u;
+        if (half) {
+            switch ((rows + 31u) / 32u) {
+                case 1: gemm_block<G, SYM, ACT, MODE, 1, MODE == 0>(args, sub, rows, tile, smem); break;
+                case 2: gemm_block<G, SYM, ACT, MODE, 2, MODE == 0>(args, sub, rows, tile, smem); break;
+                case 3: gemm_block<G, SYM, ACT, MODE, 3, MODE == 0>(args, sub, rows, tile, smem); break;
+                default: gemm_block<G, SYM, ACT, MODE, 4, MODE == 0>(args, sub, rows, tile, smem); break;
+            }
+        } else {
+            switch ((rows + 31u) / 32u) {
+                case 1: gemm_block<G, SYM, ACT, MODE, 1, false>(args, sub, rows, tile, smem); break;
+                case 2: gemm_block<G, SYM, ACT, MODE, 2, false>(args, sub, rows, tile, smem); break;
+                case 3: gemm_block<G, SYM, ACT, MODE, 3, false>(args, sub, rows, tile, smem); break;
+                default: gemm_block<G, SYM, ACT, MODE, 4, false>(args, sub, rows, tile, smem); break;
+            }
         }
     }
 }
