@@ -585,3 +585,34 @@ def test_fused_gate_up_down_rejects_unaligned_act(tsg, ctx, gemma_layer):
                               empty(t * k * d), k, d, f)
     assert e.value.status == 2  # TSG_ERR_ALIGNMENT
     ctx.synchronize()
+
+
+def test_grouped_gemm_skips_and_reports_expert_past_layer(tsg, ctx, gemma_layer):
+    """A block list written on the device is not seen by the host: a block
+    naming an expert past the layer is skipped by the grouped GEMM (two-launch
+    and fused forms) and tsg_ctx_synchronize reports it; the other blocks'
+    rows are written as usual."""
+    configure(ctx, 32, "sym")
+    layer = gemma_layer[0]
+    d, f, k, t = 2816, 704, 8, 4
+    g = tsg.PrefillGroupedRoutedMoE(tsg.MoE(ctx))
+    pairs = np.zeros(t * k, oracle.PAIR_DTYPE)
+    pairs["token"] = np.repeat(np.arange(t, dtype=np.uint32), k)
+    pairs["rank"] = np.tile(np.arange(k, dtype=np.uint32), t)
+    blocks = np.array([(3, 0, 16, 0), (500, 16, 16, 16)], dtype=oracle.BLOCK_DTYPE)
+    hidden = dev(wl.f16_normal(np.random.default_rng(5), t * d))
+    P, B = dev(pairs), dev(blocks.view(np.uint32))
+    for fused in (False, True):
+        act, part = empty(t * k * f, fill=NAN16), empty(t * k * d, fill=NAN16)
+        if fused:
+            g.encode_gate_up_down(layer, hidden, d, P, B, 2, act, part, k, d, f)
+        else:
+            g.encode_gate_up(layer, hidden, d, P, B, 2, act, d, f)
+            g.encode_down(layer, act, P, B, 2, part, k, d, f)
+        with pytest.raises(tsg.TsgError) as e:
+            ctx.synchronize()
+        assert "past the layer" in str(e.value)
+        a = host(act, np.uint16).reshape(t * k, f)
+        assert np.all(np.isfinite(oracle.f16_to_float(a[:16]))), "the valid block's rows"
+        assert np.all(a[16:] == NAN16), "the skipped block wrote nothing"
+    ctx.synchronize()  # the error word was cleared

@@ -170,6 +170,10 @@ extern "C" tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream) {
             return fail(TSG_ERR_INVALID_ARGUMENT,
                         "rows path: a device block had no rows, more than 8, or an expert past "
                         "the layer; it was skipped");
+        if (err & kErrGemmBlock)
+            return fail(TSG_ERR_INVALID_ARGUMENT,
+                        "grouped GEMM: a routed block named an expert past the layer; it was "
+                        "skipped and its rows were not written");
         if (err & kErrGemmWait)
             return fail(TSG_ERR_HIP, "fused grouped GEMM: a down item timed out waiting for its "
                                      "block's gate/up tiles, or an XCD queue was not drained; "

@@ -889,6 +889,12 @@ __device__ void gemm_work_item(const GemmArgs& args, uint32_t nb, uint32_t pid, 
 template <int G, bool SYM, int ACT, int MODE>
 __device__ __forceinline__ void gemm_item(const GemmArgs& args, const tsg_routed_block& blk,
                                           uint32_t tile, uint8_t* smem) {
+    // a block list written on the device is not checked on the host: an
+    // expert past the layer is skipped (its weights would lie outside it)
+    if (MODE != 2 && blk.local_slot >= args.num_experts) {
+        if (threadIdx.x == 0) atomicOr(args.error, kErrGemmBlock);
+        return;
+    }
     for (uint32_t r0 = 0; r0 < blk.row_count; r0 += kGemmRows) {
         if (r0) block_barrier();  // every wave is done with the previous pass's LDS
         tsg_routed_block sub = blk;

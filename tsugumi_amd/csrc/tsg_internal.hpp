@@ -120,6 +120,7 @@ constexpr uint32_t kErrGroupExpertRange = 2u;
 constexpr uint32_t kErrGroupBlocks = 4u;
 constexpr uint32_t kErrRowsBlock = 8u;  // a device-list rows-path block it cannot take
 constexpr uint32_t kErrGemmWait = 16u;  // the fused GEMM: a wait timed out or a queue not drained
+constexpr uint32_t kErrGemmBlock = 32u;  // a grouped-GEMM block names an expert past the layer
 constexpr uint32_t kSyncLogitWord = 1088;  // tagged 64-bit logits, kMaxExperts per group
 static_assert(kSyncLogitWord + kDecodeGroups * 2 * kMaxExperts <= kMaxCounters, "sync area overflow");
 static_assert(kSyncLogitWord % 2 == 0, "64-bit words must be aligned");
