@@ -388,6 +388,45 @@ __device__ __forceinline__ void staged_chunk_sums(const uint16_t* dst, uint32_t 
 // `row_index` (may be NULL) maps staged row r to source row row_index[r].
 // COHERENT reads the source with agent-coherent loads (data written earlier
 // in the same launch by other blocks).
+// One staging pass split in two, for callers that issue other loads in
+// between: the pass's global loads of units q0 .. q0 + blockDim * PT (of
+// `total`, bpr units of 8 halves per row) into v, then their LDS stores.
+// Loads complete in issue order, so a store that waits for v waits for
+// nothing issued after the pass's loads.
+template <int PT, bool COHERENT = false>
+__device__ __forceinline__ void stage_act_load(const uint16_t* __restrict__ src,
+                                               uint32_t src_stride, uint32_t total, uint32_t bpr,
+                                               uint32_t q0, const uint32_t* row_index,
+                                               uint4 (&v)[PT]) {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+        // plain loads clamp (a repeated unit is a cache hit and keeps the
+        // loads branch-free); coherent loads skip: each is a memory-side
+        // access, and repeats of one unit would all queue on one line
+        const uint32_t q_raw = q0 + threadIdx.x + i * blockDim.x;
+        const uint32_t q = min(q_raw, total - 1u);
+        const uint32_t r = q / bpr, b = q - r * bpr;
+        const uint32_t sr = row_index ? row_index[r] : r;
+        const uint16_t* sp = src + (uint64_t)sr * src_stride + b * 8u;
+        if constexpr (COHERENT) v[i] = q_raw < total ? ld_coherent16(sp) : make_uint4(0, 0, 0, 0);
+        else v[i] = *reinterpret_cast<const uint4*>(sp);
+    }
+}
+template <int PT>
+__device__ __forceinline__ void stage_act_store(uint32_t total, uint32_t bpr, uint32_t q0,
+                                                uint16_t* dst, uint32_t dst_stride,
+                                                const uint4 (&v)[PT]) {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+        const uint32_t q = q0 + threadIdx.x + i * blockDim.x;
+        if (q < total) {
+            const uint32_t r = q / bpr, b = q - r * bpr;
+            *reinterpret_cast<uint4*>(dst + (size_t)r * dst_stride + (b >> 2) * kChunkLds +
+                                      (b & 3u) * 8u) = pair_permute(v[i]);
+        }
+    }
+}
+
 template <bool SYM, int PER_THREAD = 4, bool COHERENT = false>
 __device__ __forceinline__ void stage_act_rows(const uint16_t* __restrict__ src,
                                                uint32_t src_stride, uint32_t rows, uint32_t n,
@@ -398,28 +437,8 @@ __device__ __forceinline__ void stage_act_rows(const uint16_t* __restrict__ src,
     const uint32_t total = rows * bpr;
     for (uint32_t q0 = 0; q0 < total; q0 += blockDim.x * PER_THREAD) {
         uint4 v[PER_THREAD];
-#pragma unroll
-        for (int i = 0; i < PER_THREAD; ++i) {
-            // plain loads clamp (a repeated unit is a cache hit and keeps the
-            // loads branch-free); coherent loads skip: each is a memory-side
-            // access, and repeats of one unit would all queue on one line
-            const uint32_t q_raw = q0 + threadIdx.x + i * blockDim.x;
-            const uint32_t q = min(q_raw, total - 1u);
-            const uint32_t r = q / bpr, b = q - r * bpr;
-            const uint32_t sr = row_index ? row_index[r] : r;
-            const uint16_t* sp = src + (uint64_t)sr * src_stride + b * 8u;
-            if constexpr (COHERENT) v[i] = q_raw < total ? ld_coherent16(sp) : make_uint4(0, 0, 0, 0);
-            else v[i] = *reinterpret_cast<const uint4*>(sp);
-        }
-#pragma unroll
-        for (int i = 0; i < PER_THREAD; ++i) {
-            const uint32_t q = q0 + threadIdx.x + i * blockDim.x;
-            if (q < total) {
-                const uint32_t r = q / bpr, b = q - r * bpr;
-                *reinterpret_cast<uint4*>(dst + (size_t)r * dst_stride + (b >> 2) * kChunkLds +
-                                          (b & 3u) * 8u) = pair_permute(v[i]);
-            }
-        }
+        stage_act_load<PER_THREAD, COHERENT>(src, src_stride, total, bpr, q0, row_index, v);
+        stage_act_store<PER_THREAD>(total, bpr, q0, dst, dst_stride, v);
     }
     if constexpr (!SYM) {
         __syncthreads();
