@@ -421,8 +421,9 @@ __global__ __launch_bounds__(1024) void phase1_kernel(BlobSource src, tsg_expert
     }
     const GULane l = gu_lane(src, o, d, G, slot, fr, live);
     ChunkBatch<kGUBatch> bt;
-    load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, 0u, threadIdx.x & 15u, d / 32u, bt);
-    stage_act_rows<SYM>(x, 0u, 1u, d, xs, 0u, xsum);
+    stage_act_rows_around<SYM>(x, 0u, 1u, d, xs, 0u, xsum, nullptr, [&] {
+        load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, 0u, threadIdx.x & 15u, d / 32u, bt);
+    });
     __syncthreads();
     uint16_t v;
     if (phase1_compute<G, SYM, ACT>(l, bt, xs, xsum, d, v)) acts[l.slot * f + l.fr] = v;
@@ -445,8 +446,9 @@ __global__ __launch_bounds__(1024) void phase2_kernel(BlobSource src, tsg_expert
     const uint32_t row = blockIdx.x * rows_per_block + (threadIdx.x >> 6);
     ChunkBatch<kDBatch> bt;
     uint16_t res_bits;
-    phase2_prefetch<G, SYM>(src, o, residual, d, f, row, bt, res_bits);
-    stage_act_rows<SYM>(acts, f, kTopK, f, as, slot_h, asum);
+    stage_act_rows_around<SYM>(acts, f, kTopK, f, as, slot_h, asum, nullptr, [&] {
+        phase2_prefetch<G, SYM>(src, o, residual, d, f, row, bt, res_bits);
+    });
     __syncthreads();
     phase2_body<G, SYM>(src, o, as, slot_h, asum, routing_w, res_bits, y, d, f, row, bt, true);
 }

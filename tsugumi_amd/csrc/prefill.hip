@@ -1142,26 +1142,14 @@ __device__ __forceinline__ void rows_gate_up_body(const GemmArgs& args, const ts
     const uint8_t* w = blob + (is_up ? args.o.up_w : args.o.gate_w) + (uint64_t)fr * (d / 2u);
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + (is_up ? args.o.up_s : args.o.gate_s)) + (uint64_t)fr * ngroups;
     const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + (is_up ? args.o.up_b : args.o.gate_b)) + (uint64_t)fr * ngroups;
-    // The staging's first pass is issued before the weights: loads complete
-    // in issue order, so its LDS stores then wait for the activation rows (L2)
-    // and not for the weights (HBM), which stream in while the stores and the
-    // first chunks run. Its row indices cost one round trip first.
+    // the staging's loads go out before the weights (stage_act_rows_around);
+    // its row indices cost one round trip first
     if (threadIdx.x < rows) tok[threadIdx.x] = args.pairs[blk.pair_start + threadIdx.x].token;
     __syncthreads();
-    const uint32_t bpr = d / 8u, total = rows * bpr;
-    uint4 sv[4];
-    stage_act_load<4>(args.a, args.a_stride, total, bpr, 0u, tok, sv);
     ChunkBatch<kGUBatch> bt;
-    load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, 0u, j, nchunks, bt);
-    stage_act_store<4>(total, bpr, 0u, xs, row_h, sv);
-    for (uint32_t q0 = 4u * blockDim.x; q0 < total; q0 += 4u * blockDim.x) {
-        stage_act_load<4>(args.a, args.a_stride, total, bpr, q0, tok, sv);
-        stage_act_store<4>(total, bpr, q0, xs, row_h, sv);
-    }
-    if constexpr (!SYM) {
-        __syncthreads();
-        staged_chunk_sums(xs, row_h, rows, d, xsum);
-    }
+    stage_act_rows_around<SYM>(args.a, args.a_stride, rows, d, xs, row_h, xsum, tok, [&] {
+        load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, 0u, j, nchunks, bt);
+    });
     __syncthreads();
     float acc[kRowsMax];
 #pragma unroll
@@ -1202,27 +1190,16 @@ __device__ __forceinline__ void rows_down_body(const GemmArgs& args, const tsg_r
     const uint8_t* w = blob + args.o.down_w + (uint64_t)rr * (f / 2u);
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + args.o.down_s) + (uint64_t)rr * ngroups;
     const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + args.o.down_b) + (uint64_t)rr * ngroups;
-    // the staging's loads go out before the weights (see rows_gate_up_body);
-    // its rows are consecutive, so no index load comes first
-    const uint16_t* arow = args.a + (uint64_t)blk.local_row * f;
-    const uint32_t bpr = f / 8u, total = rows * bpr;
-    uint4 sv[4];
-    stage_act_load<4>(arow, f, total, bpr, 0u, nullptr, sv);
+    // the staging's loads go out before the weights (stage_act_rows_around)
     ChunkBatch<kDBatch> bt;
-    load_batch<G, SYM, kDBatch, kDLanes>(w, sc, bi, 0u, j, nchunks, bt);
-    if (threadIdx.x < rows) {
-        const tsg_token_expert_pair pr = args.pairs[blk.pair_start + threadIdx.x];
-        dst[threadIdx.x] = (pr.token * args.top_k + pr.rank) * d;
-    }
-    stage_act_store<4>(total, bpr, 0u, as, row_h, sv);
-    for (uint32_t q0 = 4u * blockDim.x; q0 < total; q0 += 4u * blockDim.x) {
-        stage_act_load<4>(arow, f, total, bpr, q0, nullptr, sv);
-        stage_act_store<4>(total, bpr, q0, as, row_h, sv);
-    }
-    if constexpr (!SYM) {
-        __syncthreads();
-        staged_chunk_sums(as, row_h, rows, f, asum);
-    }
+    stage_act_rows_around<SYM>(args.a + (uint64_t)blk.local_row * f, f, rows, f, as, row_h, asum,
+                               nullptr, [&] {
+                                   load_batch<G, SYM, kDBatch, kDLanes>(w, sc, bi, 0u, j, nchunks, bt);
+                                   if (threadIdx.x < rows) {
+                                       const tsg_token_expert_pair pr = args.pairs[blk.pair_start + threadIdx.x];
+                                       dst[threadIdx.x] = (pr.token * args.top_k + pr.rank) * d;
+                                   }
+                               });
     __syncthreads();
     float acc[kRowsMax];
 #pragma unroll

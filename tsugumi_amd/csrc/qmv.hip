@@ -38,8 +38,9 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint8_t* __restrict__ w,
     const uint16_t* sr = scales + (uint64_t)rr * ngroups;
     const uint16_t* br = biases + (uint64_t)rr * ngroups;
     ChunkBatch<kGUBatch> bt;
-    load_batch<G, SYM, kGUBatch, kGULanes, WA>(wr, sr, br, 0u, j, nchunks, bt);
-    stage_act_rows<SYM>(x, x_stride, t, n, xs, row_h, xsum);
+    stage_act_rows_around<SYM>(x, x_stride, t, n, xs, row_h, xsum, nullptr, [&] {
+        load_batch<G, SYM, kGUBatch, kGULanes, WA>(wr, sr, br, 0u, j, nchunks, bt);
+    });
     __syncthreads();
     float acc[T];
 #pragma unroll

@@ -98,8 +98,9 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(const uint8_t* __re
     const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + (is_up ? o.up_b : o.gate_b)) +
                          (uint64_t)pr * ngroups;
     ChunkBatch<kGUBatch> bt;
-    load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, 0u, j, nchunks, bt);
-    stage_act_rows<SYM>(x, x_stride, R == 1 ? 1u : rows, d, xs, row_h, xsum);
+    stage_act_rows_around<SYM>(x, x_stride, R == 1 ? 1u : rows, d, xs, row_h, xsum, nullptr, [&] {
+        load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, 0u, j, nchunks, bt);
+    });
     __syncthreads();
     float acc[R];
 #pragma unroll
@@ -138,9 +139,10 @@ __global__ __launch_bounds__(kGateThreads) void shared_down_kernel(
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(blob + o.down_s) + (uint64_t)rr * ngroups;
     const uint16_t* bi = reinterpret_cast<const uint16_t*>(blob + o.down_b) + (uint64_t)rr * ngroups;
     ChunkBatch<kGUBatch> bt;
-    load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, 0u, j, nchunks, bt);
     const uint32_t nr = R == 1 ? 1u : rows;
-    stage_act_rows<SYM>(act, f, nr, f, as, row_h, asum);
+    stage_act_rows_around<SYM>(act, f, nr, f, as, row_h, asum, nullptr, [&] {
+        load_batch<G, SYM, kGUBatch, kGULanes>(w, sc, bi, 0u, j, nchunks, bt);
+    });
     float logit0 = 0.0f;
     if constexpr (R == 1) {
         logit0 = gate_logit_block(x, gate_w, d, red);  // synchronises

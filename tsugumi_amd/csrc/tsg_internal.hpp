@@ -446,6 +446,38 @@ __device__ __forceinline__ void stage_act_rows(const uint16_t* __restrict__ src,
     }
 }
 
+// stage_act_rows with other loads issued between the first pass's loads and
+// its LDS stores: `between()` issues them (the GEMV's weight batch). Loads
+// complete in issue order, so the stores wait for the activation rows only
+// and the weights stream in while the stores and the first chunks run;
+// issued the other way round, the stores would wait for every weight.
+template <bool SYM, class Between, int PER_THREAD = 4>
+__device__ __forceinline__ void stage_act_rows_around(const uint16_t* __restrict__ src,
+                                                      uint32_t src_stride, uint32_t rows,
+                                                      uint32_t n, uint16_t* dst,
+                                                      uint32_t dst_stride, float* sums,
+                                                      const uint32_t* row_index,
+                                                      Between&& between) {
+    const uint32_t bpr = n / 8u;
+    const uint32_t total = rows * bpr;
+    if (total == 0u) {  // nothing to stage (and no unit to clamp to)
+        between();
+        return;
+    }
+    uint4 v[PER_THREAD];
+    stage_act_load<PER_THREAD>(src, src_stride, total, bpr, 0u, row_index, v);
+    between();
+    stage_act_store<PER_THREAD>(total, bpr, 0u, dst, dst_stride, v);
+    for (uint32_t q0 = blockDim.x * PER_THREAD; q0 < total; q0 += blockDim.x * PER_THREAD) {
+        stage_act_load<PER_THREAD>(src, src_stride, total, bpr, q0, row_index, v);
+        stage_act_store<PER_THREAD>(total, bpr, q0, dst, dst_stride, v);
+    }
+    if constexpr (!SYM) {
+        __syncthreads();
+        staged_chunk_sums(dst, dst_stride, rows, n, sums);
+    }
+}
+
 // Activations of chunk c in the staged layout.
 __device__ __forceinline__ const h2_t* staged_chunk(const uint16_t* xs, uint32_t c) {
     return reinterpret_cast<const h2_t*>(xs + c * kChunkLds);
