@@ -637,7 +637,7 @@ def test_decode_layer_shared_expert(tsg, ctx, d, f, ne, sf, group, scheme):
                                  (1024, 2816), (2816, 8192)])
 def test_qmv_projection_shapes(tsg, ctx, m, n):
     """DequantInt4GEMV's decode projection shapes (DequantInt4GEMV.swift:13-20):
-    encode against DequantInt4GemvRef within the GEMV tolerance, and 8 rows
+    encode against DequantInt4GemvRef within the north star's 1e-3, and 8 rows
     through encodeRows / encodeRowsWide (split into launches that fit the LDS
     at n = 8192) bit-equal to 8 single-row calls."""
     configure(ctx, 32, "sym")
@@ -652,7 +652,8 @@ def test_qmv_projection_shapes(tsg, ctx, m, n):
     q.encode(W, S, S, dev(np.ascontiguousarray(xs[0])), y, m, n)
     ref = oracle.dequant_int4_gemv_ref(packed, scales, None, oracle.f16_to_float(xs[0]), n, 32)
     rel = oracle.relative_error(oracle.f16_to_float(host(y, np.uint16)), ref)
-    assert rel <= kc.FP16_REDUCTION
+    print(f"  rel={rel:.3e}", flush=True)
+    assert rel <= kc.NORTH_STAR
     yr = empty(8 * m)
     q.encode_rows_wide(W, S, S, dev(xs), n, yr, m, 8, m, n)
     rows = host(yr, np.uint16).reshape(8, m)
