@@ -52,8 +52,9 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
 // One block per expert e: rank_of[p] = position of pair p among the pairs of
 // expert e in (token, rank) order; counts[e] = their number. Thread i owns
 // the consecutive tokens [i * tpt, (i + 1) * tpt): it counts its matches,
-// one block scan places them, and a second pass over the same (cached)
-// indices writes the ranks.
+// one block scan places them, and a second pass over the same indices (kept
+// in registers for top-8 up to 4096 tokens, else re-read from the cache)
+// writes the ranks.
 __global__ __launch_bounds__(1024) void group_rank_kernel(const uint32_t* __restrict__ idx,
                                                           uint32_t t, uint32_t k,
                                                           uint32_t* __restrict__ rank_of,
@@ -63,6 +64,40 @@ __global__ __launch_bounds__(1024) void group_rank_kernel(const uint32_t* __rest
     const uint32_t tpt = (t + 1023u) / 1024u;
     const uint32_t p0 = min(threadIdx.x * tpt, t) * k, p1 = min(threadIdx.x * tpt + tpt, t) * k;
     uint32_t c = 0;
+    constexpr uint32_t kKeep = 4;  // tokens per thread kept in registers (t <= 4096)
+    if (k == 8u && tpt <= kKeep && (reinterpret_cast<uintptr_t>(idx) & 15u) == 0) {
+        // top-8 routing up to 4096 tokens: the thread's indices stay in
+        // registers between the count and the rank pass
+        uint4 va[kKeep], vb[kKeep];
+#pragma unroll
+        for (uint32_t i = 0; i < kKeep; ++i) {
+            const uint32_t p = p0 + 8u * i;
+            if (p < p1) {
+                va[i] = *reinterpret_cast<const uint4*>(idx + p);
+                vb[i] = *reinterpret_cast<const uint4*>(idx + p + 4u);
+            } else {
+                va[i] = vb[i] = make_uint4(~0u, ~0u, ~0u, ~0u);  // matches no expert
+            }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kKeep; ++i)
+            c += (va[i].x == e) + (va[i].y == e) + (va[i].z == e) + (va[i].w == e) +
+                 (vb[i].x == e) + (vb[i].y == e) + (vb[i].z == e) + (vb[i].w == e);
+        uint32_t total;
+        uint32_t before = block_exclusive_scan<1024>(c, wave_tot, total);
+        if (c) {
+#pragma unroll
+            for (uint32_t i = 0; i < kKeep; ++i) {
+                const uint32_t v[8] = {va[i].x, va[i].y, va[i].z, va[i].w,
+                                       vb[i].x, vb[i].y, vb[i].z, vb[i].w};
+#pragma unroll
+                for (uint32_t q = 0; q < 8u; ++q)
+                    if (v[q] == e) rank_of[p0 + 8u * i + q] = before++;
+            }
+        }
+        if (threadIdx.x == 0) counts[e] = total;
+        return;
+    }
     if (k == 8u && (reinterpret_cast<uintptr_t>(idx) & 15u) == 0) {
         for (uint32_t p = p0; p < p1; p += 8u) {
             const uint4 a = *reinterpret_cast<const uint4*>(idx + p);
