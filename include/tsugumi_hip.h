@@ -463,7 +463,10 @@ tsg_status tsg_prefill_group_pairs_device_noalloc(tsg_ctx* ctx, tsg_stream strea
  * multiples of 64; at group size 32 the scale/bias sub-tensor offsets must be
  * 4-byte aligned (TSG_ERR_ALIGNMENT).
  * n_blocks_device: optional device count bounding `blocks` (may be NULL, then
- * n_blocks is used). */
+ * n_blocks is used). A block naming an expert past the layer is skipped and
+ * tsg_ctx_synchronize reports TSG_ERR_INVALID_ARGUMENT (the list may live on
+ * the device, out of the host's sight); the same holds for
+ * tsg_prefill_moe_down and tsg_prefill_moe_gate_up_down. */
 tsg_status tsg_prefill_moe_gate_up(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
                                    const uint16_t* hidden, uint32_t hidden_stride_elements,
                                    const tsg_token_expert_pair* sorted_pairs,

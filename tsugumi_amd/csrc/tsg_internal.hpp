@@ -114,7 +114,8 @@ constexpr uint32_t kSyncErrorWord = 1056;  // device-side error bits (kErr*), re
 // not grouped); a device grouping whose work list did not fit max_blocks; a
 // device-list rows-path block with no rows, more than 8, or an expert past
 // the layer (skipped); the fused grouped GEMM's down item that waited too long
-// for its block's gate/up tiles, or an XCD queue no workgroup drained.
+// for its block's gate/up tiles, or an XCD queue no workgroup drained; a
+// grouped-GEMM block (device list) naming an expert past the layer (skipped).
 constexpr uint32_t kErrDecodeTimeout = 1u;
 constexpr uint32_t kErrGroupExpertRange = 2u;
 constexpr uint32_t kErrGroupBlocks = 4u;
