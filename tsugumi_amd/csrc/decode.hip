@@ -503,7 +503,8 @@ __device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t payload) {
 // the wave sets the error word and returns.
 template <int N, typename Addr, typename Use>
 __device__ __forceinline__ void poll_tagged(const DecodeSync& sy, uint32_t tag, uint32_t live,
-                                            Addr&& addr, Use&& use) {
+                                            Addr&& addr, Use&& use,
+                                            uint32_t err_bit = kErrDecodeTimeout) {
     uint32_t pending = live;
     for (uint32_t spins = 0;; ++spins) {
         uint64_t w[N];
@@ -519,7 +520,7 @@ __device__ __forceinline__ void poll_tagged(const DecodeSync& sy, uint32_t tag, 
         }
         if (__all(pending == 0u)) return;
         if (spins > kSpinLimit) {
-            if ((threadIdx.x & 63u) == 0) atomicOr(sy.error, kErrDecodeTimeout);
+            if ((threadIdx.x & 63u) == 0) atomicOr(sy.error, err_bit);
             return;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -856,8 +857,13 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
     const uint32_t nchunks = d / 8u;
     uint32_t gains[4] = {0u, 0u, 0u, 0u};
     if constexpr (SELECT && !STAGE) load_expert_gains(pes, ne, gains);
-    // STAGE: thread t's expert gain, for the last block (requested early)
+    // STAGE: thread t's expert gain, for the selecting block (requested early),
+    // and the launch epoch (the tag of this launch's logits is epoch + 1)
     const uint32_t my_gain = (STAGE && threadIdx.x < ne) ? pes[threadIdx.x] : 0u;
+    uint32_t* const r_epoch = counters + kRouterEpochWord;
+    uint64_t* const r_logits = reinterpret_cast<uint64_t*>(counters + kRouterLogitWord);
+    uint32_t epoch0 = 0;
+    if (STAGE && threadIdx.x == 0) epoch0 = ld_coherent(r_epoch);
     uint4 wv[kRouterChunks], ev[kRouterChunks], xv[kRouterChunks];
     if (e < ne) {
         const uint16_t* wr = w + (uint64_t)e * d;
@@ -870,20 +876,22 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
                 xv[i] = *reinterpret_cast<const uint4*>(hidden + (uint64_t)r0 * hidden_stride + cc * 8u);
         }
     }
+    __shared__ uint32_t s_tag;
     if constexpr (STAGE) {
         for (uint32_t q = threadIdx.x; q < nr * nchunks; q += blockDim.x) {
             const uint32_t r = q / nchunks, c = q - r * nchunks;
             xrows[q] = *reinterpret_cast<const uint4*>(hidden + (uint64_t)(r0 + r) * hidden_stride + c * 8u);
         }
+        if (threadIdx.x == 0) s_tag = epoch0 + 1u == 0u ? 1u : epoch0 + 1u;  // words start at tag 0
         __syncthreads();
+        const uint32_t tag = s_tag;
         for (uint32_t r = wave; r < nr; r += kStageWaves) {
 #pragma unroll
             for (int i = 0; i < kRouterChunks; ++i)
                 xv[i] = xrows[r * nchunks + min(lane + 64u * i, nchunks - 1u)];
             const float acc = router_chunks_dot(wv, xv, ev, nchunks, lane);
             if (lane == 0)
-                st_coherent(reinterpret_cast<uint32_t*>(logits) + (uint64_t)(r0 + r) * logits_stride + e,
-                            __float_as_uint(acc));
+                st_coherent(r_logits + (uint64_t)r * kMaxExperts + e, tagged(tag, __float_as_uint(acc)));
         }
     } else if (e < ne) {
         for (uint32_t r = 0; r < nr; ++r) {
@@ -905,17 +913,25 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
         }
     }
     if constexpr (SELECT) {
-        // logits travel by agent-coherent stores/loads: completing this
-        // block's stores before it counts itself is all the last block needs
+        // STAGE: block 0 selects, polling the other blocks' tagged logits (the
+        // launch's blocks are co-resident: one per expert; the wait is
+        // bounded); the other blocks leave once posted. Otherwise the last
+        // block to finish selects: logits travel by agent-coherent
+        // stores/loads, and completing this block's stores before it counts
+        // itself is all the last block needs.
         __shared__ uint32_t is_last;
-        wait_vector_memory();
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const uint32_t done = atomicAdd(&counters[blockIdx.y], 1u);
-            is_last = (done == gridDim.x - 1u) ? 1u : 0u;
+        if constexpr (STAGE) {
+            if (blockIdx.x != 0) return;
+        } else {
+            wait_vector_memory();
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                const uint32_t done = atomicAdd(&counters[blockIdx.y], 1u);
+                is_last = (done == gridDim.x - 1u) ? 1u : 0u;
+            }
+            __syncthreads();
         }
-        __syncthreads();
-        if (is_last) {
+        if (STAGE || is_last) {
             if constexpr (STAGE) {
                 __shared__ uint32_t s_gain[kMaxExperts];
                 __shared__ __align__(16) uint64_t s_cand[kStageWaves][kMaxExperts + kCandBatch];
@@ -929,14 +945,19 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
                 const uint32_t ne4 = (ne + 3u) & ~3u;
                 const uint32_t r = wave;  // one row per wave
                 if (r < nr) {
-                    uint32_t key[4];
+                    uint32_t key[4], bits[4] = {0u, 0u, 0u, 0u}, live = 0u;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (lane + 64u * j < ne) live |= 1u << j;
+                    DecodeSync sy;
+                    sy.error = counters + kSyncErrorWord;
+                    poll_tagged<4>(sy, s_tag, live,
+                                   [&](int j) { return r_logits + (uint64_t)r * kMaxExperts + lane + 64u * j; },
+                                   [&](int j, uint32_t b) { bits[j] = b; }, kErrRouterWait);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const uint32_t ej = lane + 64u * j;
-                        const float v = ej < ne ? __uint_as_float(ld_coherent(
-                                                      reinterpret_cast<const uint32_t*>(logits) +
-                                                      (uint64_t)(r0 + r) * logits_stride + ej))
-                                                : -INFINITY;
+                        const float v = ej < ne ? __uint_as_float(bits[j]) : -INFINITY;
                         key[j] = (v == v && v != -INFINITY) ? order_key(v) : 0u;
                     }
                     if (lane < kTopK) {
@@ -969,13 +990,16 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
                     out_idx[(uint64_t)r0 * kTopK + t] = my_id;
                     out_w[(uint64_t)r0 * kTopK + t] = (uint16_t)my_wb;
                 }
+                // every block has posted (the polls saw all tags): the next
+                // launch may use tag + 1
+                if (t == 0) st_coherent(r_epoch, s_tag);
             } else {
                 for (uint32_t r = wave; r < nr; r += kRouterWaves)
                     wave_topk_softmax(logits + (uint64_t)(r0 + r) * logits_stride, ne, gains,
                                       out_idx + (uint64_t)(r0 + r) * kTopK,
                                       out_w + (uint64_t)(r0 + r) * kTopK);
+                if (threadIdx.x == 0) atomicExch(&counters[blockIdx.y], 0u);
             }
-            if (threadIdx.x == 0) atomicExch(&counters[blockIdx.y], 0u);
         }
     }
 }

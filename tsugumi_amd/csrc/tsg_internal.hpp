@@ -98,7 +98,7 @@ namespace tsg {
 constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kMaxRouterRows = 8;      // MoE.maxRouterRows (verify rows)
 constexpr uint32_t kMaxPromptRows = 4096;   // rows one router launch may route
-constexpr uint32_t kMaxCounters = 8192;
+constexpr uint32_t kMaxCounters = 12288;
 constexpr uint32_t kGemmSchedBlocks = 65536;             // routed blocks the fused GEMM takes
 constexpr uint32_t kGemmSchedWords = 16u + kGemmSchedBlocks;
 // Words of ctx->counters used by the one-launch decode layer (below them, words
@@ -115,15 +115,23 @@ constexpr uint32_t kSyncErrorWord = 1056;  // device-side error bits (kErr*), re
 // device-list rows-path block with no rows, more than 8, or an expert past
 // the layer (skipped); the fused grouped GEMM's down item that waited too long
 // for its block's gate/up tiles, or an XCD queue no workgroup drained; a
-// grouped-GEMM block (device list) naming an expert past the layer (skipped).
+// grouped-GEMM block (device list) naming an expert past the layer (skipped);
+// the staged router's selector that timed out waiting for a logit.
 constexpr uint32_t kErrDecodeTimeout = 1u;
 constexpr uint32_t kErrGroupExpertRange = 2u;
 constexpr uint32_t kErrGroupBlocks = 4u;
 constexpr uint32_t kErrRowsBlock = 8u;  // a device-list rows-path block it cannot take
 constexpr uint32_t kErrGemmWait = 16u;  // the fused GEMM: a wait timed out or a queue not drained
 constexpr uint32_t kErrGemmBlock = 32u;  // a grouped-GEMM block names an expert past the layer
+constexpr uint32_t kErrRouterWait = 64u;  // the staged router's selector timed out on a logit
 constexpr uint32_t kSyncLogitWord = 1088;  // tagged 64-bit logits, kMaxExperts per group
 static_assert(kSyncLogitWord + kDecodeGroups * 2 * kMaxExperts <= kMaxCounters, "sync area overflow");
+// The staged router's hand-off (rows <= kMaxRouterRows): its launch epoch and
+// tagged 64-bit logits, kMaxExperts per row.
+constexpr uint32_t kRouterEpochWord = 5248;
+constexpr uint32_t kRouterLogitWord = 5376;
+static_assert(kRouterEpochWord >= kSyncLogitWord + kDecodeGroups * 2 * kMaxExperts, "router area");
+static_assert(kRouterLogitWord + kMaxRouterRows * 2 * kMaxExperts <= kMaxCounters, "router area overflow");
 static_assert(kSyncLogitWord % 2 == 0, "64-bit words must be aligned");
 // Per-group hand-off regions of the one-launch layer (ctx->act_replicas):
 // group g's region holds kHandoffWords tagged 64-bit words, its slot's
