@@ -98,7 +98,13 @@ const char* tsg_status_string(tsg_status status);
 /* Library version "major.minor.patch". */
 const char* tsg_version(void);
 
-/* MetalContext.init (MetalContext.swift:79-100): binds `device`. */
+/* MetalContext.init (MetalContext.swift:79-100): binds `device`. The context
+ * owns small device scratch that several entry points share (router logits
+ * and their hand-off words, completion counters, the decode layer's hand-off
+ * regions, the fused GEMM's queues): calls on one context run in stream
+ * order, as the reference's encoders append to one command buffer; a caller
+ * that issues on several streams orders them with events or uses one context
+ * per stream. */
 tsg_status tsg_ctx_create(int device, tsg_ctx** out);
 void tsg_ctx_destroy(tsg_ctx* ctx);
 /* MetalContext.setAffineGroupSize / setAffineScheme (MetalContext.swift:135-175).
