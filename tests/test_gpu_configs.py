@@ -616,3 +616,32 @@ def test_grouped_gemm_skips_and_reports_expert_past_layer(tsg, ctx, gemma_layer)
         assert np.all(np.isfinite(oracle.f16_to_float(a[:16]))), "the valid block's rows"
         assert np.all(a[16:] == NAN16), "the skipped block wrote nothing"
     ctx.synchronize()  # the error word was cleared
+
+
+def test_fused_gate_up_down_empty_device_list(tsg, ctx, gemma_layer):
+    """A device count of zero (no routed block) runs the fused launch to its
+    end without work, writes nothing and reports nothing; the next launch on
+    the same context still runs a real list (the schedule was left reset)."""
+    configure(ctx, 32, "sym")
+    layer = gemma_layer[0]
+    d, f, k, t = 2816, 704, 8, 4
+    g = tsg.PrefillGroupedRoutedMoE(tsg.MoE(ctx))
+    pairs = np.zeros(t * k, oracle.PAIR_DTYPE)
+    pairs["token"] = np.repeat(np.arange(t, dtype=np.uint32), k)
+    pairs["rank"] = np.tile(np.arange(k, dtype=np.uint32), t)
+    blocks = np.array([(3, 0, t * k, 0)], dtype=oracle.BLOCK_DTYPE)
+    hidden = dev(wl.f16_normal(np.random.default_rng(9), t * d))
+    P, B = dev(pairs), dev(blocks.view(np.uint32))
+    act, part = empty(t * k * f, fill=NAN16), empty(t * k * d, fill=NAN16)
+    g.encode_gate_up_down(layer, hidden, d, P, B, 1, act, part, k, d, f,
+                          n_blocks_device=dev(np.zeros(1, np.uint32)))
+    ctx.synchronize()
+    assert np.all(host(act, np.uint16) == NAN16) and np.all(host(part, np.uint16) == NAN16)
+    a2, p2 = empty(t * k * f, fill=NAN16), empty(t * k * d, fill=NAN16)
+    g.encode_gate_up(layer, hidden, d, P, B, 1, a2, d, f)
+    g.encode_down(layer, a2, P, B, 1, p2, k, d, f)
+    g.encode_gate_up_down(layer, hidden, d, P, B, 1, act, part, k, d, f,
+                          n_blocks_device=dev(np.ones(1, np.uint32)))
+    ctx.synchronize()
+    assert np.array_equal(host(act, np.uint16), host(a2, np.uint16))
+    assert np.array_equal(host(part, np.uint16), host(p2, np.uint16))
