@@ -558,12 +558,22 @@ def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, n
         sact = torch.empty(m * f, dtype=torch.int16, device="cuda")
         sout = torch.empty(n_layers * m * h, dtype=torch.int16, device="cuda")
     stream = torch.cuda.Stream()
+    # the shared branch depends only on the layer's input: it runs on a second
+    # stream (default priority) beside the routed path and joins at the
+    # layer's end (the shared-expert entry points use no context scratch)
+    side = torch.cuda.Stream()
 
     def body():
         for l in range(n_layers):
             x = hidden[l * m * h:(l + 1) * m * h]
             il, wl = idx[l * m * k:(l + 1) * m * k], wts[l * m * k:(l + 1) * m * k]
             nb = nbs[l:l + 1]
+            if shared is not None:
+                side.wait_stream(stream)
+                blob, o, gw = shared[l]
+                tsg.encode_shared_expert_rows(moe, blob, o, x, h, gw, sact,
+                                              sout[l * m * h:(l + 1) * m * h], m, h, f,
+                                              stream=side)
             moe.encode_router_gemma4_bf16_rows_grouped(routers[l], x, h, ones_h, ones_e, il, wl,
                                                        m, ne, h, sp, off, cnt, blocks,
                                                        max_blocks, nb, stream=stream)
@@ -572,10 +582,7 @@ def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, n
             red.encode_reduce_token_major(part, wl, h2[l * m * h:(l + 1) * m * h], m, k, h,
                                           stream=stream)
             if shared is not None:
-                blob, o, gw = shared[l]
-                tsg.encode_shared_expert_rows(moe, blob, o, x, h, gw, sact,
-                                              sout[l * m * h:(l + 1) * m * h], m, h, f,
-                                              stream=stream)
+                stream.wait_stream(side)
 
     ms = time_graph(torch, stream, body, reps=8)
     ctx.synchronize()

@@ -104,7 +104,8 @@ const char* tsg_version(void);
  * regions, the fused GEMM's queues): calls on one context run in stream
  * order, as the reference's encoders append to one command buffer; a caller
  * that issues on several streams orders them with events or uses one context
- * per stream. */
+ * per stream. The shared-expert entry points use no such scratch and may run
+ * beside the routed path. */
 tsg_status tsg_ctx_create(int device, tsg_ctx** out);
 void tsg_ctx_destroy(tsg_ctx* ctx);
 /* MetalContext.setAffineGroupSize / setAffineScheme (MetalContext.swift:135-175).
