@@ -195,6 +195,43 @@ def test_rows_path_matches_decode_bitwise(tsg, ctx):
     assert e.value.status == 4
 
 
+@pytest.mark.parametrize("form", ["host", "device"])
+def test_rows_path_many_blocks_matches_decode_bitwise(tsg, ctx, form):
+    """A launch with more rows blocks than the device holds at once (24 x 64
+    gate/up workgroups): every row still equals decode phase 1 bit for bit
+    (PrefillRoutedMoERowsVsDecodeTests.swift:23-166). 8 tokens, each routed to
+    all 8 experts, one row per block, through the host and device block
+    lists."""
+    configure(ctx, 32, "sym")
+    d, f, nt = 576, 384, 8
+    rng = oracle.SplitMix64(0x4D6)
+    parts = [[oracle.quantize_int4(rng.uniforms(-0.3, 0.3, r * c_).reshape(r, c_), 32, True)
+              for (r, c_) in ((f, d), (f, d), (d, f))] for _ in range(8)]
+    layer, offs, blobs = _upload_layer(tsg, ctx, parts, True)
+    x = oracle.seed_tree_key(0x4D6, "rows-many-blocks").uniforms_f16(-0.8, 0.8, nt * d)
+    moe = tsg.MoE(ctx)
+    idx = dev(np.arange(8, dtype=np.uint32))
+    want = np.empty((nt, 8, f), np.uint16)
+    for t in range(nt):
+        acts = empty(8 * f)
+        moe.encode_phase1_resident(layer, idx, dev(x[t * d:(t + 1) * d]), acts, d, f)
+        want[t] = host(acts, np.uint16).reshape(8, f)
+    n = nt * 8
+    pairs = np.array([(i // 8, i % 8, i % 8, 0x3C00) for i in range(n)], dtype=oracle.PAIR_DTYPE)
+    blocks = np.array([(i % 8, i, 1, i) for i in range(n)], dtype=oracle.BLOCK_DTYPE)
+    ract, parts_out = empty(n * f), empty(nt * 8 * d)
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    if form == "host":
+        g.encode_streamed_rows(layer, dev(x), d, dev(pairs), blocks, ract, parts_out, 8, d, f)
+    else:
+        g.encode_streamed_rows_device(layer, dev(x), d, dev(pairs), dev(blocks),
+                                      n, dev(np.array([n], np.uint32)), ract, parts_out, 8, d, f)
+    ctx.synchronize()
+    got = host(ract, np.uint16).reshape(nt, 8, f)
+    for t in range(nt):
+        assert np.array_equal(got[t], want[t]), f"token {t}"
+
+
 @pytest.mark.parametrize("t,k,d", [(37, 8, 2816), (5, 4, 104), (5, 3, 104), (7, 8, 100)])
 def test_reduce_token_major_bit_exact(tsg, ctx, t, k, d):
     """16-byte vector form (d % 8 == 0, k in 1, 2, 4, 8) and the scalar form
