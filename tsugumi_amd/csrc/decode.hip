@@ -862,10 +862,13 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
     const uint32_t my_gain = (STAGE && threadIdx.x < ne) ? pes[threadIdx.x] : 0u;
     uint32_t* const r_epoch = counters + kRouterEpochWord;
     uint64_t* const r_logits = reinterpret_cast<uint64_t*>(counters + kRouterLogitWord);
-    uint32_t epoch0 = 0;
-    if (STAGE && threadIdx.x == 0) epoch0 = ld_coherent(r_epoch);
+    // every thread reads the epoch (one request per wave), without a branch,
+    // so its wait lands at the tag's first use and not before the weight loads
+    const uint32_t epoch0 = STAGE ? ld_coherent(r_epoch) : 0u;
     uint4 wv[kRouterChunks], ev[kRouterChunks], xv[kRouterChunks];
-    if (e < ne) {
+    // (staged: the grid is one block per expert, so e < ne; unconditional
+    // loads keep the compiler's waits on later loads precise)
+    if (STAGE || e < ne) {
         const uint16_t* wr = w + (uint64_t)e * d;
 #pragma unroll
         for (int i = 0; i < kRouterChunks; ++i) {
@@ -878,9 +881,29 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
     }
     __shared__ uint32_t s_tag;
     if constexpr (STAGE) {
-        for (uint32_t q = threadIdx.x; q < nr * nchunks; q += blockDim.x) {
-            const uint32_t r = q / nchunks, c = q - r * nchunks;
-            xrows[q] = *reinterpret_cast<const uint4*>(hidden + (uint64_t)(r0 + r) * hidden_stride + c * 8u);
+        // the rows go to LDS in passes of kStageUnits 16-byte units per
+        // thread, every load of a pass issued before any of its stores: one
+        // memory round trip per pass, not one per unit (units past the end
+        // repeat the last one and store nothing)
+        constexpr uint32_t kStageUnits = 4;
+        const uint32_t total = nr * nchunks;
+        for (uint32_t q0 = 0; q0 < total; q0 += blockDim.x * kStageUnits) {
+            u32x4_t v[kStageUnits];
+#pragma unroll
+            for (uint32_t i = 0; i < kStageUnits; ++i) {
+                const uint32_t q = min(q0 + threadIdx.x + i * blockDim.x, total - 1u);
+                const uint32_t r = q / nchunks, c = q - r * nchunks;
+                v[i] = *reinterpret_cast<const u32x4_t*>(hidden + (uint64_t)(r0 + r) * hidden_stride + c * 8u);
+            }
+            // keeps the compiler from sinking each load into its conditional
+            // store below (which would make the round trips serial again)
+#pragma unroll
+            for (uint32_t i = 0; i < kStageUnits; ++i) asm volatile("" : "+v"(v[i]));
+#pragma unroll
+            for (uint32_t i = 0; i < kStageUnits; ++i) {
+                const uint32_t q = q0 + threadIdx.x + i * blockDim.x;
+                if (q < total) xrows[q] = make_uint4(v[i].x, v[i].y, v[i].z, v[i].w);
+            }
         }
         if (threadIdx.x == 0) s_tag = epoch0 + 1u == 0u ? 1u : epoch0 + 1u;  // words start at tag 0
         __syncthreads();
