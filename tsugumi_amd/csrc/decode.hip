@@ -1110,8 +1110,10 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
         for (int i = 0; i < kRouterChunks; ++i)
             rw[i] = *reinterpret_cast<const uint4*>(w_row + min(lane + 64u * i, units - 1u) * 8u);
     }
-    uint32_t epoch = 0;
-    if (t == 0) epoch = ld_coherent(sy.epoch);
+    // every thread reads the epoch (one request per wave), without a branch:
+    // a load inside `if (t == 0)` left wave 0 waiting for it, and for its
+    // router row issued before it, ahead of its x / es loads
+    const uint32_t epoch = ld_coherent(sy.epoch);
     const uint32_t gain = t < ne ? global_ptr(a.pes)[t] : 0u;
     const bool two = units > blockDim.x;
     const uint16_t* xg = global_ptr(a.x);
