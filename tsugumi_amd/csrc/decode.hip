@@ -559,6 +559,9 @@ struct DecodeLayerArgs {
     uint16_t* sh_acts;     // the shared activations, also returned to the caller
     uint32_t sh_f;
     uint32_t ss_off;       // dynamic LDS: staged shared activations
+    // the block size: blockDim.x is a kernarg load of its own, whose wait the
+    // compiler put ahead of the first phase's loads
+    uint32_t threads;
 };
 
 // Down row `row` of one slot on 8 lanes (lane = 8 r + j of the wave): the
@@ -1058,10 +1061,15 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     // The arguments are copied to LDS once: under SGPR pressure the compiler
     // re-reads kernel arguments instead of spilling, and a kernarg reload in
     // a loop costs a memory round trip each time; an LDS copy costs cycles.
+    // One word per thread, with no loop over blockDim (reading blockDim is a
+    // kernarg load of its own, a second round trip before this one): blocks
+    // have at least 128 threads (a poll wave beside the down rows).
     __shared__ DecodeLayerArgs a;
-    static_assert(sizeof(DecodeLayerArgs) % 4 == 0, "args copy");
-    for (uint32_t i = threadIdx.x; i < sizeof(DecodeLayerArgs) / 4; i += blockDim.x)
-        reinterpret_cast<uint32_t*>(&a)[i] = reinterpret_cast<const uint32_t*>(&a_arg)[i];
+    static_assert(sizeof(DecodeLayerArgs) % 4 == 0 && sizeof(DecodeLayerArgs) / 4 <= 128,
+                  "args copy: one word per thread");
+    if (threadIdx.x < sizeof(DecodeLayerArgs) / 4)
+        reinterpret_cast<uint32_t*>(&a)[threadIdx.x] =
+            reinterpret_cast<const uint32_t*>(&a_arg)[threadIdx.x];
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t s_tag;
     __shared__ uint16_t s_w[kTopK];
@@ -1091,7 +1099,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     // group polls its own copy, so 32 blocks, not 256, read each word
     uint64_t* logits = sy.logits + grp * kMaxExperts;
     uint64_t* gacts = handoff + (size_t)grp * kHandoffWords;
-    const uint32_t nwaves = blockDim.x >> 6;
+    const uint32_t nthreads = a.threads, nwaves = nthreads >> 6;
     const bool sh_wave = SH && wave == nwaves - 1u;
     const uint32_t share = (a.rows + kDecodeGroups - 1u) / kDecodeGroups;  // combine rows
 
@@ -1115,7 +1123,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     // router row issued before it, ahead of its x / es loads
     const uint32_t epoch = ld_coherent(sy.epoch);
     const uint32_t gain = t < ne ? global_ptr(a.pes)[t] : 0u;
-    const bool two = units > blockDim.x;
+    const bool two = units > nthreads;
     const uint16_t* xg = global_ptr(a.x);
     const uint16_t* hg = global_ptr(a.router_hidden);
     const uint16_t* eg = global_ptr(a.es);
@@ -1123,7 +1131,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         if (i == 1 && !two) break;
-        const uint32_t q = min(t + i * blockDim.x, units - 1u) * 8u;
+        const uint32_t q = min(t + i * nthreads, units - 1u) * 8u;
         xv[i] = *reinterpret_cast<const uint4*>(xg + q);
         if (router_block) {
             hv[i] = *reinterpret_cast<const uint4*>(hg + q);
@@ -1133,7 +1141,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     if (t < kMaxExperts) s_gains[t] = gain;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const uint32_t q = t + i * blockDim.x;
+        const uint32_t q = t + i * nthreads;
         if (q >= units) break;
         *reinterpret_cast<uint4*>(xs + (q >> 2) * kChunkLds + (q & 3u) * 8u) = pair_permute(xv[i]);
         if (!router_block) continue;
@@ -1550,6 +1558,7 @@ tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
             hipSuccess ||
         (uint64_t)per_cu * (uint64_t)moe->ctx->num_cus < kDecodeBlocks)
         return TSG_ERR_DECLINED;
+    a.threads = threads;
     hipLaunchKernelGGL(kern, dim3(kDecodeBlocks), dim3(threads), lds, stream, a);
     return check_launch("decode_layer");
 }
