@@ -1057,19 +1057,27 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
 __host__ __device__ constexpr uint32_t decode_layer_max_threads(bool sh) { return sh ? 768u : 1024u; }
 
 template <int G, bool SYM, int ACT, bool SH>
-__global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_kernel(DecodeLayerArgs a_arg) {
+// The values the first phase's loads need come as separate leading scalar
+// arguments (14 dwords) so that, built with kernarg preloading, the dispatch
+// hands them over in SGPRs: the loads go out with no memory round trip before
+// them. k_ne_rr = ne | router_rows << 16, k_d_thr = d | threads << 16.
+__global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_kernel(
+    const uint16_t* k_router_w, const uint16_t* k_hidden, const uint16_t* k_es,
+    const uint16_t* k_pes, const uint16_t* k_x, uint32_t* k_sync, uint32_t k_ne_rr,
+    uint32_t k_d_thr, DecodeLayerArgs a_arg) {
     // The arguments are copied to LDS once: under SGPR pressure the compiler
     // re-reads kernel arguments instead of spilling, and a kernarg reload in
     // a loop costs a memory round trip each time; an LDS copy costs cycles.
-    // One word per thread, with no loop over blockDim (reading blockDim is a
-    // kernarg load of its own, a second round trip before this one): blocks
-    // have at least 128 threads (a poll wave beside the down rows).
+    // One word per thread (blocks have at least 128 threads: a poll wave
+    // beside the down rows), loaded by every thread (clamped) so the
+    // compiler's waits on the loads after it stay exact, stored once the
+    // first phase's loads are out.
     __shared__ DecodeLayerArgs a;
-    static_assert(sizeof(DecodeLayerArgs) % 4 == 0 && sizeof(DecodeLayerArgs) / 4 <= 128,
+    constexpr uint32_t kArgWords = sizeof(DecodeLayerArgs) / 4;
+    static_assert(sizeof(DecodeLayerArgs) % 4 == 0 && kArgWords <= 128,
                   "args copy: one word per thread");
-    if (threadIdx.x < sizeof(DecodeLayerArgs) / 4)
-        reinterpret_cast<uint32_t*>(&a)[threadIdx.x] =
-            reinterpret_cast<const uint32_t*>(&a_arg)[threadIdx.x];
+    const uint32_t arg_word =
+        reinterpret_cast<const uint32_t*>(&a_arg)[min((uint32_t)threadIdx.x, kArgWords - 1u)];
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t s_tag;
     __shared__ uint16_t s_w[kTopK];
@@ -1079,6 +1087,45 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     __shared__ uint16_t s_sout[kMaxCombineRows];  // SH: shared output of the combine rows
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
     const uint32_t grp = blockIdx.x % kDecodeGroups, mem = blockIdx.x / kDecodeGroups;
+
+    // Every load of the first phase goes out before any is waited for: this
+    // wave's router row first (the routing waits on it), the epoch, the
+    // per-expert gains, x for the gate/up dot products, and x and es for the
+    // router products.
+    const uint32_t d0 = k_d_thr & 0xFFFFu, nthreads = k_d_thr >> 16;
+    const uint32_t ne0 = k_ne_rr & 0xFFFFu, router_rows = k_ne_rr >> 16;
+    const uint32_t units = d0 / 8u;  // units <= 2 * blockDim (host-checked)
+    const uint32_t er = blockIdx.x + kDecodeBlocks * wave;
+    const bool router_wave = wave < router_rows && er < ne0;
+    const bool router_block = blockIdx.x < ne0;  // holds at least one router row
+    uint4 rw[kRouterChunks];
+    if (router_wave) {
+        const uint16_t* w_row = global_ptr(k_router_w) + (uint64_t)er * d0;
+#pragma unroll
+        for (int i = 0; i < kRouterChunks; ++i)
+            rw[i] = *reinterpret_cast<const uint4*>(w_row + min(lane + 64u * i, units - 1u) * 8u);
+    }
+    // every thread reads the epoch (one request per wave), without a branch:
+    // a load inside `if (t == 0)` left wave 0 waiting for it, and for its
+    // router row issued before it, ahead of its x / es loads
+    const uint32_t epoch = ld_coherent(global_ptr(k_sync) + kSyncEpochWord);
+    const uint32_t gain = t < ne0 ? global_ptr(k_pes)[t] : 0u;
+    const bool two = units > nthreads;
+    const uint16_t* xg = global_ptr(k_x);
+    const uint16_t* hg = global_ptr(k_hidden);
+    const uint16_t* eg = global_ptr(k_es);
+    uint4 xv[2], hv[2], ev[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (i == 1 && !two) break;
+        const uint32_t q = min(t + i * nthreads, units - 1u) * 8u;
+        xv[i] = *reinterpret_cast<const uint4*>(xg + q);
+        if (router_block) {
+            hv[i] = *reinterpret_cast<const uint4*>(hg + q);
+            ev[i] = *reinterpret_cast<const uint4*>(eg + q);
+        }
+    }
+    if (t < kArgWords) reinterpret_cast<uint32_t*>(&a)[t] = arg_word;
     if (t < kTopK) {
         s_idx[t] = 0u;
         s_fill[t] = 0u;
@@ -1099,45 +1146,10 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     // group polls its own copy, so 32 blocks, not 256, read each word
     uint64_t* logits = sy.logits + grp * kMaxExperts;
     uint64_t* gacts = handoff + (size_t)grp * kHandoffWords;
-    const uint32_t nthreads = a.threads, nwaves = nthreads >> 6;
+    const uint32_t nwaves = nthreads >> 6;
     const bool sh_wave = SH && wave == nwaves - 1u;
     const uint32_t share = (a.rows + kDecodeGroups - 1u) / kDecodeGroups;  // combine rows
 
-    // Every load of the first phase goes out before any is waited for: this
-    // wave's router row first (the routing waits on it), the epoch, the
-    // per-expert gains, x for the gate/up dot products, and x and es for the
-    // router products.
-    const uint32_t units = d / 8u;  // units <= 2 * blockDim (host-checked)
-    const uint32_t er = blockIdx.x + kDecodeBlocks * wave;
-    const bool router_wave = wave < a.router_rows && er < ne;
-    const bool router_block = blockIdx.x < ne;  // holds at least one router row
-    uint4 rw[kRouterChunks];
-    if (router_wave) {
-        const uint16_t* w_row = global_ptr(a.router_w) + (uint64_t)er * d;
-#pragma unroll
-        for (int i = 0; i < kRouterChunks; ++i)
-            rw[i] = *reinterpret_cast<const uint4*>(w_row + min(lane + 64u * i, units - 1u) * 8u);
-    }
-    // every thread reads the epoch (one request per wave), without a branch:
-    // a load inside `if (t == 0)` left wave 0 waiting for it, and for its
-    // router row issued before it, ahead of its x / es loads
-    const uint32_t epoch = ld_coherent(sy.epoch);
-    const uint32_t gain = t < ne ? global_ptr(a.pes)[t] : 0u;
-    const bool two = units > nthreads;
-    const uint16_t* xg = global_ptr(a.x);
-    const uint16_t* hg = global_ptr(a.router_hidden);
-    const uint16_t* eg = global_ptr(a.es);
-    uint4 xv[2], hv[2], ev[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        if (i == 1 && !two) break;
-        const uint32_t q = min(t + i * nthreads, units - 1u) * 8u;
-        xv[i] = *reinterpret_cast<const uint4*>(xg + q);
-        if (router_block) {
-            hv[i] = *reinterpret_cast<const uint4*>(hg + q);
-            ev[i] = *reinterpret_cast<const uint4*>(eg + q);
-        }
-    }
     if (t < kMaxExperts) s_gains[t] = gain;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -1559,7 +1571,9 @@ tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
         (uint64_t)per_cu * (uint64_t)moe->ctx->num_cus < kDecodeBlocks)
         return TSG_ERR_DECLINED;
     a.threads = threads;
-    hipLaunchKernelGGL(kern, dim3(kDecodeBlocks), dim3(threads), lds, stream, a);
+    hipLaunchKernelGGL(kern, dim3(kDecodeBlocks), dim3(threads), lds, stream, a.router_w,
+                       a.router_hidden, a.es, a.pes, a.x, a.sync_words, a.ne | (a.router_rows << 16),
+                       a.d | (threads << 16), a);
     return check_launch("decode_layer");
 }
 
