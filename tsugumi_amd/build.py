@@ -32,16 +32,16 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
          "-munsafe-fp-atomics"]
 
 
-# Per-source flags. decode.hip: the dispatch preloads the first 14 argument
-# dwords of its kernels into SGPRs (the one-launch decode layer passes what
-# its first loads need there); where the firmware does not, each kernel's
-# prologue loads them as usual.
-SOURCE_FLAGS = {"decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"]}
+# HIP sources: the dispatch preloads the first 14 argument dwords of each
+# kernel into SGPRs (the latency-bound kernels pass what their first loads
+# need there, ahead of any by-value struct, which is never preloaded); where
+# the firmware does not, each kernel's prologue loads them as usual.
+HIP_FLAGS = ["-mllvm", "-amdgpu-kernarg-preload-count=14"]
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(os.path.basename(src))[0] + ".o")
-    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, [])]
+    cmd = [HIPCC, *FLAGS, *(HIP_FLAGS if src.endswith(".hip") else [])]
     if src.endswith(".cpp"):  # host-only C++; may call the HIP runtime API
         cmd += ["-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include")]
     cmd += ["-c", os.path.join(CSRC, src), "-o", obj]

@@ -844,12 +844,15 @@ constexpr uint32_t kStageWaves = 8;  // the staged form: one wave per row
 static_assert(kMaxRouterRows <= kStageWaves, "one row per wave");
 
 template <bool SELECT, bool STAGE, bool GROUP>
+// The parameters its first loads need come first (14 dwords, preloaded into
+// SGPRs by the dispatch where the firmware does so).
 __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kernel(
-    const uint16_t* __restrict__ w, const uint16_t* __restrict__ hidden, uint32_t hidden_stride,
+    const uint16_t* __restrict__ w, const uint16_t* __restrict__ hidden,
     const uint16_t* __restrict__ es, const uint16_t* __restrict__ pes,
-    float* __restrict__ logits, uint32_t logits_stride, uint32_t* __restrict__ counters,
-    uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w, uint32_t ne, uint32_t d,
-    uint32_t rows, uint32_t top_k, RouterGroupOut grp) {
+    uint32_t* __restrict__ counters, uint32_t hidden_stride, uint32_t ne, uint32_t d,
+    uint32_t rows, float* __restrict__ logits, uint32_t logits_stride,
+    uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w, uint32_t top_k,
+    RouterGroupOut grp) {
     static_assert(!GROUP || (SELECT && STAGE), "the grouping follows a staged selection");
     static_assert(!STAGE || SELECT, "the staged form selects");
     extern __shared__ __align__(16) uint4 xrows[];  // STAGE: the block's rows, d / 8 units each
@@ -1453,19 +1456,19 @@ tsg_status router_launch(tsg_moe* moe, hipStream_t stream, const uint16_t* w,
                                             hipFuncAttributeMaxDynamicSharedMemorySize,
                                             64 * 1024));
             hipLaunchKernelGGL(kern, sgrid, dim3(64u * kStageWaves), stage, stream, w, hidden,
-                               stride, es, pes,
-                               ctx->logits, kMaxExperts, ctx->counters, out_idx, out_w, ne, d,
-                               rows, top_k, group ? *group : RouterGroupOut{});
+                               es, pes, ctx->counters, stride, ne, d, rows, ctx->logits,
+                               kMaxExperts, out_idx, out_w, top_k,
+                               group ? *group : RouterGroupOut{});
         }
         else
             hipLaunchKernelGGL((router_kernel<true, false, false>), grid, dim3(256), 0, stream, w,
-                               hidden, stride, es, pes, ctx->logits, kMaxExperts, ctx->counters,
-                               out_idx, out_w, ne, d, rows, top_k, RouterGroupOut{});
+                               hidden, es, pes, ctx->counters, stride, ne, d, rows, ctx->logits,
+                               kMaxExperts, out_idx, out_w, top_k, RouterGroupOut{});
     } else {
         TSG_REQUIRE(logits_out, TSG_ERR_INVALID_ARGUMENT, "out_logits is NULL");
         hipLaunchKernelGGL((router_kernel<false, false, false>), grid, dim3(256), 0, stream, w,
-                           hidden, stride, es, pes, logits_out, ne, ctx->counters, out_idx, out_w,
-                           ne, d, rows, top_k, RouterGroupOut{});
+                           hidden, es, pes, ctx->counters, stride, ne, d, rows, logits_out, ne,
+                           out_idx, out_w, top_k, RouterGroupOut{});
     }
     return check_launch("router");
 }

@@ -1265,10 +1265,16 @@ __global__ __launch_bounds__(kRowsThreads) void rows_down_kernel(GemmArgs args, 
 // capacity and blocks past the count exit. A block the rows path cannot take
 // (no rows, more than kRowsMax, an expert past the layer) is skipped and sets
 // kErrRowsBlock, which tsg_ctx_synchronize reports.
-__device__ __forceinline__ bool rows_device_block(const GemmArgs& args, tsg_routed_block& blk) {
-    const uint32_t n = min(*args.n_blocks_device, args.n_blocks);
+// The list, its device count and its capacity come as leading scalar kernel
+// arguments (preloaded into SGPRs by the dispatch), so the first load needs
+// no kernarg round trip; the struct's fields arrive meanwhile.
+__device__ __forceinline__ bool rows_device_block(const GemmArgs& args,
+                                                  const tsg_routed_block* blocks,
+                                                  const uint32_t* n_dev, uint32_t n_blocks,
+                                                  tsg_routed_block& blk) {
+    const uint32_t n = min(*n_dev, n_blocks);
     if (blockIdx.y >= n) return false;
-    blk = args.blocks[blockIdx.y];
+    blk = blocks[blockIdx.y];
     if (blk.row_count == 0 || blk.row_count > kRowsMax || blk.local_slot >= args.num_experts) {
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicOr(args.error, kErrRowsBlock);
         return false;
@@ -1277,16 +1283,21 @@ __device__ __forceinline__ bool rows_device_block(const GemmArgs& args, tsg_rout
 }
 
 template <int G, bool SYM, int ACT>
-__global__ __launch_bounds__(kRowsThreads) void rows_gate_up_dev_kernel(GemmArgs args) {
+__global__ __launch_bounds__(kRowsThreads) void rows_gate_up_dev_kernel(
+    const tsg_routed_block* k_blocks, const uint32_t* k_n_dev, uint32_t k_n_blocks,
+    GemmArgs args) {
     tsg_routed_block blk;
-    if (rows_device_block(args, blk)) rows_gate_up_body<G, SYM, ACT>(args, blk, kRowsMax);
+    if (rows_device_block(args, k_blocks, k_n_dev, k_n_blocks, blk))
+        rows_gate_up_body<G, SYM, ACT>(args, blk, kRowsMax);
 }
 
 template <int G, bool SYM>
-__global__ __launch_bounds__(kRowsThreads) void rows_down_dev_kernel(GemmArgs args,
-                                                                     uint16_t* partials) {
+__global__ __launch_bounds__(kRowsThreads) void rows_down_dev_kernel(
+    const tsg_routed_block* k_blocks, const uint32_t* k_n_dev, uint32_t k_n_blocks,
+    uint16_t* partials, GemmArgs args) {
     tsg_routed_block blk;
-    if (rows_device_block(args, blk)) rows_down_body<G, SYM>(args, blk, kRowsMax, partials);
+    if (rows_device_block(args, k_blocks, k_n_dev, k_n_blocks, blk))
+        rows_down_body<G, SYM>(args, blk, kRowsMax, partials);
 }
 
 // ------------------------------------------------------------ host side
@@ -1692,13 +1703,13 @@ extern "C" tsg_status tsg_prefill_moe_rows_device(tsg_moe* moe, tsg_stream strea
     do {                                                                                           \
         if (moe->activation == TSG_ACT_SILU)                                                       \
             hipLaunchKernelGGL((rows_gate_up_dev_kernel<GG, SS, TSG_ACT_SILU>), g1,                \
-                               dim3(kRowsThreads), l1, s, a);                                      \
+                               dim3(kRowsThreads), l1, s, blocks, n_blocks_device, max_blocks, a); \
         else                                                                                       \
             hipLaunchKernelGGL((rows_gate_up_dev_kernel<GG, SS, TSG_ACT_GELU_TANH>), g1,           \
-                               dim3(kRowsThreads), l1, s, a);                                      \
+                               dim3(kRowsThreads), l1, s, blocks, n_blocks_device, max_blocks, a); \
         if ((st = check_launch("rows gate/up (device list)"))) return st;                         \
-        hipLaunchKernelGGL((rows_down_dev_kernel<GG, SS>), g2, dim3(kRowsThreads), l2, s, a2,      \
-                           partials);                                                              \
+        hipLaunchKernelGGL((rows_down_dev_kernel<GG, SS>), g2, dim3(kRowsThreads), l2, s, blocks,  \
+                           n_blocks_device, max_blocks, partials, a2);                             \
         return check_launch("rows down (device list)");                                           \
     } while (0)
     if (ctx->group_size == 32) {
