@@ -16,20 +16,23 @@ constexpr uint32_t kMaxRows = 8;
 // WA: the weights' alignment, 16 or 2 (a weights pointer bound at a 2-byte
 // offset, DequantInt4GEMV.swift:93-96: every row starts at the same offset
 // modulo 16, since a row is a multiple of 16 bytes).
-template <int G, bool SYM, int T, int WA>
-__global__ __launch_bounds__(256) void qmv_kernel(const uint8_t* __restrict__ w,
-                                                  const uint16_t* __restrict__ scales,
-                                                  const uint16_t* __restrict__ biases,
-                                                  const uint16_t* __restrict__ x,
-                                                  uint32_t x_stride, uint16_t* __restrict__ y,
-                                                  uint32_t y_stride, uint32_t t, uint32_t m,
-                                                  uint32_t n) {
+// RPB rows per block (16 lanes each), so the block size is a constant. The
+// parameters the first loads need fill the first 14 dwords, which the
+// dispatch preloads into SGPRs: no kernel-argument load comes before them.
+template <int G, bool SYM, int T, int WA, uint32_t RPB>
+__global__ __launch_bounds__(16 * RPB) void qmv_kernel(const uint8_t* __restrict__ w,
+                                                       const uint16_t* __restrict__ scales,
+                                                       const uint16_t* __restrict__ biases,
+                                                       const uint16_t* __restrict__ x,
+                                                       uint16_t* __restrict__ y, uint32_t n,
+                                                       uint32_t m, uint32_t t, uint32_t x_stride,
+                                                       uint32_t y_stride) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t row_h = lds_chunks_halves(n);
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                        // T rows
     float* xsum = reinterpret_cast<float*>(smem + (size_t)T * row_h * 2u);  // T * n / 32
 
-    const uint32_t row = blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
+    const uint32_t row = blockIdx.x * RPB + (threadIdx.x >> 4);
     const uint32_t j = threadIdx.x & 15u;
     const bool live = row < m;
     const uint32_t rr = live ? row : 0u;
@@ -38,9 +41,11 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint8_t* __restrict__ w,
     const uint16_t* sr = scales + (uint64_t)rr * ngroups;
     const uint16_t* br = biases + (uint64_t)rr * ngroups;
     ChunkBatch<kGUBatch> bt;
-    stage_act_rows_around<SYM>(x, x_stride, t, n, xs, row_h, xsum, nullptr, [&] {
+    auto issue_weights = [&] {
         load_batch<G, SYM, kGUBatch, kGULanes, WA>(wr, sr, br, 0u, j, nchunks, bt);
-    });
+    };
+    stage_act_rows_around<SYM, decltype(issue_weights)&, 4, 16u * RPB>(x, x_stride, t, n, xs, row_h,
+                                                                       xsum, nullptr, issue_weights);
     __syncthreads();
     float acc[T];
 #pragma unroll
@@ -88,10 +93,14 @@ tsg_status launch_qmv(hipStream_t s, const uint8_t* w, const uint16_t* sc, const
     const uint32_t rpb = m < 4096u ? 4u : 16u;
     const dim3 grid((m + rpb - 1u) / rpb), block(16u * rpb);
     const size_t lds_per_row = (size_t)lds_chunks_halves(n) * 2u + (SYM ? 0u : (n / 32u) * 4u);
-#define TSG_QMV_CASE(TT)                                                               \
-    case TT:                                                                           \
-        hipLaunchKernelGGL((qmv_kernel<G, SYM, TT, WA>), grid, block, lds_per_row * TT, s, \
-                           w, sc, bi, x, xs, y, ys, t, m, n);                          \
+#define TSG_QMV_CASE(TT)                                                                        \
+    case TT:                                                                                    \
+        if (rpb == 4u)                                                                          \
+            hipLaunchKernelGGL((qmv_kernel<G, SYM, TT, WA, 4u>), grid, block, lds_per_row * TT, \
+                               s, w, sc, bi, x, y, n, m, t, xs, ys);                            \
+        else                                                                                    \
+            hipLaunchKernelGGL((qmv_kernel<G, SYM, TT, WA, 16u>), grid, block, lds_per_row * TT, \
+                               s, w, sc, bi, x, y, n, m, t, xs, ys);                            \
         break;
     switch (t) {
         TSG_QMV_CASE(1)

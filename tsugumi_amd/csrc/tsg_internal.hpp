@@ -401,8 +401,15 @@ __device__ __forceinline__ void staged_chunk_sums(const uint16_t* dst, uint32_t 
 // between: the pass's global loads of units q0 .. q0 + blockDim * PT (of
 // `total`, bpr units of 8 halves per row) into v, then their LDS stores.
 // Loads complete in issue order, so a store that waits for v waits for
-// nothing issued after the pass's loads.
-template <int PT, bool COHERENT = false>
+// nothing issued after the pass's loads. NT: the block size when the caller
+// knows it at compile time (reading blockDim is a kernel-argument load of its
+// own), 0 for blockDim.x.
+template <uint32_t NT>
+__device__ __forceinline__ uint32_t block_threads() {
+    if constexpr (NT != 0) return NT;
+    else return blockDim.x;
+}
+template <int PT, bool COHERENT = false, uint32_t NT = 0>
 __device__ __forceinline__ void stage_act_load(const uint16_t* __restrict__ src,
                                                uint32_t src_stride, uint32_t total, uint32_t bpr,
                                                uint32_t q0, const uint32_t* row_index,
@@ -412,7 +419,7 @@ __device__ __forceinline__ void stage_act_load(const uint16_t* __restrict__ src,
         // plain loads clamp (a repeated unit is a cache hit and keeps the
         // loads branch-free); coherent loads skip: each is a memory-side
         // access, and repeats of one unit would all queue on one line
-        const uint32_t q_raw = q0 + threadIdx.x + i * blockDim.x;
+        const uint32_t q_raw = q0 + threadIdx.x + i * block_threads<NT>();
         const uint32_t q = min(q_raw, total - 1u);
         const uint32_t r = q / bpr, b = q - r * bpr;
         const uint32_t sr = row_index ? row_index[r] : r;
@@ -421,13 +428,13 @@ __device__ __forceinline__ void stage_act_load(const uint16_t* __restrict__ src,
         else v[i] = *reinterpret_cast<const uint4*>(sp);
     }
 }
-template <int PT>
+template <int PT, uint32_t NT = 0>
 __device__ __forceinline__ void stage_act_store(uint32_t total, uint32_t bpr, uint32_t q0,
                                                 uint16_t* dst, uint32_t dst_stride,
                                                 const uint4 (&v)[PT]) {
 #pragma unroll
     for (int i = 0; i < PT; ++i) {
-        const uint32_t q = q0 + threadIdx.x + i * blockDim.x;
+        const uint32_t q = q0 + threadIdx.x + i * block_threads<NT>();
         if (q < total) {
             const uint32_t r = q / bpr, b = q - r * bpr;
             *reinterpret_cast<uint4*>(dst + (size_t)r * dst_stride + (b >> 2) * kChunkLds +
@@ -460,7 +467,7 @@ __device__ __forceinline__ void stage_act_rows(const uint16_t* __restrict__ src,
 // complete in issue order, so the stores wait for the activation rows only
 // and the weights stream in while the stores and the first chunks run;
 // issued the other way round, the stores would wait for every weight.
-template <bool SYM, class Between, int PER_THREAD = 4>
+template <bool SYM, class Between, int PER_THREAD = 4, uint32_t NT = 0>
 __device__ __forceinline__ void stage_act_rows_around(const uint16_t* __restrict__ src,
                                                       uint32_t src_stride, uint32_t rows,
                                                       uint32_t n, uint16_t* dst,
@@ -474,12 +481,13 @@ __device__ __forceinline__ void stage_act_rows_around(const uint16_t* __restrict
         return;
     }
     uint4 v[PER_THREAD];
-    stage_act_load<PER_THREAD>(src, src_stride, total, bpr, 0u, row_index, v);
+    stage_act_load<PER_THREAD, false, NT>(src, src_stride, total, bpr, 0u, row_index, v);
     between();
-    stage_act_store<PER_THREAD>(total, bpr, 0u, dst, dst_stride, v);
-    for (uint32_t q0 = blockDim.x * PER_THREAD; q0 < total; q0 += blockDim.x * PER_THREAD) {
-        stage_act_load<PER_THREAD>(src, src_stride, total, bpr, q0, row_index, v);
-        stage_act_store<PER_THREAD>(total, bpr, q0, dst, dst_stride, v);
+    stage_act_store<PER_THREAD, NT>(total, bpr, 0u, dst, dst_stride, v);
+    const uint32_t pass = block_threads<NT>() * PER_THREAD;
+    for (uint32_t q0 = pass; q0 < total; q0 += pass) {
+        stage_act_load<PER_THREAD, false, NT>(src, src_stride, total, bpr, q0, row_index, v);
+        stage_act_store<PER_THREAD, NT>(total, bpr, q0, dst, dst_stride, v);
     }
     if constexpr (!SYM) {
         __syncthreads();
