@@ -750,13 +750,21 @@ struct RouterGroupLds {
     uint32_t wave_tot[kMaxExperts / 64u];
 };
 
+// Inclusive prefix sum over the wave on DPP moves (no LDS round trips): row
+// shifts by 1, 2, 4, 8 within each 16-lane row (lanes shifted in from outside
+// the row add 0), then lane 15's sum added to row 1 and row 3 (row_bcast:15)
+// and lane 31's to rows 2 and 3 (row_bcast:31).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_add(uint32_t v) {
+    return v + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, false);
+}
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
-    const uint32_t lane = threadIdx.x & 63u;
-#pragma unroll
-    for (uint32_t d = 1; d < 64u; d <<= 1) {
-        const uint32_t u = __shfl_up(v, d);
-        v += lane >= d ? u : 0u;
-    }
+    v = dpp_add<0x111, 0xF>(v);  // row_shr:1
+    v = dpp_add<0x112, 0xF>(v);  // row_shr:2
+    v = dpp_add<0x114, 0xF>(v);  // row_shr:4
+    v = dpp_add<0x118, 0xF>(v);  // row_shr:8
+    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
     return v;
 }
 
@@ -792,9 +800,11 @@ __device__ void group_router_rows(const uint32_t* pe, const uint32_t* pw, uint32
     lds_barrier();
     uint32_t pos = 0;
     if (my_pair) {
+        // the earlier tokens' mask words, read together (tok < kMaxRouterRows)
         uint32_t rank = 0;
-        for (uint32_t u = 0; u < tok; ++u)
-            rank += (L.mask[u * kMaskWords + (my_e >> 5)] >> (my_e & 31u)) & 1u;
+#pragma unroll
+        for (uint32_t u = 0; u < kMaxRouterRows; ++u)
+            rank += u < tok ? (L.mask[u * kMaskWords + (my_e >> 5)] >> (my_e & 31u)) & 1u : 0u;
         pos = L.off[my_e] + rank;
     }
     // every LDS read is done: the results leave
