@@ -499,9 +499,19 @@ __device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t payload) {
 // One wave reads up to N tagged words per lane (word k at addr(k), for k in
 // `live`, a lane's bit mask) until each carries `tag`, handing each payload to
 // use(k, payload) once; every pass re-reads only the words still missing, so
-// words already in cost no further traffic. Bounded: after kSpinLimit passes
-// the wave sets the error word and returns.
-template <int N, typename Addr, typename Use>
+// words already in cost no further traffic. Between passes the wave sleeps
+// SLEEP x 64 cycles: the polls' agent-coherent loads are served from the
+// memory side, and polling faster slowed the hand-offs and the expert stream
+// they share it with (measured per hand-off, below). Bounded: after
+// kSpinLimit passes the wave sets the error word and returns.
+// Decode layer, sleep 1 / 2 / 3 on every hand-off, µs per layer: 14.55 / 13.80 /
+// 13.97 on one box, 13.76 / 13.83 / (3 on two of three) 13.97 on another; 2 is
+// within 0.5 % of the best on both.
+constexpr int kPollSleepLogits = 2;
+constexpr int kPollSleepActs = 2;
+constexpr int kPollSleepParts = 2;
+constexpr int kPollSleepRouter = 1;  // the staged router: one polling block
+template <int N, int SLEEP, typename Addr, typename Use>
 __device__ __forceinline__ void poll_tagged(const DecodeSync& sy, uint32_t tag, uint32_t live,
                                             Addr&& addr, Use&& use,
                                             uint32_t err_bit = kErrDecodeTimeout) {
@@ -523,7 +533,7 @@ __device__ __forceinline__ void poll_tagged(const DecodeSync& sy, uint32_t tag, 
             if ((threadIdx.x & 63u) == 0) atomicOr(sy.error, err_bit);
             return;
         }
-        __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(SLEEP);
     }
 }
 
@@ -990,7 +1000,7 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
                         if (lane + 64u * j < ne) live |= 1u << j;
                     DecodeSync sy;
                     sy.error = counters + kSyncErrorWord;
-                    poll_tagged<4>(sy, s_tag, live,
+                    poll_tagged<4, kPollSleepRouter>(sy, s_tag, live,
                                    [&](int j) { return r_logits + (uint64_t)r * kMaxExperts + lane + 64u * j; },
                                    [&](int j, uint32_t b) { bits[j] = b; }, kErrRouterWait);
 #pragma unroll
@@ -1222,7 +1232,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
         uint32_t live = 0;
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) live |= lane + 64u * j < ne ? 1u << j : 0u;
-        poll_tagged<4>(sy, tag, live, [&](int j) { return logits + lane + 64u * j; },
+        poll_tagged<4, kPollSleepLogits>(sy, tag, live, [&](int j) { return logits + lane + 64u * j; },
                        [&](int j, uint32_t bits) {
                            const float v = __uint_as_float(bits);
                            key[j] = (v == v && v != -INFINITY) ? order_key(v) : 0u;
@@ -1325,7 +1335,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
             uint32_t live = 0;
 #pragma unroll
             for (uint32_t k = 0; k < 16; ++k) live |= i0 + lane + 64u * k < f ? 1u << k : 0u;
-            poll_tagged<16>(sy, tag, live, [&](int k) { return gacts + i0 + lane + 64u * k; },
+            poll_tagged<16, kPollSleepActs>(sy, tag, live, [&](int k) { return gacts + i0 + lane + 64u * k; },
                             [&](int k, uint32_t bits) {
                                 const uint32_t i = i0 + lane + 64u * k, c = i & 31u;
                                 as[(i >> 5) * kChunkLds + (c >> 3) * 8u + paired_pos(c & 7u)] =
@@ -1338,7 +1348,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
             uint32_t live = 0;
 #pragma unroll
             for (uint32_t k = 0; k < kMaxSharedF / 64u; ++k) live |= lane + 64u * k < a.sh_f ? 1u << k : 0u;
-            poll_tagged<kMaxSharedF / 64u>(sy, tag, live, [&](int k) { return shacts + lane + 64u * k; },
+            poll_tagged<kMaxSharedF / 64u, kPollSleepActs>(sy, tag, live, [&](int k) { return shacts + lane + 64u * k; },
                                            [&](int k, uint32_t bits) {
                                                const uint32_t i = lane + 64u * k, c = i & 31u;
                                                ss[(i >> 5) * kChunkLds + (c >> 3) * 8u + paired_pos(c & 7u)] =
@@ -1391,7 +1401,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
         if constexpr (SH) res = s_sout[lane < share ? lane : 0u];
         else res = global_ptr(a.residual)[live ? crow : 0u];
         float vq[kTopK];
-        poll_tagged<kTopK>(sy, tag, live ? 0xFFu : 0u,
+        poll_tagged<kTopK, kPollSleepParts>(sy, tag, live ? 0xFFu : 0u,
                            [&](int q) { return parts + (size_t)q * kHandoffWords + crow; },
                            [&](int q, uint32_t bits) { vq[q] = __uint_as_float(bits); });
         if (live) {
