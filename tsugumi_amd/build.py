@@ -37,11 +37,15 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
 # need there, ahead of any by-value struct, which is never preloaded); where
 # the firmware does not, each kernel's prologue loads them as usual.
 HIP_FLAGS = ["-mllvm", "-amdgpu-kernarg-preload-count=14"]
+# prefill.hip: its atomics are all single-lane; the atomic optimizer would turn
+# the fused GEMM's fetch of its next work item into a wave-wide form that
+# waits for the result right after issue instead of where it is used.
+SOURCE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(os.path.basename(src))[0] + ".o")
-    cmd = [HIPCC, *FLAGS, *(HIP_FLAGS if src.endswith(".hip") else [])]
+    cmd = [HIPCC, *FLAGS, *(HIP_FLAGS if src.endswith(".hip") else []), *SOURCE_FLAGS.get(src, [])]
     if src.endswith(".cpp"):  # host-only C++; may call the HIP runtime API
         cmd += ["-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include")]
     cmd += ["-c", os.path.join(CSRC, src), "-o", obj]

@@ -361,6 +361,11 @@ __device__ __forceinline__ uint32_t lds_read_u16(uint32_t addr) {
     asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(addr));
     return v;
 }
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
 template <int NT>
 __device__ __forceinline__ void lds_wait(u32x4_t (&a)[NT]) {
     if constexpr (NT == 1) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]));
@@ -818,12 +823,17 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     const uint32_t ncols = MODE == 0 ? args.f : args.d;
     const uint32_t live = ncols - col0 < kCols ? ncols - col0 : kCols;  // multiple of 64
     constexpr uint32_t kPieces = kCols / 8u;  // 16-byte pieces per row
+    // The tile's LDS reads are inline ds_reads: a plain LDS read after the
+    // direct-to-LDS loads makes the compiler wait for every outstanding vector
+    // memory operation first, and on gfx9 that count includes this loop's own
+    // global stores, so each store waited for the one before it to complete.
     for (uint32_t p = threadIdx.x; p < rows * kPieces; p += kGemmThreads) {
         const uint32_t r = p / kPieces, cg = p - r * kPieces;
         if (cg * 8u >= live) continue;
-        const uint4 v = *reinterpret_cast<const uint4*>(otile + r * kStride + cg * 8u);
-        const uint32_t dst = MODE == 0 ? (blk.local_row + r) * args.f : odst[r];
-        *reinterpret_cast<uint4*>(args.out + dst + col0 + cg * 8u) = v;
+        u32x4_t v = lds_read16<0>(lds_addr(otile + r * kStride + cg * 8u));
+        uint32_t dst = MODE == 0 ? (blk.local_row + r) * args.f : lds_read_b32(lds_addr(odst + r));
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v), "+v"(dst));
+        *reinterpret_cast<u32x4_t*>(args.out + dst + col0 + cg * 8u) = v;
     }
 }
 
@@ -1055,10 +1065,16 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_fused_kernel(GemmArg
             __syncthreads();
             gemm_item<G, SYM, ACT, 1>(dn, dn.blocks[yb], tile, smem);
         }
-        __syncthreads();  // the item's LDS is free
-        if (threadIdx.x == 0) word[0] = next;
-        __syncthreads();
-        item = word[0];
+        // LDS-only barriers and LDS accesses the compiler does not see: a
+        // __syncthreads() (its release fence) or a plain LDS access after the
+        // direct-to-LDS loads would wait for this item's epilogue stores to
+        // complete, and nothing in this launch reads a down item's partials
+        lds_barrier();  // the item's LDS is free
+        if (threadIdx.x == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(word)), "v"(next) : "memory");
+        lds_barrier();
+        item = lds_read_b32(lds_addr(word));
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(item));
+        item = __builtin_amdgcn_readfirstlane(item);
     }
     if (threadIdx.x == 0) word[1] = atomicAdd(sc.exited, 1u) == gridDim.x - 1u ? 1u : 0u;
     __syncthreads();
