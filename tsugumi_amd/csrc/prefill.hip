@@ -653,9 +653,15 @@ __device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uin
 // idle; the up accumulators reach waves 0-1 through the LDS before the
 // activation. Every accumulator sees the same MFMA sequence as in a full
 // tile, so the results are identical.
+// The fused launch's next work item index: the last dword of the weight
+// ring's stage 2, which every epilogue leaves free and an item first writes
+// (by direct-to-LDS load) only after its first barrier.
+constexpr uint32_t kNextWord = kGemmBBase + 3u * kGemmBStage - 4u;
+
 template <int G, bool SYM, int ACT, int MODE, int NT, bool HALF>
 __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_routed_block& blk,
-                                           uint32_t rows, uint32_t tile, uint8_t* smem) {
+                                           uint32_t rows, uint32_t tile, uint8_t* smem,
+                                           bool post, uint32_t next) {
     static_assert(!HALF || MODE == 0, "only the gate/up GEMM has half tiles");
     const uint32_t lane = threadIdx.x & 63u, h = lane >> 5, m = lane & 31u;
     GemmLane L;
@@ -778,12 +784,17 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     static_assert(kGemmRows * kStride * 2u + kGemmRows * 4u <= gemm_lds_bytes(true),
                   "output tile and row destinations fit the LDS");
     block_barrier();  // every wave is done reading the rings
+    // the fused launch's next item index, posted where the epilogue does not
+    // write (its atomic is long complete: the loads are drained above)
+    static_assert(kGemmRows * kStride * 2u + kGemmRows * 4u <= kNextWord, "next word is free");
+    if (post && threadIdx.x == 0)
+        asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(smem + kNextWord)), "v"(next) : "memory");
     if (MODE == 1 && threadIdx.x < rows) odst[threadIdx.x] = row_dst;
     if (MODE == 2 && threadIdx.x < rows) odst[threadIdx.x] = (blk.local_row + threadIdx.x) * args.d;
     if constexpr (HALF) {
         // waves 2-3 hand their up accumulators to waves 0-1, past the tile
         constexpr uint32_t kXch = kGemmRows * kStride * 2u;
-        static_assert(kXch + 2u * NT * 16u * 64u * 4u <= gemm_lds_bytes(true), "exchange fits");
+        static_assert(kXch + 2u * NT * 16u * 64u * 4u <= kNextWord, "exchange fits below the next word");
         float* xch = reinterpret_cast<float*>(smem + kXch);
         const uint32_t pair = L.wave & 1u;
         if (L.wave >= 2u) {
@@ -933,11 +944,14 @@ __device__ void gemm_work_item(const GemmArgs& args, uint32_t nb, uint32_t pid, 
 // kGemmRows runs as consecutive passes.
 template <int G, bool SYM, int ACT, int MODE>
 __device__ __forceinline__ void gemm_item(const GemmArgs& args, const tsg_routed_block& blk,
-                                          uint32_t tile, uint8_t* smem) {
+                                          uint32_t tile, uint8_t* smem, bool post = false,
+                                          uint32_t next = 0u) {
     // a block list written on the device is not checked on the host: an
     // expert past the layer is skipped (its weights would lie outside it)
     if (MODE != 2 && blk.local_slot >= args.num_experts) {
         if (threadIdx.x == 0) atomicOr(args.error, kErrGemmBlock);
+        if (post && threadIdx.x == 0)
+            asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(smem + kNextWord)), "v"(next) : "memory");
         return;
     }
     for (uint32_t r0 = 0; r0 < blk.row_count; r0 += kGemmRows) {
@@ -951,17 +965,17 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& args, const tsg_routed
         const bool half = MODE == 0 && args.f - tile * 128u <= 64u;
         if (half) {
             switch ((rows + 31u) / 32u) {
-                case 1: gemm_block<G, SYM, ACT, MODE, 1, MODE == 0>(args, sub, rows, tile, smem); break;
-                case 2: gemm_block<G, SYM, ACT, MODE, 2, MODE == 0>(args, sub, rows, tile, smem); break;
-                case 3: gemm_block<G, SYM, ACT, MODE, 3, MODE == 0>(args, sub, rows, tile, smem); break;
-                default: gemm_block<G, SYM, ACT, MODE, 4, MODE == 0>(args, sub, rows, tile, smem); break;
+                case 1: gemm_block<G, SYM, ACT, MODE, 1, MODE == 0>(args, sub, rows, tile, smem, post, next); break;
+                case 2: gemm_block<G, SYM, ACT, MODE, 2, MODE == 0>(args, sub, rows, tile, smem, post, next); break;
+                case 3: gemm_block<G, SYM, ACT, MODE, 3, MODE == 0>(args, sub, rows, tile, smem, post, next); break;
+                default: gemm_block<G, SYM, ACT, MODE, 4, MODE == 0>(args, sub, rows, tile, smem, post, next); break;
             }
         } else {
             switch ((rows + 31u) / 32u) {
-                case 1: gemm_block<G, SYM, ACT, MODE, 1, false>(args, sub, rows, tile, smem); break;
-                case 2: gemm_block<G, SYM, ACT, MODE, 2, false>(args, sub, rows, tile, smem); break;
-                case 3: gemm_block<G, SYM, ACT, MODE, 3, false>(args, sub, rows, tile, smem); break;
-                default: gemm_block<G, SYM, ACT, MODE, 4, false>(args, sub, rows, tile, smem); break;
+                case 1: gemm_block<G, SYM, ACT, MODE, 1, false>(args, sub, rows, tile, smem, post, next); break;
+                case 2: gemm_block<G, SYM, ACT, MODE, 2, false>(args, sub, rows, tile, smem, post, next); break;
+                case 3: gemm_block<G, SYM, ACT, MODE, 3, false>(args, sub, rows, tile, smem, post, next); break;
+                default: gemm_block<G, SYM, ACT, MODE, 4, false>(args, sub, rows, tile, smem, post, next); break;
             }
         }
     }
@@ -1047,7 +1061,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_fused_kernel(GemmArg
         if (threadIdx.x == 0) next = atomicAdd(&sc.next[xcc], 1u);
         if (item < n_gu) {
             const uint32_t yb = xcc + Q * (item / T0), tile = item % T0;
-            gemm_item<G, SYM, ACT, 0>(gu, gu.blocks[yb], tile, smem);
+            gemm_item<G, SYM, ACT, 0>(gu, gu.blocks[yb], tile, smem, true, next);
             wait_vmcnt<0>();  // this wave's activation stores are in the L2
             __syncthreads();
             if (threadIdx.x == 0) atomicAdd(&sc.done[yb], 1u);
@@ -1063,16 +1077,15 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_fused_kernel(GemmArg
                 }
             }
             __syncthreads();
-            gemm_item<G, SYM, ACT, 1>(dn, dn.blocks[yb], tile, smem);
+            gemm_item<G, SYM, ACT, 1>(dn, dn.blocks[yb], tile, smem, true, next);
         }
-        // LDS-only barriers and LDS accesses the compiler does not see: a
+        // An LDS-only barrier and an LDS read the compiler does not see: a
         // __syncthreads() (its release fence) or a plain LDS access after the
         // direct-to-LDS loads would wait for this item's epilogue stores to
-        // complete, and nothing in this launch reads a down item's partials
-        lds_barrier();  // the item's LDS is free
-        if (threadIdx.x == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(word)), "v"(next) : "memory");
-        lds_barrier();
-        item = lds_read_b32(lds_addr(word));
+        // complete, and nothing in this launch reads a down item's partials.
+        // The item posted the next index at its epilogue (gemm_block).
+        lds_barrier();  // the item's LDS is free, the next index visible
+        item = lds_read_b32(lds_addr(smem + kNextWord));
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(item));
         item = __builtin_amdgcn_readfirstlane(item);
     }
