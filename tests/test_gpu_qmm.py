@@ -31,6 +31,7 @@ def operands(rng, n, k, g):
 @pytest.mark.parametrize("t,n,k,g,scheme", [
     (1, 2816, 2816, 64, "affine"), (37, 4096, 2816, 32, "sym"), (300, 2816, 4096, 64, "sym"),
     (2048, 2816, 2816, 32, "affine"), (129, 704, 2816, 32, "sym"), (255, 8192, 2816, 64, "affine"),
+    (2048, 4096, 2816, 32, "sym"),
 ])
 def test_qmm_matches_oracle(tsg, t, n, k, g, scheme):
     print(f"qmm t={t} n={n} k={k} g{g} {scheme}", flush=True)
@@ -50,6 +51,33 @@ def test_qmm_matches_oracle(tsg, t, n, k, g, scheme):
                                 oracle.f16_to_float(ref.ravel()))
     print(f"  rel={rel:.3e}")
     assert rel <= kc.NORTH_STAR
+    ctx.close()
+
+
+@pytest.mark.parametrize("scheme", ["sym", "affine"])
+def test_qmm_narrow_tiles_equal_wide_tiles_bitwise(tsg, scheme):
+    """Below 256 workgroups of 256 columns the QMM runs 128-column tiles (one
+    weight tile per wave); each column keeps the same MFMA sequence, so the
+    results are the wide tiles' bit for bit. T = 2048: N = 4096 runs 256 wide
+    workgroups, its first 2816 weight rows as N = 2816 176 -> 352 narrow ones;
+    the shared 2816 columns must agree exactly."""
+    t, k, g, n_wide, n_narrow = 2048, 2816, 32, 4096, 2816
+    print(f"qmm narrow vs wide {scheme}", flush=True)
+    sym = scheme == "sym"
+    ctx = tsg.Context(0, group_size=g)
+    ctx.set_affine_scheme(scheme)
+    rng = np.random.default_rng(4242 + sym)
+    packed, scales, biases = operands(rng, n_wide, k, g)
+    xb = oracle.f16_bits(rng.normal(0, 1, t * k).astype(np.float32))
+    q = tsg.PrefillInt4QMM(ctx)
+    y_wide, y_narrow = empty(t * n_wide), empty(t * n_narrow)
+    sg = n_narrow * (k // g)
+    q.encode(dev(packed), dev(scales), None if sym else dev(biases), dev(xb), y_wide, t, n_wide, k)
+    q.encode(dev(np.ascontiguousarray(packed[:n_narrow])), dev(scales[:sg].copy()),
+             None if sym else dev(biases[:sg].copy()), dev(xb), y_narrow, t, n_narrow, k)
+    wide = host(y_wide, np.uint16).reshape(t, n_wide)[:, :n_narrow]
+    narrow = host(y_narrow, np.uint16).reshape(t, n_narrow)
+    assert np.array_equal(wide, narrow)
     ctx.close()
 
 

@@ -454,6 +454,7 @@ struct GemmArgs {
     const uint8_t* dense_s;     // MODE 2: scales (the weights are at layer_base)
     const uint8_t* dense_b;     // MODE 2: biases (the scales again under sym)
     uint32_t ntiles;            // weight-row tiles per routed block
+    uint32_t dense_narrow;      // MODE 2: 128-column tiles, one 32-row weight tile per wave
     uint32_t num_experts;       // experts of the layer (device block lists are checked)
     uint32_t* error;            // the context's device error word
 };
@@ -647,7 +648,9 @@ __device__ __forceinline__ void gemm_chunk(const GemmLane& L, uint8_t* smem, uin
 
 // MODE 0: gate/up + activation; MODE 1: down + scatter; MODE 2: dense
 // projection y[t, n] (the down sub-tensor's geometry, rows taken in order).
-// HALF (gate/up only, a column tile with 64 live columns): waves 0-1 run the
+// HALF, dense GEMM: a 128-column tile, wave w the 32 weight rows 32 w .. of
+// it as one tile (acc[.][0]).
+// HALF, gate/up (a column tile with 64 live columns): waves 0-1 run the
 // gate rows of columns 0-31 and 32-63 and waves 2-3 the up rows of the same
 // columns, one weight tile each instead of two tiles on two waves with two
 // idle; the up accumulators reach waves 0-1 through the LDS before the
@@ -662,7 +665,7 @@ template <int G, bool SYM, int ACT, int MODE, int NT, bool HALF>
 __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_routed_block& blk,
                                            uint32_t rows, uint32_t tile, uint8_t* smem,
                                            bool post, uint32_t next) {
-    static_assert(!HALF || MODE == 0, "only the gate/up GEMM has half tiles");
+    static_assert(!HALF || MODE != 1, "the down GEMM has no half tiles");
     const uint32_t lane = threadIdx.x & 63u, h = lane >> 5, m = lane & 31u;
     GemmLane L;
     L.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -684,8 +687,10 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
         s_off[0] = args.o.gate_s, s_off[1] = args.o.up_s;
         z_off[0] = args.o.gate_b, z_off[1] = args.o.up_b;
     } else {
-        row0[0] = tile * 256u + 64u * L.wave;
-        row0[1] = row0[0] + 32u;
+        // HALF (dense only): 128 columns, wave w one tile of 32 (both tile
+        // slots load it; the second copy is not read)
+        row0[0] = HALF ? tile * 128u + 32u * L.wave : tile * 256u + 64u * L.wave;
+        row0[1] = HALF ? row0[0] : row0[0] + 32u;
         L.live = row0[0] < args.d;
         w_off[0] = w_off[1] = args.o.down_w;
         s_off[0] = s_off[1] = args.o.down_s;
@@ -738,7 +743,7 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     const uint32_t swzb_m = ((m >> 2) ^ (m >> 3)) & 1u;
     L.b_rd = base + kGemmBBase + L.wave * kGemmBWave + 32u * m + 16u * (h ^ swzb_m);
     L.s_rd = base + kGemmSBase + L.wave * kGemmSWave + 16u * m;
-    if (HALF && L.wave >= 2u) {  // waves 2-3 read their up tile in the tile-0 slots
+    if (MODE == 0 && HALF && L.wave >= 2u) {  // waves 2-3 read their up tile in the tile-0 slots
         L.b_rd += kGemmBTile;
         L.s_rd += 512u;
         L.s_own[0] = L.s_own[1];
@@ -775,7 +780,7 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     // acc[i][t][v] of lane l: row 32 i + 8 (v / 4) + 4 h + v % 4 of the block,
     // weight row n_t (column m of tile t). Rows are padded by 16 bytes so the
     // two half-waves' 2-byte writes (4 rows apart) fall in different banks.
-    constexpr uint32_t kCols = MODE == 0 ? 128u : 256u;  // columns per block
+    constexpr uint32_t kCols = MODE == 0 || HALF ? 128u : 256u;  // columns per block
     constexpr uint32_t kStride = kCols + 8u;             // halves per LDS row
     static_assert(kGemmRows * kStride * 2u <= gemm_lds_bytes(true), "output tile fits the LDS");
     uint16_t* otile = reinterpret_cast<uint16_t*>(smem);
@@ -791,7 +796,7 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
         asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(smem + kNextWord)), "v"(next) : "memory");
     if (MODE == 1 && threadIdx.x < rows) odst[threadIdx.x] = row_dst;
     if (MODE == 2 && threadIdx.x < rows) odst[threadIdx.x] = (blk.local_row + threadIdx.x) * args.d;
-    if constexpr (HALF) {
+    if constexpr (HALF && MODE == 0) {
         // waves 2-3 hand their up accumulators to waves 0-1, past the tile
         constexpr uint32_t kXch = kGemmRows * kStride * 2u;
         static_assert(kXch + 2u * NT * 16u * 64u * 4u <= kNextWord, "exchange fits below the next word");
@@ -811,8 +816,8 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
                 for (int v = 0; v < 16; ++v) acc[i][1][v] = xch[((pair * NT + i) * 16u + v) * 64u + lane];
         }
     }
-    if (L.live && (!HALF || L.wave < 2u)) {
-        const uint32_t c0 = MODE == 0 ? 32u * L.wave + m : 64u * L.wave + m;
+    if (L.live && (!HALF || MODE != 0 || L.wave < 2u)) {
+        const uint32_t c0 = MODE == 0 || HALF ? 32u * L.wave + m : 64u * L.wave + m;
 #pragma unroll
         for (int i = 0; i < NT; ++i) {
 #pragma unroll
@@ -824,13 +829,13 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
                     otile[mm * kStride + c0] = f32_to_f16(gate_activation<ACT>(gt) * up);
                 } else {
                     otile[mm * kStride + c0] = f32_to_f16(acc[i][0][v]);
-                    otile[mm * kStride + c0 + 32u] = f32_to_f16(acc[i][1][v]);
+                    if constexpr (!HALF) otile[mm * kStride + c0 + 32u] = f32_to_f16(acc[i][1][v]);
                 }
             }
         }
     }
     block_barrier();
-    const uint32_t col0 = MODE == 0 ? tile * 128u : tile * 256u;
+    const uint32_t col0 = MODE == 0 || HALF ? tile * 128u : tile * 256u;
     const uint32_t ncols = MODE == 0 ? args.f : args.d;
     const uint32_t live = ncols - col0 < kCols ? ncols - col0 : kCols;  // multiple of 64
     constexpr uint32_t kPieces = kCols / 8u;  // 16-byte pieces per row
@@ -961,14 +966,14 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& args, const tsg_routed
         sub.local_row += r0;
         const uint32_t rows = blk.row_count - r0 < kGemmRows ? blk.row_count - r0 : kGemmRows;
         // gate/up column tiles hold 128 columns, the last one 64 when F is an
-        // odd multiple of 64
-        const bool half = MODE == 0 && args.f - tile * 128u <= 64u;
+        // odd multiple of 64; dense tiles hold 128 columns when dense_narrow
+        const bool half = MODE == 0 ? args.f - tile * 128u <= 64u : MODE == 2 && args.dense_narrow;
         if (half) {
             switch ((rows + 31u) / 32u) {
-                case 1: gemm_block<G, SYM, ACT, MODE, 1, MODE == 0>(args, sub, rows, tile, smem, post, next); break;
-                case 2: gemm_block<G, SYM, ACT, MODE, 2, MODE == 0>(args, sub, rows, tile, smem, post, next); break;
-                case 3: gemm_block<G, SYM, ACT, MODE, 3, MODE == 0>(args, sub, rows, tile, smem, post, next); break;
-                default: gemm_block<G, SYM, ACT, MODE, 4, MODE == 0>(args, sub, rows, tile, smem, post, next); break;
+                case 1: gemm_block<G, SYM, ACT, MODE, 1, MODE != 1>(args, sub, rows, tile, smem, post, next); break;
+                case 2: gemm_block<G, SYM, ACT, MODE, 2, MODE != 1>(args, sub, rows, tile, smem, post, next); break;
+                case 3: gemm_block<G, SYM, ACT, MODE, 3, MODE != 1>(args, sub, rows, tile, smem, post, next); break;
+                default: gemm_block<G, SYM, ACT, MODE, 4, MODE != 1>(args, sub, rows, tile, smem, post, next); break;
             }
         } else {
             switch ((rows + 31u) / 32u) {
@@ -1393,8 +1398,15 @@ tsg_status gemm_dispatch(const tsg_moe* moe, hipStream_t s, const GemmArgs& a, u
 template <int G, bool SYM>
 tsg_status launch_dense_qmm(hipStream_t s, const GemmArgs& a) {
     GemmArgs args = a;
-    args.ntiles = (a.d + 255u) / 256u;
     args.n_blocks = (a.dense_rows + kGemmRows - 1u) / kGemmRows;
+    // 256-column tiles while they cover the 256 CUs; below that, 128-column
+    // tiles (one 32-row weight tile per wave, the same MFMA sequence per
+    // column, so the same results), twice the workgroups. T = 2048: N = 2816
+    // runs 352 narrow workgroups instead of 176 wide ones, 0.84-0.88 of the
+    // N = 4096 call's time in the same run against 0.92 wide; N = 4096 (256
+    // wide workgroups) was no faster as 512 narrow ones and keeps wide tiles
+    args.dense_narrow = (uint64_t)((a.d + 255u) / 256u) * args.n_blocks < 256u ? 1u : 0u;
+    args.ntiles = args.dense_narrow ? (a.d + 127u) / 128u : (a.d + 255u) / 256u;
     TSG_REQUIRE((uint64_t)args.ntiles * args.n_blocks <= 0x7FFFFFFFu, TSG_ERR_UNSUPPORTED,
                 "qmm: %u row blocks x %u tiles exceed the grid", args.n_blocks, args.ntiles);
     auto kern = moe_gemm_kernel<G, SYM, TSG_ACT_GELU_TANH, 2>;  // ACT unused in mode 2
