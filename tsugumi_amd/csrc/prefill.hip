@@ -1402,8 +1402,8 @@ tsg_status launch_dense_qmm(hipStream_t s, const GemmArgs& a) {
     // 256-column tiles while they cover the 256 CUs; below that, 128-column
     // tiles (one 32-row weight tile per wave, the same MFMA sequence per
     // column, so the same results), twice the workgroups. T = 2048: N = 2816
-    // runs 352 narrow workgroups instead of 176 wide ones, 0.84-0.88 of the
-    // N = 4096 call's time in the same run against 0.92 wide; N = 4096 (256
+    // runs 352 narrow workgroups instead of 176 wide ones, 0.84-0.92 of the
+    // N = 4096 call's time in the same run against 0.92-0.95 wide; N = 4096 (256
     // wide workgroups) was no faster as 512 narrow ones and keeps wide tiles
     args.dense_narrow = (uint64_t)((a.d + 255u) / 256u) * args.n_blocks < 256u ? 1u : 0u;
     args.ntiles = args.dense_narrow ? (a.d + 127u) / 128u : (a.d + 255u) / 256u;
