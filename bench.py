@@ -340,6 +340,13 @@ def run_prefill_shape(tsg, torch, ctx, args, layer, t, h, f, e, zipf_s, act, lay
         totals += [ev[i].elapsed_time(ev[i + 1]) for i in range(4)]
     per = totals / reps  # ms
     nblocks = int(nb.cpu()[0])
+    # MFMA work issued: each routed block runs ceil(rows / 32) 32-row slices
+    # (PrefillMoEGEMMBench.swift:141-143 pads rows to the tier's block rows)
+    row_counts = blocks.view(-1, 4)[:nblocks, 2].cpu().numpy().astype(np.int64)
+    padded_rows = int(((row_counts + 31) // 32 * 32).sum())
+    if int(row_counts.sum()) != t * k:
+        raise RuntimeError(f"prefill T={t}: routed blocks hold {row_counts.sum()} rows, not {t * k}")
+    padded_flop = 2 * padded_rows * 3 * f * h
     # outputs of the measured work: every routed row written, finite
     out_ok = bool(torch.isfinite(h2.view(torch.float16).float()).all()) and \
         bool(torch.isfinite(partials.view(torch.float16).float()).all())
@@ -401,6 +408,7 @@ def run_prefill_shape(tsg, torch, ctx, args, layer, t, h, f, e, zipf_s, act, lay
                 group_us=float(per[0]) * 1e3, reduce_us=float(per[3]) * 1e3,
                 burst_gemm_us=float(per[1] + per[2]) * 1e3,
                 gemm_tflops=flop / (gemm_ms * 1e-3) / 1e12,
+                padded_tflops=padded_flop / (gemm_ms * 1e-3) / 1e12, padded_flop=padded_flop,
                 layer_tflops=flop / (total_ms * 1e-3) / 1e12, blocks=nblocks, flop=flop)
 
 
@@ -826,11 +834,14 @@ def run_verify(tsg, torch, ctx, args, layers, routers):
 def attainable_gemm(torch):
     """The attainable dense fp16 GEMM rate on this GPU (torch.matmul ->
     hipBLASLt, fp16 in, fp32 accumulate): a square 8192^3 GEMM, and the
-    prefill layer's gate/up work as one dense GEMM (16,384 rows x 1,408
-    columns x K 2,816), the second denominator of the prefill fraction."""
+    prefill layer's two GEMMs as dense ones of the same shapes (gate/up:
+    16,384 rows x 1,408 columns x K 2,816; down: 16,384 x 2,816 x K 704),
+    whose combined rate is the layer-shape denominator of the prefill
+    fraction."""
     out = {}
     for name, (m, n, k) in (("square_8192", (8192, 8192, 8192)),
-                            ("layer_gate_up_dense", (PREFILL_T * TOPK, 2 * F, H))):
+                            ("layer_gate_up_dense", (PREFILL_T * TOPK, 2 * F, H)),
+                            ("layer_down_dense", (PREFILL_T * TOPK, H, F))):
         a = torch.randn(m, k, dtype=torch.float16, device="cuda")
         b = torch.randn(k, n, dtype=torch.float16, device="cuda")
         stream = torch.cuda.Stream()
@@ -843,6 +854,11 @@ def attainable_gemm(torch):
         ms = time_graph(torch, stream, body, reps=4) / 10
         out[name] = {"shape_mnk": [m, n, k], "us": round(ms * 1e3, 2),
                      "TFLOPs": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1)}
+        del a, b, c
+    gu, dn = out["layer_gate_up_dense"], out["layer_down_dense"]
+    lf = sum(2.0 * m * n * k for m, n, k in (gu["shape_mnk"], dn["shape_mnk"]))
+    out["layer_dense"] = {"us": round(gu["us"] + dn["us"], 2),
+                          "TFLOPs": round(lf / ((gu["us"] + dn["us"]) * 1e-6) / 1e12, 1)}
     log(f"attainable fp16 GEMM (torch.matmul): {out}")
     return out
 
@@ -864,6 +880,10 @@ def prefill_summary(pre):
                              "form (moe_gemm_kernel gate/up, then down)",
             "gemm_TFLOPs": round(pre["gemm_tflops"], 2),
             "frac_mfma_peak": round(pre["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+            "padded_TFLOPs": round(pre["padded_tflops"], 2),
+            "padded_flop_per_layer": pre["padded_flop"],
+            "padded_measure": "MFMA work issued (each routed block's rows rounded up to 32-row "
+                              "slices) over the same sustained time",
             "layer_TFLOPs": round(pre["layer_tflops"], 2),
             "flop_per_layer": pre["flop"], "routed_blocks": pre["blocks"]}
 
@@ -1130,6 +1150,8 @@ def main():
             out["prefill"]["attainable_fp16_gemm"] = att
             out["prefill"]["frac_attainable_square"] = round(
                 pre["gemm_tflops"] / att["square_8192"]["TFLOPs"], 4)
+            out["prefill"]["frac_attainable_layer_shape"] = round(
+                pre["gemm_tflops"] / att["layer_dense"]["TFLOPs"], 4)
         except Exception as exc:  # noqa: BLE001 - reported, not hidden
             log(f"attainable GEMM failed: {exc}")
     try:

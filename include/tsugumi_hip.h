@@ -86,6 +86,28 @@ typedef struct tsg_routed_block {
     uint32_t local_slot, pair_start, row_count, local_row;
 } tsg_routed_block;
 
+/* The layouts above are shared with the reference's Swift/Metal structs
+ * byte for byte; these checks hold them (PrefillRouterTests.swift:12-19 pins
+ * the pair's size and field offsets; MoE.swift:4-29 the 36-byte offsets). */
+#ifdef __cplusplus
+#define TSG_LAYOUT_ASSERT(cond, msg) static_assert(cond, msg)
+#else
+#define TSG_LAYOUT_ASSERT(cond, msg) _Static_assert(cond, msg)
+#endif
+TSG_LAYOUT_ASSERT(sizeof(tsg_expert_offsets) == 36, "MoEExpertOffsets is 36 bytes");
+TSG_LAYOUT_ASSERT(offsetof(tsg_expert_offsets, down_b) == 32, "MoEExpertOffsets.downB at 32");
+TSG_LAYOUT_ASSERT(sizeof(tsg_token_expert_pair) == 16, "PrefillTokenExpertPair is 16 bytes");
+TSG_LAYOUT_ASSERT(offsetof(tsg_token_expert_pair, token) == 0 &&
+                      offsetof(tsg_token_expert_pair, expert) == 4 &&
+                      offsetof(tsg_token_expert_pair, rank) == 8 &&
+                      offsetof(tsg_token_expert_pair, weight_bits) == 12,
+                  "PrefillTokenExpertPair field offsets 0/4/8/12");
+TSG_LAYOUT_ASSERT(sizeof(tsg_moe_group) == 12, "PrefillMoEGroup is 12 bytes");
+TSG_LAYOUT_ASSERT(sizeof(tsg_moe_tile) == 16, "PrefillMoETile is 16 bytes");
+TSG_LAYOUT_ASSERT(sizeof(tsg_routed_block) == 16, "PrefillRoutedGEMMBlock is 16 bytes");
+TSG_LAYOUT_ASSERT(offsetof(tsg_routed_block, local_row) == 12, "PrefillRoutedGEMMBlock.localRow at 12");
+#undef TSG_LAYOUT_ASSERT
+
 typedef struct tsg_ctx tsg_ctx;     /* MetalContext                      */
 typedef struct tsg_moe tsg_moe;     /* MoE / PrefillGroupedRoutedMoE      */
 typedef struct tsg_layer tsg_layer; /* one HBM-resident MoEPack layer     */
@@ -508,23 +530,29 @@ tsg_status tsg_prefill_moe_gate_up_down(tsg_moe* moe, tsg_stream stream, const t
 /* encodeStreamedRows (PrefillGroupedRoutedMoE.swift:793-917,
  * prefill.metal:1489-1721): verify-width blocks (row_count <= 8), decode's
  * per-row arithmetic with each weight read once per block; writes act rows
- * (act_scratch, (max local_row + rows) * f fp16) and route partials. `blocks`
- * is a HOST array (the reference passes it with setBytes); local_slot is the
- * expert id in the resident layer. Returns TSG_ERR_DECLINED when a block holds
- * more than 8 rows. */
+ * (act_scratch: block rows local_row .. local_row + row_count - 1, each f
+ * fp16) and route partials. act_scratch holds max_rows rows (the reference's
+ * maxRows, the rows the scratch was sized for). `blocks` is a HOST array (the
+ * reference passes it with setBytes); local_slot is the expert id in the
+ * resident layer. Returns TSG_ERR_DECLINED, with nothing launched, when a
+ * block holds no rows or more than 8, or when a block's rows reach past
+ * max_rows (`guard rows <= maxRows else { return 0 }`,
+ * PrefillGroupedRoutedMoE.swift:830). */
 tsg_status tsg_prefill_moe_rows(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
                                 const uint16_t* hidden, uint32_t hidden_stride_elements,
                                 const tsg_token_expert_pair* sorted_pairs,
                                 const tsg_routed_block* blocks, uint32_t n_blocks,
-                                uint16_t* act_scratch, uint16_t* route_partials,
-                                uint32_t top_k, uint32_t d, uint32_t f);
+                                uint16_t* act_scratch, uint32_t max_rows,
+                                uint16_t* route_partials, uint32_t top_k, uint32_t d,
+                                uint32_t f);
 /* encodeStreamedRows with the block list left on the device, where
  * tsg_prefill_group_pairs_device (any tile_rows >= the token count) writes it:
  * the verify block's grouping (RealForwardRunner.swift:2116-2151) without a
  * host round trip. blocks holds max_blocks entries (<= 65535), the first
  * *n_blocks_device of them live; each live block gives exactly
- * tsg_prefill_moe_rows' results for it. A live block with no rows, more than
- * 8, or an expert past the layer is skipped and tsg_ctx_synchronize reports
+ * tsg_prefill_moe_rows' results for it. act_scratch holds max_rows rows of f
+ * fp16. A live block with no rows, more than 8, rows past max_rows or an
+ * expert past the layer is skipped and tsg_ctx_synchronize reports
  * TSG_ERR_INVALID_ARGUMENT (the host form declines such a list up front).
  * No counterpart entry in the reference, which reads the grouping back to the
  * host. */
@@ -533,8 +561,8 @@ tsg_status tsg_prefill_moe_rows_device(tsg_moe* moe, tsg_stream stream, const ts
                                        const tsg_token_expert_pair* sorted_pairs,
                                        const tsg_routed_block* blocks, uint32_t max_blocks,
                                        const uint32_t* n_blocks_device, uint16_t* act_scratch,
-                                       uint16_t* route_partials, uint32_t top_k, uint32_t d,
-                                       uint32_t f);
+                                       uint32_t max_rows, uint16_t* route_partials,
+                                       uint32_t top_k, uint32_t d, uint32_t f);
 /* PrefillMoE.encodeReduceTokenMajor (PrefillMoE.swift:11-38):
  * h2[t,d] = half(sum_{r<top_k} fma(w[t,r], P[(t*top_k + r), d])). */
 tsg_status tsg_prefill_moe_reduce_token_major(tsg_ctx* ctx, tsg_stream stream,

@@ -146,3 +146,40 @@ def test_token_expert_pairs_match_oracle(tsg):
     got = tsg.PrefillRouter.make_token_expert_pairs(idx, w, t, k)
     ref = oracle.make_token_expert_pairs(idx, w, t, k)
     assert np.array_equal(np.asarray(got), np.asarray(ref))
+
+
+def test_struct_layouts_match_the_reference(tsg, tmp_path):
+    """The boundary's structs are the reference's byte for byte: the pair is
+    16 bytes with fields at 0/4/8/12 (PrefillRouterTests.swift:12-19), the
+    expert offsets 36 (MoE.swift:4-29), group 12, tile 16 and routed block 16
+    (PrefillMoEGrouping.swift:3-29, PrefillGroupedRoutedMoE.swift:20-25). The
+    header's own static assertions are compiled as C11 and as C++17, and the
+    ctypes and numpy mirrors are held to the same sizes and offsets."""
+    import ctypes
+    import os
+    import shutil
+    import subprocess
+
+    from tsugumi_amd import _abi
+    sizes = {_abi.ExpertOffsets: 36, _abi.TokenExpertPair: 16, _abi.MoEGroup: 12,
+             _abi.MoETile: 16, _abi.RoutedBlock: 16}
+    for cls, size in sizes.items():
+        assert ctypes.sizeof(cls) == size, cls.__name__
+    assert [getattr(_abi.TokenExpertPair, f).offset
+            for f in ("token", "expert", "rank", "weight_bits")] == [0, 4, 8, 12]
+    assert _abi.RoutedBlock.local_row.offset == 12
+    assert tsg.PAIR_DTYPE.itemsize == 16 and tsg.BLOCK_DTYPE.itemsize == 16
+    assert tsg.GROUP_DTYPE.itemsize == 12 and tsg.TILE_DTYPE.itemsize == 16
+    assert [tsg.PAIR_DTYPE.fields[f][1] for f in ("token", "expert", "rank", "weight_bits")] == \
+        [0, 4, 8, 12]
+    header = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                          "include", "tsugumi_hip.h")
+    src = tmp_path / "layout.c"
+    src.write_text(f'#include "{header}"\nint main(void) {{ return 0; }}\n')
+    for cc, std in (("gcc", "-std=c11"), ("g++", "-std=c++17")):
+        if shutil.which(cc) is None:
+            pytest.skip(f"{cc} not installed")
+        lang = ["-x", "c++"] if cc == "g++" else []
+        r = subprocess.run([cc, std, "-fsyntax-only", "-Wall", "-Werror", *lang, str(src)],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr

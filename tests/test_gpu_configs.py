@@ -618,6 +618,40 @@ def test_grouped_gemm_skips_and_reports_expert_past_layer(tsg, ctx, gemma_layer)
     ctx.synchronize()  # the error word was cleared
 
 
+def test_fused_gate_up_down_zero_row_blocks(tsg, ctx, gemma_layer):
+    """Routed blocks with no rows, between real ones, are no-ops in both
+    forms: the fused launch (64 blocks, 1,088 items, so every workgroup takes
+    several and meets zero-row items after others) equals the two launches
+    bit for bit and drains its schedule, twice in a row."""
+    configure(ctx, 32, "sym")
+    layer = gemma_layer[0]
+    d, f, k, t = 2816, 704, 8, 64
+    g = tsg.PrefillGroupedRoutedMoE(tsg.MoE(ctx))
+    pairs = np.zeros(t * k, oracle.PAIR_DTYPE)
+    pairs["token"] = np.repeat(np.arange(t, dtype=np.uint32), k)
+    pairs["rank"] = np.tile(np.arange(k, dtype=np.uint32), t)
+    pairs["weight_bits"] = 0x3C00
+    blocks = np.zeros(64, oracle.BLOCK_DTYPE)
+    for i in range(64):
+        real = i % 2 == 0
+        j = i // 2
+        blocks[i] = ((7 * i) % 128, 16 * j, 16 if real else 0, 16 * j)
+    pairs["expert"] = np.repeat(blocks["local_slot"][::2], 16)
+    hidden = dev(wl.f16_normal(np.random.default_rng(11), t * d))
+    P, B = dev(pairs), dev(blocks.view(np.uint32))
+    a2, p2 = empty(t * k * f, fill=NAN16), empty(t * k * d, fill=NAN16)
+    g.encode_gate_up(layer, hidden, d, P, B, 64, a2, d, f)
+    g.encode_down(layer, a2, P, B, 64, p2, k, d, f)
+    want_a, want_p = host(a2, np.uint16), host(p2, np.uint16)
+    assert np.all(np.isfinite(oracle.f16_to_float(want_p)))
+    for rep in range(2):
+        a1, p1 = empty(t * k * f, fill=NAN16), empty(t * k * d, fill=NAN16)
+        g.encode_gate_up_down(layer, hidden, d, P, B, 64, a1, p1, k, d, f)
+        ctx.synchronize()
+        assert np.array_equal(host(a1, np.uint16), want_a), f"act differs (launch {rep})"
+        assert np.array_equal(host(p1, np.uint16), want_p), f"partials differ (launch {rep})"
+
+
 def test_fused_gate_up_down_empty_device_list(tsg, ctx, gemma_layer):
     """A device count of zero (no routed block) runs the fused launch to its
     end without work, writes nothing and reports nothing; the next launch on

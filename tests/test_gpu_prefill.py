@@ -9,6 +9,8 @@ from tests import kernelcheck as kc
 from tests import workloads as wl
 from tests.gpu_util import dev, empty, f16_fill_bits, host
 
+NAN16 = f16_fill_bits(float("nan"))
+
 pytestmark = pytest.mark.gpu
 
 
@@ -193,6 +195,56 @@ def test_rows_path_matches_decode_bitwise(tsg, ctx):
         tsg.PrefillGroupedRoutedMoE(moe).encode_streamed_rows(layer, dev(x), d, dev(pairs), bad,
                                                               ract, parts_out, 8, d, f)
     assert e.value.status == 4
+
+
+def test_rows_path_declines_tile_past_scratch(tsg, ctx):
+    """encodeStreamedRows returns 0 when the tile's activation rows exceed
+    the scratch it was sized for (PrefillGroupedRoutedMoE.swift:830, `guard
+    rows <= maxRows`): the host form declines before any launch and leaves
+    the outputs untouched; the device form skips the block and reports it at
+    synchronisation; a tile that fits exactly runs."""
+    configure(ctx, 32, "sym")
+    d, f = 576, 384
+    rng = oracle.SplitMix64(0x4D7)
+    parts = [[oracle.quantize_int4(rng.uniforms(-0.3, 0.3, r * c_).reshape(r, c_), 32, True)
+              for (r, c_) in ((f, d), (f, d), (d, f))] for _ in range(2)]
+    layer, offs, blobs = _upload_layer(tsg, ctx, parts, True)
+    x = oracle.seed_tree_key(0x4D7, "rows-max-rows").uniforms_f16(-0.8, 0.8, 3 * d)
+    moe = tsg.MoE(ctx)
+    g = tsg.PrefillGroupedRoutedMoE(moe)
+    # expert 0 takes tokens 0..2, expert 1 tokens 0..1: 5 activation rows
+    pairs = np.array([(0, 0, 0, 0x3C00), (1, 0, 0, 0x3C00), (2, 0, 0, 0x3C00),
+                      (0, 1, 1, 0x3C00), (1, 1, 1, 0x3C00)], dtype=oracle.PAIR_DTYPE)
+    blocks = np.array([(0, 0, 3, 0), (1, 3, 2, 3)], dtype=oracle.BLOCK_DTYPE)
+    act, part = empty(5 * f, fill=NAN16), empty(3 * 2 * d, fill=NAN16)
+    for max_rows in (0, 3, 4):
+        with pytest.raises(tsg.TsgError) as e:
+            g.encode_streamed_rows(layer, dev(x), d, dev(pairs), blocks, act, part, 2, d, f,
+                                   max_rows=max_rows)
+        assert e.value.status == 4, max_rows
+    ctx.synchronize()
+    assert np.all(host(act, np.uint16) == np.uint16(NAN16 & 0xFFFF))
+    assert np.all(host(part, np.uint16) == np.uint16(NAN16 & 0xFFFF))
+    # the device form: block 1 reaches past 4 rows, so it is skipped and reported
+    g.encode_streamed_rows_device(layer, dev(x), d, dev(pairs), dev(blocks), 2,
+                                  dev(np.array([2], np.uint32)), act, part, 2, d, f, max_rows=4)
+    with pytest.raises(tsg.TsgError) as e:
+        ctx.synchronize()
+    assert e.value.status == 1
+    got = host(part, np.uint16).reshape(3, 2, d)
+    assert not np.any(np.isnan(oracle.f16_to_float(got[:, 0])))
+    assert np.all(got[:2, 1] == np.uint16(NAN16 & 0xFFFF))
+    # exactly 5 rows: both forms run and agree bit for bit
+    act2, part2 = empty(5 * f), empty(3 * 2 * d, fill=NAN16)
+    g.encode_streamed_rows(layer, dev(x), d, dev(pairs), blocks, act2, part2, 2, d, f, max_rows=5)
+    act3, part3 = empty(5 * f), empty(3 * 2 * d, fill=NAN16)
+    g.encode_streamed_rows_device(layer, dev(x), d, dev(pairs), dev(blocks), 2,
+                                  dev(np.array([2], np.uint32)), act3, part3, 2, d, f, max_rows=5)
+    ctx.synchronize()
+    p2 = host(part2, np.uint16).reshape(3, 2, d)
+    assert np.array_equal(p2, host(part3, np.uint16).reshape(3, 2, d))
+    assert not np.any(np.isnan(oracle.f16_to_float(p2[:, 0])))
+    assert not np.any(np.isnan(oracle.f16_to_float(p2[:2, 1])))
 
 
 @pytest.mark.parametrize("form", ["host", "device"])

@@ -70,6 +70,16 @@ def _np_ptr(a: np.ndarray):
     return a.ctypes.data
 
 
+def _scratch_rows(scratch, f: int, max_rows) -> int:
+    """Rows of f elements a scratch buffer holds: max_rows when given, else
+    what the tensor's size allows (an address given as an int needs max_rows)."""
+    if max_rows is not None:
+        return int(max_rows)
+    if scratch is None or isinstance(scratch, int):
+        raise ValueError("max_rows is required when the scratch is not a tensor")
+    return int(scratch.numel()) // int(f) if f else 0
+
+
 def offsets_from(seq) -> ExpertOffsets:
     if isinstance(seq, ExpertOffsets):
         return seq
@@ -647,21 +657,27 @@ class PrefillGroupedRoutedMoE:
 
     def encode_streamed_rows_device(self, layer, hidden, hidden_stride, sorted_pairs, blocks,
                                     max_blocks, n_blocks_device, act_scratch, route_partials,
-                                    top_k, d, f, stream=None):
+                                    top_k, d, f, stream=None, max_rows=None):
         """encode_streamed_rows with the block list (and its count) on the
         device, as group_pairs_device writes them."""
         check(self.lib.tsg_prefill_moe_rows_device(
             self.moe.handle, _stream(stream), layer.handle, _ptr(hidden), hidden_stride,
             _ptr(sorted_pairs), _ptr(blocks), max_blocks, _ptr(n_blocks_device),
-            _ptr(act_scratch), _ptr(route_partials), top_k, d, f))
+            _ptr(act_scratch), _scratch_rows(act_scratch, f, max_rows), _ptr(route_partials),
+            top_k, d, f))
 
     def encode_streamed_rows(self, layer, hidden, hidden_stride, sorted_pairs, host_blocks,
-                             act_scratch, route_partials, top_k, d, f, stream=None):
+                             act_scratch, route_partials, top_k, d, f, stream=None,
+                             max_rows=None):
+        """encodeStreamedRows (PrefillGroupedRoutedMoE.swift:793-917). max_rows
+        is the activation scratch's capacity in rows of f (the reference's
+        maxRows); by default, what act_scratch holds. A tile it cannot take
+        raises TsugumiError with TSG_ERR_DECLINED (the reference returns 0)."""
         hb = np.ascontiguousarray(host_blocks, BLOCK_DTYPE)
         check(self.lib.tsg_prefill_moe_rows(
             self.moe.handle, _stream(stream), layer.handle, _ptr(hidden), hidden_stride,
             _ptr(sorted_pairs), _np_ptr(hb) if hb.size else None, hb.size, _ptr(act_scratch),
-            _ptr(route_partials), top_k, d, f))
+            _scratch_rows(act_scratch, f, max_rows), _ptr(route_partials), top_k, d, f))
 
 
 class PrefillMoE:

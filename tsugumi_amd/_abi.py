@@ -152,9 +152,9 @@ SIGNATURES = {
     "tsg_prefill_moe_down": (C.c_int, [P, P, P, P, P, P, U32, P, P, U32, U32, U32]),
     "tsg_prefill_moe_gate_up_down": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, P, U32, U32,
                                                U32]),
-    "tsg_prefill_moe_rows": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, U32, U32]),
-    "tsg_prefill_moe_rows_device": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, P, U32, U32,
-                                              U32]),
+    "tsg_prefill_moe_rows": (C.c_int, [P, P, P, P, U32, P, P, U32, P, U32, P, U32, U32, U32]),
+    "tsg_prefill_moe_rows_device": (C.c_int, [P, P, P, P, U32, P, P, U32, P, P, U32, P, U32,
+                                              U32, U32]),
     "tsg_prefill_moe_reduce_token_major": (C.c_int, [P, P, P, P, P, U32, U32, U32]),
     "tsg_prefill_int4_qmm": (C.c_int, [P, P, P, P, P, P, P, U32, U32, U32]),
     "tsg_prefill_layer_tail": (C.c_int, [P, P, P, P, P, P, P, U32, U32, U32, U32, U32,

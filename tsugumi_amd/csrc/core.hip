@@ -75,6 +75,14 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
     TSG_HIP_TRY(hipGetDeviceCount(&count));
     TSG_REQUIRE(device >= 0 && device < count, TSG_ERR_INVALID_ARGUMENT,
                 "device %d out of range (%d devices)", device, count);
+    // the context's set-up runs with `device` current; the caller's current
+    // device is restored on every return
+    int prev = 0;
+    TSG_HIP_TRY(hipGetDevice(&prev));
+    struct Restore {
+        int dev;
+        ~Restore() { (void)hipSetDevice(dev); }
+    } restore{prev};
     TSG_HIP_TRY(hipSetDevice(device));
     hipDeviceProp_t prop;
     TSG_HIP_TRY(hipGetDeviceProperties(&prop, device));
@@ -85,10 +93,16 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
     TSG_REQUIRE(ctx != nullptr, TSG_ERR_OUT_OF_MEMORY, "host allocation failed");
     ctx->device = device;
     ctx->num_cus = prop.multiProcessorCount;
-    int n_xcc = 1;
+    // The fused grouped GEMM keeps every item of a routed block on one XCD
+    // (one queue per XCD); an XCD count it cannot map one to one onto its
+    // queues (unknown, not a power of two, more than kMaxGemmQueues) leaves
+    // the fused launch off (gemm_queues = 0) and the two-launch form runs.
+    int n_xcc = 0;
     if (hipDeviceGetAttribute(&n_xcc, hipDeviceAttributeNumberOfXccs, device) != hipSuccess)
-        n_xcc = 1;
-    ctx->gemm_queues = n_xcc >= 8 ? 8u : n_xcc >= 4 ? 4u : n_xcc >= 2 ? 2u : 1u;
+        n_xcc = 0;
+    ctx->gemm_queues = n_xcc > 0 && (uint32_t)n_xcc <= kMaxGemmQueues && (n_xcc & (n_xcc - 1)) == 0
+                           ? (uint32_t)n_xcc
+                           : 0u;
     hipError_t e = hipMalloc(&ctx->counters, sizeof(uint32_t) * kMaxCounters);
     if (e == hipSuccess)
         e = hipMalloc(&ctx->logits, sizeof(float) * kMaxPromptRows * kMaxExperts);

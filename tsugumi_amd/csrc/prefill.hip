@@ -456,6 +456,7 @@ struct GemmArgs {
     uint32_t ntiles;            // weight-row tiles per routed block
     uint32_t dense_narrow;      // MODE 2: 128-column tiles, one 32-row weight tile per wave
     uint32_t num_experts;       // experts of the layer (device block lists are checked)
+    uint32_t max_rows;          // rows path, device list: rows of the activation scratch
     uint32_t* error;            // the context's device error word
 };
 
@@ -953,10 +954,19 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& args, const tsg_routed
                                           uint32_t next = 0u) {
     // a block list written on the device is not checked on the host: an
     // expert past the layer is skipped (its weights would lie outside it)
-    if (MODE != 2 && blk.local_slot >= args.num_experts) {
-        if (threadIdx.x == 0) atomicOr(args.error, kErrGemmBlock);
-        if (post && threadIdx.x == 0)
-            asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(smem + kNextWord)), "v"(next) : "memory");
+    const bool bad_expert = MODE != 2 && blk.local_slot >= args.num_experts;
+    if (bad_expert || blk.row_count == 0) {
+        // No pass runs (a block with no rows is a no-op, as in the two-launch
+        // form), so the fused launch's next index is posted here instead of in
+        // the epilogue; the barrier first lets every wave read the index the
+        // previous item posted in the same word (the block takes this branch
+        // as a whole: blk is uniform).
+        if (bad_expert && threadIdx.x == 0) atomicOr(args.error, kErrGemmBlock);
+        if (post) {
+            lds_barrier();
+            if (threadIdx.x == 0)
+                asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(smem + kNextWord)), "v"(next) : "memory");
+        }
         return;
     }
     for (uint32_t r0 = 0; r0 < blk.row_count; r0 += kGemmRows) {
@@ -1031,13 +1041,12 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmArgs args
 // launch between the two GEMMs. Launches that share a context's schedule
 // words must not overlap (one stream, or ordered streams).
 struct FusedSched {
-    uint32_t* next;    // kXcds queue heads
+    uint32_t* next;    // kMaxGemmQueues queue heads
     uint32_t* exited;  // workgroups that have left
     uint32_t* done;    // gate/up tiles finished, per routed block (cap entries)
     uint32_t cap;
     uint32_t queues;   // 1, 2, 4 or 8
 };
-constexpr uint32_t kXcds = 8;
 constexpr uint32_t kFusedSpinLimit = 1u << 18;
 
 template <int G, bool SYM, int ACT>
@@ -1297,8 +1306,9 @@ __global__ __launch_bounds__(kRowsThreads) void rows_down_kernel(GemmArgs args, 
 // The device-list forms: the block list and its count were written on the
 // device (tsg_prefill_group_pairs_device), the grid covers the list's
 // capacity and blocks past the count exit. A block the rows path cannot take
-// (no rows, more than kRowsMax, an expert past the layer) is skipped and sets
-// kErrRowsBlock, which tsg_ctx_synchronize reports.
+// (no rows, more than kRowsMax, rows past the activation scratch, an expert
+// past the layer) is skipped and sets kErrRowsBlock, which
+// tsg_ctx_synchronize reports.
 // The list, its device count and its capacity come as leading scalar kernel
 // arguments (preloaded into SGPRs by the dispatch), so the first load needs
 // no kernarg round trip; the struct's fields arrive meanwhile.
@@ -1309,7 +1319,8 @@ __device__ __forceinline__ bool rows_device_block(const GemmArgs& args,
     const uint32_t n = min(*n_dev, n_blocks);
     if (blockIdx.y >= n) return false;
     blk = blocks[blockIdx.y];
-    if (blk.row_count == 0 || blk.row_count > kRowsMax || blk.local_slot >= args.num_experts) {
+    if (blk.row_count == 0 || blk.row_count > kRowsMax || blk.local_slot >= args.num_experts ||
+        (uint64_t)blk.local_row + blk.row_count > args.max_rows) {
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicOr(args.error, kErrRowsBlock);
         return false;
     }
@@ -1367,7 +1378,7 @@ tsg_status launch_fused(const tsg_moe* moe, hipStream_t s, GemmArgs gu, GemmArgs
     const tsg_ctx* ctx = moe->ctx;
     FusedSched sc;
     sc.next = ctx->gemm_sched;
-    sc.exited = ctx->gemm_sched + kXcds;
+    sc.exited = ctx->gemm_sched + kMaxGemmQueues;
     sc.done = ctx->gemm_sched + 16u;
     sc.cap = max_blocks;
     sc.queues = ctx->gemm_queues;
@@ -1396,16 +1407,16 @@ tsg_status gemm_dispatch(const tsg_moe* moe, hipStream_t s, const GemmArgs& a, u
 // Dense projection: blocks of 128 rows of x in order, 256 output columns per
 // workgroup (the down GEMM's tiling).
 template <int G, bool SYM>
-tsg_status launch_dense_qmm(hipStream_t s, const GemmArgs& a) {
+tsg_status launch_dense_qmm(hipStream_t s, const GemmArgs& a, uint32_t num_cus) {
     GemmArgs args = a;
     args.n_blocks = (a.dense_rows + kGemmRows - 1u) / kGemmRows;
-    // 256-column tiles while they cover the 256 CUs; below that, 128-column
+    // 256-column tiles while they cover the device's CUs; below that, 128-column
     // tiles (one 32-row weight tile per wave, the same MFMA sequence per
     // column, so the same results), twice the workgroups. T = 2048: N = 2816
     // runs 352 narrow workgroups instead of 176 wide ones, 0.84-0.92 of the
     // N = 4096 call's time in the same run against 0.92-0.95 wide; N = 4096 (256
     // wide workgroups) was no faster as 512 narrow ones and keeps wide tiles
-    args.dense_narrow = (uint64_t)((a.d + 255u) / 256u) * args.n_blocks < 256u ? 1u : 0u;
+    args.dense_narrow = (uint64_t)((a.d + 255u) / 256u) * args.n_blocks < num_cus ? 1u : 0u;
     args.ntiles = args.dense_narrow ? (a.d + 127u) / 128u : (a.d + 255u) / 256u;
     TSG_REQUIRE((uint64_t)args.ntiles * args.n_blocks <= 0x7FFFFFFFu, TSG_ERR_UNSUPPORTED,
                 "qmm: %u row blocks x %u tiles exceed the grid", args.n_blocks, args.ntiles);
@@ -1602,6 +1613,12 @@ extern "C" tsg_status tsg_prefill_moe_gate_up_down(
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
     hipStream_t s = as_stream(stream);
+    if (ctx->gemm_queues == 0) {
+        // XCD count unknown or not one queue per XCD: the two launches (the
+        // same results; the hand-off between the GEMMs is the launch boundary)
+        if ((st = gemm_dispatch<0>(moe, s, gu, n_blocks))) return st;
+        return gemm_dispatch<1>(moe, s, dn, n_blocks);
+    }
     if (ctx->group_size == 32)
         return sym ? launch_fused<32, true>(moe, s, gu, dn, n_blocks)
                    : launch_fused<32, false>(moe, s, gu, dn, n_blocks);
@@ -1631,18 +1648,25 @@ extern "C" tsg_status tsg_prefill_moe_rows(tsg_moe* moe, tsg_stream stream,
                                            uint32_t hidden_stride,
                                            const tsg_token_expert_pair* pairs,
                                            const tsg_routed_block* blocks, uint32_t n_blocks,
-                                           uint16_t* act_scratch, uint16_t* partials,
-                                           uint32_t top_k, uint32_t d, uint32_t f) {
+                                           uint16_t* act_scratch, uint32_t max_rows,
+                                           uint16_t* partials, uint32_t top_k, uint32_t d,
+                                           uint32_t f) {
     tsg_status st = check_layer_moe(moe, layer);
     if (st) return st;
     if (n_blocks == 0) return TSG_OK;
     TSG_REQUIRE(blocks, TSG_ERR_INVALID_ARGUMENT, "blocks is NULL");
-    // The host chooses the rows path from the grouping and it declines blocks
-    // wider than its cap (PrefillGroupedRoutedMoE.swift:808-830).
+    // The host chooses the rows path from the grouping, and it declines blocks
+    // wider than its cap and a tile whose activation rows exceed the scratch
+    // it was sized for (PrefillGroupedRoutedMoE.swift:808-830).
     for (uint32_t i = 0; i < n_blocks; ++i) {
         if (blocks[i].row_count == 0 || blocks[i].row_count > kRowsMax)
             return fail(TSG_ERR_DECLINED, "rows path takes 1..%u rows per block, block %u has %u",
                         kRowsMax, i, blocks[i].row_count);
+        if ((uint64_t)blocks[i].local_row + blocks[i].row_count > max_rows)
+            return fail(TSG_ERR_DECLINED,
+                        "block %u's activation rows %u..%u reach past the scratch's %u rows", i,
+                        blocks[i].local_row, blocks[i].local_row + blocks[i].row_count - 1u,
+                        max_rows);
         // the block list is on the host: an expert id past the layer would
         // make the kernels read outside it
         TSG_REQUIRE(blocks[i].local_slot < layer->num_experts, TSG_ERR_INVALID_ARGUMENT,
@@ -1714,8 +1738,9 @@ extern "C" tsg_status tsg_prefill_moe_rows_device(tsg_moe* moe, tsg_stream strea
                                                   const tsg_routed_block* blocks,
                                                   uint32_t max_blocks,
                                                   const uint32_t* n_blocks_device,
-                                                  uint16_t* act_scratch, uint16_t* partials,
-                                                  uint32_t top_k, uint32_t d, uint32_t f) {
+                                                  uint16_t* act_scratch, uint32_t max_rows,
+                                                  uint16_t* partials, uint32_t top_k, uint32_t d,
+                                                  uint32_t f) {
     tsg_status st = check_layer_moe(moe, layer);
     if (st) return st;
     TSG_REQUIRE(n_blocks_device && top_k > 0 && act_scratch && partials, TSG_ERR_INVALID_ARGUMENT,
@@ -1727,6 +1752,7 @@ extern "C" tsg_status tsg_prefill_moe_rows_device(tsg_moe* moe, tsg_stream strea
                              n_blocks_device, act_scratch, d, f, top_k)))
         return st;
     TSG_REQUIRE(aligned16(act_scratch), TSG_ERR_ALIGNMENT, "act_scratch must be 16-byte aligned");
+    a.max_rows = max_rows;
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
     // LDS for the widest block the rows path takes
@@ -1829,8 +1855,10 @@ extern "C" tsg_status tsg_prefill_int4_qmm(tsg_ctx* ctx, tsg_stream stream,
     a.top_k = 1;
     a.dense_rows = t;
     hipStream_t hs = as_stream(stream);
-    if (g == 32) return sym ? launch_dense_qmm<32, true>(hs, a) : launch_dense_qmm<32, false>(hs, a);
-    return sym ? launch_dense_qmm<64, true>(hs, a) : launch_dense_qmm<64, false>(hs, a);
+    const uint32_t cus = (uint32_t)ctx->num_cus;
+    if (g == 32)
+        return sym ? launch_dense_qmm<32, true>(hs, a, cus) : launch_dense_qmm<32, false>(hs, a, cus);
+    return sym ? launch_dense_qmm<64, true>(hs, a, cus) : launch_dense_qmm<64, false>(hs, a, cus);
 }
 
 // The GEMM's own fp16 staging, un-paired (test hook for bit-exact dequant).

@@ -56,8 +56,9 @@ struct tsg_ctx {
     uint32_t* gemm_sched = nullptr;     // kGemmSchedWords
     int num_cus = 256;
     // the fused GEMM's queue count: the device's XCDs (8 on an MI355X in its
-    // one-partition mode), rounded down to a power of two, at most 8
-    uint32_t gemm_queues = 8;
+    // one-partition mode) when that is a power of two of at most 8, else 0
+    // (the fused launch is not used)
+    uint32_t gemm_queues = 0;
 };
 
 struct tsg_moe {
@@ -99,6 +100,7 @@ constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kMaxRouterRows = 8;      // MoE.maxRouterRows (verify rows)
 constexpr uint32_t kMaxPromptRows = 4096;   // rows one router launch may route
 constexpr uint32_t kMaxCounters = 12288;
+constexpr uint32_t kMaxGemmQueues = 8;                 // the fused GEMM's per-XCD queues
 constexpr uint32_t kGemmSchedBlocks = 65536;             // routed blocks the fused GEMM takes
 constexpr uint32_t kGemmSchedWords = 16u + kGemmSchedBlocks;
 // Words of ctx->counters used by the one-launch decode layer (below them, words
