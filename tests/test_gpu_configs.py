@@ -458,7 +458,7 @@ def run_prefill_full(tsg, ctx, layer, offs, blobs, t, d, f, ne, s, act, seed):
     hidden = wl.f16_normal(rng, t * d)
     moe = tsg.MoE(ctx, gate_activation=act)
     g = tsg.PrefillGroupedRoutedMoE(moe)
-    tile = 128
+    tile = 256  # the routed GEMM's pass
     max_blocks = t * k // tile + ne
     sp, off, cnt = empty(t * k * 4, np.uint32), empty(ne, np.uint32), empty(ne, np.uint32)
     blocks, nb = empty(max_blocks * 4, np.uint32), empty(1, np.uint32)
@@ -493,7 +493,7 @@ def run_prefill_full(tsg, ctx, layer, offs, blobs, t, d, f, ne, s, act, seed):
 
 def test_gemma_prefill_t2048_full_size(tsg, ctx, gemma_layer):
     """configs[3] at its real size: T = 2048, top-8 Zipf(1.1) over 128 experts.
-    The head expert holds well over 1,000 rows, so it runs as many 128-row work
+    The head expert holds well over 1,000 rows, so it runs as many 256-row work
     items dealt across the XCDs; all of them are checked."""
     configure(ctx, 32, "sym")
     layer, offs, blobs = gemma_layer
@@ -514,7 +514,7 @@ def test_qwen_prefill_t4096_silu(tsg, ctx, qwen_layer):
     assert rel_p <= kc.NORTH_STAR and rel <= kc.NORTH_STAR
 
 
-def run_fused_vs_two_launches(tsg, ctx, layer, t, d, f, ne, s, act, seed, tile=128,
+def run_fused_vs_two_launches(tsg, ctx, layer, t, d, f, ne, s, act, seed, tile=256,
                               device_list=True):
     """tsg_prefill_moe_gate_up_down against tsg_prefill_moe_gate_up then
     tsg_prefill_moe_down on the same grouping: act and route partials equal
@@ -548,7 +548,8 @@ def run_fused_vs_two_launches(tsg, ctx, layer, t, d, f, ne, s, act, seed, tile=1
     return n_blocks
 
 
-@pytest.mark.parametrize("shape", ["gemma-t2048", "qwen-t4096", "gemma-t5", "gemma-t301-host"])
+@pytest.mark.parametrize("shape", ["gemma-t2048", "gemma-t2048-tile128", "qwen-t4096", "gemma-t5",
+                                   "gemma-t301-host"])
 def test_fused_gate_up_down_matches_two_launches(tsg, ctx, gemma_layer, qwen_layer, shape):
     """The fused persistent GEMM equals the two grouped GEMMs bit for bit at
     configs[3] and configs[4]'s prefill sizes, at a verify-sized chunk (fewer
@@ -558,6 +559,9 @@ def test_fused_gate_up_down_matches_two_launches(tsg, ctx, gemma_layer, qwen_lay
     if shape == "gemma-t2048":
         run_fused_vs_two_launches(tsg, ctx, gemma_layer[0], 2048, 2816, 704, 128, 1.1, "gelu",
                                   0xF05E)
+    elif shape == "gemma-t2048-tile128":  # blocks of at most 4 of the pass's 8 slices
+        run_fused_vs_two_launches(tsg, ctx, gemma_layer[0], 2048, 2816, 704, 128, 1.1, "gelu",
+                                  0xF05F, tile=128)
     elif shape == "qwen-t4096":
         run_fused_vs_two_launches(tsg, ctx, qwen_layer[0], 4096, 2048, 512, 256, 1.0, "silu",
                                   0xF06E)

@@ -18,7 +18,12 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libtsugumi_hip.so")
 FLOORS_LIB = os.path.join(HERE, "libtsugumi_floors.so")
+# the grouped GEMM's kernels build as one translation unit per (group size,
+# scheme), in parallel with the rest
+GEMM_SOURCES = ["gemm_g32_sym.hip", "gemm_g32_affine.hip", "gemm_g64_sym.hip",
+                "gemm_g64_affine.hip"]
 SOURCES = ["core.hip", "decode.hip", "qmv.hip", "shared.hip", "prefill.hip", "tail.hip",
+           *GEMM_SOURCES,
            "host_routing.cpp",
            "moepack.cpp"]
 FLOORS_SOURCES = ["floors.hip"]
@@ -37,10 +42,11 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
 # need there, ahead of any by-value struct, which is never preloaded); where
 # the firmware does not, each kernel's prologue loads them as usual.
 HIP_FLAGS = ["-mllvm", "-amdgpu-kernarg-preload-count=14"]
-# prefill.hip: its atomics are all single-lane; the atomic optimizer would turn
-# the fused GEMM's fetch of its next work item into a wave-wide form that
+# The grouped GEMM's atomics are all single-lane; the atomic optimizer would
+# turn the fused GEMM's fetch of its next work item into a wave-wide form that
 # waits for the result right after issue instead of where it is used.
-SOURCE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
+SOURCE_FLAGS = {src: ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]
+                for src in ["prefill.hip", *GEMM_SOURCES]}
 
 
 def _compile(src: str) -> str:
