@@ -355,8 +355,8 @@ def run_prefill_shape(tsg, torch, ctx, args, layer, t, h, f, e, zipf_s, act, lay
     # the fused persistent launch (tsg_prefill_moe_gate_up_down) gives the two
     # GEMMs' bits: checked here on the measured inputs
     want = partials.clone()
-    partials.fill_(0)
     with torch.cuda.stream(stream):
+        partials.fill_(0)  # on the launch's stream: ordered before the fused GEMM
         g.encode_gate_up_down(layer, hidden, h, sp, blocks, max_blocks, act_buf, partials, k, h, f,
                               n_blocks_device=nb, stream=stream)
     ctx.synchronize(stream)
@@ -1079,6 +1079,10 @@ def main():
                     help="time the decode layer's floors (empty launch, expert stream) and exit")
     ap.add_argument("--verify-only", action="store_true",
                     help="run only the verify M=5 figures (configs[2], for profiling) and exit")
+    ap.add_argument("--qwen-only", action="store_true",
+                    help="run only the Qwen-shaped figures (configs[4], for profiling) and exit")
+    ap.add_argument("--qmv-only", action="store_true",
+                    help="run only the single QMV figure (configs[0], for profiling) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -1090,6 +1094,12 @@ def main():
         print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
         sys.exit(1)
     ctx = tsg.Context(0, group_size=GROUP, scheme="sym")
+    if args.qwen_only:
+        print(json.dumps({"qwen35": run_qwen(tsg, torch, args)}), flush=True)
+        return
+    if args.qmv_only:
+        print(json.dumps({"qmv": run_qmv(tsg, torch, ctx)}), flush=True)
+        return
     log(f"building {LAYERS} resident layers ({LAYERS * E * gemma_offsets()[1] / 1e9:.2f} GB)")
     layers, bufs, routers, offs, stride = make_layers(tsg, ctx, torch, LAYERS)
     if args.traffic_probe:
