@@ -17,6 +17,8 @@ Workload (BASELINE.json configs[1] and [3]):
 Also reported, under "other_configs" (skipped with --no-extra-configs):
   qmv        configs[0]: one int4 QMV, K=2816, N=704 (sym group 32), as
              back-to-back launches in a HIP graph (launch-bound).
+  router_int8  the INT8-affine router (MoE.init's default router format) at
+             the Gemma router shape, back-to-back launches.
   verify_m5  configs[2]: Gemma speculative verify, M=5 tokens whose top-8
              sets overlap (union about 16), 30 layers, rows path + reduce.
   qwen35     configs[4]: Qwen3.5-MoE-35B-A3B-shaped layer (H=2048, 256
@@ -721,6 +723,45 @@ def run_qmv(tsg, torch, ctx):
             "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def run_router_int8(tsg, torch, ctx):
+    """encodeRouterGemma4 (the INT8-affine router, MoE.swift:201-257) at the
+    Gemma router shape: 128 experts x 2816 uint8 codes with bf16 scale and
+    bias per group of 32, one fp16 row, top-8. 256 calls per graph replay."""
+    ne, d, g = E, H, GROUP
+    w = torch.empty(ne * d, dtype=torch.uint8, device="cuda")
+    tsg.generators.bytes(w, 0x18A1)
+    sc = torch.empty(ne * (d // g), dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(sc, 0x18A2, 0.002, True, 1.0)
+    bi = torch.empty(ne * (d // g), dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(bi, 0x18A3, 0.1, False, 1.0)
+    x = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(x, 0x18A4, 1.0)
+    es = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(es, 0x18A5, 0.1, True, 1.0)
+    pes = torch.empty(ne, dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(pes, 0x18A6, 0.1, True, 1.0)
+    idx = torch.empty(8, dtype=torch.int32, device="cuda")
+    wts = torch.empty(8, dtype=torch.int16, device="cuda")
+    ctx.set_affine_group_size(g)
+    moe = tsg.MoE(ctx, router_weight_bits=8)
+    stream = torch.cuda.Stream()
+    calls = 256
+
+    def body():
+        for _ in range(calls):
+            moe.encode_router_gemma4(w, sc, bi, x, es, pes, idx, wts, ne, d, stream=stream)
+
+    us = time_graph(torch, stream, body, reps=8) * 1000.0 / calls
+    nbytes = ne * d + 2 * ne * (d // g) * 2 + 2 * d * 2 + ne * 2 + 8 * 4 + 8 * 2
+    ids = idx.cpu().numpy()
+    if len(set(ids.tolist())) != 8 or ids.min() < 0 or ids.max() >= ne:
+        raise RuntimeError(f"router_int8 selected {ids}")
+    log(f"router int8 {ne}x{d} g{g}: {us:.3f} us/call ({nbytes / (us * 1e-6) / 1e9:.1f} GB/s)")
+    return {"workload": f"INT8-affine router, {ne} experts x {d}, group {g}, top-8, "
+                        "back-to-back launches", "us_per_call": round(us, 3),
+            "bytes_per_call": nbytes, "GBps": round(nbytes / (us * 1e-6) / 1e9, 2)}
+
+
 def run_tail(tsg, torch, ctx):
     """Layer tail after the prefill MoE, T=2048, top-8, D=2816: the token-major
     reduce then PrefillLayerTail (two launches), and the reduce-fused tail (one
@@ -1083,6 +1124,8 @@ def main():
                     help="run only the Qwen-shaped figures (configs[4], for profiling) and exit")
     ap.add_argument("--qmv-only", action="store_true",
                     help="run only the single QMV figure (configs[0], for profiling) and exit")
+    ap.add_argument("--router-int8-only", action="store_true",
+                    help="run only the INT8-affine router figure (for profiling) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -1096,6 +1139,9 @@ def main():
     ctx = tsg.Context(0, group_size=GROUP, scheme="sym")
     if args.qwen_only:
         print(json.dumps({"qwen35": run_qwen(tsg, torch, args)}), flush=True)
+        return
+    if args.router_int8_only:
+        print(json.dumps({"router_int8": run_router_int8(tsg, torch, ctx)}), flush=True)
         return
     if args.qmv_only:
         print(json.dumps({"qmv": run_qmv(tsg, torch, ctx)}), flush=True)
@@ -1173,6 +1219,7 @@ def main():
         # is reported in its entry and does not void the headline)
         extra = {}
         for name, fn in (("qmv", lambda: run_qmv(tsg, torch, ctx)),
+                         ("router_int8", lambda: run_router_int8(tsg, torch, ctx)),
                          ("layer_tail", lambda: run_tail(tsg, torch, ctx)),
                          ("dense_qmm", lambda: run_dense_qmm(tsg, torch, ctx)),
                          ("verify_m5", lambda: run_verify(tsg, torch, ctx, args, layers, routers)),

@@ -173,7 +173,10 @@ void tsg_layer_destroy(tsg_layer* layer);
  * MoE (Kernels/MoE/MoE.swift:42-662). */
 
 /* MoE.init(context:routerWeightBits:gateActivation:) (MoE.swift:123-199).
- * router_weight_bits: 16 (bf16, the QAT checkpoints' router). */
+ * router_weight_bits: 8 (INT8-affine router, tsg_moe_router_int8) or 16 (bf16,
+ * the QAT checkpoints' router: every other router entry point and the
+ * one-launch layers). An entry point of the other format returns
+ * TSG_ERR_INVALID_ARGUMENT (the reference's precondition). */
 tsg_status tsg_moe_create(tsg_ctx* ctx, uint32_t router_weight_bits,
                           tsg_activation gate_activation, tsg_moe** out);
 void tsg_moe_destroy(tsg_moe* moe);
@@ -183,6 +186,20 @@ void tsg_moe_destroy(tsg_moe* moe);
  * softmax over the k, times per_expert_scale -> fp16 weights. One launch;
  * indices and weights stay on the device. top_k == 8, num_experts <= 256. */
 tsg_status tsg_moe_router_bf16(tsg_moe* moe, tsg_stream stream, const uint16_t* weights,
+                               const uint16_t* hidden, const uint16_t* effective_scale,
+                               const uint16_t* per_expert_scale, uint32_t* out_indices,
+                               uint16_t* out_weights, uint32_t num_experts, uint32_t d,
+                               uint32_t top_k);
+/* encodeRouterGemma4 (MoE.swift:201-257; kernel moe.metal:136-183): the
+ * INT8-affine router. Row e of `weights` is d uint8 codes, with bf16 scales and
+ * biases per group of the context's group size (Quantization.quantizeInt8Affine,
+ * Quantization.swift:243-287): logit_e = sum_i (q * scale + bias) * (hidden[i] *
+ * effective_scale[i]) in fp32, then the same top-k, softmax and gain as
+ * tsg_moe_router_bf16. d a multiple of 64 and of the group size, d <= 4096;
+ * top_k == 8, num_experts <= 256; weights, hidden and effective_scale on 16
+ * bytes. Requires a MoE created with router_weight_bits 8. */
+tsg_status tsg_moe_router_int8(tsg_moe* moe, tsg_stream stream, const uint8_t* weights,
+                               const uint16_t* scales, const uint16_t* biases,
                                const uint16_t* hidden, const uint16_t* effective_scale,
                                const uint16_t* per_expert_scale, uint32_t* out_indices,
                                uint16_t* out_weights, uint32_t num_experts, uint32_t d,

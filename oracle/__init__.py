@@ -139,6 +139,12 @@ def _declare(L):
     L.tsgo_router_logits_canonical.argtypes = [_u16p, _u16p, C.c_int, _u16p, C.c_int, C.c_int,
                                                C.c_int, _f32p]
     L.tsgo_topk_softmax.argtypes = [_f32p, C.c_int, C.c_int, _f32p, _i32p, _u16p]
+    L.tsgo_quantize_int8_affine.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, _u8p, _u16p,
+                                            _u16p]
+    L.tsgo_dequantize_int8_affine.argtypes = [_u8p, _u16p, _u16p, C.c_int, C.c_int, C.c_int,
+                                              _f32p]
+    L.tsgo_router_logits_int8_canonical.argtypes = [_u8p, _u16p, _u16p, _u16p, _u16p, C.c_int,
+                                                    C.c_int, C.c_int, _f32p]
     L.tsgo_make_token_expert_pairs.argtypes = [_u32p, _u16p, C.c_int, C.c_int, C.c_void_p]
     L.tsgo_group_pairs.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                    _u64p, C.c_int, C.c_int, C.c_void_p, _u32p, _u32p,
@@ -401,6 +407,7 @@ def router_reference(w_rows, x, top_k, per_expert_scale):
     x = np.ascontiguousarray(x, np.float32)
     pes = np.ascontiguousarray(per_expert_scale, np.float32)
     ne, d = w_rows.shape
+    assert ne >= top_k, "routerReference ranks at least top_k experts"
     idx = np.empty(top_k, np.int32)
     w = np.empty(top_k, np.float32)
     lib().tsgo_router_reference(_p(w_rows, C.c_float), _p(x, C.c_float), ne, d, top_k,
@@ -417,6 +424,50 @@ def router_logits_canonical(w_bf16, hidden_f16, stride, es_bf16, rows, num_exper
     lib().tsgo_router_logits_canonical(_p(w, C.c_uint16), _p(h, C.c_uint16), stride,
                                        _p(es, C.c_uint16), rows, num_experts, d,
                                        _p(out, C.c_float))
+    return out
+
+
+def quantize_int8_affine(w: np.ndarray, group: int):
+    """Quantization.quantizeInt8Affine (Quantization.swift:243-287) per row of
+    `w` [rows, n]: (packed uint8 [rows, n], scale bits, bias bits [rows, n/group])."""
+    w = np.ascontiguousarray(np.atleast_2d(w), np.float32)
+    rows, n = w.shape
+    assert n % group == 0
+    packed = np.empty((rows, n), np.uint8)
+    scales = np.empty((rows, n // group), np.uint16)
+    biases = np.empty((rows, n // group), np.uint16)
+    lib().tsgo_quantize_int8_affine(_p(w, C.c_float), rows, n, group, _p(packed, C.c_uint8),
+                                    _p(scales, C.c_uint16), _p(biases, C.c_uint16))
+    return packed, scales, biases
+
+
+def dequantize_int8_affine(packed, scales, biases, group: int) -> np.ndarray:
+    """Quantization.dequantizeInt8Affine (Quantization.swift:289-303)."""
+    packed = np.ascontiguousarray(np.atleast_2d(packed), np.uint8)
+    rows, n = packed.shape
+    s = np.ascontiguousarray(scales, np.uint16).reshape(rows, n // group)
+    b = np.ascontiguousarray(biases, np.uint16).reshape(rows, n // group)
+    out = np.empty((rows, n), np.float32)
+    lib().tsgo_dequantize_int8_affine(_p(packed, C.c_uint8), _p(s, C.c_uint16),
+                                      _p(b, C.c_uint16), rows, n, group, _p(out, C.c_float))
+    return out
+
+
+def router_logits_int8_canonical(packed, scales, biases, hidden_f16, es_bf16, num_experts, d,
+                                 group):
+    """INT8-affine router logits in the MI355X kernel's summation order (see
+    tsg_oracle.h)."""
+    w = np.ascontiguousarray(packed, np.uint8).ravel()
+    s = np.ascontiguousarray(scales, np.uint16).ravel()
+    b = np.ascontiguousarray(biases, np.uint16).ravel()
+    h = np.ascontiguousarray(hidden_f16, np.uint16).ravel()
+    es = np.ascontiguousarray(es_bf16, np.uint16).ravel()
+    assert w.size == num_experts * d and s.size == num_experts * (d // group)
+    out = np.empty(num_experts, np.float32)
+    lib().tsgo_router_logits_int8_canonical(_p(w, C.c_uint8), _p(s, C.c_uint16),
+                                            _p(b, C.c_uint16), _p(h, C.c_uint16),
+                                            _p(es, C.c_uint16), num_experts, d, group,
+                                            _p(out, C.c_float))
     return out
 
 

@@ -556,6 +556,94 @@ void tsgo_router_logits_canonical(const uint16_t* w_bf16, const uint16_t* hidden
     }
 }
 
+/* ------------------------------------------------------------------------ */
+/* INT8 affine — Quantization.swift:243-303 (Infrastructure/ModelIO)         */
+/* ------------------------------------------------------------------------ */
+
+void tsgo_quantize_int8_affine(const float* w, int rows, int n, int group, uint8_t* packed,
+                               uint16_t* scales, uint16_t* biases) {
+    const int n_groups = n / group;
+    for (int r = 0; r < rows; ++r) {
+        const float* row = w + (size_t)r * n;
+        for (int g = 0; g < n_groups; ++g) {
+            float wmin = INFINITY, wmax = -INFINITY;
+            for (int k = 0; k < group; ++k) {
+                const float v = row[g * group + k];
+                if (v < wmin) wmin = v;
+                if (v > wmax) wmax = v;
+            }
+            const float scale_f = wmax == wmin ? 1.0f : (wmax - wmin) / 255.0f;
+            const uint16_t s_bits = tsgo_bf16_bits(scale_f);
+            const uint16_t b_bits = tsgo_bf16_bits(wmin);
+            scales[(size_t)r * n_groups + g] = s_bits;
+            biases[(size_t)r * n_groups + g] = b_bits;
+            const float scale = tsgo_bf16_to_float(s_bits);
+            const float bias = tsgo_bf16_to_float(b_bits);
+            const float inv_scale = scale == 0.0f ? 0.0f : 1.0f / scale;
+            for (int k = 0; k < group; ++k) {
+                const float centred = row[g * group + k] - bias;
+                int q = swift_round_to_int(centred * inv_scale);
+                q = q < 0 ? 0 : (q > 255 ? 255 : q);
+                packed[(size_t)r * n + g * group + k] = (uint8_t)q;
+            }
+        }
+    }
+}
+
+void tsgo_dequantize_int8_affine(const uint8_t* packed, const uint16_t* scales,
+                                 const uint16_t* biases, int rows, int n, int group, float* out) {
+    const int n_groups = n / group;
+    for (int r = 0; r < rows; ++r)
+        for (int g = 0; g < n_groups; ++g) {
+            const float scale = tsgo_bf16_to_float(scales[(size_t)r * n_groups + g]);
+            const float bias = tsgo_bf16_to_float(biases[(size_t)r * n_groups + g]);
+            for (int k = 0; k < group; ++k) {
+                const size_t i = (size_t)r * n + g * group + k;
+                const float prod = (float)packed[i] * scale;
+                out[i] = prod + bias;
+            }
+        }
+}
+
+void tsgo_router_logits_int8_canonical(const uint8_t* w, const uint16_t* scales,
+                                       const uint16_t* biases, const uint16_t* hidden_f16,
+                                       const uint16_t* es_bf16, int num_experts, int d,
+                                       int group, float* out_logits) {
+    const int nunits = d / 16, n_groups = d / group;
+    for (int e = 0; e < num_experts; ++e) {
+        const uint8_t* wr = w + (size_t)e * d;
+        float p[64];
+        for (int l = 0; l < 64; ++l) {
+            float acc = 0.0f;
+            for (int u = l; u < nunits; u += 64) {
+                float qx = 0.0f, sx = 0.0f;
+                for (int k = 0; k < 16; ++k) {
+                    const int i = u * 16 + k;
+                    const float x = tsgo_f16_to_float(hidden_f16[i]) * tsgo_bf16_to_float(es_bf16[i]);
+                    qx = fmaf((float)wr[i], x, qx);
+                    sx = sx + x;
+                }
+                const int g = u * 16 / group;
+                acc = fmaf(tsgo_bf16_to_float(scales[(size_t)e * n_groups + g]), qx, acc);
+                acc = fmaf(tsgo_bf16_to_float(biases[(size_t)e * n_groups + g]), sx, acc);
+            }
+            p[l] = acc;
+        }
+        /* the 64 partials as in tsgo_router_logits_canonical */
+        float r[4];
+        for (int k = 0; k < 4; ++k) {
+            float* q = p + 16 * k;
+            float t[16];
+            for (int l = 0; l < 16; ++l) t[l] = q[l] + q[l ^ 1];
+            for (int l = 0; l < 16; ++l) q[l] = t[l] + t[l ^ 2];
+            for (int l = 0; l < 16; ++l) t[l] = q[l] + q[(l & 8) | (7 - (l & 7))];
+            for (int l = 0; l < 16; ++l) q[l] = t[l] + t[15 - l];
+            r[k] = q[0];
+        }
+        out_logits[e] = (r[0] + r[1]) + (r[2] + r[3]);
+    }
+}
+
 void tsgo_topk_softmax(const float* logits, int num_experts, int top_k,
                        const float* per_expert_scale, int32_t* out_idx, uint16_t* out_w) {
     int top_idx[64];

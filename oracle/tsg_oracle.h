@@ -20,6 +20,9 @@
  *   GELU ............ known points from the reference's MoEReferenceTests
  *   router .......... brute-force top-k over fp64 logits on tie-free draws,
  *                     explicit tie cases (lower index wins)
+ *   INT8 affine ..... exact ramps (q = k), half-step ties rounding away from
+ *                     zero, constant groups, round-trip bounds; its router
+ *                     logits against fp64 on the dequantised rows
  *   grouping/planner  the literal golden arrays of the reference's tests
  *   prefill ref ..... fp64 brute force (before the fp16 roundings) within
  *                     fp16 error bounds; reduce: closed form
@@ -101,6 +104,30 @@ void tsgo_moe_apply_streamed_routed(const uint8_t* const* blobs, const uint32_t*
                                     const float* x, const float* residual,
                                     const float* routing_weights, int top_k,
                                     int d, int f, int group, int symmetric, int act, float* y);
+
+/* ---- INT8 affine (Quantization.swift:243-303) ---- */
+/* quantizeInt8Affine: per group of `group` along each row, scale =
+ * bf16((wmax - wmin) / 255) (1 when wmax == wmin), bias = bf16(wmin),
+ * q = clamp(round_half_away((w - bias) * (1 / scale)), 0, 255) with the bf16
+ * scale and bias as floats. packed [rows * n], scales/biases [rows * n/group]. */
+void tsgo_quantize_int8_affine(const float* w, int rows, int n, int group, uint8_t* packed,
+                               uint16_t* scales, uint16_t* biases);
+/* dequantizeInt8Affine: float(q) * scale + bias, two roundings. */
+void tsgo_dequantize_int8_affine(const uint8_t* packed, const uint16_t* scales,
+                                 const uint16_t* biases, int rows, int n, int group, float* out);
+/* INT8-affine router logits (moe.metal:136-183 semantics) in the MI355X
+ * kernel's summation order (restated from tsugumi_amd/csrc/decode.hip
+ * router_int8_kernel): for each expert, 64 partial sums p_l over the
+ * 16-element units u = l, l+64, ...; per unit, in element order,
+ * qx = fma(q, x, qx) and sx = sx + x (x = hidden * es in fp32), then
+ * acc = fma(scale, qx, acc), acc = fma(bias, sx, acc); the 64 partials reduce
+ * as tsgo_router_logits_canonical's. Parity pinned by exact-arithmetic inputs
+ * and the fp32 error bound against fp64 on random inputs
+ * (tests/test_oracle_router_int8.py). */
+void tsgo_router_logits_int8_canonical(const uint8_t* w, const uint16_t* scales,
+                                       const uint16_t* biases, const uint16_t* hidden_f16,
+                                       const uint16_t* es_bf16, int num_experts, int d,
+                                       int group, float* out_logits);
 
 /* ---- router (TsugumiKernelCheck/main.swift:384-402) ---- */
 void tsgo_router_reference(const float* w, const float* x, int num_experts, int d,

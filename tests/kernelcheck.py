@@ -104,6 +104,65 @@ def router_case(d, ne, group, seed, draw):
                 wts=wts)
 
 
+def router_int8_case(d, ne, group, seed, draw):
+    """checkRouter(weightBits: 8) fixture (main.swift:409-520): uniform rows
+    quantised by quantizeInt8Affine at the context's group size; the expected
+    top-8 is routerReference over the dequantised rows."""
+    label = f"router-int8 d={d} experts={ne}"
+    rng = oracle.seed_tree_key(seed + draw, f"{label}-g{group}")
+    raw = rng.uniforms(-0.2, 0.2, ne * d).reshape(ne, d)
+    packed, scales, biases = oracle.quantize_int8_affine(raw, group)
+    wf = oracle.dequantize_int8_affine(packed, scales, biases, group)
+    hidden = rng.uniforms_f16(-1.0, 1.0, d)
+    es_bits = oracle.bf16_bits(rng.uniforms(0.5, 1.5, d))
+    pes_bits = oracle.bf16_bits(rng.uniforms(0.8, 1.2, ne))
+    x = oracle.f16_to_float(hidden) * oracle.bf16_to_float(es_bits)
+    # routerReference ranks at least top-k experts
+    idx, wts = oracle.router_reference(wf, x, 8, oracle.bf16_to_float(pes_bits)) \
+        if ne >= 8 else (None, None)
+    return dict(packed=packed, scales=scales, biases=biases, hidden=hidden, es_bits=es_bits,
+                pes_bits=pes_bits, idx=idx, wts=wts)
+
+
+def router_topk_test_case(kind):
+    """The two cases of RouterTopKTests (Tests/Tsugumi/Core/Kernels/MoE/
+    RouterTopKTests.swift:17-69): 16 experts, d = 128, INT8 rows at group 64.
+    "spread": rows offset by 0.01 per expert (seed 0xA5B61234); "near_tie":
+    one pattern scaled per expert, experts 7 and 8 at gains 0.5 and
+    0.5 * (1 + 1e-4) (seed 0x71E0F4A). The expected result is the test's own:
+    hidden and scales unrounded, top-8 of the dequantised rows' logits."""
+    ne, d = 16, 128
+    if kind == "spread":
+        rng = oracle.SplitMix64(0xA5B61234)
+        w = np.empty((ne, d), np.float32)
+        for e in range(ne):
+            w[e] = rng.uniforms(-0.05, 0.05, d) + np.float32(e) * np.float32(0.01)
+        hidden = rng.uniforms(-1.0, 1.0, d)
+        inv_sqrt_d = np.float32(1.0) / np.sqrt(np.float32(d))
+        es = rng.uniforms(0.5, 1.5, d) * inv_sqrt_d
+        pes = rng.uniforms(0.6, 1.4, ne)
+    else:
+        rng = oracle.SplitMix64(0x71E0F4A)
+        pattern = rng.uniforms(0.2, 1.0, d)
+        hidden = rng.uniforms(0.5, 1.5, d)
+        gains = np.zeros(ne, np.float32)
+        for e in range(7):
+            gains[e] = np.float32(1.0) - np.float32(e) * np.float32(0.05)
+        gains[7] = np.float32(0.5)
+        gains[8] = np.float32(0.5) * (np.float32(1.0) + np.float32(1e-4))
+        for e in range(9, ne):
+            gains[e] = np.float32(0.4) - np.float32(e - 9) * np.float32(0.02)
+        w = (gains[:, None] * pattern[None, :]).astype(np.float32)
+        es = np.ones(d, np.float32)
+        pes = np.ones(ne, np.float32)
+    packed, scales, biases = oracle.quantize_int8_affine(w, 64)
+    wf = oracle.dequantize_int8_affine(packed, scales, biases, 64)
+    idx, wts = oracle.router_reference(wf, (hidden * es).astype(np.float32), 8, pes)
+    return dict(ne=ne, d=d, packed=packed, scales=scales, biases=biases,
+                hidden=oracle.f16_bits(hidden), es_bits=oracle.bf16_bits(es),
+                pes_bits=oracle.bf16_bits(pes), idx=idx, wts=wts)
+
+
 def prefill_router_case(t, d, ne, kind, group, seed):
     """checkPrefillRouterBF16 fixture (main.swift:525-548); stride d + 16."""
     stride = d + 16

@@ -1,0 +1,113 @@
+"""GPU parity: the INT8-affine router (tsg_moe_router_int8, encodeRouterGemma4,
+MoE.swift:201-257) on the reference's KernelCheck fixture (checkRouter(weightBits:
+8), main.swift:409-520, seed 0xD1) and its RouterTopKTests cases, against the
+oracle's routerReference and its restatement of the kernel's summation order."""
+import numpy as np
+import pytest
+
+import oracle
+from tests import kernelcheck as kc
+from tests.gpu_util import dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tsg():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import tsugumi_amd
+    return tsugumi_amd
+
+
+@pytest.fixture(scope="module")
+def ctx(tsg):
+    return tsg.Context(0)
+
+
+def run_int8_router(moe, c, ne, d):
+    idx, wts = empty(8, np.uint32), empty(8)
+    moe.encode_router_gemma4(dev(c["packed"]), dev(c["scales"]), dev(c["biases"]),
+                             dev(c["hidden"]), dev(c["es_bits"]), dev(c["pes_bits"]), idx, wts,
+                             ne, d)
+    return host(idx, np.uint32), host(wts, np.uint16)
+
+
+def kernel_order_selection(c, ne, d, group):
+    logits = oracle.router_logits_int8_canonical(c["packed"], c["scales"], c["biases"],
+                                                 c["hidden"], c["es_bits"], ne, d, group)
+    return oracle.topk_softmax(logits, 8, oracle.bf16_to_float(c["pes_bits"]))
+
+
+@pytest.mark.parametrize("group", [64, 32])
+def test_router_int8_kernelcheck(tsg, ctx, group):
+    """checkRouter(weightBits: 8, d: 2816, experts: 128, draws: 4, seed: 0xD1):
+    indices equal routerReference's over the dequantised rows, weights within
+    Tolerance.fp16Reduction; indices equal, and weights within one fp16 ulp of,
+    the kernel rule applied to the oracle's kernel-order logits."""
+    ctx.set_affine_group_size(group)
+    d, ne = 2816, 128
+    moe = tsg.MoE(ctx, router_weight_bits=8)
+    for draw in range(4):
+        c = kc.router_int8_case(d, ne, group, 0xD1, draw)
+        gi, gw = run_int8_router(moe, c, ne, d)
+        assert list(gi) == list(c["idx"]), f"g{group} draw {draw}: gpu={gi} cpu={c['idx']}"
+        assert oracle.relative_error(oracle.f16_to_float(gw), c["wts"]) <= kc.FP16_REDUCTION
+        ci, cw = kernel_order_selection(c, ne, d, group)
+        assert list(gi) == list(ci)
+        assert np.max(np.abs(gw.astype(np.int32) - cw.astype(np.int32))) <= 1
+
+
+@pytest.mark.parametrize("kind", ["spread", "near_tie"])
+def test_router_int8_reference_router_tests(tsg, ctx, kind):
+    """RouterTopKTests.productionRouterMatchesReference and
+    productionRouterResolvesNearTieLikeReference (RouterTopKTests.swift:17-69):
+    16 experts, d = 128, group 64; same indices, weights within 5e-3."""
+    ctx.set_affine_group_size(64)
+    c = kc.router_topk_test_case(kind)
+    moe = tsg.MoE(ctx, router_weight_bits=8)
+    gi, gw = run_int8_router(moe, c, c["ne"], c["d"])
+    assert list(gi) == list(c["idx"]), f"{kind}: gpu={gi} cpu={c['idx']}"
+    assert np.abs(oracle.f16_to_float(gw) - c["wts"]).max() < 5e-3
+    ci, _ = kernel_order_selection(c, c["ne"], c["d"], 64)
+    assert list(gi) == list(ci)
+
+
+def test_router_int8_small_and_ragged_expert_counts(tsg, ctx):
+    """Expert counts that leave waves of the last block without a row, and
+    fewer experts than top-8 (the unfilled slots keep expert 0, weight 0)."""
+    ctx.set_affine_group_size(32)
+    d = 2048
+    moe = tsg.MoE(ctx, router_weight_bits=8)
+    for ne in (5, 37, 256):
+        c = kc.router_int8_case(d, ne, 32, 0xD1, 7)
+        gi, gw = run_int8_router(moe, c, ne, d)
+        ci, cw = kernel_order_selection(c, ne, d, 32)
+        assert list(gi) == list(ci), f"ne={ne}: gpu={gi} oracle={ci}"
+        assert np.max(np.abs(gw.astype(np.int32) - cw.astype(np.int32))) <= 1
+
+
+def test_router_formats_are_checked(tsg, ctx):
+    """Each router entry point takes only its own weight format (the
+    reference's preconditions, MoE.swift:213-214, 269-270), and the INT8
+    router's row geometry (d a multiple of 64 and of the group size)."""
+    ctx.set_affine_group_size(64)
+    d, ne = 2816, 128
+    c = kc.router_int8_case(d, ne, 64, 0xD1, 0)
+    m8 = tsg.MoE(ctx, router_weight_bits=8)
+    m16 = tsg.MoE(ctx, router_weight_bits=16)
+    idx, wts = empty(8, np.uint32), empty(8)
+    with pytest.raises(tsg.TsgError) as e:
+        run_int8_router(m16, c, ne, d)
+    assert e.value.status == tsg._abi.TSG_ERR_INVALID_ARGUMENT
+    w16 = dev(np.zeros(ne * d, np.uint16))
+    with pytest.raises(tsg.TsgError) as e:
+        m8.encode_router_gemma4_bf16(w16, dev(c["hidden"]), dev(c["es_bits"]),
+                                     dev(c["pes_bits"]), idx, wts, ne, d)
+    assert e.value.status == tsg._abi.TSG_ERR_INVALID_ARGUMENT
+    with pytest.raises(tsg.TsgError) as e:
+        run_int8_router(m8, c, ne, d - 32)
+    assert e.value.status == tsg._abi.TSG_ERR_INVALID_ARGUMENT
+    with pytest.raises(tsg.TsgError):
+        tsg.MoE(ctx, router_weight_bits=4)

@@ -324,7 +324,9 @@ class MoEPack:
 
 class MoE:
     """MoE (MoE.swift:42-662): router + top-8, phase 1 gate/up + activation,
-    phase 2 down + weighted combine."""
+    phase 2 down + weighted combine. `router_weight_bits` 16 (bf16 router, the
+    QAT checkpoints') is this façade's default; the reference's MoE.init
+    defaults to 8 (INT8-affine router, encode_router_gemma4)."""
 
     def __init__(self, ctx: Context, router_weight_bits: int = 16,
                  gate_activation: str = "gelu"):
@@ -339,6 +341,16 @@ class MoE:
         """One-launch decode layer when it fits (default) or the three-launch
         sequence; both give identical bits."""
         check(self.lib.tsg_moe_set_fused_decode(self.handle, int(enabled)))
+
+    def encode_router_gemma4(self, weights, scales, biases, hidden, effective_scale,
+                             per_expert_scale, out_indices, out_weights, num_experts, d,
+                             top_k=8, stream=None):
+        """encodeRouterGemma4 (MoE.swift:201-257): the INT8-affine router
+        (router_weight_bits=8)."""
+        check(self.lib.tsg_moe_router_int8(
+            self.handle, _stream(stream), _ptr(weights), _ptr(scales), _ptr(biases),
+            _ptr(hidden), _ptr(effective_scale), _ptr(per_expert_scale), _ptr(out_indices),
+            _ptr(out_weights), num_experts, d, top_k))
 
     def encode_router_gemma4_bf16(self, weights, hidden, effective_scale, per_expert_scale,
                                   out_indices, out_weights, num_experts, d, top_k=8,

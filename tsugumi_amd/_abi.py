@@ -109,6 +109,7 @@ SIGNATURES = {
     "tsg_moe_create": (C.c_int, [P, U32, C.c_int, C.POINTER(P)]),
     "tsg_moe_destroy": (None, [P]),
     "tsg_moe_router_bf16": (C.c_int, [P, P, P, P, P, P, P, P, U32, U32, U32]),
+    "tsg_moe_router_int8": (C.c_int, [P, P, P, P, P, P, P, P, P, P, U32, U32, U32]),
     "tsg_moe_router_bf16_rows": (C.c_int, [P, P, P, P, U32, P, P, P, P, U32, U32, U32, U32]),
     "tsg_moe_router_bf16_rows_grouped": (C.c_int, [P, P, P, P, U32, P, P, P, P, U32, U32, U32,
                                                    U32, P, P, P, P, U32, P]),

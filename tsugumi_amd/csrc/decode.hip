@@ -1053,6 +1053,105 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
     }
 }
 
+// INT8-affine router (encodeRouterGemma4, MoE.swift:201-257; arithmetic of
+// moe.metal:136-183): logit_e = sum_i (q_i * scale_g + bias_g) * x_i with
+// x_i = hidden_i * es_i in fp32, as sum_g scale_g * (q . x)_g + bias_g *
+// (sum x)_g. Block b holds experts 4b .. 4b + 3, one per wave. Lane l takes the
+// 16-byte units u = l, l + 64, ... of its row (16 weights, each unit inside one
+// group of G >= 16) with every load in flight before the arithmetic (units
+// past the row end read the last unit again and add +0); per unit,
+// in element order, qx = fma(q, x, qx) and sx = sx + x, then acc = fma(scale,
+// qx, acc), acc = fma(bias, sx, acc). The lane sums reduce as the BF16
+// router's (group16_sum, then (r0 + r1) + (r2 + r3)). The last block to
+// finish selects on one wave (wave_topk_softmax), as the one-row BF16 router.
+constexpr int kInt8Units = 4;  // 16-byte units per lane: d <= 4096
+
+// One 16-weight unit: qx = fma(q, x, qx) and sx = sx + x in element order
+// (x = hidden * es rounded to fp32 before both uses: nothing contracted), then
+// acc = fma(scale, qx, acc), acc = fma(bias, sx, acc).
+__device__ __forceinline__ float int8_unit_dot(const u32x4_t& wq, const u32x4_t (&xv)[2],
+                                               const u32x4_t (&ev)[2], float scale, float bias,
+                                               float acc) {
+#pragma clang fp contract(off)
+    const uint32_t qa[4] = {wq.x, wq.y, wq.z, wq.w};
+    const uint32_t xa[8] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w};
+    const uint32_t ea[8] = {ev[0].x, ev[0].y, ev[0].z, ev[0].w, ev[1].x, ev[1].y, ev[1].z, ev[1].w};
+    float qx = 0.0f, sx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t hw = xa[k >> 1], ew = ea[k >> 1];
+        const float h = f16_to_f32((uint16_t)((k & 1) ? hw >> 16 : hw & 0xFFFFu));
+        const float s = __uint_as_float((k & 1) ? ew & 0xFFFF0000u : ew << 16);
+        const float x = h * s;
+        const float q = (float)((qa[k >> 2] >> (8 * (k & 3))) & 0xFFu);
+        qx = __builtin_fmaf(q, x, qx);
+        sx = sx + x;
+    }
+    acc = __builtin_fmaf(scale, qx, acc);
+    return __builtin_fmaf(bias, sx, acc);
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void router_int8_kernel(
+    const uint8_t* __restrict__ w, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ hidden,
+    const uint16_t* __restrict__ es, const uint16_t* __restrict__ pes,
+    uint32_t* __restrict__ counters, uint32_t ne, uint32_t d, float* __restrict__ logits,
+    uint32_t* __restrict__ out_idx, uint16_t* __restrict__ out_w) {
+    static_assert(G % 16 == 0, "a unit lies inside one group");
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t e = blockIdx.x * kRouterWaves + wave;
+    const uint32_t nunits = d / 16u, ngroups = d / G;
+    uint32_t gains[4];
+    load_expert_gains(pes, ne, gains);
+    if (e < ne) {
+        const uint8_t* wr = w + (uint64_t)e * d;
+        u32x4_t wq[kInt8Units], xv[kInt8Units][2], ev[kInt8Units][2];
+        uint32_t sb[kInt8Units], bb[kInt8Units];
+#pragma unroll
+        for (int i = 0; i < kInt8Units; ++i) {
+            const uint32_t u = min(lane + 64u * i, nunits - 1u);
+            wq[i] = *reinterpret_cast<const u32x4_t*>(wr + u * 16u);
+            xv[i][0] = *reinterpret_cast<const u32x4_t*>(hidden + u * 16u);
+            xv[i][1] = *reinterpret_cast<const u32x4_t*>(hidden + u * 16u + 8u);
+            ev[i][0] = *reinterpret_cast<const u32x4_t*>(es + u * 16u);
+            ev[i][1] = *reinterpret_cast<const u32x4_t*>(es + u * 16u + 8u);
+            const uint32_t g = e * ngroups + u * 16u / G;
+            sb[i] = scales[g];
+            bb[i] = biases[g];
+        }
+        // every load is issued before the first use (the compiler would
+        // otherwise interleave the units' loads with the arithmetic)
+#pragma unroll
+        for (int i = 0; i < kInt8Units; ++i)
+            asm volatile("" : "+v"(wq[i]), "+v"(xv[i][0]), "+v"(xv[i][1]), "+v"(ev[i][0]),
+                         "+v"(ev[i][1]), "+v"(sb[i]), "+v"(bb[i]));
+        // units past the row end (a clamped copy of the last one) enter with
+        // scale and bias 0 and add +0: no branch, so no load waits behind one
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kInt8Units; ++i) {
+            const bool live = lane + 64u * i < nunits;
+            acc = int8_unit_dot(wq[i], xv[i], ev[i], live ? bf16_to_f32((uint16_t)sb[i]) : 0.0f,
+                                live ? bf16_to_f32((uint16_t)bb[i]) : 0.0f, acc);
+        }
+        acc = group16_sum(acc);
+        const float logit =
+            (lane_value(acc, 0) + lane_value(acc, 16)) + (lane_value(acc, 32) + lane_value(acc, 48));
+        if (lane == 0) st_coherent(reinterpret_cast<uint32_t*>(logits) + e, __float_as_uint(logit));
+    }
+    // logits travel by agent-coherent stores/loads; completing this block's
+    // stores before it counts itself is all the last block needs
+    __shared__ uint32_t is_last;
+    wait_vector_memory();
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = atomicAdd(&counters[0], 1u) == gridDim.x - 1u ? 1u : 0u;
+    __syncthreads();
+    if (!is_last) return;
+    if (wave == 0) wave_topk_softmax(logits, ne, gains, out_idx, out_w);
+    if (threadIdx.x == 0) atomicExch(&counters[0], 0u);
+}
+
 // One decode MoE layer in one launch (kDecodeBlocks blocks, all co-resident).
 // Per group g: router logits -> top-8 (every block) -> gate/up + activation of
 // slot g (pairs per block) -> down rows of slot g -> partials -> slot-ordered
@@ -1454,6 +1553,8 @@ tsg_status router_launch(tsg_moe* moe, hipStream_t stream, const uint16_t* w,
                 "router weights, hidden and effective_scale must be 16-byte aligned");
     TSG_REQUIRE(rows > 0 && rows <= kMaxPromptRows, TSG_ERR_INVALID_ARGUMENT,
                 "rows=%u not in 1..%u", rows, kMaxPromptRows);
+    TSG_REQUIRE(moe->router_weight_bits == 16, TSG_ERR_INVALID_ARGUMENT,
+                "BF16 router encode on a %u-bit router", moe->router_weight_bits);
     tsg_ctx* ctx = moe->ctx;
     const dim3 grid((ne + kRouterWaves - 1) / kRouterWaves, (rows + kRouterRows - 1) / kRouterRows);
     // a few rows of one y-block are staged in LDS (same sums, no per-row
@@ -1658,8 +1759,6 @@ extern "C" tsg_status tsg_moe_create(tsg_ctx* ctx, uint32_t bits, tsg_activation
     *out = nullptr;
     TSG_REQUIRE(bits == 8 || bits == 16, TSG_ERR_INVALID_ARGUMENT,
                 "Unsupported router weight bits: %u (expected 8 or 16)", bits);
-    TSG_REQUIRE(bits == 16, TSG_ERR_UNSUPPORTED,
-                "the INT8 affine router is not built; QAT checkpoints ship a BF16 router");
     TSG_REQUIRE(act == TSG_ACT_GELU_TANH || act == TSG_ACT_SILU, TSG_ERR_INVALID_ARGUMENT,
                 "unknown gate activation %d", (int)act);
     tsg_moe* m = new tsg_moe();
@@ -1730,6 +1829,42 @@ extern "C" tsg_status tsg_moe_router_logits_bf16(tsg_moe* moe, tsg_stream stream
     if (st) return st;
     return router_launch(moe, as_stream(stream), w, hidden, d, es, nullptr, nullptr, nullptr,
                          out_logits, 1, ne, d, kTopK, false);
+}
+
+// encodeRouterGemma4 (MoE.swift:201-257): the INT8-affine router on a MoE
+// created with 8-bit router weights, at the context's group size.
+extern "C" tsg_status tsg_moe_router_int8(tsg_moe* moe, tsg_stream stream, const uint8_t* w,
+                                          const uint16_t* scales, const uint16_t* biases,
+                                          const uint16_t* hidden, const uint16_t* es,
+                                          const uint16_t* pes, uint32_t* out_idx,
+                                          uint16_t* out_w, uint32_t ne, uint32_t d,
+                                          uint32_t top_k) {
+    tsg_status st = check_moe(moe);
+    if (st) return st;
+    TSG_REQUIRE(moe->router_weight_bits == 8, TSG_ERR_INVALID_ARGUMENT,
+                "INT8 router encode on a %u-bit router", moe->router_weight_bits);
+    const uint32_t g = moe->ctx->group_size;
+    TSG_REQUIRE(top_k == kTopK, TSG_ERR_INVALID_ARGUMENT, "topK must be %u, got %u", kTopK, top_k);
+    TSG_REQUIRE(ne > 0 && ne <= kMaxExperts, TSG_ERR_INVALID_ARGUMENT,
+                "numExperts %u not in 1..%u", ne, kMaxExperts);
+    // the reference walks a row in 64-element steps (MoE.swift:215-217)
+    TSG_REQUIRE(d > 0 && d % 64u == 0 && d % g == 0 && d <= 16u * 64u * kInt8Units,
+                TSG_ERR_INVALID_ARGUMENT,
+                "d=%u must be a positive multiple of 64 and of the group size %u, at most %u", d,
+                g, 16u * 64u * kInt8Units);
+    TSG_REQUIRE(w && scales && biases && hidden && es && pes && out_idx && out_w,
+                TSG_ERR_INVALID_ARGUMENT, "NULL router operand");
+    TSG_REQUIRE(aligned16(w) && aligned16(hidden) && aligned16(es), TSG_ERR_ALIGNMENT,
+                "router weights, hidden and effective_scale must be 16-byte aligned");
+    TSG_REQUIRE(((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases) |
+                  reinterpret_cast<uintptr_t>(pes)) & 1u) == 0,
+                TSG_ERR_ALIGNMENT, "scales, biases and per_expert_scale must be 2-byte aligned");
+    tsg_ctx* ctx = moe->ctx;
+    const dim3 grid((ne + kRouterWaves - 1) / kRouterWaves);
+    auto kern = g == 32 ? router_int8_kernel<32> : router_int8_kernel<64>;
+    hipLaunchKernelGGL(kern, grid, dim3(64u * kRouterWaves), 0, as_stream(stream), w, scales,
+                       biases, hidden, es, pes, ctx->counters, ne, d, ctx->logits, out_idx, out_w);
+    return check_launch("router_int8");
 }
 
 extern "C" tsg_status tsg_moe_phase1(tsg_moe* moe, tsg_stream stream,
@@ -1820,6 +1955,9 @@ tsg_status decode_layer_impl(tsg_moe* moe, tsg_stream stream, const tsg_layer* l
                              uint32_t f, uint32_t top_k, const SharedBranch* sh) {
     tsg_status st = check_moe(moe);
     if (st) return st;
+    TSG_REQUIRE(moe->router_weight_bits == 16, TSG_ERR_INVALID_ARGUMENT,
+                "the one-launch layer runs the BF16 router; this MoE has %u-bit router weights",
+                moe->router_weight_bits);
     if ((st = check_decode_shape(moe->ctx, d, f, top_k))) return st;
     TSG_REQUIRE(layer, TSG_ERR_INVALID_ARGUMENT, "layer is NULL");
     TSG_REQUIRE(ne > 0 && ne <= layer->num_experts && ne <= kMaxExperts, TSG_ERR_INVALID_ARGUMENT,

@@ -556,7 +556,6 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& args, const tsg_route
     // dead waves (a tile past the last weight row) load row 0's data, run
     // the same loop and store nothing
     if (!wave_live) row0[0] = row0[1] = 0u;
-    const uint32_t nrows = MODE == 0 ? args.f : args.d;
     {
         const uint32_t r = lane >> 1;
         const uint32_t swzb = ((r >> 2) ^ (r >> 3)) & 1u;
