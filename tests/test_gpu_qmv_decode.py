@@ -633,11 +633,13 @@ def test_decode_layer_shared_expert(tsg, ctx, d, f, ne, sf, group, scheme):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m,n", [(4096, 2816), (2048, 2816), (2816, 4096), (8192, 2816),
-                                 (1024, 2816), (2816, 8192)])
+@pytest.mark.parametrize("m,n", [(704, 2816), (4096, 2816), (2048, 2816), (2816, 4096),
+                                 (8192, 2816), (1024, 2816), (2816, 8192)])
 def test_qmv_projection_shapes(tsg, ctx, m, n):
-    """DequantInt4GEMV's decode projection shapes (DequantInt4GEMV.swift:13-20):
-    encode against DequantInt4GemvRef within the north star's 1e-3, and 8 rows
+    """DequantInt4GEMV's decode projection shapes (DequantInt4GEMV.swift:13-20)
+    and the single QMV of the benchmark's first configuration (W[704 x 2816],
+    symmetric group 32, scales |N(0, 0.02)| / 7, x ~ N(0, 1)): encode against
+    DequantInt4GemvRef within the north star's 1e-3, and 8 rows
     through encodeRows / encodeRowsWide (split into launches that fit the LDS
     at n = 8192) bit-equal to 8 single-row calls."""
     configure(ctx, 32, "sym")
