@@ -111,3 +111,50 @@ def test_router_formats_are_checked(tsg, ctx):
     assert e.value.status == tsg._abi.TSG_ERR_INVALID_ARGUMENT
     with pytest.raises(tsg.TsgError):
         tsg.MoE(ctx, router_weight_bits=4)
+
+
+def test_int8_router_decode_layer_gemma_shape(tsg, ctx):
+    """The decode layer of a MoE with the INT8-affine router (MoE.init's
+    default): encodeRouterGemma4, then phase 1 and phase 2 on the
+    HBM-resident Gemma-shaped layer with the expert ids read on the device
+    (RealForwardRunner's per-layer sequence, RealForwardRunner.swift:3104-3330).
+    Routing bit-exact against the oracle's kernel-order logits and top-k rule;
+    y within 1e-3 of MoeRef.applyStreamedRouted over the chosen experts."""
+    import torch
+    from tests.test_gpu_qmv_decode import make_gemma_layer
+    ctx.set_affine_group_size(32)
+    ctx.set_affine_scheme("sym")
+    d, f, ne = 2816, 704, 128
+    layer, buf, offs, stride = make_gemma_layer(tsg, ctx, 0x5EE8)
+    rng = np.random.default_rng(0x1D8)
+    raw = rng.normal(0.0, 1.0 / np.sqrt(d), (ne, d)).astype(np.float32)
+    packed, scales, biases = oracle.quantize_int8_affine(raw, 32)
+    x = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(x, 0xA18, 1.0)
+    es = np.full(d, 0x3F80, np.uint16)
+    pes = oracle.bf16_bits(rng.uniform(0.8, 1.2, ne).astype(np.float32))
+    moe = tsg.MoE(ctx, router_weight_bits=8)
+    idx, wts = empty(8, np.uint32), empty(8)
+    acts, y = empty(8 * f), empty(d)
+    moe.encode_router_gemma4(dev(packed), dev(scales), dev(biases), x, dev(es), dev(pes), idx,
+                             wts, ne, d)
+    moe.encode_phase1_resident(layer, idx, x, acts, d, f)
+    moe.encode_phase2_resident(layer, idx, acts, wts, x, y, d, f)
+    gi, gw = host(idx, np.uint32), host(wts, np.uint16)
+    xb = host(x, np.uint16)
+    logits = oracle.router_logits_int8_canonical(packed, scales, biases, xb, es, ne, d, 32)
+    ci, cw = oracle.topk_softmax(logits, 8, oracle.bf16_to_float(pes))
+    assert list(gi) == list(ci)
+    assert np.max(np.abs(gw.astype(np.int32) - cw.astype(np.int32))) <= 1
+    image = host(buf, np.uint8)
+    blobs = [np.ascontiguousarray(image[e * stride:(e + 1) * stride]) for e in gi]
+    xf = oracle.f16_to_float(xb)
+    ref = oracle.moe_apply_streamed_routed(blobs, np.array(offs, np.uint32), xf, xf,
+                                           oracle.f16_to_float(gw), d, f, 32, symmetric=True)
+    rel = oracle.relative_error(oracle.f16_to_float(host(y, np.uint16)), ref)
+    print(f"int8-router decode layer: experts={list(gi)} rel={rel:.3e}")
+    assert rel <= kc.NORTH_STAR
+    # the one-launch layer runs the BF16 router: refused for an 8-bit MoE
+    with pytest.raises(tsg.TsgError):
+        moe.encode_decode_layer(layer, dev(np.zeros(ne * d, np.uint16)), x, dev(es), dev(pes),
+                                x, x, y, idx, wts, acts, ne, d, f)
