@@ -356,9 +356,11 @@ def run_prefill_shape(tsg, torch, ctx, args, layer, t, h, f, e, zipf_s, act, lay
         raise RuntimeError(f"prefill T={t} produced non-finite outputs")
     # the fused persistent launch (tsg_prefill_moe_gate_up_down) gives the two
     # GEMMs' bits: checked here on the measured inputs
-    want = partials.clone()
+    # the copy, the clearing and the fused launch all on the launch's stream,
+    # in that order (torch's current stream is another one)
     with torch.cuda.stream(stream):
-        partials.fill_(0)  # on the launch's stream: ordered before the fused GEMM
+        want = partials.clone()
+        partials.fill_(0)
         g.encode_gate_up_down(layer, hidden, h, sp, blocks, max_blocks, act_buf, partials, k, h, f,
                               n_blocks_device=nb, stream=stream)
     ctx.synchronize(stream)
