@@ -19,6 +19,7 @@ Also reported, under "other_configs" (skipped with --no-extra-configs):
              back-to-back launches in a HIP graph (launch-bound).
   router_int8  the INT8-affine router (MoE.init's default router format) at
              the Gemma router shape, back-to-back launches.
+  decode_int8_router  the headline decode layer with that router, one launch.
   verify_m5  configs[2]: Gemma speculative verify, M=5 tokens whose top-8
              sets overlap (union about 16), 30 layers, rows path + reduce.
   qwen35     configs[4]: Qwen3.5-MoE-35B-A3B-shaped layer (H=2048, 256
@@ -764,6 +765,58 @@ def run_router_int8(tsg, torch, ctx):
             "bytes_per_call": nbytes, "GBps": round(nbytes / (us * 1e-6) / 1e9, 2)}
 
 
+def run_decode_int8(tsg, torch, ctx, layers):
+    """The headline decode layer with the INT8-affine router (MoE.init's
+    default router format, tsg_moe_decode_layer_int8) over the same 30
+    resident layers: 8 tokens x 30 layers per graph replay, a fresh N(0,1)
+    input per (token, layer). Algorithmic bytes per layer: the 8 experts, the
+    router's 128 x 2816 codes and its group-32 scales and biases, x / es /
+    residual / y rows and the gains."""
+    n_in, ng = 8, H // GROUP
+    rw = torch.empty(LAYERS * E * H, dtype=torch.uint8, device="cuda")
+    tsg.generators.bytes(rw, 0x8A1)
+    rs = torch.empty(LAYERS * E * ng, dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(rs, 0x8A2, 0.0002, True, 1.0)
+    rb = torch.empty(LAYERS * E * ng, dtype=torch.int16, device="cuda")
+    tsg.generators.bf16_normal(rb, 0x8A3, 0.02, False, 1.0)
+    ones_h = torch.full((H,), 0x3F80, dtype=torch.int16, device="cuda")
+    ones_e = torch.full((E,), 0x3F80, dtype=torch.int16, device="cuda")
+    inputs = torch.empty(n_in * LAYERS * H, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(inputs, 0x8A4, 1.0)
+    ys = torch.empty(LAYERS * H, dtype=torch.int16, device="cuda")
+    idx = torch.empty(LAYERS * TOPK, dtype=torch.int32, device="cuda")
+    wts = torch.empty(LAYERS * TOPK, dtype=torch.int16, device="cuda")
+    acts = torch.empty(TOPK * F, dtype=torch.int16, device="cuda")
+    ctx.set_affine_group_size(GROUP)
+    moe = tsg.MoE(ctx, router_weight_bits=8)
+    stream = torch.cuda.Stream()
+
+    def body():
+        for k in range(n_in):
+            for l in range(LAYERS):
+                x = inputs[(k * LAYERS + l) * H:(k * LAYERS + l + 1) * H]
+                moe.encode_decode_layer_int8(
+                    layers[l], rw[l * E * H:(l + 1) * E * H], rs[l * E * ng:(l + 1) * E * ng],
+                    rb[l * E * ng:(l + 1) * E * ng], x, ones_h, ones_e, x, x,
+                    ys[l * H:(l + 1) * H], idx[l * TOPK:(l + 1) * TOPK],
+                    wts[l * TOPK:(l + 1) * TOPK], acts, E, H, F, stream=stream)
+
+    us = time_graph(torch, stream, body, reps=4) * 1000.0 / (n_in * LAYERS)
+    ctx.synchronize()
+    ids = idx.view(LAYERS, TOPK).cpu().numpy()
+    if any(len(set(r.tolist())) != TOPK for r in ids) or ids.min() < 0 or ids.max() >= E:
+        raise RuntimeError("decode_int8: a layer's top-8 is not 8 distinct experts")
+    if not bool(torch.isfinite(ys.view(torch.float16).float()).all()):
+        raise RuntimeError("decode_int8 produced non-finite outputs")
+    nbytes = TOPK * shape_offsets(H, F)[2] + E * H + 2 * E * ng * 2 + 5 * H * 2 + E * 2
+    log(f"decode layer, INT8 router: {us:.3f} us/layer ({nbytes / (us * 1e-6) / 1e9:.1f} GB/s)")
+    return {"workload": "gemma4-26b-a4b decode MoE layer with the INT8-affine router (group 32), "
+                        "one launch, 30 resident layers",
+            "us_per_layer": round(us, 3), "bytes_per_layer": nbytes,
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 2),
+            "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def run_tail(tsg, torch, ctx):
     """Layer tail after the prefill MoE, T=2048, top-8, D=2816: the token-major
     reduce then PrefillLayerTail (two launches), and the reduce-fused tail (one
@@ -1222,6 +1275,7 @@ def main():
         extra = {}
         for name, fn in (("qmv", lambda: run_qmv(tsg, torch, ctx)),
                          ("router_int8", lambda: run_router_int8(tsg, torch, ctx)),
+                         ("decode_int8_router", lambda: run_decode_int8(tsg, torch, ctx, layers)),
                          ("layer_tail", lambda: run_tail(tsg, torch, ctx)),
                          ("dense_qmm", lambda: run_dense_qmm(tsg, torch, ctx)),
                          ("verify_m5", lambda: run_verify(tsg, torch, ctx, args, layers, routers)),

@@ -282,6 +282,24 @@ tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream, const tsg_layer
                                 uint16_t* out_weights, uint16_t* acts_scratch,
                                 uint32_t num_experts, uint32_t d, uint32_t f, uint32_t top_k);
 
+/* tsg_moe_decode_layer with the INT8-affine router (a MoE created with
+ * router_weight_bits 8; encodeRouterGemma4, MoE.swift:201-257, then the two
+ * phases, as RealForwardRunner.swift:3104-3330 encodes them per layer): the
+ * router's arithmetic is tsg_moe_router_int8's (same logits, same selection),
+ * in the one launch or, when that does not fit, as tsg_moe_router_int8 +
+ * phase 1 + phase 2; both give identical bits. router_weights are d uint8
+ * codes per expert row (16-byte aligned), router_scales / router_biases bf16
+ * per group of the context's group size (2-byte aligned); d a multiple of 64
+ * and of the group size, d <= 4096. */
+tsg_status tsg_moe_decode_layer_int8(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                     const uint8_t* router_weights, const uint16_t* router_scales,
+                                     const uint16_t* router_biases, const uint16_t* router_hidden,
+                                     const uint16_t* effective_scale,
+                                     const uint16_t* per_expert_scale, const uint16_t* x,
+                                     const uint16_t* residual, uint16_t* y, uint32_t* out_indices,
+                                     uint16_t* out_weights, uint16_t* acts_scratch,
+                                     uint32_t num_experts, uint32_t d, uint32_t f, uint32_t top_k);
+
 /* The Qwen-family layer: the shared branch of
  * QwenForwardRunner.encodeSharedExpert (QwenForwardRunner.swift:1548-1578)
  * and the routed experts on top of it with residual = y = sharedOut

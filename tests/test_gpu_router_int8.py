@@ -119,7 +119,9 @@ def test_int8_router_decode_layer_gemma_shape(tsg, ctx):
     HBM-resident Gemma-shaped layer with the expert ids read on the device
     (RealForwardRunner's per-layer sequence, RealForwardRunner.swift:3104-3330).
     Routing bit-exact against the oracle's kernel-order logits and top-k rule;
-    y within 1e-3 of MoeRef.applyStreamedRouted over the chosen experts."""
+    y within 1e-3 of MoeRef.applyStreamedRouted over the chosen experts; the
+    one-launch INT8 layer (and its three-launch form) equal to that sequence
+    bit for bit."""
     import torch
     from tests.test_gpu_qmv_decode import make_gemma_layer
     ctx.set_affine_group_size(32)
@@ -154,7 +156,78 @@ def test_int8_router_decode_layer_gemma_shape(tsg, ctx):
     rel = oracle.relative_error(oracle.f16_to_float(host(y, np.uint16)), ref)
     print(f"int8-router decode layer: experts={list(gi)} rel={rel:.3e}")
     assert rel <= kc.NORTH_STAR
-    # the one-launch layer runs the BF16 router: refused for an 8-bit MoE
+    # tsg_moe_decode_layer_int8: one launch, and forced to three launches,
+    # both the bits of the sequence above
+    for fused in (True, False):
+        moe.set_fused_decode(fused)
+        idx2, wts2, acts2, y2 = empty(8, np.uint32), empty(8), empty(8 * f), empty(d)
+        moe.encode_decode_layer_int8(layer, dev(packed), dev(scales), dev(biases), x, dev(es),
+                                     dev(pes), x, x, y2, idx2, wts2, acts2, ne, d, f)
+        ctx.synchronize()  # reports a one-launch hand-off timeout
+        assert np.array_equal(host(idx2, np.uint32), gi), f"fused={fused}"
+        assert np.array_equal(host(wts2, np.uint16), gw), f"fused={fused}"
+        assert np.array_equal(host(y2, np.uint16), host(y, np.uint16)), f"fused={fused}"
+    moe.set_fused_decode(True)
+    # each decode-layer entry takes only its own router format
     with pytest.raises(tsg.TsgError):
         moe.encode_decode_layer(layer, dev(np.zeros(ne * d, np.uint16)), x, dev(es), dev(pes),
                                 x, x, y, idx, wts, acts, ne, d, f)
+    m16 = tsg.MoE(ctx, router_weight_bits=16)
+    with pytest.raises(tsg.TsgError):
+        m16.encode_decode_layer_int8(layer, dev(packed), dev(scales), dev(biases), x, dev(es),
+                                     dev(pes), x, x, y, idx, wts, acts, ne, d, f)
+
+
+@pytest.mark.parametrize("d,f,ne,group,scheme,act", [
+    (2816, 704, 128, 32, "sym", "gelu"),
+    (2048, 512, 256, 64, "affine", "silu"),
+    (768, 256, 32, 32, "affine", "gelu"),
+])
+def test_int8_decode_layer_one_launch_matches_three(tsg, ctx, d, f, ne, group, scheme, act):
+    """tsg_moe_decode_layer_int8 in one launch and as router + phase 1 + phase
+    2 give the same bits; routing bit-exact against the oracle's kernel-order
+    INT8 logits, y within 1e-3 of MoeRef.applyStreamedRouted."""
+    import torch
+    from tests.test_gpu_qmv_decode import make_layer
+    ctx.set_affine_group_size(group)
+    ctx.set_affine_scheme(scheme)
+    sym = scheme == "sym"
+    layer, buf, offs, stride = make_layer(tsg, ctx, 0x4321 + d, ne, d, f, group, sym)
+    rng = np.random.default_rng(d + ne)
+    raw = rng.normal(0.0, 1.0 / np.sqrt(d), (ne, d)).astype(np.float32)
+    packed, scales, biases = oracle.quantize_int8_affine(raw, group)
+    es_bits = oracle.bf16_bits(rng.uniform(0.5, 1.5, d).astype(np.float32))
+    pes_bits = oracle.bf16_bits(np.linspace(0.8, 1.2, ne).astype(np.float32))
+    x = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(x, 0xC12 + d, 1.0)
+    res = torch.empty(d, dtype=torch.int16, device="cuda")
+    tsg.generators.f16_normal(res, 0xC14 + d, 0.5)
+    moe = tsg.MoE(ctx, router_weight_bits=8, gate_activation=act)
+    outs = {}
+    for fused in (True, False):
+        moe.set_fused_decode(fused)
+        y, idx, wts, acts = empty(d), empty(8, np.uint32), empty(8), empty(8 * f)
+        moe.encode_decode_layer_int8(layer, dev(packed), dev(scales), dev(biases), x,
+                                     dev(es_bits), dev(pes_bits), x, res, y, idx, wts, acts,
+                                     ne, d, f)
+        ctx.synchronize()  # raises if the one-launch hand-off timed out
+        outs[fused] = [host(t, np.uint16 if t is not idx else np.uint32)
+                       for t in (y, idx, wts, acts)]
+    for a, b in zip(outs[True], outs[False]):
+        assert np.array_equal(a, b)
+    y, gi, gw, _ = outs[True]
+    xb = host(x, np.uint16)
+    logits = oracle.router_logits_int8_canonical(packed, scales, biases, xb, es_bits, ne, d,
+                                                 group)
+    ci, cw = oracle.topk_softmax(logits, 8, oracle.bf16_to_float(pes_bits))
+    assert list(gi) == list(ci)
+    assert np.max(np.abs(gw.astype(np.int32) - cw.astype(np.int32))) <= 1
+    image = host(buf, np.uint8)
+    blobs = [np.ascontiguousarray(image[e * stride:(e + 1) * stride]) for e in gi]
+    ref = oracle.moe_apply_streamed_routed(
+        blobs, np.array(offs, np.uint32), oracle.f16_to_float(xb),
+        oracle.f16_to_float(host(res, np.uint16)), oracle.f16_to_float(gw), d, f, group,
+        symmetric=sym, act=1 if act == "silu" else 0)
+    rel = oracle.relative_error(oracle.f16_to_float(y), ref)
+    print(f"int8 decode layer d={d} f={f} ne={ne} g{group} {scheme} {act}: rel={rel:.3e}")
+    assert rel <= kc.NORTH_STAR

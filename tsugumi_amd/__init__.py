@@ -436,6 +436,18 @@ class MoE:
             _ptr(residual), _ptr(y), _ptr(out_indices), _ptr(out_weights), _ptr(acts_scratch),
             num_experts, d, f, top_k))
 
+    def encode_decode_layer_int8(self, layer: ResidentLayer, router_weights, router_scales,
+                                 router_biases, router_hidden, effective_scale,
+                                 per_expert_scale, x, residual, y, out_indices, out_weights,
+                                 acts_scratch, num_experts, d, f, top_k=8, stream=None):
+        """The decode layer with the INT8-affine router (router_weight_bits=8)."""
+        check(self.lib.tsg_moe_decode_layer_int8(
+            self.handle, _stream(stream), layer.handle, _ptr(router_weights),
+            _ptr(router_scales), _ptr(router_biases), _ptr(router_hidden),
+            _ptr(effective_scale), _ptr(per_expert_scale), _ptr(x), _ptr(residual), _ptr(y),
+            _ptr(out_indices), _ptr(out_weights), _ptr(acts_scratch), num_experts, d, f,
+            top_k))
+
     def close(self) -> None:
         if getattr(self, "handle", None):
             self.lib.tsg_moe_destroy(self.handle)

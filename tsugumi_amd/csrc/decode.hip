@@ -543,7 +543,9 @@ struct DecodeLayerArgs {
     const uint8_t* layer_base;
     uint64_t expert_stride;
     tsg_expert_offsets o;
-    const uint16_t* router_w;
+    const uint16_t* router_w;   // bf16 rows, or uint8 codes for the INT8 router
+    const uint16_t* router_s;   // INT8 router: bf16 group scales and biases
+    const uint16_t* router_b;
     const uint16_t* router_hidden;
     const uint16_t* es;
     const uint16_t* pes;
@@ -1066,29 +1068,69 @@ __global__ __launch_bounds__(STAGE ? 64u * kStageWaves : 256u) void router_kerne
 // finish selects on one wave (wave_topk_softmax), as the one-row BF16 router.
 constexpr int kInt8Units = 4;  // 16-byte units per lane: d <= 4096
 
-// One 16-weight unit: qx = fma(q, x, qx) and sx = sx + x in element order
-// (x = hidden * es rounded to fp32 before both uses: nothing contracted), then
-// acc = fma(scale, qx, acc), acc = fma(bias, sx, acc).
+// One 16-weight unit against its 16 products x = hidden * es (fp32): qx =
+// fma(q, x, qx) and sx = sx + x in element order, then acc = fma(scale, qx,
+// acc), acc = fma(bias, sx, acc). Nothing is contracted.
+__device__ __forceinline__ float int8_unit_dot_x(const u32x4_t& wq, const float (&x)[16],
+                                                 float scale, float bias, float acc) {
+#pragma clang fp contract(off)
+    const uint32_t qa[4] = {wq.x, wq.y, wq.z, wq.w};
+    float qx = 0.0f, sx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float q = (float)((qa[k >> 2] >> (8 * (k & 3))) & 0xFFu);
+        qx = __builtin_fmaf(q, x[k], qx);
+        sx = sx + x[k];
+    }
+    acc = __builtin_fmaf(scale, qx, acc);
+    return __builtin_fmaf(bias, sx, acc);
+}
+
+// The same with the products formed here from the fp16 hidden and bf16 es
+// words (each rounded to fp32 before its two uses).
 __device__ __forceinline__ float int8_unit_dot(const u32x4_t& wq, const u32x4_t (&xv)[2],
                                                const u32x4_t (&ev)[2], float scale, float bias,
                                                float acc) {
 #pragma clang fp contract(off)
-    const uint32_t qa[4] = {wq.x, wq.y, wq.z, wq.w};
     const uint32_t xa[8] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w};
     const uint32_t ea[8] = {ev[0].x, ev[0].y, ev[0].z, ev[0].w, ev[1].x, ev[1].y, ev[1].z, ev[1].w};
-    float qx = 0.0f, sx = 0.0f;
+    float x[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
         const uint32_t hw = xa[k >> 1], ew = ea[k >> 1];
         const float h = f16_to_f32((uint16_t)((k & 1) ? hw >> 16 : hw & 0xFFFFu));
         const float s = __uint_as_float((k & 1) ? ew & 0xFFFF0000u : ew << 16);
-        const float x = h * s;
-        const float q = (float)((qa[k >> 2] >> (8 * (k & 3))) & 0xFFu);
-        qx = __builtin_fmaf(q, x, qx);
-        sx = sx + x;
+        x[k] = h * s;
     }
-    acc = __builtin_fmaf(scale, qx, acc);
-    return __builtin_fmaf(bias, sx, acc);
+    return int8_unit_dot_x(wq, x, scale, bias, acc);
+}
+
+// One INT8 router row on one wave with the products x * es taken from LDS
+// (fp32, element order): router_int8_kernel's units, sums and reduction, so
+// the same logit bit for bit. wq[i] is unit lane + 64 i of the row (clamped),
+// sb / bb its group's scale and bias bits.
+__device__ __forceinline__ float router_dot_int8_staged(const uint4 (&wq)[kRouterChunks],
+                                                        const uint32_t (&sb)[4],
+                                                        const uint32_t (&bb)[4], const float* xe,
+                                                        uint32_t nunits, uint32_t lane) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t uu = lane + 64u * i;
+        const bool live = uu < nunits;
+        const uint32_t u = live ? uu : nunits - 1u;
+        float x[16];
+#pragma unroll
+        for (int k = 0; k < 16; k += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(xe + u * 16u + k);
+            x[k] = v.x, x[k + 1] = v.y, x[k + 2] = v.z, x[k + 3] = v.w;
+        }
+        const u32x4_t w = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+        acc = int8_unit_dot_x(w, x, live ? bf16_to_f32((uint16_t)sb[i]) : 0.0f,
+                              live ? bf16_to_f32((uint16_t)bb[i]) : 0.0f, acc);
+    }
+    acc = group16_sum(acc);
+    return (lane_value(acc, 0) + lane_value(acc, 16)) + (lane_value(acc, 32) + lane_value(acc, 48));
 }
 
 template <int G>
@@ -1178,11 +1220,13 @@ __global__ __launch_bounds__(256) void router_int8_kernel(
 // 1024-thread bound allows, and does not spill.
 __host__ __device__ constexpr uint32_t decode_layer_max_threads(bool sh) { return sh ? 768u : 1024u; }
 
-template <int G, bool SYM, int ACT, bool SH>
+template <int G, bool SYM, int ACT, bool SH, bool R8>
 // The values the first phase's loads need come as separate leading scalar
 // arguments (14 dwords) so that, built with kernarg preloading, the dispatch
 // hands them over in SGPRs: the loads go out with no memory round trip before
 // them. k_ne_rr = ne | router_rows << 16, k_d_thr = d | threads << 16.
+// R8: the router is INT8-affine (router_int8_kernel's arithmetic): k_router_w
+// holds uint8 codes, a_arg.router_s / router_b the group scales and biases.
 __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_kernel(
     const uint16_t* k_router_w, const uint16_t* k_hidden, const uint16_t* k_es,
     const uint16_t* k_pes, const uint16_t* k_x, uint32_t* k_sync, uint32_t k_ne_rr,
@@ -1221,11 +1265,20 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     const bool router_wave = wave < router_rows && er < ne0;
     const bool router_block = blockIdx.x < ne0;  // holds at least one router row
     uint4 rw[kRouterChunks];
+    uint32_t rsb[4], rbb[4];  // R8: the units' group scale and bias bits
     if (router_wave) {
-        const uint16_t* w_row = global_ptr(k_router_w) + (uint64_t)er * d0;
+        if constexpr (R8) {
+            const uint32_t nunits = d0 / 16u;
+            const uint8_t* w_row = reinterpret_cast<const uint8_t*>(global_ptr(k_router_w)) + (uint64_t)er * d0;
 #pragma unroll
-        for (int i = 0; i < kRouterChunks; ++i)
-            rw[i] = *reinterpret_cast<const uint4*>(w_row + min(lane + 64u * i, units - 1u) * 8u);
+            for (int i = 0; i < 4; ++i)
+                rw[i] = *reinterpret_cast<const uint4*>(w_row + min(lane + 64u * i, nunits - 1u) * 16u);
+        } else {
+            const uint16_t* w_row = global_ptr(k_router_w) + (uint64_t)er * d0;
+#pragma unroll
+            for (int i = 0; i < kRouterChunks; ++i)
+                rw[i] = *reinterpret_cast<const uint4*>(w_row + min(lane + 64u * i, units - 1u) * 8u);
+        }
     }
     // every thread reads the epoch (one request per wave), without a branch:
     // a load inside `if (t == 0)` left wave 0 waiting for it, and for its
@@ -1245,6 +1298,22 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
         if (router_block) {
             hv[i] = *reinterpret_cast<const uint4*>(hg + q);
             ev[i] = *reinterpret_cast<const uint4*>(eg + q);
+        }
+    }
+    if constexpr (R8) {
+        // the group scales and biases, whose pointers are kernel arguments
+        // not preloaded: their loads wait for that read, so they go out after
+        // every load that needs nothing but the preloaded arguments
+        if (router_wave) {
+            const uint16_t* rs = a_arg.router_s;
+            const uint16_t* rb = a_arg.router_b;
+            const uint32_t ngroups = d0 / G, nunits = d0 / 16u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t g = er * ngroups + min(lane + 64u * i, nunits - 1u) * 16u / G;
+                rsb[i] = rs[g];
+                rbb[i] = rb[g];
+            }
         }
     }
     if (t < kArgWords) reinterpret_cast<uint32_t*>(&a)[t] = arg_word;
@@ -1297,7 +1366,8 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     __syncthreads();
     const uint32_t tag = s_tag;
     if (router_wave) {
-        const float s = router_dot_staged(rw, xe, units, lane);
+        const float s = R8 ? router_dot_int8_staged(rw, rsb, rbb, xe, d0 / 16u, lane)
+                           : router_dot_staged(rw, xe, units, lane);
         if (lane < kDecodeGroups)
             st_coherent(sy.logits + lane * kMaxExperts + er, tagged(tag, __float_as_uint(s)));
     }
@@ -1668,7 +1738,7 @@ tsg_status phase2_dispatch(tsg_moe* moe, hipStream_t stream, const BlobSource& s
 // The fused one-launch decode layer, when every block fits on the device at
 // once (the rendezvous need all blocks resident). Returns TSG_ERR_DECLINED
 // otherwise and the caller runs the three-kernel sequence.
-template <int G, bool SYM, int ACT, bool SH>
+template <int G, bool SYM, int ACT, bool SH, bool R8>
 tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
     const auto up64 = [](uint32_t v) { return (v + 63u) / 64u * 64u; };
     uint32_t threads = 32u * a.pairs;                               // gate/up pairs
@@ -1685,7 +1755,7 @@ tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
         a.ss_off = (uint32_t)((lds + 15u) & ~(size_t)15u);
         lds = a.ss_off + p2_slot_halves(a.sh_f) * 2u + (SYM ? 0u : (a.sh_f / 32u) * 4u);
     }
-    auto kern = decode_layer_kernel<G, SYM, ACT, SH>;
+    auto kern = decode_layer_kernel<G, SYM, ACT, SH, R8>;
     int per_cu = 0;
     if (threads > decode_layer_max_threads(SH) || a.ne > kMaxExperts || a.f > kMaxFusedDim || a.d > kMaxFusedDim ||
         (a.rows + kDecodeGroups - 1u) / kDecodeGroups > kMaxCombineRows ||
@@ -1701,14 +1771,14 @@ tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
     return check_launch("decode_layer");
 }
 
-template <bool SH>
+template <bool SH, bool R8>
 tsg_status fused_dispatch(tsg_moe* moe, hipStream_t stream, const DecodeLayerArgs& a) {
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
     const bool silu = moe->activation == TSG_ACT_SILU;
 #define TSG_FU(GG, SS)                                                             \
-    return silu ? launch_fused<GG, SS, TSG_ACT_SILU, SH>(moe, stream, a)           \
-                : launch_fused<GG, SS, TSG_ACT_GELU_TANH, SH>(moe, stream, a)
+    return silu ? launch_fused<GG, SS, TSG_ACT_SILU, SH, R8>(moe, stream, a)       \
+                : launch_fused<GG, SS, TSG_ACT_GELU_TANH, SH, R8>(moe, stream, a)
     if (ctx->group_size == 32) {
         if (sym) TSG_FU(32, true);
         TSG_FU(32, false);
@@ -1833,14 +1903,11 @@ extern "C" tsg_status tsg_moe_router_logits_bf16(tsg_moe* moe, tsg_stream stream
 
 // encodeRouterGemma4 (MoE.swift:201-257): the INT8-affine router on a MoE
 // created with 8-bit router weights, at the context's group size.
-extern "C" tsg_status tsg_moe_router_int8(tsg_moe* moe, tsg_stream stream, const uint8_t* w,
-                                          const uint16_t* scales, const uint16_t* biases,
-                                          const uint16_t* hidden, const uint16_t* es,
-                                          const uint16_t* pes, uint32_t* out_idx,
-                                          uint16_t* out_w, uint32_t ne, uint32_t d,
-                                          uint32_t top_k) {
-    tsg_status st = check_moe(moe);
-    if (st) return st;
+tsg_status router_int8_launch(tsg_moe* moe, hipStream_t stream, const uint8_t* w,
+                              const uint16_t* scales, const uint16_t* biases,
+                              const uint16_t* hidden, const uint16_t* es, const uint16_t* pes,
+                              uint32_t* out_idx, uint16_t* out_w, uint32_t ne, uint32_t d,
+                              uint32_t top_k) {
     TSG_REQUIRE(moe->router_weight_bits == 8, TSG_ERR_INVALID_ARGUMENT,
                 "INT8 router encode on a %u-bit router", moe->router_weight_bits);
     const uint32_t g = moe->ctx->group_size;
@@ -1862,9 +1929,21 @@ extern "C" tsg_status tsg_moe_router_int8(tsg_moe* moe, tsg_stream stream, const
     tsg_ctx* ctx = moe->ctx;
     const dim3 grid((ne + kRouterWaves - 1) / kRouterWaves);
     auto kern = g == 32 ? router_int8_kernel<32> : router_int8_kernel<64>;
-    hipLaunchKernelGGL(kern, grid, dim3(64u * kRouterWaves), 0, as_stream(stream), w, scales,
-                       biases, hidden, es, pes, ctx->counters, ne, d, ctx->logits, out_idx, out_w);
+    hipLaunchKernelGGL(kern, grid, dim3(64u * kRouterWaves), 0, stream, w, scales, biases,
+                       hidden, es, pes, ctx->counters, ne, d, ctx->logits, out_idx, out_w);
     return check_launch("router_int8");
+}
+
+extern "C" tsg_status tsg_moe_router_int8(tsg_moe* moe, tsg_stream stream, const uint8_t* w,
+                                          const uint16_t* scales, const uint16_t* biases,
+                                          const uint16_t* hidden, const uint16_t* es,
+                                          const uint16_t* pes, uint32_t* out_idx,
+                                          uint16_t* out_w, uint32_t ne, uint32_t d,
+                                          uint32_t top_k) {
+    tsg_status st = check_moe(moe);
+    if (st) return st;
+    return router_int8_launch(moe, as_stream(stream), w, scales, biases, hidden, es, pes,
+                              out_idx, out_w, ne, d, top_k);
 }
 
 extern "C" tsg_status tsg_moe_phase1(tsg_moe* moe, tsg_stream stream,
@@ -1947,17 +2026,34 @@ struct SharedBranch {
     uint32_t f;
 };
 
+// The INT8 router's tensors (encodeRouterGemma4's weights, scales, biases).
+struct RouterInt8 {
+    const uint8_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+};
+
 tsg_status decode_layer_impl(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
                              const uint16_t* router_w, const uint16_t* router_hidden,
                              const uint16_t* es, const uint16_t* pes, const uint16_t* x,
                              const uint16_t* residual, uint16_t* y, uint32_t* out_idx,
                              uint16_t* out_w, uint16_t* acts, uint32_t ne, uint32_t d,
-                             uint32_t f, uint32_t top_k, const SharedBranch* sh) {
+                             uint32_t f, uint32_t top_k, const SharedBranch* sh,
+                             const RouterInt8* r8 = nullptr) {
     tsg_status st = check_moe(moe);
     if (st) return st;
-    TSG_REQUIRE(moe->router_weight_bits == 16, TSG_ERR_INVALID_ARGUMENT,
-                "the one-launch layer runs the BF16 router; this MoE has %u-bit router weights",
-                moe->router_weight_bits);
+    TSG_REQUIRE(moe->router_weight_bits == (r8 ? 8u : 16u), TSG_ERR_INVALID_ARGUMENT,
+                "%s router weights on a MoE created with %u-bit router weights",
+                r8 ? "INT8" : "BF16", moe->router_weight_bits);
+    if (r8) {
+        router_w = reinterpret_cast<const uint16_t*>(r8->w);
+        const uint32_t g = moe->ctx->group_size;
+        TSG_REQUIRE(r8->s && r8->b, TSG_ERR_INVALID_ARGUMENT, "NULL router scales/biases");
+        TSG_REQUIRE(((reinterpret_cast<uintptr_t>(r8->s) | reinterpret_cast<uintptr_t>(r8->b)) & 1u) == 0,
+                    TSG_ERR_ALIGNMENT, "router scales and biases must be 2-byte aligned");
+        TSG_REQUIRE(d % 64u == 0 && d % g == 0, TSG_ERR_INVALID_ARGUMENT,
+                    "d=%u must be a multiple of 64 and of the group size %u (INT8 router)", d, g);
+    }
     if ((st = check_decode_shape(moe->ctx, d, f, top_k))) return st;
     TSG_REQUIRE(layer, TSG_ERR_INVALID_ARGUMENT, "layer is NULL");
     TSG_REQUIRE(ne > 0 && ne <= layer->num_experts && ne <= kMaxExperts, TSG_ERR_INVALID_ARGUMENT,
@@ -1976,6 +2072,8 @@ tsg_status decode_layer_impl(tsg_moe* moe, tsg_stream stream, const tsg_layer* l
     a.expert_stride = layer->expert_stride;
     a.o = layer->offsets;
     a.router_w = router_w;
+    a.router_s = r8 ? r8->s : nullptr;
+    a.router_b = r8 ? r8->b : nullptr;
     a.router_hidden = router_hidden;
     a.es = es;
     a.pes = pes;
@@ -2001,7 +2099,9 @@ tsg_status decode_layer_impl(tsg_moe* moe, tsg_stream stream, const tsg_layer* l
         a.sh_f = sh->f;
     }
     if (!moe->unfused_decode) {
-        st = sh ? fused_dispatch<true>(moe, s, a) : fused_dispatch<false>(moe, s, a);
+        // (no one-launch form of the shared branch with the INT8 router)
+        st = r8 ? (sh ? TSG_ERR_DECLINED : fused_dispatch<false, true>(moe, s, a))
+                : (sh ? fused_dispatch<true, false>(moe, s, a) : fused_dispatch<false, false>(moe, s, a));
         if (st != TSG_ERR_DECLINED) return st;
     }
     if (sh) {
@@ -2012,8 +2112,10 @@ tsg_status decode_layer_impl(tsg_moe* moe, tsg_stream stream, const tsg_layer* l
             return st;
         residual = y;
     }
-    if ((st = router_launch(moe, s, router_w, router_hidden, d, es, pes, out_idx, out_w, nullptr,
-                            1, ne, d, top_k, true)))
+    if ((st = r8 ? router_int8_launch(moe, s, r8->w, r8->s, r8->b, router_hidden, es, pes,
+                                      out_idx, out_w, ne, d, top_k)
+                 : router_launch(moe, s, router_w, router_hidden, d, es, pes, out_idx, out_w,
+                                 nullptr, 1, ne, d, top_k, true)))
         return st;
     BlobSource src;
     if ((st = blobs_from_layer(layer, out_idx, &src))) return st;
@@ -2032,6 +2134,17 @@ extern "C" tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream,
                                            uint32_t top_k) {
     return decode_layer_impl(moe, stream, layer, router_w, router_hidden, es, pes, x, residual, y,
                              out_idx, out_w, acts, ne, d, f, top_k, nullptr);
+}
+
+extern "C" tsg_status tsg_moe_decode_layer_int8(
+    tsg_moe* moe, tsg_stream stream, const tsg_layer* layer, const uint8_t* router_w,
+    const uint16_t* router_scales, const uint16_t* router_biases, const uint16_t* router_hidden,
+    const uint16_t* es, const uint16_t* pes, const uint16_t* x, const uint16_t* residual,
+    uint16_t* y, uint32_t* out_idx, uint16_t* out_w, uint16_t* acts, uint32_t ne, uint32_t d,
+    uint32_t f, uint32_t top_k) {
+    const RouterInt8 r8{router_w, router_scales, router_biases};
+    return decode_layer_impl(moe, stream, layer, nullptr, router_hidden, es, pes, x, residual, y,
+                             out_idx, out_w, acts, ne, d, f, top_k, nullptr, &r8);
 }
 
 extern "C" tsg_status tsg_moe_decode_layer_shared(
