@@ -9,7 +9,8 @@
 - configs[3] at its real size (T = 2048, Zipf(1.1), Gemma) and configs[4]
   prefill (T = 4096, Zipf(1.0), Qwen-shaped, SiLU): device grouping ->
   gate/up GEMM -> down GEMM -> reduce, every pair of the head expert and
-  every pair of every 16th token recomputed on the CPU.
+  every pair of every 16th token and the edge rows of every routed block
+  recomputed on the CPU.
 """
 import numpy as np
 import pytest
@@ -451,7 +452,8 @@ def test_shared_expert_rows_matches_one_row_form(tsg, ctx, rows, scheme):
 
 def run_prefill_full(tsg, ctx, layer, offs, blobs, t, d, f, ne, s, act, seed):
     """Device grouping -> gate/up -> down -> reduce at full size; the head
-    expert and every 16th token recomputed by the oracle."""
+    expert, every 16th token and the first and last row of every routed
+    block recomputed by the oracle."""
     k = 8
     rng = np.random.default_rng(seed)
     idx, w = wl.zipf_routing(rng, t, ne, k, s)
@@ -472,7 +474,11 @@ def run_prefill_full(tsg, ctx, layer, offs, blobs, t, d, f, ne, s, act, seed):
     tsg.PrefillMoE(ctx).encode_reduce_token_major(partials, dev(w), h2, t, k, d)
     want = oracle.group_pairs(oracle.make_token_expert_pairs(idx, w, t, k), t, k, ne)
     assert np.array_equal(host(sp, np.uint32).view(oracle.PAIR_DTYPE), want["sorted_pairs"])
-    sub, _, tokens, head, head_rows = wl.sampled_pairs(want["sorted_pairs"], t)
+    # every routed block's first and last row too: each GEMM work item's edges
+    n_blocks = int(host(nb, np.uint32)[0])
+    bl = host(blocks, np.uint32).reshape(-1, 4)[:n_blocks]
+    edges = np.concatenate([bl[:, 1], bl[:, 1] + bl[:, 2] - 1]).astype(np.int64)
+    sub, _, tokens, head, head_rows = wl.sampled_pairs(want["sorted_pairs"], t, extra_pos=edges)
     oracle.set_threads(16)
     P = oracle.prefill_moe_ref(blobs, offs, hidden, d, sub, k, d, f, 32, True,
                                act=1 if act == "silu" else 0)
@@ -484,7 +490,6 @@ def run_prefill_full(tsg, ctx, layer, offs, blobs, t, d, f, ne, s, act, seed):
     ref_h2 = oracle.reduce_token_major(Ps, w[tokens], tokens.size, k, d)
     gh = host(h2, np.uint16).reshape(t, d)[tokens]
     rel = oracle.relative_error(oracle.f16_to_float(gh), oracle.f16_to_float(ref_h2))
-    n_blocks = int(host(nb, np.uint32)[0])
     print(f"prefill T={t} E={ne} {act}: head expert {head} ({head_rows} rows), "
           f"{n_blocks} routed blocks, {sub.size} pairs checked: partials rel={rel_p:.3e} "
           f"h2 rel={rel:.3e}")

@@ -101,14 +101,17 @@ def rows_blocks(grouped) -> np.ndarray:
                       int(g["pair_start"])) for g in grouped["groups"]], dtype=oracle.BLOCK_DTYPE)
 
 
-def sampled_pairs(sorted_pairs: np.ndarray, t: int, every: int = 16):
+def sampled_pairs(sorted_pairs: np.ndarray, t: int, every: int = 16, extra_pos=None):
     """The pairs a full-size check recomputes on the CPU: every pair of the
-    largest expert (the one split over the most GEMM work items) and every
-    pair of every `every`-th token. Returns (subset in sorted order, its
-    positions in sorted_pairs, the sampled tokens)."""
+    largest expert (the one split over the most GEMM work items), every pair
+    of every `every`-th token, and the positions `extra_pos` (e.g. the first
+    and last row of every routed block). Returns (subset in sorted order, its
+    positions in sorted_pairs, the sampled tokens, the head expert, its rows)."""
     experts, counts = np.unique(sorted_pairs["expert"], return_counts=True)
     head = experts[np.argmax(counts)]
     tokens = np.arange(0, t, every)
     keep = (sorted_pairs["expert"] == head) | np.isin(sorted_pairs["token"], tokens)
+    if extra_pos is not None:
+        keep[np.asarray(extra_pos, np.int64)] = True
     pos = np.nonzero(keep)[0]
     return sorted_pairs[pos], pos, tokens, int(head), int(counts.max())
