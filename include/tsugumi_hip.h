@@ -173,10 +173,10 @@ void tsg_layer_destroy(tsg_layer* layer);
  * MoE (Kernels/MoE/MoE.swift:42-662). */
 
 /* MoE.init(context:routerWeightBits:gateActivation:) (MoE.swift:123-199).
- * router_weight_bits: 8 (INT8-affine router, tsg_moe_router_int8) or 16 (bf16,
- * the QAT checkpoints' router: every other router entry point and the
- * one-launch layers). An entry point of the other format returns
- * TSG_ERR_INVALID_ARGUMENT (the reference's precondition). */
+ * router_weight_bits: 8 (INT8-affine router: tsg_moe_router_int8,
+ * tsg_moe_decode_layer_int8) or 16 (bf16, the QAT checkpoints' router: every
+ * other router entry point and decode layer). An entry point of the other
+ * format returns TSG_ERR_INVALID_ARGUMENT (the reference's precondition). */
 tsg_status tsg_moe_create(tsg_ctx* ctx, uint32_t router_weight_bits,
                           tsg_activation gate_activation, tsg_moe** out);
 void tsg_moe_destroy(tsg_moe* moe);
