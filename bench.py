@@ -537,15 +537,17 @@ def run_rows_path(tsg, torch, ctx, moe, layers, n_layers, m, h, f, ne, seed, sha
 
 
 def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, ne, seed,
-                     shared=None):
+                     shared=None, fused=True):
     """M tokens through n_layers whole layers with nothing on the host: the
     router rows (RealForwardRunner.swift:1826-1872) and the grouping of their
     pairs (:2116-2151) in one launch, the rows path over the device block
     list and the token-major reduce; `shared` (Qwen) adds the
     shared expert over the M rows (two launches). The M hidden states of a layer
     share a common part (x0 + 0.35 N(0,1)), so their top-8 sets overlap (a
-    union of about 12-20). Returns us per layer, the mean union and the
-    launches per layer."""
+    union of about 12-20). `fused`: the whole routed layer as one launch
+    (tsg_moe_verify_layer); otherwise the router + grouping launch, the two
+    rows-path launches and the reduce. Returns us per layer, the mean union
+    and the launches per layer."""
     k = TOPK
     rng = np.random.default_rng(seed)
     hid = np.empty((n_layers, m, h), np.float32)
@@ -582,19 +584,27 @@ def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, n
             il, wl = idx[l * m * k:(l + 1) * m * k], wts[l * m * k:(l + 1) * m * k]
             nb = nbs[l:l + 1]
             if shared is not None:
-                side.wait_stream(stream)
+                # beside the four launches on a second stream; ahead of the one
+                # launch on the same stream (that launch needs every CU)
+                if not fused:
+                    side.wait_stream(stream)
                 blob, o, gw = shared[l]
                 tsg.encode_shared_expert_rows(moe, blob, o, x, h, gw, sact,
                                               sout[l * m * h:(l + 1) * m * h], m, h, f,
-                                              stream=side)
-            moe.encode_router_gemma4_bf16_rows_grouped(routers[l], x, h, ones_h, ones_e, il, wl,
-                                                       m, ne, h, sp, off, cnt, blocks,
-                                                       max_blocks, nb, stream=stream)
-            g.encode_streamed_rows_device(layers[l], x, h, sp, blocks, max_blocks, nb, act, part,
-                                          k, h, f, stream=stream)
-            red.encode_reduce_token_major(part, wl, h2[l * m * h:(l + 1) * m * h], m, k, h,
-                                          stream=stream)
-            if shared is not None:
+                                              stream=stream if fused else side)
+            if fused:
+                moe.encode_verify_layer(layers[l], routers[l], x, ones_h, ones_e, x, h,
+                                        h2[l * m * h:(l + 1) * m * h], il, wl, m, ne, h, f,
+                                        stream=stream)
+            else:
+                moe.encode_router_gemma4_bf16_rows_grouped(routers[l], x, h, ones_h, ones_e, il,
+                                                           wl, m, ne, h, sp, off, cnt, blocks,
+                                                           max_blocks, nb, stream=stream)
+                g.encode_streamed_rows_device(layers[l], x, h, sp, blocks, max_blocks, nb, act,
+                                              part, k, h, f, stream=stream)
+                red.encode_reduce_token_major(part, wl, h2[l * m * h:(l + 1) * m * h], m, k, h,
+                                              stream=stream)
+            if shared is not None and not fused:
                 stream.wait_stream(side)
 
     ms = time_graph(torch, stream, body, reps=8)
@@ -604,8 +614,11 @@ def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, n
         raise RuntimeError("verify layer produced non-finite outputs")
     if shared is not None and not bool(torch.isfinite(sout.view(torch.float16).float()).all()):
         raise RuntimeError("shared expert rows produced non-finite outputs")
-    unions = nbs.cpu().numpy()
-    launches = 1 + 2 + 1 + (2 if shared is not None else 0)
+    ids = idx.view(n_layers, m * k).cpu().numpy()
+    unions = [len(set(r.tolist())) for r in ids]
+    if not fused and not np.array_equal(nbs.cpu().numpy(), unions):
+        raise RuntimeError("device grouping's block count differs from the routing's union")
+    launches = (1 if fused else 1 + 2 + 1) + (2 if shared is not None else 0)
     return ms * 1000.0 / n_layers, float(np.mean(unions)), launches
 
 
@@ -675,9 +688,12 @@ def run_qwen(tsg, torch, args):
     log(f"qwen decode M=1: {us1:.3f} us/layer ({bytes1 / (us1 * 1e-6) / 1e9:.1f} GB/s)")
     us3, u3, nl3 = run_verify_layer(tsg, torch, ctx, moe, layers, routers, nl, 3, h, f, e,
                                     0x3333, shared=shared)
+    us34, u34, nl34 = run_verify_layer(tsg, torch, ctx, moe, layers, routers, nl, 3, h, f, e,
+                                       0x3333, shared=shared, fused=False)
     bytes3 = u3 * payload + payload + e * h * 2 + h * 2
     log(f"qwen decode M=3 whole layer: {us3:.3f} us/layer over a mean union of {u3:.1f} "
-        f"experts ({bytes3 / (us3 * 1e-6) / 1e9:.1f} GB/s)")
+        f"experts ({bytes3 / (us3 * 1e-6) / 1e9:.1f} GB/s); routed part as four launches "
+        f"{us34:.3f} us")
     pre = run_prefill_shape(tsg, torch, ctx, args, layers[0], QW_T, h, f, e, 1.0, "silu",
                             layers=layers)
     return {"workload": "qwen3.5-moe-35b-a3b-shaped layer (configs[4]): H=2048, 256 experts "
@@ -689,9 +705,12 @@ def run_qwen(tsg, torch, args):
             "decode_m3": {"us_per_layer": round(us3, 3), "mean_union": round(u3, 2),
                           "GBps": round(bytes3 / (us3 * 1e-6) / 1e9, 2),
                           "bytes_per_layer": int(bytes3), "launches_per_layer": nl3,
-                          "path": "whole layer on the device: router rows + grouping (one "
-                                  "launch), rows path over the device block list, reduce, shared "
-                                  "expert over the 3 rows (2 launches)"},
+                          "path": "routed experts in one launch (tsg_moe_verify_layer: router "
+                                  "rows, top-8, grouping, rows path, reduce) beside the shared "
+                                  "expert over the 3 rows (2 launches, second stream)",
+                          "four_launches": {"us_per_layer": round(us34, 3),
+                                            "mean_union": round(u34, 2),
+                                            "launches_per_layer": nl34}},
             "prefill_t4096": prefill_summary(pre)}
 
 
@@ -904,16 +923,20 @@ def run_dense_qmm(tsg, torch, ctx):
 
 def run_verify(tsg, torch, ctx, args, layers, routers):
     """Gemma verify, M=5 over a union of about 12-20 experts, 30
-    layers: the whole layer (router rows, device grouping, rows path, reduce),
-    and the rows path alone with the routing precomputed."""
+    layers: the whole layer (router rows, top-8, grouping, rows path, reduce)
+    in one launch, the same as four launches, and the rows path alone with
+    the routing precomputed."""
     moe = tsg.MoE(ctx)
     us, u, nl = run_verify_layer(tsg, torch, ctx, moe, layers, routers, LAYERS, 5, H, F, E,
                                  0x5E5E)
+    us4, u4, nl4 = run_verify_layer(tsg, torch, ctx, moe, layers, routers, LAYERS, 5, H, F, E,
+                                    0x5E5E, fused=False)
     us0, u0 = run_rows_path(tsg, torch, ctx, moe, layers, LAYERS, 5, H, F, E, 0x5E5E)
     _, _, payload = shape_offsets(H, F)
     b = u * payload + ROUTER_BYTES
-    log(f"verify M=5 whole layer: {us:.3f} us/layer over a mean union of {u:.1f} experts "
-        f"({b / (us * 1e-6) / 1e9:.1f} GB/s); rows path alone {us0:.3f} us")
+    log(f"verify M=5 whole layer, one launch: {us:.3f} us/layer over a mean union of {u:.1f} "
+        f"experts ({b / (us * 1e-6) / 1e9:.1f} GB/s); four launches {us4:.3f} us; rows path "
+        f"alone {us0:.3f} us")
     return {"workload": "gemma4-26b-a4b verify, M=5 (draft 4 + 1), union ~12-20, 30 layers "
                         "(configs[2])",
             "us_per_layer": round(us, 3), "mean_union": round(u, 2),
@@ -921,8 +944,12 @@ def run_verify(tsg, torch, ctx, args, layers, routers):
             "GBps": round(b / (us * 1e-6) / 1e9, 2),
             "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "launches_per_layer": nl,
-            "path": "whole layer on the device: router rows + grouping (one launch), rows "
-                    "path over the device block list, token-major reduce",
+            "path": "whole layer in one launch (tsg_moe_verify_layer): router rows, top-8, "
+                    "grouping, rows path over the routed experts, token-major reduce",
+            "four_launches": {"us_per_layer": round(us4, 3), "mean_union": round(u4, 2),
+                              "launches_per_layer": nl4,
+                              "path": "router rows + grouping (one launch), rows path over the "
+                                      "device block list (two), token-major reduce"},
             "rows_path_only": {"us_per_layer": round(us0, 3), "mean_union": round(u0, 2),
                                "path": "rows path + reduce, routing precomputed on the host"}}
 

@@ -282,6 +282,32 @@ tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream, const tsg_layer
                                 uint16_t* out_weights, uint16_t* acts_scratch,
                                 uint32_t num_experts, uint32_t d, uint32_t f, uint32_t top_k);
 
+/* One whole verify MoE layer of row_count <= 8 tokens on a resident layer, in
+ * one launch: the router rows and top-8 of every token
+ * (encodeRouterGemma4BF16Rows, MoE.swift:404-466), the grouping of their
+ * pairs by expert (RealForwardRunner.swift:2116-2151), gate/up + activation
+ * and down over the union of routed experts (encodeStreamedRows,
+ * PrefillGroupedRoutedMoE.swift:793-917) and the token-major weighted sum
+ * (PrefillMoE.encodeReduceTokenMajor, PrefillMoE.swift:11-38): the
+ * composition RealForwardRunner.swift:1826-2151 encodes per verify layer.
+ * h2 [row_count, d], out_indices / out_weights [row_count, 8] are bit for bit
+ * what tsg_moe_router_bf16_rows_grouped + tsg_prefill_moe_rows_device +
+ * tsg_prefill_moe_reduce_token_major give. router_hidden feeds the router
+ * (with effective_scale), x the experts (they may alias), both rows
+ * hidden_stride elements apart. Returns TSG_ERR_DECLINED, with nothing
+ * launched, for row_count 0 or > 8, num_experts < 8, d or f not a multiple of
+ * 64 or above 4096, or when the launch's blocks cannot all be resident (the
+ * caller then encodes those three calls). No counterpart entry in the
+ * reference, which encodes the steps as separate dispatches. */
+tsg_status tsg_moe_verify_layer(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
+                                const uint16_t* router_weights, const uint16_t* router_hidden,
+                                const uint16_t* effective_scale,
+                                const uint16_t* per_expert_scale, const uint16_t* x,
+                                uint32_t hidden_stride_elements, uint16_t* h2,
+                                uint32_t* out_indices, uint16_t* out_weights,
+                                uint32_t row_count, uint32_t num_experts, uint32_t d, uint32_t f,
+                                uint32_t top_k);
+
 /* tsg_moe_decode_layer with the INT8-affine router (a MoE created with
  * router_weight_bits 8; encodeRouterGemma4, MoE.swift:201-257, then the two
  * phases, as RealForwardRunner.swift:3104-3330 encodes them per layer): the

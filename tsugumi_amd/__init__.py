@@ -436,6 +436,21 @@ class MoE:
             _ptr(residual), _ptr(y), _ptr(out_indices), _ptr(out_weights), _ptr(acts_scratch),
             num_experts, d, f, top_k))
 
+    def encode_verify_layer(self, layer: ResidentLayer, router_weights, router_hidden,
+                            effective_scale, per_expert_scale, x, hidden_stride, h2,
+                            out_indices, out_weights, row_count, num_experts, d, f, top_k=8,
+                            stream=None):
+        """One verify layer of row_count <= 8 tokens in one launch: the rows
+        router's top-8, the grouping, the rows path over the routed experts and
+        the token-major sum (encodeRouterGemma4BF16Rows + grouping +
+        encodeStreamedRows + encodeReduceTokenMajor), the same bits. Raises
+        TsgError(TSG_ERR_DECLINED) when the one launch does not fit."""
+        check(self.lib.tsg_moe_verify_layer(
+            self.handle, _stream(stream), layer.handle, _ptr(router_weights),
+            _ptr(router_hidden), _ptr(effective_scale), _ptr(per_expert_scale), _ptr(x),
+            hidden_stride, _ptr(h2), _ptr(out_indices), _ptr(out_weights), row_count,
+            num_experts, d, f, top_k))
+
     def encode_decode_layer_int8(self, layer: ResidentLayer, router_weights, router_scales,
                                  router_biases, router_hidden, effective_scale,
                                  per_expert_scale, x, residual, y, out_indices, out_weights,

@@ -108,6 +108,7 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
         e = hipMalloc(&ctx->logits, sizeof(float) * kMaxPromptRows * kMaxExperts);
     if (e == hipSuccess)
         e = hipMalloc(&ctx->act_replicas, sizeof(uint16_t) * kActReplicas * kActReplicaHalves);
+    if (e == hipSuccess) e = hipMalloc(&ctx->verify_words, sizeof(uint64_t) * kVerifyWords);
     if (e == hipSuccess) e = hipMalloc(&ctx->gemm_sched, sizeof(uint32_t) * kGemmSchedWords);
     if (e == hipSuccess) e = hipMemset(ctx->gemm_sched, 0, sizeof(uint32_t) * kGemmSchedWords);
     if (e == hipSuccess) e = hipMemset(ctx->counters, 0, sizeof(uint32_t) * kMaxCounters);
@@ -117,6 +118,7 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
     // issue again, so the regions start at tag 0.
     if (e == hipSuccess)
         e = hipMemset(ctx->act_replicas, 0, sizeof(uint16_t) * kActReplicas * kActReplicaHalves);
+    if (e == hipSuccess) e = hipMemset(ctx->verify_words, 0, sizeof(uint64_t) * kVerifyWords);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     // this device's address of the no-alloc grouping scratch (device current)
     const tsg_status st = e == hipSuccess ? group_noalloc_setup(ctx) : TSG_OK;
@@ -124,6 +126,7 @@ extern "C" tsg_status tsg_ctx_create(int device, tsg_ctx** out) {
         (void)hipFree(ctx->counters);
         (void)hipFree(ctx->logits);
         (void)hipFree(ctx->act_replicas);
+        (void)hipFree(ctx->verify_words);
         (void)hipFree(ctx->gemm_sched);
         delete ctx;
         if (st != TSG_OK) return st;
@@ -140,6 +143,7 @@ extern "C" void tsg_ctx_destroy(tsg_ctx* ctx) {
     (void)hipFree(ctx->counters);
     (void)hipFree(ctx->logits);
     (void)hipFree(ctx->act_replicas);
+    (void)hipFree(ctx->verify_words);
     (void)hipFree(ctx->gemm_sched);
     delete ctx;
 }

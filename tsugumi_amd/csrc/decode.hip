@@ -1588,6 +1588,498 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     }
 }
 
+// ----------------------------------------------- one-launch verify layer
+
+// One verify MoE layer of `rows` <= 8 tokens in one launch (kDecodeBlocks
+// blocks of kVerifyThreads, all co-resident), the composition the verify step
+// encodes per layer (RealForwardRunner.swift:1826-1872 router rows,
+// :2116-2151 grouping, PrefillGroupedRoutedMoE.swift:793-917 encodeStreamedRows,
+// PrefillMoE.swift:11-38 encodeReduceTokenMajor) with the same arithmetic as
+// those separate launches, so every output is bit for bit theirs:
+//  1. router: block e < ne holds router row e in registers; wave r < rows dots
+//     it with token r's row (router_chunks_dot, the staged rows router's sum)
+//     and posts the logit to the kDecodeGroups replicas (tagged words);
+//  2. every block polls its group's replica and selects each token's top-8 on
+//     wave r (wave_select_top8 + slot_softmax_lane, the rows router's steps),
+//     then groups the rows * 8 pairs by (expert, pair) on one wave: slot u is
+//     the u-th routed expert, its rows its pairs in token order (the device
+//     grouping's sorted order);
+//  3. gate/up: the U * f (slot, f) pairs are dealt to the blocks in equal
+//     contiguous ranges, 32 lanes a pair (the rows path's lane geometry and
+//     per-row steps over the slot's rows, picked from the staged token rows);
+//     each activation row entry is posted as a tagged word;
+//  4. down: the U * d (slot, row) outputs likewise; a block's range covers at
+//     most two slots, whose activation rows it gathers into LDS; each route
+//     partial half(down . act) is posted as a tagged word;
+//  5. the token-major sum h2[t, n] = half(sum_r fma(w[t, r], P[t, r, n]))
+//     over the blocks' equal ranges of the rows * d outputs.
+// The next pass's weights of a wave are requested before the current pass
+// runs (two gate/up passes, then two down passes ahead of the activation
+// gather). The tag is the verify epoch + 1; every block posts an arrival
+// word once it holds the tag, and block 0 advances the epoch after seeing all
+// of them. Polls are bounded (timeouts set the error word).
+constexpr uint32_t kVerifyThreads = 512;  // 8 waves of up to 256 VGPRs
+constexpr uint32_t kVerifyWaves = kVerifyThreads / 64u;
+constexpr int kVerifyXUnits = (int)((kMaxRouterRows * 512u + kVerifyThreads - 1u) / kVerifyThreads);
+// A unit (a gate/up pair or a down row) of a slot with m rows costs
+// kVerifyUnitBase + kVerifyRowCost * m in the split of the units over the
+// blocks: its weight bytes and its rows' dot products. Measured at configs[2]
+// (bench.py, alternating runs): 3 + m 34.7-35.0 us per layer, 5 + m 35.7,
+// 8 + m 36.4, 1 + m 35.8-36.0, 1 + 2 m 38.5, an equal split 37.8.
+constexpr uint32_t kVerifyUnitBase = 3;
+constexpr uint32_t kVerifyRowCost = 1;
+constexpr uint32_t kRowsInOrder = 0xFAC688u;  // rows 0..7 as 3-bit picks
+
+struct VerifyLayerArgs {
+    const uint8_t* layer_base;
+    uint64_t expert_stride;
+    tsg_expert_offsets o;
+    uint16_t* h2;
+    uint32_t* out_idx;
+    uint16_t* out_w;
+    uint64_t* words;
+    uint32_t* sync_words;
+    uint32_t ne, d, f, rows;
+};
+
+// Dynamic LDS of the verify layer, in bytes from 0: the token rows in element
+// order (router), the same rows in the GEMV's staged layout, their chunk sums
+// (affine), and two slots' activation rows with their sums.
+struct VerifyLds {
+    uint32_t xs, xsum, as, asum, bytes;
+};
+__host__ __device__ __forceinline__ VerifyLds verify_lds(uint32_t rows, uint32_t d, uint32_t f,
+                                                         bool sym) {
+    VerifyLds l;
+    l.xs = rows * d * 2u;
+    l.xsum = l.xs + rows * lds_chunks_halves(d) * 2u;
+    l.as = (l.xsum + (sym ? 0u : rows * (d / 32u) * 4u) + 15u) & ~15u;
+    l.asum = l.as + 2u * rows * lds_chunks_halves(f) * 2u;
+    l.bytes = l.asum + (sym ? 0u : 2u * rows * (f / 32u) * 4u);
+    return l;
+}
+
+
+template <int G, bool SYM, int ACT>
+// The values the first loads need are leading scalar arguments (14 dwords,
+// preloaded into SGPRs): k_ne_rows = ne | rows << 16, k_d_stride = d |
+// hidden stride << 16.
+__global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
+    const uint16_t* k_router_w, const uint16_t* k_hidden, const uint16_t* k_es,
+    const uint16_t* k_pes, const uint16_t* k_x, uint32_t* k_sync, uint32_t k_ne_rows,
+    uint32_t k_d_stride, VerifyLayerArgs a_arg) {
+    __shared__ VerifyLayerArgs a;
+    constexpr uint32_t kArgWords = sizeof(VerifyLayerArgs) / 4;
+    static_assert(sizeof(VerifyLayerArgs) % 4 == 0 && kArgWords <= kVerifyThreads, "args copy");
+    const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
+    const uint32_t arg_word = reinterpret_cast<const uint32_t*>(&a_arg)[min(t, kArgWords - 1u)];
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ uint32_t s_tag, s_nslots;
+    __shared__ uint32_t s_gains[kMaxExperts];
+    __shared__ __align__(16) uint64_t s_cand[kMaxRouterRows][kMaxExperts + kCandBatch];
+    __shared__ uint32_t s_sid[kMaxRouterRows][kTopK], s_sfill[kMaxRouterRows][kTopK];
+    __shared__ uint32_t s_skey[kMaxRouterRows][kTopK];
+    __shared__ uint32_t s_pe[kVerifyPairs], s_pw[kVerifyPairs];  // pair p = 8 t + r
+    __shared__ uint32_t s_sp[kVerifyPairs];                      // sorted row -> pair
+    __shared__ uint32_t s_uexp[kVerifyPairs], s_ustart[kVerifyPairs + 1];
+    __shared__ uint32_t s_cnt[kMaxExperts], s_off[kMaxExperts];  // the grouping
+    __shared__ uint32_t s_mask[kMaxRouterRows * kMaskWords], s_wtot[kMaxExperts / 64u];
+    __shared__ uint32_t s_bad;
+    __shared__ uint32_t s_split[4];  // gate/up pairs [0, 1), down outputs [2, 3)
+
+    const uint32_t ne = k_ne_rows & 0xFFFFu, rows = k_ne_rows >> 16;
+    const uint32_t d = k_d_stride & 0xFFFFu, stride = k_d_stride >> 16;
+    const uint32_t units = d / 8u;  // 16-byte units of a row
+    const bool router_wave = blockIdx.x < ne && wave < rows;
+    // every load of the first phase goes out before any is waited for: the
+    // router row and es (router waves), the epoch, the gains, the token rows
+    uint4 rw[kRouterChunks], rev[kRouterChunks];
+    if (router_wave) {
+        const uint16_t* w_row = global_ptr(k_router_w) + (uint64_t)blockIdx.x * d;
+        const uint16_t* eg = global_ptr(k_es);
+#pragma unroll
+        for (int i = 0; i < kRouterChunks; ++i) {
+            const uint32_t cc = min(lane + 64u * i, units - 1u);
+            rw[i] = *reinterpret_cast<const uint4*>(w_row + cc * 8u);
+            rev[i] = *reinterpret_cast<const uint4*>(eg + cc * 8u);
+        }
+    }
+    const uint32_t epoch = ld_coherent(global_ptr(k_sync) + kVerifyEpochWord);
+    const uint32_t gain = t < ne ? global_ptr(k_pes)[t] : 0u;
+    const uint32_t total = rows * units;
+    const bool same = k_x == k_hidden;
+    const uint16_t* hg = global_ptr(k_hidden);
+    const uint16_t* xg = global_ptr(k_x);
+    uint4 hv[kVerifyXUnits], xv[kVerifyXUnits];
+#pragma unroll
+    for (int i = 0; i < kVerifyXUnits; ++i) {
+        if ((uint32_t)i * kVerifyThreads >= total) break;
+        const uint32_t q = min(t + (uint32_t)i * kVerifyThreads, total - 1u);
+        const uint32_t r = q / units, c = q - r * units;
+        hv[i] = *reinterpret_cast<const uint4*>(hg + (uint64_t)r * stride + c * 8u);
+        if (!same) xv[i] = *reinterpret_cast<const uint4*>(xg + (uint64_t)r * stride + c * 8u);
+    }
+    if (t < kArgWords) reinterpret_cast<uint32_t*>(&a)[t] = arg_word;
+    if (t < kMaxExperts) {
+        s_gains[t] = gain;
+        s_cnt[t] = 0u;
+    }
+    if (t < kMaxRouterRows * kMaskWords) s_mask[t] = 0u;
+    if (t == 0) s_bad = 0u;
+    const uint32_t row_h = lds_chunks_halves(d);
+    const VerifyLds ld0 = verify_lds(rows, d, 0u, SYM);
+    uint4* xn = reinterpret_cast<uint4*>(smem);
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem + ld0.xs);
+    float* xsum = reinterpret_cast<float*>(smem + ld0.xsum);
+#pragma unroll
+    for (int i = 0; i < kVerifyXUnits; ++i) {
+        if ((uint32_t)i * kVerifyThreads >= total) break;
+        const uint32_t q = t + (uint32_t)i * kVerifyThreads;
+        if (q < total) {
+            const uint32_t r = q / units, c = q - r * units;
+            xn[q] = hv[i];
+            *reinterpret_cast<uint4*>(xs + r * row_h + (c >> 2) * kChunkLds + (c & 3u) * 8u) =
+                pair_permute(same ? hv[i] : xv[i]);
+        }
+    }
+    if (t == 0) {
+        const uint32_t tg = epoch + 1u;
+        s_tag = tg ? tg : 1u;  // the words start at tag 0
+    }
+    __syncthreads();
+    const uint32_t tag = s_tag;
+    const uint32_t f = a.f;
+    uint64_t* words = global_ptr(a.words);
+    DecodeSync sy{};
+    sy.error = global_ptr(a.sync_words) + kSyncErrorWord;
+    const uint32_t grp = blockIdx.x % kDecodeGroups;
+
+    // 1. router row blockIdx.x against token row `wave`
+    if (router_wave) {
+        uint4 xr[kRouterChunks];
+#pragma unroll
+        for (int i = 0; i < kRouterChunks; ++i) xr[i] = xn[wave * units + min(lane + 64u * i, units - 1u)];
+        const float s = router_chunks_dot(rw, xr, rev, units, lane);
+        if (lane < kDecodeGroups)
+            st_coherent(words + lane * kVerifyLogitRegion + wave * kMaxExperts + blockIdx.x,
+                        tagged(tag, __float_as_uint(s)));
+    }
+    if (t == 0) st_coherent(words + kVerifyArriveWord + blockIdx.x, tagged(tag, 1u));
+    if constexpr (!SYM) staged_chunk_sums(xs, row_h, rows, d, xsum);
+
+    // 2. token `wave`'s top-8 from this group's replica
+    if (wave < rows) {
+        uint32_t key[4] = {0u, 0u, 0u, 0u};
+        uint32_t live = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) live |= lane + 64u * j < ne ? 1u << j : 0u;
+        const uint64_t* lg = words + grp * kVerifyLogitRegion + wave * kMaxExperts;
+        poll_tagged<4, kPollSleepLogits>(sy, tag, live, [&](int j) { return lg + lane + 64u * j; },
+                                         [&](int j, uint32_t bits) {
+                                             const float v = __uint_as_float(bits);
+                                             key[j] = (v == v && v != -INFINITY) ? order_key(v) : 0u;
+                                         });
+        if (lane < kTopK) {
+            s_sid[wave][lane] = 0u;
+            s_sfill[wave][lane] = 0u;
+            s_skey[wave][lane] = 0u;
+        }
+        wave_select_top8(key, (ne + 3u) & ~3u, s_cand[wave], s_sid[wave], s_sfill[wave],
+                         s_skey[wave]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // one wave: LDS in order
+        const uint32_t sl = lane & (kTopK - 1u);
+        const uint32_t id = s_sid[wave][sl];
+        const float my_s = s_sfill[wave][sl] ? order_key_value(s_skey[wave][sl]) : -INFINITY;
+        const uint16_t wb = slot_softmax_lane(my_s, bf16_to_f32((uint16_t)s_gains[id]));
+        if (lane < kTopK) {
+            s_pe[wave * kTopK + lane] = id;
+            s_pw[wave * kTopK + lane] = wb;
+            if (!s_sfill[wave][lane]) s_bad = 1u;
+        }
+    }
+    __syncthreads();
+    // Fewer than 8 eligible logits for a token (NaN or -inf scores) leave
+    // slots unfilled, naming expert 0 twice or more in one token: every block
+    // sees it (the same selection everywhere), writes NaN for its outputs and
+    // the launch reports it; the routing outputs are still written.
+    const uint32_t np = rows * kTopK;
+    const uint32_t nc_all = rows * d;
+    const uint32_t cb0 = blockIdx.x * nc_all / kDecodeBlocks;
+    const uint32_t cb1 = (blockIdx.x + 1u) * nc_all / kDecodeBlocks;
+    const auto epoch_advance = [&] {
+        // every block has read the epoch once its arrival word is in: the
+        // next launch may use tag + 1
+        if (blockIdx.x == 0 && wave == kVerifyWaves - 1u) {
+            poll_tagged<kDecodeBlocks / 64u, kPollSleepActs>(
+                sy, tag, (1u << (kDecodeBlocks / 64u)) - 1u,
+                [&](int j) { return words + kVerifyArriveWord + lane + 64u * j; },
+                [&](int, uint32_t) {});
+            if (lane == 0) st_coherent(global_ptr(a.sync_words) + kVerifyEpochWord, tag);
+        }
+    };
+    if (s_bad) {
+        if (blockIdx.x == 0 && t < np) {
+            global_ptr(a.out_idx)[t] = s_pe[t];
+            global_ptr(a.out_w)[t] = (uint16_t)s_pw[t];
+        }
+        if (blockIdx.x == 0 && t == 0) atomicOr(sy.error, kErrRowsBlock);
+        for (uint32_t c = cb0 + t; c < cb1; c += kVerifyThreads) global_ptr(a.h2)[c] = 0x7E00u;
+        epoch_advance();
+        return;
+    }
+    // The grouping (group_router_rows' counting sort, in LDS): per-expert
+    // counts and per-token expert masks, one scan over the experts (counts
+    // and presence packed), then pair p's sorted row = its expert's offset +
+    // the earlier tokens that chose the expert; slot u is the u-th expert
+    // present, its rows those pairs in token order.
+    const bool my_pair = t < np;
+    const uint32_t my_e = my_pair ? s_pe[t] : 0u, my_tok = t / kTopK;
+    if (my_pair) {
+        atomicAdd(&s_cnt[my_e], 1u);
+        atomicOr(&s_mask[my_tok * kMaskWords + (my_e >> 5)], 1u << (my_e & 31u));
+    }
+    lds_barrier();
+    const uint32_t ecnt = t < ne ? s_cnt[t] : 0u;
+    const uint32_t packed = ecnt | ((ecnt ? 1u : 0u) << 16);
+    const uint32_t incl = t < kMaxExperts ? wave_inclusive_scan(packed) : 0u;
+    if (t < kMaxExperts && lane == 63u) s_wtot[wave] = incl;
+    lds_barrier();
+    if (t < kMaxExperts) {
+        uint32_t base = 0, total = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < kMaxExperts / 64u; ++w) {
+            base += w < wave ? s_wtot[w] : 0u;
+            total += s_wtot[w];
+        }
+        const uint32_t excl = base + incl - packed;
+        s_off[t] = excl & 0xFFFFu;
+        if (ecnt) {
+            s_uexp[excl >> 16] = t;
+            s_ustart[excl >> 16] = excl & 0xFFFFu;
+        }
+        if (t == 0) {
+            s_nslots = total >> 16;
+            s_ustart[total >> 16] = np;
+        }
+    }
+    lds_barrier();
+    if (my_pair) {
+        uint32_t rank = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < kMaxRouterRows; ++q)
+            rank += q < my_tok ? (s_mask[q * kMaskWords + (my_e >> 5)] >> (my_e & 31u)) & 1u : 0u;
+        s_sp[s_off[my_e] + rank] = t;
+        if (blockIdx.x == 0) {
+            global_ptr(a.out_idx)[t] = my_e;
+            global_ptr(a.out_w)[t] = (uint16_t)s_pw[t];
+        }
+    }
+    // This block's ranges of the gate/up pairs (per slot f, 0) and the down
+    // outputs (per slot d, 2): block b takes the units whose cost falls in
+    // [b C / NB, (b + 1) C / NB) of the total C; down ranges start on even
+    // outputs (row pairs never straddle a slot: d is even).
+    if (t >= 64u && t < 68u) {
+        const uint32_t q = t - 64u, per = q < 2u ? a.f : d;
+        const uint32_t nsl = s_nslots;
+        uint32_t total = 0;
+        for (uint32_t u = 0; u < nsl; ++u)
+            total += per * (kVerifyUnitBase + kVerifyRowCost * (s_ustart[u + 1u] - s_ustart[u]));
+        const uint32_t cpos = (uint32_t)((uint64_t)(blockIdx.x + (q & 1u)) * total / kDecodeBlocks);
+        uint32_t pc = 0, unit = nsl * per;
+        for (uint32_t u = 0; u < nsl; ++u) {
+            const uint32_t w = kVerifyUnitBase + kVerifyRowCost * (s_ustart[u + 1u] - s_ustart[u]);
+            if (cpos < pc + per * w) {
+                unit = u * per + (cpos - pc + w - 1u) / w;
+                break;
+            }
+            pc += per * w;
+        }
+        s_split[q] = q < 2u ? unit : unit & ~1u;
+    }
+    __syncthreads();
+    const uint32_t nslots = s_nslots;
+    const uint8_t* layer_base = global_ptr(a.layer_base);
+    uint64_t* acts_w = words + kVerifyActWord;
+
+    // 3. gate/up: this block's pairs [pb0, pb0 + npb) of the nslots * f. A
+    // 16-lane group takes one pair, its gate row and its up row (lane j holds
+    // chunks j, j + 16, ... of both, the rows path's lane geometry and per-row
+    // steps over the slot's rows, picked from the staged token rows), so each
+    // staged activation chunk is read from LDS once for the two rows; a wave
+    // takes 4 pairs per pass.
+    const uint32_t np_all = nslots * f;
+    const uint32_t pb0 = s_split[0], npb = s_split[1] - pb0;
+    const uint32_t j16 = lane & 15u;
+    const uint32_t nck_d = d / 32u;
+    for (uint32_t k0 = 4u * wave; k0 < npb; k0 += 4u * kVerifyWaves) {  // wave-uniform
+        const uint32_t k = k0 + (lane >> 4);
+        const bool live = k < npb;
+        const uint32_t p = min(pb0 + k, np_all - 1u);
+        const uint32_t u = p / f, fi = p - u * f;
+        const uint32_t start = s_ustart[u], m = s_ustart[u + 1u] - start;
+        const uint8_t* blob = layer_base + (uint64_t)s_uexp[u] * a.expert_stride;
+        const uint32_t ng = d / G;
+        const uint8_t* gw = blob + a.o.gate_w + (uint64_t)fi * (d / 2u);
+        const uint8_t* uw = blob + a.o.up_w + (uint64_t)fi * (d / 2u);
+        const uint16_t* gs = reinterpret_cast<const uint16_t*>(blob + a.o.gate_s) + (uint64_t)fi * ng;
+        const uint16_t* us = reinterpret_cast<const uint16_t*>(blob + a.o.up_s) + (uint64_t)fi * ng;
+        const uint16_t* gb = reinterpret_cast<const uint16_t*>(blob + a.o.gate_b) + (uint64_t)fi * ng;
+        const uint16_t* ub = reinterpret_cast<const uint16_t*>(blob + a.o.up_b) + (uint64_t)fi * ng;
+        ChunkBatch<kGUBatch> bg, bu;
+        load_batch<G, SYM, kGUBatch, kGULanes>(gw, gs, gb, 0u, j16, nck_d, bg);
+        load_batch<G, SYM, kGUBatch, kGULanes>(uw, us, ub, 0u, j16, nck_d, bu);
+        uint32_t rt = 0;
+#pragma unroll
+        for (uint32_t r = 0; r < kMaxRouterRows; ++r)
+            rt |= (s_sp[start + min(r, m - 1u)] >> 3) << (3u * r);  // the rows' tokens, 3 bits each
+        float ag[kMaxRouterRows], au[kMaxRouterRows];
+#pragma unroll
+        for (uint32_t r = 0; r < kMaxRouterRows; ++r) {
+            ag[r] = 0.0f;
+            au[r] = 0.0f;
+        }
+        gemv_batches_picked2<G, SYM, kGUBatch, kGULanes, (int)kMaxRouterRows>(
+            gw, gs, gb, uw, us, ub, j16, nck_d, bg, bu, xs, row_h, xsum, rt, m, ag, au);
+#pragma unroll
+        for (uint32_t r = 0; r < kMaxRouterRows; ++r) {
+            const float gsum = group16_sum(ag[r]), usum = group16_sum(au[r]);
+            if (live && j16 == 0 && r < m)
+                st_coherent(acts_w + (uint64_t)(start + r) * f + fi,
+                            tagged(tag, f32_to_f16(gate_activation<ACT>(gsum) * usum)));
+        }
+    }
+
+    // 4. down: this block's outputs [qb0, qb0 + nqb) of the nslots * d (at
+    // most d of them: two slots at most). An 8-lane group takes two adjacent
+    // output rows (the ranges start on even outputs and d is even, so both
+    // are of one slot; lane j holds chunks j, j + 8, ... of both, decode's
+    // per-row steps), so each staged activation chunk is read once for the
+    // two rows; a wave takes 16 rows per pass and requests its first pass's
+    // rows before the activations are in.
+    const uint32_t nq_all = nslots * d;
+    const uint32_t qb0 = s_split[2], nqb = s_split[3] - qb0;
+    const uint32_t j8 = lane & 7u;
+    const uint32_t nck_f = f / 32u;
+    struct DownPair {
+        const uint8_t* w;
+        const uint16_t* s;
+        const uint16_t* b;
+        uint32_t u, n;
+        bool live;
+    };
+    // rows q0 + 2 k and q0 + 2 k + 1 share u; the second row's weights are
+    // f / 2 bytes and f / G groups further on
+    const auto dn_pair = [&](uint32_t k, ChunkBatch<kDBatch>& b0, ChunkBatch<kDBatch>& b1) {
+        DownPair p;
+        p.live = 2u * k < nqb;
+        const uint32_t q = min(qb0 + 2u * k, nq_all - 2u);
+        p.u = q / d;
+        p.n = q - p.u * d;
+        const uint8_t* blob = layer_base + (uint64_t)s_uexp[p.u] * a.expert_stride;
+        const uint32_t ng = f / G;
+        p.w = blob + a.o.down_w + (uint64_t)p.n * (f / 2u);
+        p.s = reinterpret_cast<const uint16_t*>(blob + a.o.down_s) + (uint64_t)p.n * ng;
+        p.b = reinterpret_cast<const uint16_t*>(blob + a.o.down_b) + (uint64_t)p.n * ng;
+        load_batch<G, SYM, kDBatch, kDLanes>(p.w, p.s, p.b, 0u, j8, nck_f, b0);
+        load_batch<G, SYM, kDBatch, kDLanes>(p.w + f / 2u, p.s + ng, p.b + ng, 0u, j8, nck_f, b1);
+        return p;
+    };
+    constexpr uint32_t kDnPass = 8u * kVerifyWaves;  // row pairs per pass of the block
+    const bool dn_a = 16u * wave < nqb;
+    DownPair da{};
+    ChunkBatch<kDBatch> da0, da1;
+    if (dn_a) da = dn_pair(8u * wave + (lane >> 3), da0, da1);
+    epoch_advance();
+    uint64_t* parts = words + kVerifyPartWord;
+    // the activation rows of the (at most two) slots the range covers
+    // (nqb == 0, block-uniform, only when nslots * d < kDecodeBlocks)
+    if (nqb != 0) {
+        const uint32_t u_lo = qb0 / d, u_hi = (qb0 + nqb - 1u) / d;
+        const uint32_t st_lo = s_ustart[u_lo], m_lo = s_ustart[u_lo + 1u] - st_lo;
+        const uint32_t st_hi = s_ustart[u_hi];
+        const uint32_t m_hi = u_hi != u_lo ? s_ustart[u_hi + 1u] - st_hi : 0u;
+        const uint32_t arows = m_lo + m_hi;  // <= 2 * rows
+        const VerifyLds ldf = verify_lds(rows, d, f, SYM);
+        uint16_t* as = reinterpret_cast<uint16_t*>(smem + ldf.as);
+        float* asum = reinterpret_cast<float*>(smem + ldf.asum);
+        const uint32_t row_hf = lds_chunks_halves(f);
+        // thread t gathers column fi = t (+ kVerifyThreads ...) of every
+        // staged row, 8 rows per poll
+        for (uint32_t fi0 = 0; fi0 < f; fi0 += kVerifyThreads) {
+            const uint32_t fi = fi0 + t;
+            const uint32_t c = fi & 31u;
+            uint16_t* dst = as + (fi >> 5) * kChunkLds + (c >> 3) * 8u + paired_pos(c & 7u);
+            for (uint32_t r0 = 0; r0 < arows; r0 += kMaxRouterRows) {
+                const uint32_t nr = min(arows - r0, kMaxRouterRows);
+                poll_tagged<kMaxRouterRows, kPollSleepActs>(
+                    sy, tag, fi < f ? (1u << nr) - 1u : 0u,
+                    [&](int k) {
+                        const uint32_t r = r0 + k;
+                        const uint32_t sr = r < m_lo ? st_lo + r : st_hi + (r - m_lo);
+                        return acts_w + (uint64_t)sr * f + fi;
+                    },
+                    [&](int k, uint32_t bits) { dst[(r0 + k) * row_hf] = (uint16_t)bits; });
+            }
+        }
+        __syncthreads();
+        if constexpr (!SYM) {
+            staged_chunk_sums(as, row_hf, arows, f, asum);
+            __syncthreads();
+        }
+        const auto dn_run = [&](const DownPair& p, ChunkBatch<kDBatch>& b0, ChunkBatch<kDBatch>& b1) {
+            const bool hi = p.u != u_lo;
+            const uint32_t st = hi ? st_hi : st_lo, m = hi ? m_hi : m_lo;
+            const uint32_t ng = f / G;
+            float a0[kMaxRouterRows], a1[kMaxRouterRows];
+#pragma unroll
+            for (uint32_t r = 0; r < kMaxRouterRows; ++r) {
+                a0[r] = 0.0f;
+                a1[r] = 0.0f;
+            }
+            gemv_batches_picked2<G, SYM, kDBatch, kDLanes, (int)kMaxRouterRows>(
+                p.w, p.s, p.b, p.w + f / 2u, p.s + ng, p.b + ng, j8, nck_f, b0, b1,
+                as + (hi ? m_lo : 0u) * row_hf, row_hf, asum + (hi ? m_lo : 0u) * nck_f,
+                kRowsInOrder, m, a0, a1);
+#pragma unroll
+            for (uint32_t r = 0; r < kMaxRouterRows; ++r) {
+                const float v0 = group8_sum(a0[r]), v1 = group8_sum(a1[r]);
+                if (p.live && j8 == 0 && r < m) {
+                    uint64_t* dst = parts + (uint64_t)s_sp[st + r] * d + p.n;
+                    st_coherent(dst, tagged(tag, (uint32_t)f32_to_f16(v0)));
+                    st_coherent(dst + 1, tagged(tag, (uint32_t)f32_to_f16(v1)));
+                }
+            }
+        };
+        if (dn_a) dn_run(da, da0, da1);
+        for (uint32_t k0 = kDnPass; 2u * k0 < nqb; k0 += kDnPass) {
+            if (2u * (k0 + 8u * wave) >= nqb) break;  // wave-uniform
+            ChunkBatch<kDBatch> dc0, dc1;
+            const DownPair dc = dn_pair(k0 + 8u * wave + (lane >> 3), dc0, dc1);
+            dn_run(dc, dc0, dc1);
+        }
+    }
+
+    // 5. the token-major sum over this block's outputs [cb0, cb1)
+    for (uint32_t c0 = cb0; c0 < cb1; c0 += kVerifyThreads) {
+        const uint32_t c = c0 + t;
+        const bool live = c < cb1;
+        const uint32_t tok = live ? c / d : 0u, n = live ? c - tok * d : 0u;
+        uint32_t pv[kTopK];
+        poll_tagged<kTopK, kPollSleepParts>(
+            sy, tag, live ? (1u << kTopK) - 1u : 0u,
+            [&](int r) { return parts + (uint64_t)(tok * kTopK + r) * d + n; },
+            [&](int r, uint32_t bits) { pv[r] = bits; });
+        if (live) {
+            float acc = 0.0f;
+#pragma unroll
+            for (uint32_t r = 0; r < kTopK; ++r)
+                acc = __builtin_fmaf(f16_to_f32((uint16_t)s_pw[tok * kTopK + r]),
+                                     f16_to_f32((uint16_t)pv[r]), acc);
+            global_ptr(a.h2)[(uint64_t)tok * d + n] = f32_to_f16(acc);
+        }
+    }
+}
+
 // ------------------------------------------------------------ host helpers
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -2198,4 +2690,99 @@ extern "C" tsg_status tsg_prefill_router_bf16(tsg_moe* moe, tsg_stream stream,
                 "queryCount %u exceeds the %u-row prompt chunk", query_count, kMaxPromptRows);
     return router_launch(moe, as_stream(stream), w, hidden, stride, es, pes, out_idx, out_w,
                          nullptr, query_count, ne, d, top_k, true);
+}
+
+// ------------------------------------------------------ verify layer (host)
+
+namespace tsg {
+namespace {
+
+template <int G, bool SYM, int ACT>
+tsg_status launch_verify(tsg_moe* moe, hipStream_t stream, const uint16_t* router_w,
+                         const uint16_t* hidden, const uint16_t* es, const uint16_t* pes,
+                         const uint16_t* x, uint32_t stride, const VerifyLayerArgs& a) {
+    const size_t lds = verify_lds(a.rows, a.d, a.f, SYM).bytes;
+    auto kern = verify_layer_kernel<G, SYM, ACT>;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(TSG_ERR_DECLINED, "verify layer: %zu bytes of LDS do not fit", lds);
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, (int)kVerifyThreads, lds) !=
+            hipSuccess ||
+        (uint64_t)per_cu * (uint64_t)moe->ctx->num_cus < kDecodeBlocks) {
+        (void)hipGetLastError();
+        return fail(TSG_ERR_DECLINED, "verify layer: %u blocks are not co-resident",
+                    kDecodeBlocks);
+    }
+    hipLaunchKernelGGL(kern, dim3(kDecodeBlocks), dim3(kVerifyThreads), lds, stream, router_w,
+                       hidden, es, pes, x, a.sync_words, a.ne | (a.rows << 16),
+                       a.d | (stride << 16), a);
+    return check_launch("verify_layer");
+}
+
+}  // namespace
+}  // namespace tsg
+
+extern "C" tsg_status tsg_moe_verify_layer(tsg_moe* moe, tsg_stream stream,
+                                           const tsg_layer* layer, const uint16_t* router_w,
+                                           const uint16_t* router_hidden, const uint16_t* es,
+                                           const uint16_t* pes, const uint16_t* x,
+                                           uint32_t hidden_stride, uint16_t* h2,
+                                           uint32_t* out_idx, uint16_t* out_w,
+                                           uint32_t row_count, uint32_t ne, uint32_t d,
+                                           uint32_t f, uint32_t top_k) {
+    tsg_status st = check_moe(moe);
+    if (st) return st;
+    TSG_REQUIRE(moe->router_weight_bits == 16u, TSG_ERR_INVALID_ARGUMENT,
+                "the verify layer takes BF16 router weights (a MoE created with 16-bit router "
+                "weights), this MoE has %u-bit ones", moe->router_weight_bits);
+    if ((st = check_decode_shape(moe->ctx, d, f, top_k))) return st;
+    TSG_REQUIRE(layer, TSG_ERR_INVALID_ARGUMENT, "layer is NULL");
+    TSG_REQUIRE(ne > 0 && ne <= layer->num_experts && ne <= kMaxExperts, TSG_ERR_INVALID_ARGUMENT,
+                "router has %u experts but the layer holds %u", ne, layer->num_experts);
+    TSG_REQUIRE(router_w && router_hidden && es && pes && x && h2 && out_idx && out_w,
+                TSG_ERR_INVALID_ARGUMENT, "NULL verify-layer operand");
+    TSG_REQUIRE(aligned16(router_w) && aligned16(router_hidden) && aligned16(es) &&
+                    aligned16(x) && hidden_stride % 8u == 0,
+                TSG_ERR_ALIGNMENT, "router weights and token rows must be 16-byte aligned");
+    TSG_REQUIRE(hidden_stride >= d, TSG_ERR_INVALID_ARGUMENT, "hidden stride %u < d=%u",
+                hidden_stride, d);
+    if (row_count == 0 || row_count > kMaxRouterRows)
+        return fail(TSG_ERR_DECLINED, "the verify layer takes 1..%u rows, got %u", kMaxRouterRows,
+                    row_count);
+    if (ne < kTopK || d % 64u || f % 64u || d > kMaxFusedDim || f > kMaxFusedDim ||
+        hidden_stride > 0xFFFFu)
+        return fail(TSG_ERR_DECLINED, "verify layer shape (ne=%u, d=%u, f=%u, stride %u) not "
+                                      "taken by the one launch", ne, d, f, hidden_stride);
+    VerifyLayerArgs a{};
+    a.layer_base = layer->base;
+    a.expert_stride = layer->expert_stride;
+    a.o = layer->offsets;
+    a.h2 = h2;
+    a.out_idx = out_idx;
+    a.out_w = out_w;
+    a.words = moe->ctx->verify_words;
+    a.sync_words = moe->ctx->counters;
+    a.ne = ne;
+    a.d = d;
+    a.f = f;
+    a.rows = row_count;
+    const tsg_ctx* ctx = moe->ctx;
+    const bool sym = ctx->scheme == TSG_SYM;
+    const bool silu = moe->activation == TSG_ACT_SILU;
+    hipStream_t s = as_stream(stream);
+#define TSG_VL(GG, SS)                                                                        \
+    return silu ? launch_verify<GG, SS, TSG_ACT_SILU>(moe, s, router_w, router_hidden, es, pes, \
+                                                      x, hidden_stride, a)                     \
+                : launch_verify<GG, SS, TSG_ACT_GELU_TANH>(moe, s, router_w, router_hidden, es, \
+                                                           pes, x, hidden_stride, a)
+    if (ctx->group_size == 32) {
+        if (sym) TSG_VL(32, true);
+        TSG_VL(32, false);
+    }
+    if (sym) TSG_VL(64, true);
+    TSG_VL(64, false);
+#undef TSG_VL
 }

@@ -91,6 +91,84 @@ __device__ __forceinline__ void compute_batch(const ChunkBatch<KB>& bt, uint32_t
     }
 }
 
+// compute_batch's several-row form for two weight rows of one lane with the
+// same chunk positions (a gate row in bt0, its up row in bt1), over rows
+// picked from a larger staging: row r is staged row (rt >> 3r) & 7 (at xs +
+// row * row_h, sums at xsum + row * nchunks). Each staged chunk of a picked
+// row is read from LDS once for both weight rows, and each weight row takes
+// compute_batch's steps (the same dot2 sequence per chunk, the same fma per
+// chunk), so its bits are the same as when it is computed alone.
+template <int G, bool SYM, int KB, int LANES, int R>
+__device__ __forceinline__ void compute_batch_picked2(const ChunkBatch<KB>& bt0,
+                                                      const ChunkBatch<KB>& bt1, uint32_t base,
+                                                      uint32_t j, uint32_t nchunks,
+                                                      const uint16_t* xs, uint32_t row_h,
+                                                      const float* xsum, uint32_t rt,
+                                                      uint32_t nrows, float* acc0, float* acc1) {
+    static_assert(R <= 8, "three bits per picked row");
+    const h2_t bias = SYM ? h2_t{(_Float16)1032.0f, (_Float16)1032.0f}
+                          : h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+        const uint32_t c = base + j + LANES * i;
+        const uint32_t cc = min(c, nchunks - 1u);
+        const bool live = c < nchunks;
+        const float s0 = bf16_to_f32((uint16_t)bt0.s[i]), s1 = bf16_to_f32((uint16_t)bt1.s[i]);
+        float b0 = 0.0f, b1 = 0.0f;
+        if constexpr (!SYM) {
+            b0 = bf16_to_f32((uint16_t)bt0.b[i]);
+            b1 = bf16_to_f32((uint16_t)bt1.b[i]);
+        }
+        h2_t q0[16], q1[16];
+        chunk_pairs(bt0.w[i], bias, q0);
+        chunk_pairs(bt1.w[i], bias, q1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if ((uint32_t)r >= nrows) break;
+            const uint32_t row = (rt >> (3 * r)) & 7u;
+            const h2_t* xp = staged_chunk(xs + (size_t)row * row_h, cc);
+            float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const h2_t x = xp[k];
+                d0 = dot2(q0[k], x, d0);
+                d1 = dot2(q1[k], x, d1);
+            }
+            float v0 = __builtin_fmaf(s0, d0, acc0[r]);
+            float v1 = __builtin_fmaf(s1, d1, acc1[r]);
+            if constexpr (!SYM) {
+                const float xsm = xsum[row * nchunks + cc];
+                v0 = __builtin_fmaf(b0, xsm, v0);
+                v1 = __builtin_fmaf(b1, xsm, v1);
+            }
+            acc0[r] = live ? v0 : acc0[r];
+            acc1[r] = live ? v1 : acc1[r];
+        }
+        // one chunk at a time: the scheduler would otherwise unpack later
+        // chunks' weights ahead (32 registers each) and spill
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Both rows' whole segments (compute_batch_picked2); bt0 / bt1 hold the first
+// batches, requested by the caller.
+template <int G, bool SYM, int KB, int LANES, int R, int WA = 16>
+__device__ __forceinline__ void gemv_batches_picked2(
+    const uint8_t* __restrict__ w0, const uint16_t* __restrict__ s0,
+    const uint16_t* __restrict__ b0, const uint8_t* __restrict__ w1,
+    const uint16_t* __restrict__ s1, const uint16_t* __restrict__ b1, uint32_t j,
+    uint32_t nchunks, ChunkBatch<KB>& bt0, ChunkBatch<KB>& bt1, const uint16_t* xs,
+    uint32_t row_h, const float* xsum, uint32_t rt, uint32_t nrows, float* acc0, float* acc1) {
+    compute_batch_picked2<G, SYM, KB, LANES, R>(bt0, bt1, 0u, j, nchunks, xs, row_h, xsum, rt, nrows,
+                                                acc0, acc1);
+    for (uint32_t base = LANES * KB; base < nchunks; base += LANES * KB) {
+        load_batch<G, SYM, KB, LANES, WA>(w0, s0, b0, base, j, nchunks, bt0);
+        load_batch<G, SYM, KB, LANES, WA>(w1, s1, b1, base, j, nchunks, bt1);
+        compute_batch_picked2<G, SYM, KB, LANES, R>(bt0, bt1, base, j, nchunks, xs, row_h, xsum, rt,
+                                                    nrows, acc0, acc1);
+    }
+}
+
 // A whole row segment: the first batch, already requested into `bt` by the
 // caller with load_batch (so its loads can go out early), then the rest
 // batch by batch. The first batch sits outside the loop so the compiler's

@@ -48,6 +48,7 @@ struct tsg_ctx {
     uint32_t* counters = nullptr;        // kMaxCounters
     float* logits = nullptr;             // kMaxPromptRows * kMaxExperts
     uint16_t* act_replicas = nullptr;    // kActReplicas * kActReplicaHalves
+    uint64_t* verify_words = nullptr;    // kVerifyWords: the one-launch verify layer's hand-offs
     // this device's copy of the no-alloc grouping scratch (a file-scope device
     // array of prefill.hip, not owned: never freed)
     uint32_t* group_rank_scratch = nullptr;
@@ -148,6 +149,21 @@ constexpr uint32_t kMaxCombineRows = 16;  // output rows one block combines: cei
 constexpr uint32_t kMaxSharedF = 512;     // shared-expert intermediate size of the one-launch layer
 
 constexpr uint32_t kTopK = 8;
+
+// The one-launch verify layer: its launch epoch (a word of ctx->counters past
+// the router areas) and its hand-off words (ctx->verify_words, tagged 64-bit):
+// per-group replicas of the rows' logits, one arrival word per block, the
+// activation rows of the sorted pairs (f words each) and the route partials of
+// the token-major pairs (d words each).
+constexpr uint32_t kVerifyEpochWord = 9600;
+static_assert(kVerifyEpochWord >= kRouterLogitWord + kMaxRouterRows * 2 * kMaxExperts &&
+                  kVerifyEpochWord < kMaxCounters, "verify epoch word");
+constexpr uint32_t kVerifyPairs = kMaxRouterRows * kTopK;  // 64
+constexpr uint32_t kVerifyLogitRegion = kMaxRouterRows * kMaxExperts;
+constexpr uint32_t kVerifyArriveWord = kDecodeGroups * kVerifyLogitRegion;
+constexpr uint32_t kVerifyActWord = kVerifyArriveWord + kDecodeBlocks;
+constexpr uint32_t kVerifyPartWord = kVerifyActWord + kVerifyPairs * kMaxFusedDim;
+constexpr uint32_t kVerifyWords = kVerifyPartWord + kVerifyPairs * kMaxFusedDim;
 
 // Pairs (t * k) tsg_prefill_group_pairs_device_noalloc takes: its file-scope
 // rank scratch holds one word per pair.
