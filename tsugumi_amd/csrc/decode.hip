@@ -1877,24 +1877,28 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
     // This block's ranges of the gate/up pairs (per slot f, 0) and the down
     // outputs (per slot d, 2): block b takes the units whose cost falls in
     // [b C / NB, (b + 1) C / NB) of the total C; down ranges start on even
-    // outputs (row pairs never straddle a slot: d is even).
-    if (t >= 64u && t < 68u) {
-        const uint32_t q = t - 64u, per = q < 2u ? a.f : d;
+    // outputs (row pairs never straddle a slot: d is even). One wave: lane u
+    // holds slot u's unit cost and its inclusive prefix; the slot of a cost
+    // position is the first lane whose prefix passes it.
+    if (wave == 1) {
         const uint32_t nsl = s_nslots;
-        uint32_t total = 0;
-        for (uint32_t u = 0; u < nsl; ++u)
-            total += per * (kVerifyUnitBase + kVerifyRowCost * (s_ustart[u + 1u] - s_ustart[u]));
-        const uint32_t cpos = (uint32_t)((uint64_t)(blockIdx.x + (q & 1u)) * total / kDecodeBlocks);
-        uint32_t pc = 0, unit = nsl * per;
-        for (uint32_t u = 0; u < nsl; ++u) {
-            const uint32_t w = kVerifyUnitBase + kVerifyRowCost * (s_ustart[u + 1u] - s_ustart[u]);
-            if (cpos < pc + per * w) {
-                unit = u * per + (cpos - pc + w - 1u) / w;
-                break;
+        const uint32_t w = lane < nsl ? kVerifyUnitBase + kVerifyRowCost * (s_ustart[lane + 1u] - s_ustart[lane]) : 0u;
+        const uint32_t wsum = wave_inclusive_scan(w);
+        const uint32_t wtot = (uint32_t)__builtin_amdgcn_readlane((int)wsum, 63);
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t per = q < 2u ? a.f : d;
+            const uint64_t cpos = (uint64_t)(blockIdx.x + (q & 1u)) * per * wtot / kDecodeBlocks;
+            const uint64_t past = __ballot(lane < nsl && (uint64_t)per * wsum > cpos);
+            uint32_t unit = nsl * per;
+            if (past) {
+                const uint32_t us = (uint32_t)__builtin_ctzll(past);
+                const uint32_t wu = (uint32_t)__builtin_amdgcn_readlane((int)w, (int)us);
+                const uint32_t pu = (uint32_t)__builtin_amdgcn_readlane((int)wsum, (int)us) - wu;
+                unit = us * per + (uint32_t)((cpos - (uint64_t)per * pu + wu - 1u) / wu);
             }
-            pc += per * w;
+            if (lane == 0) s_split[q] = q < 2u ? unit : unit & ~1u;
         }
-        s_split[q] = q < 2u ? unit : unit & ~1u;
     }
     __syncthreads();
     const uint32_t nslots = s_nslots;
