@@ -705,12 +705,15 @@ def run_qwen(tsg, torch, args):
             "decode_m3": {"us_per_layer": round(us3, 3), "mean_union": round(u3, 2),
                           "GBps": round(bytes3 / (us3 * 1e-6) / 1e9, 2),
                           "bytes_per_layer": int(bytes3), "launches_per_layer": nl3,
-                          "path": "routed experts in one launch (tsg_moe_verify_layer: router "
-                                  "rows, top-8, grouping, rows path, reduce) beside the shared "
-                                  "expert over the 3 rows (2 launches, second stream)",
+                          "path": "the shared expert over the 3 rows (2 launches), then the "
+                                  "routed experts in one launch (tsg_moe_verify_layer: router "
+                                  "rows, top-8, grouping, rows path, reduce) on the same stream",
                           "four_launches": {"us_per_layer": round(us34, 3),
                                             "mean_union": round(u34, 2),
-                                            "launches_per_layer": nl34}},
+                                            "launches_per_layer": nl34,
+                                            "path": "router rows + grouping, two rows-path "
+                                                    "launches, reduce; the shared expert beside "
+                                                    "them on a second stream"}},
             "prefill_t4096": prefill_summary(pre)}
 
 
