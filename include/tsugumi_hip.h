@@ -297,8 +297,12 @@ tsg_status tsg_moe_decode_layer(tsg_moe* moe, tsg_stream stream, const tsg_layer
  * hidden_stride elements apart. Returns TSG_ERR_DECLINED, with nothing
  * launched, for row_count 0 or > 8, num_experts < 8, d or f not a multiple of
  * 64 or above 4096, or when the launch's blocks cannot all be resident (the
- * caller then encodes those three calls). No counterpart entry in the
- * reference, which encodes the steps as separate dispatches. */
+ * caller then encodes those three calls). Its hand-off words and launch
+ * epoch live in the context: verify-layer launches on one context must not
+ * overlap (one stream, or streams ordered by events), and work on other
+ * streams meanwhile delays the launch (its blocks wait on each other);
+ * tsg_ctx_synchronize reports a hand-off wait that timed out. No counterpart
+ * entry in the reference, which encodes the steps as separate dispatches. */
 tsg_status tsg_moe_verify_layer(tsg_moe* moe, tsg_stream stream, const tsg_layer* layer,
                                 const uint16_t* router_weights, const uint16_t* router_hidden,
                                 const uint16_t* effective_scale,
@@ -351,8 +355,11 @@ tsg_status tsg_moe_decode_layer_shared(tsg_moe* moe, tsg_stream stream, const ts
 
 /* tsg_moe_decode_layer runs as one launch (grid barriers between router,
  * gate/up and down) whenever every block fits on the device at once, else as
- * router + phase 1 + phase 2 launches; both give identical bits. enabled = 0
- * forces the three-launch form (no reference counterpart; for A/B checks). */
+ * router + phase 1 + phase 2 launches; both give identical bits. The one
+ * launch keeps its hand-off words and launch epoch in the context, so such
+ * launches on one context must not overlap (one stream, or streams ordered
+ * by events). enabled = 0 forces the three-launch form (no reference
+ * counterpart; for A/B checks). */
 tsg_status tsg_moe_set_fused_decode(tsg_moe* moe, int enabled);
 
 /* ------------------------------------------------- Qwen shared expert ----
