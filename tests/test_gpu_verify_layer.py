@@ -236,3 +236,33 @@ def test_verify_layer_declines(tsg, ctx, gemma_layer):
     with pytest.raises(tsg._abi.TsgError) as e:  # the layer holds 128 experts
         moe.encode_verify_layer(layer, rw, x, es, pes, x, d, h2, idx, w, 5, 129, d, f)
     assert e.value.status == tsg._abi.TSG_ERR_INVALID_ARGUMENT
+
+
+def test_verify_layer_reports_unroutable_token(tsg, ctx, gemma_layer):
+    """A token whose router logits are all NaN leaves its top-8 unfilled: the
+    one launch writes NaN outputs, still writes the routing (expert 0 in the
+    unfilled slots), every block exits, and tsg_ctx_synchronize reports the
+    error; the next call on the context is correct again."""
+    configure(ctx, 32, "sym")
+    layer, _, _ = gemma_layer
+    d, f, ne, m = 2816, 704, 128, 3
+    moe = tsg.MoE(ctx)
+    rng = np.random.default_rng(0xBAD)
+    hidden, rw, es, pes = router_inputs(rng, m, d, ne, d)
+    bad = hidden.reshape(m, d).copy()
+    bad[1, :] = 0x7E00  # token 1: NaN hidden state, NaN logits
+    RW, ES, PES = dev(rw), dev(es), dev(pes)
+    idx, w, h2 = fused_outs(m, d)
+    moe.encode_verify_layer(layer, RW, dev(bad.ravel()), ES, PES, dev(bad.ravel()), d, h2, idx, w,
+                            m, ne, d, f)
+    with pytest.raises(tsg._abi.TsgError) as e:
+        ctx.synchronize()
+    assert e.value.status == tsg._abi.TSG_ERR_INVALID_ARGUMENT
+    assert np.isnan(oracle.f16_to_float(host(h2, np.uint16))).all()
+    assert (host(idx, np.uint32).reshape(m, K)[1] == 0).all()
+    X = dev(hidden)
+    want = separate(tsg, ctx, moe, layer, RW, X, X, ES, PES, m, d, f, ne, d)
+    idx, w, h2 = fused_outs(m, d)
+    moe.encode_verify_layer(layer, RW, X, ES, PES, X, d, h2, idx, w, m, ne, d, f)
+    ctx.synchronize()
+    assert np.array_equal(host(h2, np.uint16), want[2])

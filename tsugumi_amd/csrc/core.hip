@@ -188,6 +188,10 @@ extern "C" tsg_status tsg_ctx_synchronize(tsg_ctx* ctx, tsg_stream stream) {
             return fail(TSG_ERR_INVALID_ARGUMENT,
                         "rows path: a device block had no rows, more than 8, or an expert past "
                         "the layer; it was skipped");
+        if (err & kErrVerifyRouting)
+            return fail(TSG_ERR_INVALID_ARGUMENT,
+                        "verify layer: a token had fewer than 8 eligible router logits (NaN or "
+                        "-inf scores); the layer's outputs are NaN");
         if (err & kErrRouterWait)
             return fail(TSG_ERR_HIP, "staged router: the selecting block timed out waiting for "
                                      "the other blocks' logits; the routing is invalid");

@@ -1601,23 +1601,27 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
 //     and posts the logit to the kDecodeGroups replicas (tagged words);
 //  2. every block polls its group's replica and selects each token's top-8 on
 //     wave r (wave_select_top8 + slot_softmax_lane, the rows router's steps),
-//     then groups the rows * 8 pairs by (expert, pair) on one wave: slot u is
-//     the u-th routed expert, its rows its pairs in token order (the device
+//     then groups the rows * 8 pairs by a counting sort in LDS: slot u is the
+//     u-th routed expert, its rows its pairs in token order (the device
 //     grouping's sorted order);
-//  3. gate/up: the U * f (slot, f) pairs are dealt to the blocks in equal
-//     contiguous ranges, 32 lanes a pair (the rows path's lane geometry and
-//     per-row steps over the slot's rows, picked from the staged token rows);
-//     each activation row entry is posted as a tagged word;
-//  4. down: the U * d (slot, row) outputs likewise; a block's range covers at
-//     most two slots, whose activation rows it gathers into LDS; each route
-//     partial half(down . act) is posted as a tagged word;
+//  3. gate/up: the U * f (slot, f) pairs are split over the blocks in
+//     contiguous ranges of equal cost (a pair of a slot with m rows costs
+//     kVerifyUnitBase + kVerifyRowCost * m); a 16-lane group holds a pair's
+//     gate and up rows (the rows path's lane geometry and per-row steps over
+//     the slot's rows, picked from the staged token rows); each activation is
+//     posted as a tagged word;
+//  4. down: the U * d (slot, row) outputs likewise, an 8-lane group holding
+//     two adjacent rows; a block's range covers at most two slots, whose
+//     activation rows it gathers into LDS (each wave's first rows requested
+//     before the gather); each route partial half(down . act) is posted as a
+//     tagged word;
 //  5. the token-major sum h2[t, n] = half(sum_r fma(w[t, r], P[t, r, n]))
 //     over the blocks' equal ranges of the rows * d outputs.
-// The next pass's weights of a wave are requested before the current pass
-// runs (two gate/up passes, then two down passes ahead of the activation
-// gather). The tag is the verify epoch + 1; every block posts an arrival
-// word once it holds the tag, and block 0 advances the epoch after seeing all
-// of them. Polls are bounded (timeouts set the error word).
+// The tag is the verify epoch + 1; every block posts an arrival word once it
+// holds the tag, and block 0 advances the epoch after seeing all of them.
+// Polls are bounded (timeouts set the error word). A token with fewer than 8
+// eligible logits (NaN or -inf scores) makes every block write NaN outputs and
+// the launch report the error.
 constexpr uint32_t kVerifyThreads = 512;  // 8 waves of up to 256 VGPRs
 constexpr uint32_t kVerifyWaves = kVerifyThreads / 64u;
 constexpr int kVerifyXUnits = (int)((kMaxRouterRows * 512u + kVerifyThreads - 1u) / kVerifyThreads);
@@ -1658,7 +1662,6 @@ __host__ __device__ __forceinline__ VerifyLds verify_lds(uint32_t rows, uint32_t
     l.bytes = l.asum + (sym ? 0u : 2u * rows * (f / 32u) * 4u);
     return l;
 }
-
 
 template <int G, bool SYM, int ACT>
 // The values the first loads need are leading scalar arguments (14 dwords,
@@ -1822,7 +1825,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
             global_ptr(a.out_idx)[t] = s_pe[t];
             global_ptr(a.out_w)[t] = (uint16_t)s_pw[t];
         }
-        if (blockIdx.x == 0 && t == 0) atomicOr(sy.error, kErrRowsBlock);
+        if (blockIdx.x == 0 && t == 0) atomicOr(sy.error, kErrVerifyRouting);
         for (uint32_t c = cb0 + t; c < cb1; c += kVerifyThreads) global_ptr(a.h2)[c] = 0x7E00u;
         epoch_advance();
         return;

@@ -119,7 +119,8 @@ constexpr uint32_t kSyncErrorWord = 1056;  // device-side error bits (kErr*), re
 // the layer (skipped); the fused grouped GEMM's down item that waited too long
 // for its block's gate/up tiles, or an XCD queue no workgroup drained; a
 // grouped-GEMM block (device list) naming an expert past the layer (skipped);
-// the staged router's selector that timed out waiting for a logit.
+// the staged router's selector that timed out waiting for a logit; a verify
+// layer whose token had fewer than 8 eligible router logits.
 constexpr uint32_t kErrDecodeTimeout = 1u;
 constexpr uint32_t kErrGroupExpertRange = 2u;
 constexpr uint32_t kErrGroupBlocks = 4u;
@@ -127,6 +128,7 @@ constexpr uint32_t kErrRowsBlock = 8u;  // a device-list rows-path block it cann
 constexpr uint32_t kErrGemmWait = 16u;  // the fused GEMM: a wait timed out or a queue not drained
 constexpr uint32_t kErrGemmBlock = 32u;  // a grouped-GEMM block names an expert past the layer
 constexpr uint32_t kErrRouterWait = 64u;  // the staged router's selector timed out on a logit
+constexpr uint32_t kErrVerifyRouting = 128u;  // the verify layer: a token with fewer than 8 eligible logits
 constexpr uint32_t kSyncLogitWord = 1088;  // tagged 64-bit logits, kMaxExperts per group
 static_assert(kSyncLogitWord + kDecodeGroups * 2 * kMaxExperts <= kMaxCounters, "sync area overflow");
 // The staged router's hand-off (rows <= kMaxRouterRows): its launch epoch and
