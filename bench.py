@@ -542,12 +542,13 @@ def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, n
     router rows (RealForwardRunner.swift:1826-1872) and the grouping of their
     pairs (:2116-2151) in one launch, the rows path over the device block
     list and the token-major reduce; `shared` (Qwen) adds the
-    shared expert over the M rows (two launches). The M hidden states of a layer
+    shared expert over the M rows. The M hidden states of a layer
     share a common part (x0 + 0.35 N(0,1)), so their top-8 sets overlap (a
-    union of about 12-20). `fused`: the whole routed layer as one launch
-    (tsg_moe_verify_layer); otherwise the router + grouping launch, the two
-    rows-path launches and the reduce. Returns us per layer, the mean union
-    and the launches per layer."""
+    union of about 12-20). `fused`: the whole layer, the shared expert
+    included, as one launch (tsg_moe_verify_layer / _shared); otherwise the
+    router + grouping launch, the two rows-path launches and the reduce, with
+    the shared expert's two launches on a second stream. Returns us per
+    layer, the mean union and the launches per layer."""
     k = TOPK
     rng = np.random.default_rng(seed)
     hid = np.empty((n_layers, m, h), np.float32)
@@ -583,16 +584,20 @@ def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, n
             x = hidden[l * m * h:(l + 1) * m * h]
             il, wl = idx[l * m * k:(l + 1) * m * k], wts[l * m * k:(l + 1) * m * k]
             nb = nbs[l:l + 1]
-            if shared is not None:
-                # beside the four launches on a second stream; ahead of the one
-                # launch on the same stream (that launch needs every CU)
-                if not fused:
-                    side.wait_stream(stream)
+            if shared is not None and not fused:
+                # beside the four launches on a second stream
+                side.wait_stream(stream)
                 blob, o, gw = shared[l]
                 tsg.encode_shared_expert_rows(moe, blob, o, x, h, gw, sact,
                                               sout[l * m * h:(l + 1) * m * h], m, h, f,
-                                              stream=stream if fused else side)
-            if fused:
+                                              stream=side)
+            if fused and shared is not None:
+                blob, o, gw = shared[l]
+                moe.encode_verify_layer_shared(layers[l], routers[l], x, ones_h, ones_e, x, h,
+                                               h2[l * m * h:(l + 1) * m * h], il, wl, blob, o, gw,
+                                               sout[l * m * h:(l + 1) * m * h], m, ne, h, f,
+                                               stream=stream)
+            elif fused:
                 moe.encode_verify_layer(layers[l], routers[l], x, ones_h, ones_e, x, h,
                                         h2[l * m * h:(l + 1) * m * h], il, wl, m, ne, h, f,
                                         stream=stream)
@@ -618,7 +623,7 @@ def run_verify_layer(tsg, torch, ctx, moe, layers, routers, n_layers, m, h, f, n
     unions = [len(set(r.tolist())) for r in ids]
     if not fused and not np.array_equal(nbs.cpu().numpy(), unions):
         raise RuntimeError("device grouping's block count differs from the routing's union")
-    launches = (1 if fused else 1 + 2 + 1) + (2 if shared is not None else 0)
+    launches = 1 if fused else 1 + 2 + 1 + (2 if shared is not None else 0)
     return ms * 1000.0 / n_layers, float(np.mean(unions)), launches
 
 
@@ -705,9 +710,9 @@ def run_qwen(tsg, torch, args):
             "decode_m3": {"us_per_layer": round(us3, 3), "mean_union": round(u3, 2),
                           "GBps": round(bytes3 / (us3 * 1e-6) / 1e9, 2),
                           "bytes_per_layer": int(bytes3), "launches_per_layer": nl3,
-                          "path": "the shared expert over the 3 rows (2 launches), then the "
-                                  "routed experts in one launch (tsg_moe_verify_layer: router "
-                                  "rows, top-8, grouping, rows path, reduce) on the same stream",
+                          "path": "one launch (tsg_moe_verify_layer_shared: router rows, "
+                                  "top-8, grouping, rows path over the routed experts and the "
+                                  "shared expert, shared gate, reduce)",
                           "four_launches": {"us_per_layer": round(us34, 3),
                                             "mean_union": round(u34, 2),
                                             "launches_per_layer": nl34,

@@ -312,6 +312,28 @@ tsg_status tsg_moe_verify_layer(tsg_moe* moe, tsg_stream stream, const tsg_layer
                                 uint32_t row_count, uint32_t num_experts, uint32_t d, uint32_t f,
                                 uint32_t top_k);
 
+/* tsg_moe_verify_layer for a Qwen-family layer: the shared expert's branch
+ * over the same row_count token rows (encodeSharedExpert per row,
+ * QwenForwardRunner.swift:1548-1578, beside the routed experts of
+ * :1580-1608) in the same launch. shared_blob / shared_offsets hold its three
+ * int4 projections (the ctx's group size and scheme; gate/up [f, d], down
+ * [d, f]: its intermediate size is the routed experts' f), shared_gate_weight
+ * its bf16 gate row [d] (16-byte aligned). shared_out [row_count, d] gets
+ * bit for bit what tsg_moe_shared_expert_rows gives on x; h2 and the routing
+ * are tsg_moe_verify_layer's. Needs no act scratch (the activations pass
+ * through the context's hand-off words). Declines as tsg_moe_verify_layer,
+ * and for a MoE whose activation is not SiLU; an unroutable token makes
+ * shared_out NaN as well. No counterpart entry in the reference, which
+ * encodes the shared branch as separate dispatches. */
+tsg_status tsg_moe_verify_layer_shared(
+    tsg_moe* moe, tsg_stream stream, const tsg_layer* layer, const uint16_t* router_weights,
+    const uint16_t* router_hidden, const uint16_t* effective_scale,
+    const uint16_t* per_expert_scale, const uint16_t* x, uint32_t hidden_stride_elements,
+    uint16_t* h2, uint32_t* out_indices, uint16_t* out_weights, const void* shared_blob,
+    const tsg_expert_offsets* shared_offsets, const uint16_t* shared_gate_weight,
+    uint16_t* shared_out, uint32_t row_count, uint32_t num_experts, uint32_t d, uint32_t f,
+    uint32_t top_k);
+
 /* tsg_moe_decode_layer with the INT8-affine router (a MoE created with
  * router_weight_bits 8; encodeRouterGemma4, MoE.swift:201-257, then the two
  * phases, as RealForwardRunner.swift:3104-3330 encodes them per layer): the

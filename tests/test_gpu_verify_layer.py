@@ -13,7 +13,10 @@ its reduce, PrefillGroupedRoutedMoETests+Execution.swift:213-310):
   (every slot holds every row);
 - calls in a row with fewer rows, and HIP-graph replays of one capture with
   new inputs between them (the launch epoch advances on the device);
-- the shapes the one launch declines.
+- the shapes the one launch declines;
+- the shared form (tsg_moe_verify_layer_shared, the Qwen family's shared
+  expert in the same launch) against tsg_moe_verify_layer +
+  tsg_moe_shared_expert_rows, bit for bit, and the oracle's shared expert.
 """
 import numpy as np
 import pytest
@@ -266,3 +269,136 @@ def test_verify_layer_reports_unroutable_token(tsg, ctx, gemma_layer):
     moe.encode_verify_layer(layer, RW, X, ES, PES, X, d, h2, idx, w, m, ne, d, f)
     ctx.synchronize()
     assert np.array_equal(host(h2, np.uint16), want[2])
+
+
+def shared_expert_inputs(rng, d, f, scheme, group):
+    """One shared expert (gate/up [f, d], down [d, f]) and its bf16 gate row."""
+    if scheme == "sym":
+        image, _, soffs, sblobs = wl.random_sym_layer(rng, 1, d, f)
+    else:
+        krng = oracle.seed_tree_key(0x5B, f"verify-shared-{d}-{f}")
+        experts = [[kc.quantized_rows(krng, r, c, group, False, -0.3, 0.3)
+                    for (r, c) in ((f, d), (f, d), (d, f))]]
+        image, _, soffs, sblobs = kc.layer_image(experts, False, keep_biases=True)
+    gate_w = oracle.bf16_bits((rng.normal(0.0, 1.0 / np.sqrt(d), d)).astype(np.float32))
+    return image, soffs, sblobs[0], gate_w
+
+
+@pytest.mark.parametrize("m,pad,distinct", [(3, 0, False), (3, 32, True), (1, 0, False),
+                                            (8, 0, False)])
+def test_verify_layer_shared_matches_separate_launches(tsg, ctx, qwen_layer, m, pad, distinct):
+    """tsg_moe_verify_layer_shared at configs[4]'s shape (256 experts, d=2048,
+    f=512, shared expert f=512): h2 and the routing equal
+    tsg_moe_verify_layer's, the shared output tsg_moe_shared_expert_rows' on
+    the experts' rows, bit for bit, then calls in a row with fewer rows; the
+    shared rows against the oracle's shared expert."""
+    configure(ctx, 32, "sym")
+    (layer, offs, blobs), d, f, ne = qwen_layer, 2048, 512, 256
+    stride = d + pad
+    rng = np.random.default_rng(0x5E1 + 13 * m + pad)
+    image, soffs, sblob, gate_w = shared_expert_inputs(rng, d, f, "sym", 32)
+    SB, G = dev(image), dev(gate_w)
+    moe = tsg.MoE(ctx, gate_activation="silu")
+    _, rw, es, pes = router_inputs(rng, m, d, ne, stride)
+    RW, ES, PES = dev(rw), dev(es), dev(pes)
+    for mm in (m, max(1, m - 1)):
+        hidden = router_inputs(rng, mm, d, ne, stride)[0]
+        xin = router_inputs(rng, mm, d, ne, stride)[0] if distinct else hidden
+        RH = dev(hidden)
+        X = dev(xin) if distinct else RH
+        idx0, w0, h20 = fused_outs(mm, d)
+        moe.encode_verify_layer(layer, RW, RH, ES, PES, X, stride, h20, idx0, w0, mm, ne, d, f)
+        sact, sout0 = empty(mm * f), empty(mm * d, fill=NAN16)
+        tsg.encode_shared_expert_rows(moe, SB, soffs, X, stride, G, sact, sout0, mm, d, f)
+        idx, w, h2 = fused_outs(mm, d)
+        sout = empty(mm * d, fill=NAN16)
+        moe.encode_verify_layer_shared(layer, RW, RH, ES, PES, X, stride, h2, idx, w, SB, soffs,
+                                       G, sout, mm, ne, d, f)
+        ctx.synchronize()
+        assert np.array_equal(host(idx, np.uint32), host(idx0, np.uint32))
+        assert np.array_equal(host(w, np.uint16), host(w0, np.uint16))
+        assert np.array_equal(host(h2, np.uint16), host(h20, np.uint16)), mm
+        got = host(sout, np.uint16).reshape(mm, d).copy()
+        assert np.array_equal(got, host(sout0, np.uint16).reshape(mm, d)), mm
+        x_rows = xin.reshape(mm, stride)[:, :d]
+        for r in (0, mm - 1):
+            ref = oracle.shared_expert(sblob, soffs, x_rows[r].copy(), gate_w, d, f, 32, True)
+            rel = oracle.relative_error(oracle.f16_to_float(got[r]), oracle.f16_to_float(ref))
+            print(f"shared M={mm} pad={pad} distinct={distinct} row {r}: rel={rel:.3e}")
+            assert rel <= kc.NORTH_STAR, (mm, r, rel)
+
+
+def test_verify_layer_shared_affine_every_expert(tsg, ctx):
+    """The shared form on a small affine g64 layer of 8 experts (d = f = 320,
+    every slot holds every row) with an affine shared expert: the same bits
+    as tsg_moe_verify_layer + tsg_moe_shared_expert_rows."""
+    configure(ctx, 64, "affine")
+    try:
+        d = f = 320
+        ne, m = 8, 6
+        rng = oracle.seed_tree_key(0xB0, "verify-shared-affine")
+        experts = [[kc.quantized_rows(rng, r, c, 64, False, -0.3, 0.3)
+                    for (r, c) in ((f, d), (f, d), (d, f))] for _ in range(ne)]
+        image, stride, offs, _ = kc.layer_image(experts, False, keep_biases=True)
+        layer = upload(tsg, ctx, image, ne, stride, offs)
+        nrng = np.random.default_rng(0xB0)
+        simage, soffs, sblob, gate_w = shared_expert_inputs(nrng, d, f, "affine", 64)
+        SB, G = dev(simage), dev(gate_w)
+        hidden, rw, es, pes = router_inputs(nrng, m, d, ne, d)
+        RW, X, ES, PES = dev(rw), dev(hidden), dev(es), dev(pes)
+        moe = tsg.MoE(ctx, gate_activation="silu")
+        idx0, w0, h20 = fused_outs(m, d)
+        moe.encode_verify_layer(layer, RW, X, ES, PES, X, d, h20, idx0, w0, m, ne, d, f)
+        sact, sout0 = empty(m * f), empty(m * d, fill=NAN16)
+        tsg.encode_shared_expert_rows(moe, SB, soffs, X, d, G, sact, sout0, m, d, f)
+        idx, w, h2 = fused_outs(m, d)
+        sout = empty(m * d, fill=NAN16)
+        moe.encode_verify_layer_shared(layer, RW, X, ES, PES, X, d, h2, idx, w, SB, soffs, G,
+                                       sout, m, ne, d, f)
+        ctx.synchronize()
+        assert np.array_equal(host(idx, np.uint32), host(idx0, np.uint32))
+        assert np.array_equal(host(h2, np.uint16), host(h20, np.uint16))
+        got = host(sout, np.uint16).reshape(m, d).copy()
+        assert np.array_equal(got, host(sout0, np.uint16).reshape(m, d))
+        ref = oracle.shared_expert(sblob, soffs, hidden.reshape(m, d)[2].copy(), gate_w, d, f, 64,
+                                   False)
+        rel = oracle.relative_error(oracle.f16_to_float(got[2]), oracle.f16_to_float(ref))
+        print(f"shared affine g64 M={m}: row 2 rel={rel:.3e}")
+        assert rel <= kc.NORTH_STAR
+    finally:
+        configure(ctx, 32, "sym")
+
+
+def test_verify_layer_shared_declines_and_unroutable(tsg, ctx, qwen_layer):
+    """The shared form declines a GeGLU MoE; an unroutable token makes its
+    shared output NaN too, and the next call is correct."""
+    configure(ctx, 32, "sym")
+    (layer, offs, blobs), d, f, ne, m = qwen_layer, 2048, 512, 256, 3
+    rng = np.random.default_rng(0x5ED)
+    image, soffs, sblob, gate_w = shared_expert_inputs(rng, d, f, "sym", 32)
+    SB, G = dev(image), dev(gate_w)
+    hidden, rw, es, pes = router_inputs(rng, m, d, ne, d)
+    RW, ES, PES = dev(rw), dev(es), dev(pes)
+    idx, w, h2 = fused_outs(m, d)
+    sout = empty(m * d, fill=0)
+    with pytest.raises(tsg._abi.TsgError) as e:
+        tsg.MoE(ctx).encode_verify_layer_shared(layer, RW, dev(hidden), ES, PES, dev(hidden), d,
+                                                h2, idx, w, SB, soffs, G, sout, m, ne, d, f)
+    assert e.value.status == tsg._abi.TSG_ERR_DECLINED
+    moe = tsg.MoE(ctx, gate_activation="silu")
+    bad = hidden.reshape(m, d).copy()
+    bad[2, :] = 0x7E00
+    B = dev(bad.ravel())
+    moe.encode_verify_layer_shared(layer, RW, B, ES, PES, B, d, h2, idx, w, SB, soffs, G, sout, m,
+                                   ne, d, f)
+    with pytest.raises(tsg._abi.TsgError) as e:
+        ctx.synchronize()
+    assert e.value.status == tsg._abi.TSG_ERR_INVALID_ARGUMENT
+    assert np.isnan(oracle.f16_to_float(host(sout, np.uint16))).all()
+    X = dev(hidden)
+    sact, sout0 = empty(m * f), empty(m * d)
+    tsg.encode_shared_expert_rows(moe, SB, soffs, X, d, G, sact, sout0, m, d, f)
+    moe.encode_verify_layer_shared(layer, RW, X, ES, PES, X, d, h2, idx, w, SB, soffs, G, sout, m,
+                                   ne, d, f)
+    ctx.synchronize()
+    assert np.array_equal(host(sout, np.uint16), host(sout0, np.uint16))

@@ -451,6 +451,23 @@ class MoE:
             hidden_stride, _ptr(h2), _ptr(out_indices), _ptr(out_weights), row_count,
             num_experts, d, f, top_k))
 
+    def encode_verify_layer_shared(self, layer: ResidentLayer, router_weights, router_hidden,
+                                   effective_scale, per_expert_scale, x, hidden_stride, h2,
+                                   out_indices, out_weights, shared_blob, shared_offsets,
+                                   shared_gate_weight, shared_out, row_count, num_experts, d, f,
+                                   top_k=8, stream=None):
+        """encode_verify_layer with the Qwen family's shared expert over the
+        same rows in the same launch (its intermediate size f): shared_out
+        [row_count, d] gets encode_shared_expert_rows' bits. Raises
+        TsgError(TSG_ERR_DECLINED) when the one launch does not fit."""
+        o = offsets_from(shared_offsets)
+        check(self.lib.tsg_moe_verify_layer_shared(
+            self.handle, _stream(stream), layer.handle, _ptr(router_weights),
+            _ptr(router_hidden), _ptr(effective_scale), _ptr(per_expert_scale), _ptr(x),
+            hidden_stride, _ptr(h2), _ptr(out_indices), _ptr(out_weights), _ptr(shared_blob),
+            C.byref(o), _ptr(shared_gate_weight), _ptr(shared_out), row_count, num_experts, d,
+            f, top_k))
+
     def encode_decode_layer_int8(self, layer: ResidentLayer, router_weights, router_scales,
                                  router_biases, router_hidden, effective_scale,
                                  per_expert_scale, x, residual, y, out_indices, out_weights,

@@ -125,6 +125,8 @@ SIGNATURES = {
                                        U32]),
     "tsg_moe_verify_layer": (C.c_int, [P, P, P, P, P, P, P, P, U32, P, P, P, U32, U32, U32, U32,
                                        U32]),
+    "tsg_moe_verify_layer_shared": (C.c_int, [P, P, P, P, P, P, P, P, U32, P, P, P, P, P, P, P,
+                                              U32, U32, U32, U32, U32]),
     "tsg_moe_decode_layer_int8": (C.c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, U32,
                                             U32, U32, U32]),
     "tsg_moe_decode_layer_shared": (C.c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P,

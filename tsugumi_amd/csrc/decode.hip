@@ -1622,6 +1622,14 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
 // Polls are bounded (timeouts set the error word). A token with fewer than 8
 // eligible logits (NaN or -inf scores) makes every block write NaN outputs and
 // the launch report the error.
+// SH: the Qwen family's shared expert over the same rows (encodeSharedExpert
+// per row, QwenForwardRunner.swift:1548-1578) is one more slot with every row,
+// after the routed ones, in both splits; its pairs post
+// half(silu(half(g)) * half(u)), its down rows take the shared down kernel's
+// lane geometry (16 lanes a row) and are written as
+// half(half(down . act) * sigmoid(gate_w . x_r)) with the logits summed by
+// gate_logit_wave, so the shared output is bit for bit
+// tsg_moe_shared_expert_rows'.
 constexpr uint32_t kVerifyThreads = 512;  // 8 waves of up to 256 VGPRs
 constexpr uint32_t kVerifyWaves = kVerifyThreads / 64u;
 constexpr int kVerifyXUnits = (int)((kMaxRouterRows * 512u + kVerifyThreads - 1u) / kVerifyThreads);
@@ -1633,6 +1641,10 @@ constexpr int kVerifyXUnits = (int)((kMaxRouterRows * 512u + kVerifyThreads - 1u
 constexpr uint32_t kVerifyUnitBase = 3;
 constexpr uint32_t kVerifyRowCost = 1;
 constexpr uint32_t kRowsInOrder = 0xFAC688u;  // rows 0..7 as 3-bit picks
+// Chunks per lane per batch of a shared-expert down row (16 lanes a row, as
+// the shared down kernel; the batch size does not change a row's bits): one
+// batch up to an intermediate size of 1024.
+constexpr int kShDBatch = 2;
 
 struct VerifyLayerArgs {
     const uint8_t* layer_base;
@@ -1644,6 +1656,12 @@ struct VerifyLayerArgs {
     uint64_t* words;
     uint32_t* sync_words;
     uint32_t ne, d, f, rows;
+    // SH: the Qwen-family shared expert over the same rows (its intermediate
+    // size is f), its bf16 gate row and its [rows, d] output
+    const uint8_t* sh_blob;
+    tsg_expert_offsets sh_o;
+    const uint16_t* sh_gate_w;
+    uint16_t* sh_out;
 };
 
 // Dynamic LDS of the verify layer, in bytes from 0: the token rows in element
@@ -1663,7 +1681,7 @@ __host__ __device__ __forceinline__ VerifyLds verify_lds(uint32_t rows, uint32_t
     return l;
 }
 
-template <int G, bool SYM, int ACT>
+template <int G, bool SYM, int ACT, bool SH>
 // The values the first loads need are leading scalar arguments (14 dwords,
 // preloaded into SGPRs): k_ne_rows = ne | rows << 16, k_d_stride = d |
 // hidden stride << 16.
@@ -1689,6 +1707,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
     __shared__ uint32_t s_mask[kMaxRouterRows * kMaskWords], s_wtot[kMaxExperts / 64u];
     __shared__ uint32_t s_bad;
     __shared__ uint32_t s_split[4];  // gate/up pairs [0, 1), down outputs [2, 3)
+    __shared__ float s_glog[SH ? kMaxRouterRows : 1];  // the rows' shared-expert gate logits
 
     const uint32_t ne = k_ne_rows & 0xFFFFu, rows = k_ne_rows >> 16;
     const uint32_t d = k_d_stride & 0xFFFFu, stride = k_d_stride >> 16;
@@ -1826,7 +1845,10 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
             global_ptr(a.out_w)[t] = (uint16_t)s_pw[t];
         }
         if (blockIdx.x == 0 && t == 0) atomicOr(sy.error, kErrVerifyRouting);
-        for (uint32_t c = cb0 + t; c < cb1; c += kVerifyThreads) global_ptr(a.h2)[c] = 0x7E00u;
+        for (uint32_t c = cb0 + t; c < cb1; c += kVerifyThreads) {
+            global_ptr(a.h2)[c] = 0x7E00u;
+            if constexpr (SH) global_ptr(a.sh_out)[c] = 0x7E00u;
+        }
         epoch_advance();
         return;
     }
@@ -1882,23 +1904,28 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
     // [b C / NB, (b + 1) C / NB) of the total C; down ranges start on even
     // outputs (row pairs never straddle a slot: d is even). One wave: lane u
     // holds slot u's unit cost and its inclusive prefix; the slot of a cost
-    // position is the first lane whose prefix passes it.
+    // position is the first lane whose prefix passes it. SH: the shared
+    // expert is one more slot after the routed ones, with every row.
     if (wave == 1) {
         const uint32_t nsl = s_nslots;
         const uint32_t w = lane < nsl ? kVerifyUnitBase + kVerifyRowCost * (s_ustart[lane + 1u] - s_ustart[lane]) : 0u;
         const uint32_t wsum = wave_inclusive_scan(w);
         const uint32_t wtot = (uint32_t)__builtin_amdgcn_readlane((int)wsum, 63);
+        const uint32_t wsh = SH ? kVerifyUnitBase + kVerifyRowCost * rows : 0u;
 #pragma unroll
         for (uint32_t q = 0; q < 4u; ++q) {
             const uint32_t per = q < 2u ? a.f : d;
-            const uint64_t cpos = (uint64_t)(blockIdx.x + (q & 1u)) * per * wtot / kDecodeBlocks;
+            const uint64_t routed = (uint64_t)per * wtot, total = routed + (uint64_t)per * wsh;
+            const uint64_t cpos = (uint64_t)(blockIdx.x + (q & 1u)) * total / kDecodeBlocks;
             const uint64_t past = __ballot(lane < nsl && (uint64_t)per * wsum > cpos);
-            uint32_t unit = nsl * per;
+            uint32_t unit = (nsl + (SH ? 1u : 0u)) * per;
             if (past) {
                 const uint32_t us = (uint32_t)__builtin_ctzll(past);
                 const uint32_t wu = (uint32_t)__builtin_amdgcn_readlane((int)w, (int)us);
                 const uint32_t pu = (uint32_t)__builtin_amdgcn_readlane((int)wsum, (int)us) - wu;
                 unit = us * per + (uint32_t)((cpos - (uint64_t)per * pu + wu - 1u) / wu);
+            } else if (SH && cpos < total) {
+                unit = nsl * per + (uint32_t)((cpos - routed + wsh - 1u) / wsh);
             }
             if (lane == 0) s_split[q] = q < 2u ? unit : unit & ~1u;
         }
@@ -1914,31 +1941,40 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
     // steps over the slot's rows, picked from the staged token rows), so each
     // staged activation chunk is read from LDS once for the two rows; a wave
     // takes 4 pairs per pass.
-    const uint32_t np_all = nslots * f;
+    // SH: units past the routed pairs are the shared expert's pairs (every
+    // row, the shared kernels' epilogue half(silu(half(g)) * half(u)))
+    const uint32_t np_all = nslots * f, np_units = np_all + (SH ? f : 0u);
     const uint32_t pb0 = s_split[0], npb = s_split[1] - pb0;
     const uint32_t j16 = lane & 15u;
     const uint32_t nck_d = d / 32u;
+    uint64_t* sh_acts_w = words + kVerifySharedActWord;
     for (uint32_t k0 = 4u * wave; k0 < npb; k0 += 4u * kVerifyWaves) {  // wave-uniform
         const uint32_t k = k0 + (lane >> 4);
         const bool live = k < npb;
-        const uint32_t p = min(pb0 + k, np_all - 1u);
-        const uint32_t u = p / f, fi = p - u * f;
-        const uint32_t start = s_ustart[u], m = s_ustart[u + 1u] - start;
-        const uint8_t* blob = layer_base + (uint64_t)s_uexp[u] * a.expert_stride;
+        const uint32_t p = min(pb0 + k, np_units - 1u);
+        const bool shp = SH && p >= np_all;
+        const uint32_t u = shp ? 0u : p / f, fi = shp ? p - np_all : p - u * f;
+        const uint32_t start = shp ? 0u : s_ustart[u];
+        const uint32_t m = shp ? rows : s_ustart[u + 1u] - start;
+        const uint8_t* blob = shp ? global_ptr(a.sh_blob) : layer_base + (uint64_t)s_uexp[u] * a.expert_stride;
+        const tsg_expert_offsets& eo = shp ? a.sh_o : a.o;
         const uint32_t ng = d / G;
-        const uint8_t* gw = blob + a.o.gate_w + (uint64_t)fi * (d / 2u);
-        const uint8_t* uw = blob + a.o.up_w + (uint64_t)fi * (d / 2u);
-        const uint16_t* gs = reinterpret_cast<const uint16_t*>(blob + a.o.gate_s) + (uint64_t)fi * ng;
-        const uint16_t* us = reinterpret_cast<const uint16_t*>(blob + a.o.up_s) + (uint64_t)fi * ng;
-        const uint16_t* gb = reinterpret_cast<const uint16_t*>(blob + a.o.gate_b) + (uint64_t)fi * ng;
-        const uint16_t* ub = reinterpret_cast<const uint16_t*>(blob + a.o.up_b) + (uint64_t)fi * ng;
+        const uint8_t* gw = blob + eo.gate_w + (uint64_t)fi * (d / 2u);
+        const uint8_t* uw = blob + eo.up_w + (uint64_t)fi * (d / 2u);
+        const uint16_t* gs = reinterpret_cast<const uint16_t*>(blob + eo.gate_s) + (uint64_t)fi * ng;
+        const uint16_t* us = reinterpret_cast<const uint16_t*>(blob + eo.up_s) + (uint64_t)fi * ng;
+        const uint16_t* gb = reinterpret_cast<const uint16_t*>(blob + eo.gate_b) + (uint64_t)fi * ng;
+        const uint16_t* ub = reinterpret_cast<const uint16_t*>(blob + eo.up_b) + (uint64_t)fi * ng;
         ChunkBatch<kGUBatch> bg, bu;
         load_batch<G, SYM, kGUBatch, kGULanes>(gw, gs, gb, 0u, j16, nck_d, bg);
         load_batch<G, SYM, kGUBatch, kGULanes>(uw, us, ub, 0u, j16, nck_d, bu);
-        uint32_t rt = 0;
+        uint32_t rt = kRowsInOrder;  // the rows' tokens, 3 bits each
+        if (!shp) {
+            rt = 0u;
 #pragma unroll
-        for (uint32_t r = 0; r < kMaxRouterRows; ++r)
-            rt |= (s_sp[start + min(r, m - 1u)] >> 3) << (3u * r);  // the rows' tokens, 3 bits each
+            for (uint32_t r = 0; r < kMaxRouterRows; ++r)
+                rt |= (s_sp[start + min(r, m - 1u)] >> 3) << (3u * r);
+        }
         float ag[kMaxRouterRows], au[kMaxRouterRows];
 #pragma unroll
         for (uint32_t r = 0; r < kMaxRouterRows; ++r) {
@@ -1950,9 +1986,14 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
 #pragma unroll
         for (uint32_t r = 0; r < kMaxRouterRows; ++r) {
             const float gsum = group16_sum(ag[r]), usum = group16_sum(au[r]);
-            if (live && j16 == 0 && r < m)
-                st_coherent(acts_w + (uint64_t)(start + r) * f + fi,
-                            tagged(tag, f32_to_f16(gate_activation<ACT>(gsum) * usum)));
+            if (live && j16 == 0 && r < m) {
+                if (shp)
+                    st_coherent(sh_acts_w + (uint64_t)r * f + fi,
+                                tagged(tag, silu_mul_h(f32_to_f16(gsum), f32_to_f16(usum))));
+                else
+                    st_coherent(acts_w + (uint64_t)(start + r) * f + fi,
+                                tagged(tag, f32_to_f16(gate_activation<ACT>(gsum) * usum)));
+            }
         }
     }
 
@@ -1962,9 +2003,14 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
     // are of one slot; lane j holds chunks j, j + 8, ... of both, decode's
     // per-row steps), so each staged activation chunk is read once for the
     // two rows; a wave takes 16 rows per pass and requests its first pass's
-    // rows before the activations are in.
+    // rows before the activations are in. SH: outputs past the routed ones
+    // are the shared expert's rows, two per 16-lane group (the shared down
+    // kernel's lane geometry and steps), scaled by the token's gate.
     const uint32_t nq_all = nslots * d;
     const uint32_t qb0 = s_split[2], nqb = s_split[3] - qb0;
+    const uint32_t nqr = qb0 < nq_all ? min(nqb, nq_all - qb0) : 0u;  // routed outputs
+    const uint32_t nqs = nqb - nqr;                                    // shared rows (SH)
+    const uint32_t qs0 = nqs != 0u ? qb0 + nqr - nq_all : 0u;          // the first of them
     const uint32_t j8 = lane & 7u;
     const uint32_t nck_f = f / 32u;
     struct DownPair {
@@ -1978,7 +2024,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
     // f / 2 bytes and f / G groups further on
     const auto dn_pair = [&](uint32_t k, ChunkBatch<kDBatch>& b0, ChunkBatch<kDBatch>& b1) {
         DownPair p;
-        p.live = 2u * k < nqb;
+        p.live = 2u * k < nqr;
         const uint32_t q = min(qb0 + 2u * k, nq_all - 2u);
         p.u = q / d;
         p.n = q - p.u * d;
@@ -1992,19 +2038,33 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
         return p;
     };
     constexpr uint32_t kDnPass = 8u * kVerifyWaves;  // row pairs per pass of the block
-    const bool dn_a = 16u * wave < nqb;
+    const bool dn_a = 16u * wave < nqr;
     DownPair da{};
     ChunkBatch<kDBatch> da0, da1;
     if (dn_a) da = dn_pair(8u * wave + (lane >> 3), da0, da1);
+    // SH: the gate logits of the rows this block's shared outputs scale by
+    if (SH && nqs != 0 && wave < rows) {
+        const float g = gate_logit_wave(xg + (uint64_t)wave * stride, global_ptr(a.sh_gate_w), d);
+        if (lane == 0) s_glog[wave] = g;
+    }
     epoch_advance();
     uint64_t* parts = words + kVerifyPartWord;
     // the activation rows of the (at most two) slots the range covers
     // (nqb == 0, block-uniform, only when nslots * d < kDecodeBlocks)
     if (nqb != 0) {
         const uint32_t u_lo = qb0 / d, u_hi = (qb0 + nqb - 1u) / d;
-        const uint32_t st_lo = s_ustart[u_lo], m_lo = s_ustart[u_lo + 1u] - st_lo;
-        const uint32_t st_hi = s_ustart[u_hi];
-        const uint32_t m_hi = u_hi != u_lo ? s_ustart[u_hi + 1u] - st_hi : 0u;
+        // slot u's activation rows: the sorted rows from s_ustart[u], or
+        // (SH, u == nslots) the shared expert's rows in token order
+        const auto slot_rows = [&](uint32_t u, uint32_t& st, uint32_t& m) {
+            const bool sh = SH && u == nslots;
+            st = sh ? 0u : s_ustart[u];
+            m = sh ? rows : s_ustart[u + 1u] - st;
+            return sh ? sh_acts_w : acts_w + (uint64_t)st * f;
+        };
+        uint32_t st_lo, m_lo, st_hi = 0u, m_hi = 0u;
+        const uint64_t* src_lo = slot_rows(u_lo, st_lo, m_lo);
+        const uint64_t* src_hi = src_lo;
+        if (u_hi != u_lo) src_hi = slot_rows(u_hi, st_hi, m_hi);
         const uint32_t arows = m_lo + m_hi;  // <= 2 * rows
         const VerifyLds ldf = verify_lds(rows, d, f, SYM);
         uint16_t* as = reinterpret_cast<uint16_t*>(smem + ldf.as);
@@ -2022,8 +2082,8 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
                     sy, tag, fi < f ? (1u << nr) - 1u : 0u,
                     [&](int k) {
                         const uint32_t r = r0 + k;
-                        const uint32_t sr = r < m_lo ? st_lo + r : st_hi + (r - m_lo);
-                        return acts_w + (uint64_t)sr * f + fi;
+                        return r < m_lo ? src_lo + (uint64_t)r * f + fi
+                                        : src_hi + (uint64_t)(r - m_lo) * f + fi;
                     },
                     [&](int k, uint32_t bits) { dst[(r0 + k) * row_hf] = (uint16_t)bits; });
             }
@@ -2058,11 +2118,48 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
             }
         };
         if (dn_a) dn_run(da, da0, da1);
-        for (uint32_t k0 = kDnPass; 2u * k0 < nqb; k0 += kDnPass) {
-            if (2u * (k0 + 8u * wave) >= nqb) break;  // wave-uniform
+        for (uint32_t k0 = kDnPass; 2u * k0 < nqr; k0 += kDnPass) {
+            if (2u * (k0 + 8u * wave) >= nqr) break;  // wave-uniform
             ChunkBatch<kDBatch> dc0, dc1;
             const DownPair dc = dn_pair(k0 + 8u * wave + (lane >> 3), dc0, dc1);
             dn_run(dc, dc0, dc1);
+        }
+        if constexpr (SH) {
+            // the shared rows [qs0, qs0 + nqs): 4 row pairs per wave per pass
+            const uint32_t sh_row0 = u_lo == nslots ? 0u : m_lo;  // their staged rows
+            const uint8_t* sb = global_ptr(a.sh_blob);
+            const uint32_t ng = f / G;
+            for (uint32_t k0 = 4u * wave; 2u * k0 < nqs; k0 += 4u * kVerifyWaves) {  // wave-uniform
+                const uint32_t k = k0 + (lane >> 4);
+                const bool live = 2u * k < nqs;
+                const uint32_t n = min(qs0 + 2u * k, d - 2u);
+                const uint8_t* w = sb + a.sh_o.down_w + (uint64_t)n * (f / 2u);
+                const uint16_t* sc = reinterpret_cast<const uint16_t*>(sb + a.sh_o.down_s) + (uint64_t)n * ng;
+                const uint16_t* bi = reinterpret_cast<const uint16_t*>(sb + a.sh_o.down_b) + (uint64_t)n * ng;
+                ChunkBatch<kShDBatch> b0, b1;
+                load_batch<G, SYM, kShDBatch, kGULanes>(w, sc, bi, 0u, j16, nck_f, b0);
+                load_batch<G, SYM, kShDBatch, kGULanes>(w + f / 2u, sc + ng, bi + ng, 0u, j16, nck_f, b1);
+                float a0[kMaxRouterRows], a1[kMaxRouterRows];
+#pragma unroll
+                for (uint32_t r = 0; r < kMaxRouterRows; ++r) {
+                    a0[r] = 0.0f;
+                    a1[r] = 0.0f;
+                }
+                gemv_batches_picked2<G, SYM, kShDBatch, kGULanes, (int)kMaxRouterRows>(
+                    w, sc, bi, w + f / 2u, sc + ng, bi + ng, j16, nck_f, b0, b1,
+                    as + sh_row0 * row_hf, row_hf, asum + sh_row0 * nck_f, kRowsInOrder, rows, a0,
+                    a1);
+#pragma unroll
+                for (uint32_t r = 0; r < kMaxRouterRows; ++r) {
+                    const float v0 = group16_sum(a0[r]), v1 = group16_sum(a1[r]);
+                    if (live && j16 == 0 && r < rows) {
+                        const float gs = qwen_sigmoid(s_glog[r]);
+                        uint16_t* dst = global_ptr(a.sh_out) + (uint64_t)r * d + n;
+                        dst[0] = f32_to_f16(f16_to_f32(f32_to_f16(v0)) * gs);
+                        dst[1] = f32_to_f16(f16_to_f32(f32_to_f16(v1)) * gs);
+                    }
+                }
+            }
         }
     }
 
@@ -2704,12 +2801,12 @@ extern "C" tsg_status tsg_prefill_router_bf16(tsg_moe* moe, tsg_stream stream,
 namespace tsg {
 namespace {
 
-template <int G, bool SYM, int ACT>
+template <int G, bool SYM, int ACT, bool SH>
 tsg_status launch_verify(tsg_moe* moe, hipStream_t stream, const uint16_t* router_w,
                          const uint16_t* hidden, const uint16_t* es, const uint16_t* pes,
                          const uint16_t* x, uint32_t stride, const VerifyLayerArgs& a) {
     const size_t lds = verify_lds(a.rows, a.d, a.f, SYM).bytes;
-    auto kern = verify_layer_kernel<G, SYM, ACT>;
+    auto kern = verify_layer_kernel<G, SYM, ACT, SH>;
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
         (void)hipGetLastError();
@@ -2729,17 +2826,12 @@ tsg_status launch_verify(tsg_moe* moe, hipStream_t stream, const uint16_t* route
     return check_launch("verify_layer");
 }
 
-}  // namespace
-}  // namespace tsg
-
-extern "C" tsg_status tsg_moe_verify_layer(tsg_moe* moe, tsg_stream stream,
-                                           const tsg_layer* layer, const uint16_t* router_w,
-                                           const uint16_t* router_hidden, const uint16_t* es,
-                                           const uint16_t* pes, const uint16_t* x,
-                                           uint32_t hidden_stride, uint16_t* h2,
-                                           uint32_t* out_idx, uint16_t* out_w,
-                                           uint32_t row_count, uint32_t ne, uint32_t d,
-                                           uint32_t f, uint32_t top_k) {
+// The checks and arguments both verify entry points share.
+tsg_status verify_args(tsg_moe* moe, const tsg_layer* layer, const uint16_t* router_w,
+                       const uint16_t* router_hidden, const uint16_t* es, const uint16_t* pes,
+                       const uint16_t* x, uint32_t hidden_stride, uint16_t* h2,
+                       uint32_t* out_idx, uint16_t* out_w, uint32_t row_count, uint32_t ne,
+                       uint32_t d, uint32_t f, uint32_t top_k, VerifyLayerArgs& a) {
     tsg_status st = check_moe(moe);
     if (st) return st;
     TSG_REQUIRE(moe->router_weight_bits == 16u, TSG_ERR_INVALID_ARGUMENT,
@@ -2763,7 +2855,7 @@ extern "C" tsg_status tsg_moe_verify_layer(tsg_moe* moe, tsg_stream stream,
         hidden_stride > 0xFFFFu)
         return fail(TSG_ERR_DECLINED, "verify layer shape (ne=%u, d=%u, f=%u, stride %u) not "
                                       "taken by the one launch", ne, d, f, hidden_stride);
-    VerifyLayerArgs a{};
+    a = VerifyLayerArgs{};
     a.layer_base = layer->base;
     a.expert_stride = layer->expert_stride;
     a.o = layer->offsets;
@@ -2776,15 +2868,34 @@ extern "C" tsg_status tsg_moe_verify_layer(tsg_moe* moe, tsg_stream stream,
     a.d = d;
     a.f = f;
     a.rows = row_count;
+    return TSG_OK;
+}
+
+}  // namespace
+}  // namespace tsg
+
+extern "C" tsg_status tsg_moe_verify_layer(tsg_moe* moe, tsg_stream stream,
+                                           const tsg_layer* layer, const uint16_t* router_w,
+                                           const uint16_t* router_hidden, const uint16_t* es,
+                                           const uint16_t* pes, const uint16_t* x,
+                                           uint32_t hidden_stride, uint16_t* h2,
+                                           uint32_t* out_idx, uint16_t* out_w,
+                                           uint32_t row_count, uint32_t ne, uint32_t d,
+                                           uint32_t f, uint32_t top_k) {
+    VerifyLayerArgs a;
+    tsg_status st = verify_args(moe, layer, router_w, router_hidden, es, pes, x, hidden_stride,
+                                h2, out_idx, out_w, row_count, ne, d, f, top_k, a);
+    if (st) return st;
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
     const bool silu = moe->activation == TSG_ACT_SILU;
     hipStream_t s = as_stream(stream);
 #define TSG_VL(GG, SS)                                                                        \
-    return silu ? launch_verify<GG, SS, TSG_ACT_SILU>(moe, s, router_w, router_hidden, es, pes, \
-                                                      x, hidden_stride, a)                     \
-                : launch_verify<GG, SS, TSG_ACT_GELU_TANH>(moe, s, router_w, router_hidden, es, \
-                                                           pes, x, hidden_stride, a)
+    return silu ? launch_verify<GG, SS, TSG_ACT_SILU, false>(moe, s, router_w, router_hidden, \
+                                                             es, pes, x, hidden_stride, a)    \
+                : launch_verify<GG, SS, TSG_ACT_GELU_TANH, false>(moe, s, router_w,           \
+                                                                  router_hidden, es, pes, x,  \
+                                                                  hidden_stride, a)
     if (ctx->group_size == 32) {
         if (sym) TSG_VL(32, true);
         TSG_VL(32, false);
@@ -2792,4 +2903,47 @@ extern "C" tsg_status tsg_moe_verify_layer(tsg_moe* moe, tsg_stream stream,
     if (sym) TSG_VL(64, true);
     TSG_VL(64, false);
 #undef TSG_VL
+}
+
+extern "C" tsg_status tsg_moe_verify_layer_shared(
+    tsg_moe* moe, tsg_stream stream, const tsg_layer* layer, const uint16_t* router_w,
+    const uint16_t* router_hidden, const uint16_t* es, const uint16_t* pes, const uint16_t* x,
+    uint32_t hidden_stride, uint16_t* h2, uint32_t* out_idx, uint16_t* out_w,
+    const void* shared_blob, const tsg_expert_offsets* shared_offsets,
+    const uint16_t* shared_gate_weight, uint16_t* shared_out, uint32_t row_count, uint32_t ne,
+    uint32_t d, uint32_t f, uint32_t top_k) {
+    VerifyLayerArgs a;
+    tsg_status st = verify_args(moe, layer, router_w, router_hidden, es, pes, x, hidden_stride,
+                                h2, out_idx, out_w, row_count, ne, d, f, top_k, a);
+    if (st) return st;
+    TSG_REQUIRE(shared_blob && shared_offsets && shared_gate_weight && shared_out,
+                TSG_ERR_INVALID_ARGUMENT, "NULL shared-expert operand");
+    const tsg_expert_offsets& o = *shared_offsets;
+    const uint8_t* b = static_cast<const uint8_t*>(shared_blob);
+    TSG_REQUIRE(aligned16(b + o.gate_w) && aligned16(b + o.up_w) && aligned16(b + o.down_w),
+                TSG_ERR_ALIGNMENT, "shared weight sub-tensors must start on 16 bytes");
+    TSG_REQUIRE(((o.gate_s | o.up_s | o.down_s | o.gate_b | o.up_b | o.down_b) & 1u) == 0,
+                TSG_ERR_ALIGNMENT, "shared scale/bias offsets must be even");
+    TSG_REQUIRE(aligned16(shared_gate_weight), TSG_ERR_ALIGNMENT,
+                "the shared gate row must be 16-byte aligned");
+    if (moe->activation != TSG_ACT_SILU)
+        return fail(TSG_ERR_DECLINED, "the shared expert's one-launch form takes SiLU layers "
+                                      "(the Qwen family)");
+    a.sh_blob = b;
+    a.sh_o = o;
+    a.sh_gate_w = shared_gate_weight;
+    a.sh_out = shared_out;
+    const tsg_ctx* ctx = moe->ctx;
+    const bool sym = ctx->scheme == TSG_SYM;
+    hipStream_t s = as_stream(stream);
+#define TSG_VLS(GG, SS)                                                                  \
+    return launch_verify<GG, SS, TSG_ACT_SILU, true>(moe, s, router_w, router_hidden, es, \
+                                                     pes, x, hidden_stride, a)
+    if (ctx->group_size == 32) {
+        if (sym) TSG_VLS(32, true);
+        TSG_VLS(32, false);
+    }
+    if (sym) TSG_VLS(64, true);
+    TSG_VLS(64, false);
+#undef TSG_VLS
 }

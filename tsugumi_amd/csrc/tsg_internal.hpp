@@ -155,8 +155,9 @@ constexpr uint32_t kTopK = 8;
 // The one-launch verify layer: its launch epoch (a word of ctx->counters past
 // the router areas) and its hand-off words (ctx->verify_words, tagged 64-bit):
 // per-group replicas of the rows' logits, one arrival word per block, the
-// activation rows of the sorted pairs (f words each) and the route partials of
-// the token-major pairs (d words each).
+// activation rows of the sorted pairs (f words each), the route partials of
+// the token-major pairs (d words each) and the shared expert's activation
+// rows (f words each).
 constexpr uint32_t kVerifyEpochWord = 9600;
 static_assert(kVerifyEpochWord >= kRouterLogitWord + kMaxRouterRows * 2 * kMaxExperts &&
                   kVerifyEpochWord < kMaxCounters, "verify epoch word");
@@ -165,7 +166,8 @@ constexpr uint32_t kVerifyLogitRegion = kMaxRouterRows * kMaxExperts;
 constexpr uint32_t kVerifyArriveWord = kDecodeGroups * kVerifyLogitRegion;
 constexpr uint32_t kVerifyActWord = kVerifyArriveWord + kDecodeBlocks;
 constexpr uint32_t kVerifyPartWord = kVerifyActWord + kVerifyPairs * kMaxFusedDim;
-constexpr uint32_t kVerifyWords = kVerifyPartWord + kVerifyPairs * kMaxFusedDim;
+constexpr uint32_t kVerifySharedActWord = kVerifyPartWord + kVerifyPairs * kMaxFusedDim;
+constexpr uint32_t kVerifyWords = kVerifySharedActWord + kMaxRouterRows * kMaxFusedDim;
 
 // Pairs (t * k) tsg_prefill_group_pairs_device_noalloc takes: its file-scope
 // rank scratch holds one word per pair.
