@@ -1912,20 +1912,27 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
         const uint32_t wsum = wave_inclusive_scan(w);
         const uint32_t wtot = (uint32_t)__builtin_amdgcn_readlane((int)wsum, 63);
         const uint32_t wsh = SH ? kVerifyUnitBase + kVerifyRowCost * rows : 0u;
+        // 32-bit arithmetic: per <= kMaxFusedDim and the costs sum to at most
+        // 64 pairs' (3 + 1) plus the shared slot's 3 + 8, so (b + 1) * total
+        // < 256 * 4096 * 267 < 2^32
+        static_assert((uint64_t)kDecodeBlocks * kMaxFusedDim *
+                              (kVerifyPairs * (kVerifyUnitBase + kVerifyRowCost) +
+                               kVerifyUnitBase + kVerifyRowCost * kMaxRouterRows) <
+                          (1ull << 32), "verify split in 32 bits");
 #pragma unroll
         for (uint32_t q = 0; q < 4u; ++q) {
             const uint32_t per = q < 2u ? a.f : d;
-            const uint64_t routed = (uint64_t)per * wtot, total = routed + (uint64_t)per * wsh;
-            const uint64_t cpos = (uint64_t)(blockIdx.x + (q & 1u)) * total / kDecodeBlocks;
-            const uint64_t past = __ballot(lane < nsl && (uint64_t)per * wsum > cpos);
+            const uint32_t routed = per * wtot, total = routed + per * wsh;
+            const uint32_t cpos = (blockIdx.x + (q & 1u)) * total / kDecodeBlocks;
+            const uint64_t past = __ballot(lane < nsl && per * wsum > cpos);
             uint32_t unit = (nsl + (SH ? 1u : 0u)) * per;
             if (past) {
                 const uint32_t us = (uint32_t)__builtin_ctzll(past);
                 const uint32_t wu = (uint32_t)__builtin_amdgcn_readlane((int)w, (int)us);
                 const uint32_t pu = (uint32_t)__builtin_amdgcn_readlane((int)wsum, (int)us) - wu;
-                unit = us * per + (uint32_t)((cpos - (uint64_t)per * pu + wu - 1u) / wu);
+                unit = us * per + (cpos - per * pu + wu - 1u) / wu;
             } else if (SH && cpos < total) {
-                unit = nsl * per + (uint32_t)((cpos - routed + wsh - 1u) / wsh);
+                unit = nsl * per + (cpos - routed + wsh - 1u) / wsh;
             }
             if (lane == 0) s_split[q] = q < 2u ? unit : unit & ~1u;
         }
