@@ -1673,7 +1673,10 @@ struct VerifyLds {
 __host__ __device__ __forceinline__ VerifyLds verify_lds(uint32_t rows, uint32_t d, uint32_t f,
                                                          bool sym) {
     VerifyLds l;
-    l.xs = rows * d * 2u;
+    // every region starts on 16 bytes (the rounding changes no offset, d being
+    // a multiple of 64; it lets the compiler read the staged chunks 16 bytes
+    // at a time)
+    l.xs = (rows * d * 2u + 15u) & ~15u;
     l.xsum = l.xs + rows * lds_chunks_halves(d) * 2u;
     l.as = (l.xsum + (sym ? 0u : rows * (d / 32u) * 4u) + 15u) & ~15u;
     l.asum = l.as + 2u * rows * lds_chunks_halves(f) * 2u;
