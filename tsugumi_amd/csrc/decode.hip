@@ -1329,9 +1329,11 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     uint64_t* handoff = global_ptr(a.handoff);
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
     float* xsum = reinterpret_cast<float*>(smem + lds_chunks_halves(d) * 2u);
-    uint16_t* as = reinterpret_cast<uint16_t*>(smem + a.as_off);
-    float* asum = reinterpret_cast<float*>(smem + a.as_off + p2_slot_halves(f) * 2u);
-    float* xe = reinterpret_cast<float*>(smem + a.xe_off);
+    // the host places every region on 16 bytes; the masks let the compiler see
+    // it and read the staged chunks 16 bytes at a time
+    uint16_t* as = reinterpret_cast<uint16_t*>(smem + (a.as_off & ~15u));
+    float* asum = reinterpret_cast<float*>(smem + (a.as_off & ~15u) + p2_slot_halves(f) * 2u);
+    float* xe = reinterpret_cast<float*>(smem + (a.xe_off & ~15u));
     // expert row e's logit is computed once, by block e % kDecodeBlocks
     // (wave e / kDecodeBlocks), and posted to all kDecodeGroups regions; each
     // group polls its own copy, so 32 blocks, not 256, read each word
@@ -1512,8 +1514,9 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
                             });
         }
         if constexpr (SH) {
-            uint16_t* ss = reinterpret_cast<uint16_t*>(smem + a.ss_off);
-            float* ssum = reinterpret_cast<float*>(smem + a.ss_off + p2_slot_halves(a.sh_f) * 2u);
+            uint16_t* ss = reinterpret_cast<uint16_t*>(smem + (a.ss_off & ~15u));
+            float* ssum = reinterpret_cast<float*>(smem + (a.ss_off & ~15u) +
+                                                   p2_slot_halves(a.sh_f) * 2u);
             uint32_t live = 0;
 #pragma unroll
             for (uint32_t k = 0; k < kMaxSharedF / 64u; ++k) live |= lane + 64u * k < a.sh_f ? 1u << k : 0u;
