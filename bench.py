@@ -64,10 +64,10 @@ SUSTAIN_LAYERS = 10  # prefill layers back to back in the sustained graph
 PREFILL_FLOP = 2 * PREFILL_T * TOPK * 3 * F * H  # 194,884,141,056
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode_layer_kernel launch: rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE over `bench.py --traffic-probe` (13,977.69 KiB fetched, 320.09 KiB
+# WRITE_SIZE over `bench.py --traffic-probe` (13,973.6 KiB fetched, 320.09 KiB
 # written per dispatch), scaled by the counters of a plain 64 MiB device copy in
-# the same runs (fetch x 1.9988, write x 1.000).
-TRAFFIC_BYTES = 28936885
+# the same runs (fetch x 1.9992, write x 1.000).
+TRAFFIC_BYTES = 28934411
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
