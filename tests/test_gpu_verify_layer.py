@@ -16,7 +16,8 @@ its reduce, PrefillGroupedRoutedMoETests+Execution.swift:213-310):
 - the shapes the one launch declines;
 - the shared form (tsg_moe_verify_layer_shared, the Qwen family's shared
   expert in the same launch) against tsg_moe_verify_layer +
-  tsg_moe_shared_expert_rows, bit for bit, and the oracle's shared expert.
+  tsg_moe_shared_expert_rows, bit for bit, and the oracle's shared expert,
+  also replayed from a HIP graph.
 """
 import numpy as np
 import pytest
@@ -402,3 +403,46 @@ def test_verify_layer_shared_declines_and_unroutable(tsg, ctx, qwen_layer):
                                    ne, d, f)
     ctx.synchronize()
     assert np.array_equal(host(sout, np.uint16), host(sout0, np.uint16))
+
+
+def test_verify_layer_shared_graph_replays(tsg, ctx, qwen_layer):
+    """The shared form captured once in a HIP graph and replayed with new token
+    rows copied in between: each replay equals tsg_moe_verify_layer +
+    tsg_moe_shared_expert_rows on the same rows."""
+    import torch
+    configure(ctx, 32, "sym")
+    (layer, offs, blobs), d, f, ne, m = qwen_layer, 2048, 512, 256, 3
+    rng = np.random.default_rng(0x5EA)
+    image, soffs, sblob, gate_w = shared_expert_inputs(rng, d, f, "sym", 32)
+    SB, G = dev(image), dev(gate_w)
+    _, rw, es, pes = router_inputs(rng, m, d, ne, d)
+    RW, ES, PES = dev(rw), dev(es), dev(pes)
+    moe = tsg.MoE(ctx, gate_activation="silu")
+    X = empty(m * d)
+    X.copy_(dev(router_inputs(rng, m, d, ne, d)[0]))
+    idx, w, h2 = fused_outs(m, d)
+    sout = empty(m * d, fill=NAN16)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        moe.encode_verify_layer_shared(layer, RW, X, ES, PES, X, d, h2, idx, w, SB, soffs, G,
+                                       sout, m, ne, d, f, stream=stream)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        X.copy_(dev(router_inputs(rng, m, d, ne, d)[0]))
+        h2.fill_(NAN16)
+        sout.fill_(NAN16)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        ctx.synchronize()
+        idx0, w0, h20 = fused_outs(m, d)
+        moe.encode_verify_layer(layer, RW, X, ES, PES, X, d, h20, idx0, w0, m, ne, d, f)
+        sact, sout0 = empty(m * f), empty(m * d)
+        tsg.encode_shared_expert_rows(moe, SB, soffs, X, d, G, sact, sout0, m, d, f)
+        ctx.synchronize()
+        assert np.array_equal(host(idx, np.uint32), host(idx0, np.uint32)), rep
+        assert np.array_equal(host(h2, np.uint16), host(h20, np.uint16)), rep
+        assert np.array_equal(host(sout, np.uint16), host(sout0, np.uint16)), rep
