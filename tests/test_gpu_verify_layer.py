@@ -329,6 +329,32 @@ def test_verify_layer_shared_matches_separate_launches(tsg, ctx, qwen_layer, m, 
             assert rel <= kc.NORTH_STAR, (mm, r, rel)
 
 
+def test_verify_layer_shared_wide_shape(tsg, ctx, gemma_layer):
+    """The shared form at a shape past the compact batches (d = 2816, f = 704,
+    a shared expert of f = 704, SiLU, M = 5): the same bits as
+    tsg_moe_verify_layer + tsg_moe_shared_expert_rows."""
+    configure(ctx, 32, "sym")
+    (layer, offs, blobs), d, f, ne, m = gemma_layer, 2816, 704, 128, 5
+    rng = np.random.default_rng(0x5EB)
+    image, soffs, sblob, gate_w = shared_expert_inputs(rng, d, f, "sym", 32)
+    SB, G = dev(image), dev(gate_w)
+    hidden, rw, es, pes = router_inputs(rng, m, d, ne, d)
+    RW, X, ES, PES = dev(rw), dev(hidden), dev(es), dev(pes)
+    moe = tsg.MoE(ctx, gate_activation="silu")
+    idx0, w0, h20 = fused_outs(m, d)
+    moe.encode_verify_layer(layer, RW, X, ES, PES, X, d, h20, idx0, w0, m, ne, d, f)
+    sact, sout0 = empty(m * f), empty(m * d, fill=NAN16)
+    tsg.encode_shared_expert_rows(moe, SB, soffs, X, d, G, sact, sout0, m, d, f)
+    idx, w, h2 = fused_outs(m, d)
+    sout = empty(m * d, fill=NAN16)
+    moe.encode_verify_layer_shared(layer, RW, X, ES, PES, X, d, h2, idx, w, SB, soffs, G, sout,
+                                   m, ne, d, f)
+    ctx.synchronize()
+    assert np.array_equal(host(idx, np.uint32), host(idx0, np.uint32))
+    assert np.array_equal(host(h2, np.uint16), host(h20, np.uint16))
+    assert np.array_equal(host(sout, np.uint16), host(sout0, np.uint16))
+
+
 def test_verify_layer_shared_affine_every_expert(tsg, ctx):
     """The shared form on a small affine g64 layer of 8 experts (d = f = 320,
     every slot holds every row) with an affine shared expert: the same bits

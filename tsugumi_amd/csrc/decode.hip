@@ -1687,7 +1687,10 @@ __host__ __device__ __forceinline__ VerifyLds verify_lds(uint32_t rows, uint32_t
     return l;
 }
 
-template <int G, bool SYM, int ACT, bool SH>
+template <int G, bool SYM, int ACT, bool SH, bool Q>
+// Q: chunk batches sized for d <= 2048 and f <= 512 (4 chunks a lane for a
+// gate/up row, 2 for a down row, 1 for a shared down row), where the default
+// sizes would carry slots no lane uses; a row's bits do not depend on them.
 // The values the first loads need are leading scalar arguments (14 dwords,
 // preloaded into SGPRs): k_ne_rows = ne | rows << 16, k_d_stride = d |
 // hidden stride << 16.
@@ -1698,6 +1701,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
     __shared__ VerifyLayerArgs a;
     constexpr uint32_t kArgWords = sizeof(VerifyLayerArgs) / 4;
     static_assert(sizeof(VerifyLayerArgs) % 4 == 0 && kArgWords <= kVerifyThreads, "args copy");
+    constexpr int GUB = Q ? 4 : kGUBatch, DB = Q ? 2 : kDBatch, SDB = Q ? 1 : kShDBatch;
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
     const uint32_t arg_word = reinterpret_cast<const uint32_t*>(&a_arg)[min(t, kArgWords - 1u)];
     extern __shared__ __align__(16) uint8_t smem[];
@@ -1978,9 +1982,9 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
         const uint16_t* us = reinterpret_cast<const uint16_t*>(blob + eo.up_s) + (uint64_t)fi * ng;
         const uint16_t* gb = reinterpret_cast<const uint16_t*>(blob + eo.gate_b) + (uint64_t)fi * ng;
         const uint16_t* ub = reinterpret_cast<const uint16_t*>(blob + eo.up_b) + (uint64_t)fi * ng;
-        ChunkBatch<kGUBatch> bg, bu;
-        load_batch<G, SYM, kGUBatch, kGULanes>(gw, gs, gb, 0u, j16, nck_d, bg);
-        load_batch<G, SYM, kGUBatch, kGULanes>(uw, us, ub, 0u, j16, nck_d, bu);
+        ChunkBatch<GUB> bg, bu;
+        load_batch<G, SYM, GUB, kGULanes>(gw, gs, gb, 0u, j16, nck_d, bg);
+        load_batch<G, SYM, GUB, kGULanes>(uw, us, ub, 0u, j16, nck_d, bu);
         uint32_t rt = kRowsInOrder;  // the rows' tokens, 3 bits each
         if (!shp) {
             rt = 0u;
@@ -1994,7 +1998,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
             ag[r] = 0.0f;
             au[r] = 0.0f;
         }
-        gemv_batches_picked2<G, SYM, kGUBatch, kGULanes, (int)kMaxRouterRows>(
+        gemv_batches_picked2<G, SYM, GUB, kGULanes, (int)kMaxRouterRows>(
             gw, gs, gb, uw, us, ub, j16, nck_d, bg, bu, xs, row_h, xsum, rt, m, ag, au);
 #pragma unroll
         for (uint32_t r = 0; r < kMaxRouterRows; ++r) {
@@ -2035,7 +2039,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
     };
     // rows q0 + 2 k and q0 + 2 k + 1 share u; the second row's weights are
     // f / 2 bytes and f / G groups further on
-    const auto dn_pair = [&](uint32_t k, ChunkBatch<kDBatch>& b0, ChunkBatch<kDBatch>& b1) {
+    const auto dn_pair = [&](uint32_t k, ChunkBatch<DB>& b0, ChunkBatch<DB>& b1) {
         DownPair p;
         p.live = 2u * k < nqr;
         const uint32_t q = min(qb0 + 2u * k, nq_all - 2u);
@@ -2046,14 +2050,14 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
         p.w = blob + a.o.down_w + (uint64_t)p.n * (f / 2u);
         p.s = reinterpret_cast<const uint16_t*>(blob + a.o.down_s) + (uint64_t)p.n * ng;
         p.b = reinterpret_cast<const uint16_t*>(blob + a.o.down_b) + (uint64_t)p.n * ng;
-        load_batch<G, SYM, kDBatch, kDLanes>(p.w, p.s, p.b, 0u, j8, nck_f, b0);
-        load_batch<G, SYM, kDBatch, kDLanes>(p.w + f / 2u, p.s + ng, p.b + ng, 0u, j8, nck_f, b1);
+        load_batch<G, SYM, DB, kDLanes>(p.w, p.s, p.b, 0u, j8, nck_f, b0);
+        load_batch<G, SYM, DB, kDLanes>(p.w + f / 2u, p.s + ng, p.b + ng, 0u, j8, nck_f, b1);
         return p;
     };
     constexpr uint32_t kDnPass = 8u * kVerifyWaves;  // row pairs per pass of the block
     const bool dn_a = 16u * wave < nqr;
     DownPair da{};
-    ChunkBatch<kDBatch> da0, da1;
+    ChunkBatch<DB> da0, da1;
     if (dn_a) da = dn_pair(8u * wave + (lane >> 3), da0, da1);
     // SH: the gate logits of the rows this block's shared outputs scale by
     if (SH && nqs != 0 && wave < rows) {
@@ -2106,7 +2110,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
             staged_chunk_sums(as, row_hf, arows, f, asum);
             __syncthreads();
         }
-        const auto dn_run = [&](const DownPair& p, ChunkBatch<kDBatch>& b0, ChunkBatch<kDBatch>& b1) {
+        const auto dn_run = [&](const DownPair& p, ChunkBatch<DB>& b0, ChunkBatch<DB>& b1) {
             const bool hi = p.u != u_lo;
             const uint32_t st = hi ? st_hi : st_lo, m = hi ? m_hi : m_lo;
             const uint32_t ng = f / G;
@@ -2116,7 +2120,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
                 a0[r] = 0.0f;
                 a1[r] = 0.0f;
             }
-            gemv_batches_picked2<G, SYM, kDBatch, kDLanes, (int)kMaxRouterRows>(
+            gemv_batches_picked2<G, SYM, DB, kDLanes, (int)kMaxRouterRows>(
                 p.w, p.s, p.b, p.w + f / 2u, p.s + ng, p.b + ng, j8, nck_f, b0, b1,
                 as + (hi ? m_lo : 0u) * row_hf, row_hf, asum + (hi ? m_lo : 0u) * nck_f,
                 kRowsInOrder, m, a0, a1);
@@ -2133,7 +2137,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
         if (dn_a) dn_run(da, da0, da1);
         for (uint32_t k0 = kDnPass; 2u * k0 < nqr; k0 += kDnPass) {
             if (2u * (k0 + 8u * wave) >= nqr) break;  // wave-uniform
-            ChunkBatch<kDBatch> dc0, dc1;
+            ChunkBatch<DB> dc0, dc1;
             const DownPair dc = dn_pair(k0 + 8u * wave + (lane >> 3), dc0, dc1);
             dn_run(dc, dc0, dc1);
         }
@@ -2149,16 +2153,16 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_layer_kernel(
                 const uint8_t* w = sb + a.sh_o.down_w + (uint64_t)n * (f / 2u);
                 const uint16_t* sc = reinterpret_cast<const uint16_t*>(sb + a.sh_o.down_s) + (uint64_t)n * ng;
                 const uint16_t* bi = reinterpret_cast<const uint16_t*>(sb + a.sh_o.down_b) + (uint64_t)n * ng;
-                ChunkBatch<kShDBatch> b0, b1;
-                load_batch<G, SYM, kShDBatch, kGULanes>(w, sc, bi, 0u, j16, nck_f, b0);
-                load_batch<G, SYM, kShDBatch, kGULanes>(w + f / 2u, sc + ng, bi + ng, 0u, j16, nck_f, b1);
+                ChunkBatch<SDB> b0, b1;
+                load_batch<G, SYM, SDB, kGULanes>(w, sc, bi, 0u, j16, nck_f, b0);
+                load_batch<G, SYM, SDB, kGULanes>(w + f / 2u, sc + ng, bi + ng, 0u, j16, nck_f, b1);
                 float a0[kMaxRouterRows], a1[kMaxRouterRows];
 #pragma unroll
                 for (uint32_t r = 0; r < kMaxRouterRows; ++r) {
                     a0[r] = 0.0f;
                     a1[r] = 0.0f;
                 }
-                gemv_batches_picked2<G, SYM, kShDBatch, kGULanes, (int)kMaxRouterRows>(
+                gemv_batches_picked2<G, SYM, SDB, kGULanes, (int)kMaxRouterRows>(
                     w, sc, bi, w + f / 2u, sc + ng, bi + ng, j16, nck_f, b0, b1,
                     as + sh_row0 * row_hf, row_hf, asum + sh_row0 * nck_f, kRowsInOrder, rows, a0,
                     a1);
@@ -2814,12 +2818,12 @@ extern "C" tsg_status tsg_prefill_router_bf16(tsg_moe* moe, tsg_stream stream,
 namespace tsg {
 namespace {
 
-template <int G, bool SYM, int ACT, bool SH>
+template <int G, bool SYM, int ACT, bool SH, bool Q = false>
 tsg_status launch_verify(tsg_moe* moe, hipStream_t stream, const uint16_t* router_w,
                          const uint16_t* hidden, const uint16_t* es, const uint16_t* pes,
                          const uint16_t* x, uint32_t stride, const VerifyLayerArgs& a) {
     const size_t lds = verify_lds(a.rows, a.d, a.f, SYM).bytes;
-    auto kern = verify_layer_kernel<G, SYM, ACT, SH>;
+    auto kern = verify_layer_kernel<G, SYM, ACT, SH, Q>;
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
         (void)hipGetLastError();
@@ -2949,9 +2953,14 @@ extern "C" tsg_status tsg_moe_verify_layer_shared(
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
     hipStream_t s = as_stream(stream);
-#define TSG_VLS(GG, SS)                                                                  \
-    return launch_verify<GG, SS, TSG_ACT_SILU, true>(moe, s, router_w, router_hidden, es, \
-                                                     pes, x, hidden_stride, a)
+    // the Qwen family's shapes (d = 2048, f = 512) take the compact batches
+    const bool q = d <= 2048u && f <= 512u;
+#define TSG_VLS(GG, SS)                                                                        \
+    return q ? launch_verify<GG, SS, TSG_ACT_SILU, true, true>(moe, s, router_w, router_hidden, \
+                                                               es, pes, x, hidden_stride, a)    \
+             : launch_verify<GG, SS, TSG_ACT_SILU, true, false>(moe, s, router_w,               \
+                                                                router_hidden, es, pes, x,      \
+                                                                hidden_stride, a)
     if (ctx->group_size == 32) {
         if (sym) TSG_VLS(32, true);
         TSG_VLS(32, false);
