@@ -579,6 +579,7 @@ def test_fused_decode_layer_matches_three_launches(tsg, ctx, d, f, ne, group, sc
     (2048, 512, 256, 512, 32, "sym"),     # the Qwen3.5-MoE-35B-A3B shape
     (1024, 512, 64, 256, 64, "affine"),
     (1024, 256, 64, 1024, 32, "sym"),     # shared_f > 512: the two-step form
+    (2816, 704, 128, 512, 32, "sym"),     # d > 2048: the default chunk batches
 ])
 def test_decode_layer_shared_expert(tsg, ctx, d, f, ne, sf, group, scheme):
     """The Qwen-family layer (QwenForwardRunner.swift:1548-1608): one call gives

@@ -319,15 +319,15 @@ __device__ __forceinline__ GULane gu_lane(const Src& src, const tsg_expert_offse
 // Gate/up dot products of one pair (x staged in LDS) and the activation
 // half(act(gate) * up), the pair's entry acts[slot * f + fr]. Returns true on
 // the one lane that holds it (in `out`). `bt` holds the first batch.
-template <int G, bool SYM, int ACT>
-__device__ __forceinline__ bool phase1_compute(const GULane& l, ChunkBatch<kGUBatch>& bt,
+template <int G, bool SYM, int ACT, int KB = kGUBatch>
+__device__ __forceinline__ bool phase1_compute(const GULane& l, ChunkBatch<KB>& bt,
                                                const uint16_t* xs, const float* xsum,
                                                uint32_t d, uint16_t& out) {
     const uint32_t j = threadIdx.x & 15u;
     const bool is_up = (threadIdx.x >> 4) & 1u;
     const uint32_t nchunks = d / 32u;
     float acc[1] = {0.0f};
-    gemv_batches<G, SYM, kGUBatch, kGULanes, 1>(l.w, l.s, l.b, j, nchunks, bt, xs, 0u, xsum, 1u, acc);
+    gemv_batches<G, SYM, KB, kGULanes, 1>(l.w, l.s, l.b, j, nchunks, bt, xs, 0u, xsum, 1u, acc);
     acc[0] = group16_sum(acc[0]);
     const float up = shfl_xor(acc[0], 16);  // gate lanes receive the up sum
     out = f32_to_f16(gate_activation<ACT>(acc[0]) * up);
@@ -579,14 +579,14 @@ struct DecodeLayerArgs {
 // Down row `row` of one slot on 8 lanes (lane = 8 r + j of the wave): the
 // per-slot value of phase2_body, the same chunk split and the same sum, so
 // the combine below reproduces the unfused path bit for bit.
-template <int G, bool SYM>
+template <int G, bool SYM, int KB = kDBatch>
 __device__ __forceinline__ float slot_down_row(const uint8_t* w, const uint16_t* sc,
                                                const uint16_t* bi, const uint16_t* as,
                                                const float* asum, uint32_t f,
-                                               ChunkBatch<kDBatch>& bt) {
+                                               ChunkBatch<KB>& bt) {
     const uint32_t j = threadIdx.x & 7u, nchunks = f / 32u;
     float acc[1] = {0.0f};
-    gemv_batches<G, SYM, kDBatch, kDLanes, 1>(w, sc, bi, j, nchunks, bt, as, 0u, asum, 1u, acc);
+    gemv_batches<G, SYM, KB, kDLanes, 1>(w, sc, bi, j, nchunks, bt, as, 0u, asum, 1u, acc);
     return group8_sum(acc[0]);
 }
 
@@ -1220,7 +1220,10 @@ __global__ __launch_bounds__(256) void router_int8_kernel(
 // 1024-thread bound allows, and does not spill.
 __host__ __device__ constexpr uint32_t decode_layer_max_threads(bool sh) { return sh ? 768u : 1024u; }
 
-template <int G, bool SYM, int ACT, bool SH, bool R8>
+template <int G, bool SYM, int ACT, bool SH, bool R8, bool Q>
+// Q: chunk batches sized for d <= 2048 and f <= 512 (4 chunks a lane for a
+// gate/up row, 2 for a down row), where the default sizes carry slots no lane
+// uses; a row's bits do not depend on them.
 // The values the first phase's loads need come as separate leading scalar
 // arguments (14 dwords) so that, built with kernarg preloading, the dispatch
 // hands them over in SGPRs: the loads go out with no memory round trip before
@@ -1231,6 +1234,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     const uint16_t* k_router_w, const uint16_t* k_hidden, const uint16_t* k_es,
     const uint16_t* k_pes, const uint16_t* k_x, uint32_t* k_sync, uint32_t k_ne_rr,
     uint32_t k_d_thr, DecodeLayerArgs a_arg) {
+    constexpr int GUB = Q ? 4 : kGUBatch, DB = Q ? 2 : kDBatch;
     // The arguments are copied to LDS once: under SGPR pressure the compiler
     // re-reads kernel arguments instead of spilling, and a kernarg reload in
     // a loop costs a memory round trip each time; an LDS copy costs cycles.
@@ -1377,7 +1381,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     // SH: this block's two shared gate/up pairs (lanes 0..31 pair 2b, 32..63
     // pair 2b + 1; 16 lanes per row) and the gate logit, while the logits are
     // gathered and ranked
-    ChunkBatch<kGUBatch> sbt;
+    ChunkBatch<GUB> sbt;
     GULane sl{};
     float sh_scale = 0.0f;
     if constexpr (SH) {
@@ -1391,7 +1395,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
             sl.b = reinterpret_cast<const uint16_t*>(sb + (is_up ? a.sh_o.up_b : a.sh_o.gate_b)) + (uint64_t)pr * ng;
             sl.fr = p;
             sl.live = live;
-            load_batch<G, SYM, kGUBatch, kGULanes>(sl.w, sl.s, sl.b, 0u, lane & 15u, d / 32u, sbt);
+            load_batch<G, SYM, GUB, kGULanes>(sl.w, sl.s, sl.b, 0u, lane & 15u, d / 32u, sbt);
             sh_scale = qwen_sigmoid(gate_logit_wave(xg, global_ptr(a.sh_gate_w), d));
         }
     }
@@ -1434,14 +1438,14 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     const uint8_t* dw = blob + a.o.down_w + (uint64_t)rr * (f / 2u);
     const uint16_t* dsc = reinterpret_cast<const uint16_t*>(blob + a.o.down_s) + (uint64_t)rr * fgroups;
     const uint16_t* dbi = reinterpret_cast<const uint16_t*>(blob + a.o.down_b) + (uint64_t)rr * fgroups;
-    ChunkBatch<kDBatch> dbt;
+    ChunkBatch<DB> dbt;
     // Loads, the slot weights and the dot products in one straight-line
     // region per wave (wave 0 is always a gate/up wave: pairs >= 1), so the
     // waits before each chunk's dot product count only the loads after it.
     if (gu_wave) {
-        ChunkBatch<kGUBatch> gbt;
+        ChunkBatch<GUB> gbt;
         const GULane l = gu_lane(src, a.o, d, G, pair_live ? grp : 0u, pair_live ? fr : 0u, pair_live);
-        load_batch<G, SYM, kGUBatch, kGULanes>(l.w, l.s, l.b, 0u, t & 15u, d / 32u, gbt);
+        load_batch<G, SYM, GUB, kGULanes>(l.w, l.s, l.b, 0u, t & 15u, d / 32u, gbt);
         // the slot weights (needed only by the combine) while the loads fly
         if (wave == 0) {
             const uint32_t r = lane & (kTopK - 1u);
@@ -1452,7 +1456,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
             s_wout = w;
         }
         uint16_t act;
-        if (phase1_compute<G, SYM, ACT>(l, gbt, xs, xsum, d, act)) {
+        if (phase1_compute<G, SYM, ACT, GUB>(l, gbt, xs, xsum, d, act)) {
             global_ptr(a.acts)[grp * f + fr] = act;
             st_coherent(gacts + fr, tagged(tag, act));
         }
@@ -1468,7 +1472,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
             // act = half(silu(half(gate . x)) * half(up . x)) (shared_gate_up_kernel)
             const uint32_t j = lane & 15u, nck = d / 32u;
             float acc[1] = {0.0f};
-            gemv_batches<G, SYM, kGUBatch, kGULanes, 1>(sl.w, sl.s, sl.b, j, nck, sbt, xs, 0u, xsum, 1u,
+            gemv_batches<G, SYM, GUB, kGULanes, 1>(sl.w, sl.s, sl.b, j, nck, sbt, xs, 0u, xsum, 1u,
                                                         acc);
             const float g = group16_sum(acc[0]);
             const float u = shfl_xor(g, 16);
@@ -1496,7 +1500,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
         }
     }
 
-    if (down_wave) load_batch<G, SYM, kDBatch, kDLanes>(dw, dsc, dbi, 0u, lane & 7u, f / 32u, dbt);
+    if (down_wave) load_batch<G, SYM, DB, kDLanes>(dw, dsc, dbi, 0u, lane & 7u, f / 32u, dbt);
 
     // once this block's gate/up work is out, the last wave reads the slot's
     // activation row into LDS as its words arrive
@@ -1558,7 +1562,7 @@ __global__ __launch_bounds__(decode_layer_max_threads(SH)) void decode_layer_ker
     }
     uint64_t* parts = handoff + kMaxFusedDim;  // slot g's partials at g * kHandoffWords
     if (down_wave) {
-        const float v = slot_down_row<G, SYM>(dw, dsc, dbi, as, asum, f, dbt);
+        const float v = slot_down_row<G, SYM, DB>(dw, dsc, dbi, as, asum, f, dbt);
         if ((lane & 7u) == 0 && row_live)
             st_coherent(parts + (size_t)grp * kHandoffWords + row, tagged(tag, __float_as_uint(v)));
     }
@@ -2351,7 +2355,7 @@ tsg_status phase2_dispatch(tsg_moe* moe, hipStream_t stream, const BlobSource& s
 // The fused one-launch decode layer, when every block fits on the device at
 // once (the rendezvous need all blocks resident). Returns TSG_ERR_DECLINED
 // otherwise and the caller runs the three-kernel sequence.
-template <int G, bool SYM, int ACT, bool SH, bool R8>
+template <int G, bool SYM, int ACT, bool SH, bool R8, bool Q = false>
 tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
     const auto up64 = [](uint32_t v) { return (v + 63u) / 64u * 64u; };
     uint32_t threads = 32u * a.pairs;                               // gate/up pairs
@@ -2368,7 +2372,7 @@ tsg_status launch_fused(tsg_moe* moe, hipStream_t stream, DecodeLayerArgs a) {
         a.ss_off = (uint32_t)((lds + 15u) & ~(size_t)15u);
         lds = a.ss_off + p2_slot_halves(a.sh_f) * 2u + (SYM ? 0u : (a.sh_f / 32u) * 4u);
     }
-    auto kern = decode_layer_kernel<G, SYM, ACT, SH, R8>;
+    auto kern = decode_layer_kernel<G, SYM, ACT, SH, R8, Q>;
     int per_cu = 0;
     if (threads > decode_layer_max_threads(SH) || a.ne > kMaxExperts || a.f > kMaxFusedDim || a.d > kMaxFusedDim ||
         (a.rows + kDecodeGroups - 1u) / kDecodeGroups > kMaxCombineRows ||
@@ -2389,6 +2393,16 @@ tsg_status fused_dispatch(tsg_moe* moe, hipStream_t stream, const DecodeLayerArg
     const tsg_ctx* ctx = moe->ctx;
     const bool sym = ctx->scheme == TSG_SYM;
     const bool silu = moe->activation == TSG_ACT_SILU;
+    if constexpr (SH && !R8) {
+        // the Qwen family's shapes (d = 2048, f = 512) take the compact batches
+        if (silu && a.d <= 2048u && a.f <= 512u) {
+            if (ctx->group_size == 32)
+                return sym ? launch_fused<32, true, TSG_ACT_SILU, true, false, true>(moe, stream, a)
+                           : launch_fused<32, false, TSG_ACT_SILU, true, false, true>(moe, stream, a);
+            return sym ? launch_fused<64, true, TSG_ACT_SILU, true, false, true>(moe, stream, a)
+                       : launch_fused<64, false, TSG_ACT_SILU, true, false, true>(moe, stream, a);
+        }
+    }
 #define TSG_FU(GG, SS)                                                             \
     return silu ? launch_fused<GG, SS, TSG_ACT_SILU, SH, R8>(moe, stream, a)       \
                 : launch_fused<GG, SS, TSG_ACT_GELU_TANH, SH, R8>(moe, stream, a)
