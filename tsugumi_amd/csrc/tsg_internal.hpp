@@ -359,11 +359,16 @@ __host__ __device__ __forceinline__ uint32_t paired_pos(uint32_t k) {
 // (moe.metal:116-118). 0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)) exactly, so
 // the GELU takes one exp (v_exp_f32 on a pre-scaled argument) and one
 // reciprocal instead of a full tanhf; both are accurate to a few fp32 ulp of
-// the (1 + tanh) factor, the precision of the reference's fast-math tanh.
+// the (1 + tanh) factor, the precision of the reference's fast-math tanh. The
+// SiLU x / (1 + exp(-x)) takes the same exp and reciprocal (a few fp32 ulp, as
+// the reference's fast-math exp and division) instead of expf and an IEEE
+// division. Every path that applies the routed experts' activation (decode,
+// the rows path, the grouped GEMM) calls this function, so they agree bit for
+// bit; the Qwen shared expert's SiLU (qwen.metal) is qwen_silu.
 template <int ACT>
 __device__ __forceinline__ float gate_activation(float x) {
     if constexpr (ACT == TSG_ACT_SILU) {
-        return x / (1.0f + expf(-x));
+        return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
     } else {
         const float x3 = x * x * x;
         float inner = 0.7978845608028654f * (x + 0.044715f * x3);
